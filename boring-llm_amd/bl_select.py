@@ -1,0 +1,205 @@
+"""Python binding of libbl_select.so (the C ABI in include/bl_select.h).
+
+Mirrors the reference's sampler interface for one decode step (src/server.br:939-1037,
+src/sampling.br sample/sample_with_probs, SamplingParams of src/model.br:1565-1589): per-request
+parameters, a slot per request, and a step that returns token ids, logprobs and alternatives.
+Logits are device tensors; this module never falls back to a host implementation — it raises when
+the HIP library is missing.
+"""
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libbl_select.so")
+
+BL_OK, BL_EPARAM, BL_EDEVICE, BL_EEMPTY = 0, -1, -2, -3
+BL_EGRAMMAR, BL_EGRAMMAR_DEAD, BL_EGRAMMAR_REJECT, BL_EGRAMMAR_AMBIG = -4, -5, -6, -7
+BL_EUNSUPPORTED, BL_ETIE = -8, -9
+
+
+class BLError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"{msg} (code {code})")
+        self.code = code
+
+
+class Params(C.Structure):
+    """bl_params: SamplingParams + server extras; defaults = greedy_params() (src/model.br:1586-1589)."""
+    _fields_ = [
+        ("temperature", C.c_float), ("dynatemp_range", C.c_float), ("dynatemp_exponent", C.c_float),
+        ("top_n_sigma", C.c_float), ("top_k", C.c_int32), ("typical_p", C.c_float), ("top_p", C.c_float),
+        ("min_p", C.c_float), ("xtc_probability", C.c_float), ("xtc_threshold", C.c_float),
+        ("min_keep", C.c_int32), ("repeat_penalty", C.c_float), ("repeat_last_n", C.c_int32),
+        ("dry_multiplier", C.c_float), ("dry_base", C.c_float), ("dry_allowed_length", C.c_int32),
+        ("dry_penalty_last_n", C.c_int32), ("frequency_penalty", C.c_float), ("presence_penalty", C.c_float),
+        ("logprobs", C.c_int32), ("n_probs", C.c_int32), ("post_sampling_probs", C.c_int32),
+        ("ignore_eos", C.c_int32), ("final_softcap", C.c_float), ("logit_mul", C.c_float),
+    ]
+
+    def __init__(self, **kw):
+        super().__init__()
+        lib().bl_params_default(C.byref(self))
+        for k, v in kw.items():
+            setattr(self, k, v)
+
+
+EXPORTS = [
+    "bl_params_default", "bl_create", "bl_destroy", "bl_last_error", "bl_set_stream", "bl_set_eog",
+    "bl_slot_reset", "bl_slot_rng", "bl_slot_commit", "bl_sample_step", "bl_bind_rows", "bl_sample_step_async",
+    "bl_spec_verify", "bl_synth_logits", "bl_math_digest", "bl_workload_ids", "bl_workload_bias",
+    "bl_workload_drafts",
+]
+
+_lib = None
+
+
+def lib():
+    """Load the HIP library; raises if it has not been built (no host fallback exists)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is missing: build it with boring-llm_amd/build.sh")
+        L = C.CDLL(LIB_PATH)
+        i32p, f32p, u64p = C.POINTER(C.c_int32), C.POINTER(C.c_float), C.POINTER(C.c_uint64)
+        L.bl_params_default.argtypes = [C.c_void_p]
+        L.bl_params_default.restype = None
+        L.bl_create.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_void_p)]
+        L.bl_destroy.argtypes = [C.c_void_p]
+        L.bl_destroy.restype = None
+        L.bl_last_error.restype = C.c_char_p
+        L.bl_set_stream.argtypes = [C.c_void_p, C.c_void_p]
+        L.bl_set_eog.argtypes = [C.c_void_p, C.c_int32, i32p, C.c_int]
+        L.bl_slot_reset.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_uint64, i32p, C.c_int, i32p, C.c_int,
+                                    i32p, f32p, C.c_int]
+        L.bl_slot_rng.argtypes = [C.c_void_p, C.c_int, u64p]
+        L.bl_slot_commit.argtypes = [C.c_void_p, C.c_int, i32p, C.c_int]
+        L.bl_sample_step.argtypes = [C.c_void_p, i32p, C.c_int, C.c_void_p, C.c_int64, i32p, f32p, i32p, f32p, C.c_int]
+        L.bl_bind_rows.argtypes = [C.c_void_p, i32p, C.c_int]
+        L.bl_sample_step_async.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p,
+                                           C.c_void_p, C.c_void_p, C.c_int]
+        L.bl_spec_verify.argtypes = [C.c_void_p, i32p, C.c_int, C.c_int, C.c_void_p, C.c_int64, i32p, i32p, i32p]
+        L.bl_synth_logits.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_int, C.c_int64, C.c_int64, C.c_int,
+                                      C.c_int]
+        L.bl_math_digest.argtypes = [C.c_void_p, C.c_int, C.c_uint32, C.c_int, u64p]
+        L.bl_workload_ids.argtypes = [C.c_int, C.c_int, C.c_int64, C.c_int, C.c_int, C.c_int, i32p]
+        L.bl_workload_bias.argtypes = [C.c_int, C.c_int64, C.c_int, C.c_int, C.c_int, C.c_float, C.c_float, i32p,
+                                       f32p]
+        L.bl_workload_drafts.argtypes = [C.c_int64, C.c_int64, C.c_int, i32p, C.c_int, C.c_int, i32p]
+        _lib = L
+    return _lib
+
+
+def _arr(ctype, xs):
+    xs = list(xs)
+    return (ctype * max(len(xs), 1))(*xs), len(xs)
+
+
+def _check(rc):
+    if rc != BL_OK:
+        raise BLError(rc, lib().bl_last_error().decode())
+
+
+class Context:
+    """One device context (bl_create): `max_slots` requests, up to `max_rows` rows per call."""
+
+    def __init__(self, vocab, max_slots=8, max_rows=8, device=0):
+        self.vocab = vocab
+        self.h = C.c_void_p()
+        _check(lib().bl_create(device, max_slots, max_rows, vocab, C.byref(self.h)))
+
+    def close(self):
+        if self.h:
+            lib().bl_destroy(self.h)
+            self.h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_eog(self, eos_id, eog_ids=()):
+        a, n = _arr(C.c_int32, eog_ids)
+        _check(lib().bl_set_eog(self.h, eos_id, a, n))
+
+    def slot_reset(self, slot, params, rng_state, history=(), reply=(), bias=None):
+        h, nh = _arr(C.c_int32, history)
+        r, nr = _arr(C.c_int32, reply)
+        bias = bias or {}
+        bi, nb = _arr(C.c_int32, bias.keys())
+        bv, _ = _arr(C.c_float, bias.values())
+        _check(lib().bl_slot_reset(self.h, slot, C.byref(params), C.c_uint64(rng_state), h, nh, r, nr, bi, bv, nb))
+
+    def slot_rng(self, slot):
+        s = C.c_uint64()
+        _check(lib().bl_slot_rng(self.h, slot, C.byref(s)))
+        return s.value
+
+    def commit(self, slot, toks):
+        a, n = _arr(C.c_int32, toks)
+        _check(lib().bl_slot_commit(self.h, slot, a, n))
+
+    def sample_step(self, slots, d_logits_ptr, ld, top_stride=0):
+        """Synchronous step; returns (tokens, logprobs, top_ids, top_logprobs) as Python lists."""
+        B = len(slots)
+        s, _ = _arr(C.c_int32, slots)
+        tok = (C.c_int32 * B)()
+        lp = (C.c_float * B)()
+        ti = (C.c_int32 * max(B * top_stride, 1))()
+        tl = (C.c_float * max(B * top_stride, 1))()
+        _check(lib().bl_sample_step(self.h, s, B, C.c_void_p(d_logits_ptr), ld, tok, lp, ti, tl, top_stride))
+        tops = [list(ti[b * top_stride:(b + 1) * top_stride]) for b in range(B)]
+        tlps = [list(tl[b * top_stride:(b + 1) * top_stride]) for b in range(B)]
+        return list(tok), list(lp), tops, tlps
+
+    def bind_rows(self, slots):
+        s, n = _arr(C.c_int32, slots)
+        _check(lib().bl_bind_rows(self.h, s, n))
+
+    def sample_step_async(self, B, d_logits_ptr, ld, d_tok, d_lp=0, d_top_ids=0, d_top_lp=0, top_stride=0):
+        _check(lib().bl_sample_step_async(self.h, B, C.c_void_p(d_logits_ptr), ld, C.c_void_p(d_tok),
+                                          C.c_void_p(d_lp), C.c_void_p(d_top_ids), C.c_void_p(d_top_lp), top_stride))
+
+    def spec_verify(self, slots, k, d_rows_ptr, ld, drafts):
+        B = len(slots)
+        s, _ = _arr(C.c_int32, slots)
+        d, _ = _arr(C.c_int32, drafts)
+        tok = (C.c_int32 * (B * (k + 1)))()
+        acc = (C.c_int32 * B)()
+        _check(lib().bl_spec_verify(self.h, s, B, k, C.c_void_p(d_rows_ptr), ld, d, tok, acc))
+        return list(tok), list(acc)
+
+    def synth_logits(self, d_out_ptr, ld, cfg, seed, step, rows, vocab):
+        _check(lib().bl_synth_logits(self.h, C.c_void_p(d_out_ptr), ld, cfg, seed, step, rows, vocab))
+
+    def math_digest(self, fn, first_block, n_blocks):
+        out = (C.c_uint64 * n_blocks)()
+        _check(lib().bl_math_digest(self.h, fn, first_block, n_blocks, out))
+        return list(out)
+
+
+def workload_ids(kind, cfg, seed, row, n, vocab):
+    out = (C.c_int32 * max(n, 1))()
+    _check(lib().bl_workload_ids(kind, cfg, seed, row, n, vocab, out))
+    return list(out[:n])
+
+
+def workload_bias(cfg, seed, row, n, vocab, lo, hi):
+    ids = (C.c_int32 * max(n, 1))()
+    vals = (C.c_float * max(n, 1))()
+    _check(lib().bl_workload_bias(cfg, seed, row, n, vocab, lo, hi, ids, vals))
+    return dict(zip(ids[:n], vals[:n]))
+
+
+def workload_drafts(seed, step, seq, argmax, vocab):
+    k = len(argmax)
+    a, _ = _arr(C.c_int32, argmax)
+    out = (C.c_int32 * max(k, 1))()
+    _check(lib().bl_workload_drafts(seed, step, seq, a, k, vocab, out))
+    return list(out[:k])
+
+
+def seed_rng(seed):
+    """seed_rng of src/sampling.br:35-40 (the initial xorshift state for a request seed)."""
+    K = 88172645463325252
+    return K if seed == 0 else (seed & 0xFFFFFFFFFFFFFFFF) ^ K

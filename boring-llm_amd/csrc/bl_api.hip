@@ -1,0 +1,598 @@
+/*
+ * bl_api.hip — host side of libbl_select: contexts, per-slot state upload, the C ABI of
+ * include/bl_select.h, and the launch sequence of a step.
+ */
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/bl_select.h"
+#include "bl_internal.h"
+#include "bl_math.h"
+#include "bl_workload.h"
+
+void bl_launch_step(const bl_dev &d, const float *logits, int64_t ld, const bl_rows &rows, int B, bool need_exp,
+                    hipStream_t s);
+void bl_launch_synth(float *out, int64_t ld, int cfg, int64_t seed, int64_t step, int rows, int V, hipStream_t s);
+void bl_launch_math_digest(int fn, uint32_t first_block, int n_blocks, unsigned long long *out, hipStream_t s);
+
+static thread_local std::string g_err;
+
+static int fail(int code, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+#define HIPCHK(x)                                                                   \
+  do {                                                                              \
+    hipError_t e_ = (x);                                                            \
+    if (e_ != hipSuccess) return fail(BL_EDEVICE, "%s: %s", #x, hipGetErrorString(e_)); \
+  } while (0)
+
+struct bl_ctx {
+  int device = 0;
+  hipStream_t own = nullptr, stream = nullptr;
+  bl_dev d{};
+  std::vector<bl_slot_dev> host_slots;
+  std::vector<bool> slot_ready;
+  /* row table + outputs */
+  int32_t *d_slot = nullptr, *d_skip = nullptr, *d_tok = nullptr, *d_status = nullptr, *d_top_ids = nullptr;
+  float *d_lp = nullptr, *d_top_lp = nullptr;
+  int32_t *h_slot = nullptr, *h_tok = nullptr, *h_status = nullptr, *h_top_ids = nullptr, *h_skip = nullptr;
+  float *h_lp = nullptr, *h_top_lp = nullptr;
+  int32_t *d_commit_toks = nullptr;
+  int bound_B = 0;
+  std::vector<void *> allocs;
+};
+
+template <class T>
+static hipError_t dalloc(bl_ctx *c, T **p, size_t n) {
+  hipError_t e = hipMalloc((void **)p, n * sizeof(T) + 16);
+  if (e == hipSuccess) c->allocs.push_back(*p);
+  return e;
+}
+
+/* ------------------------------------------------------------------ commit kernel */
+/* tokens.push / reply_tokens.push for externally chosen tokens (one thread: a handful of writes) */
+__global__ void bl_k_commit(bl_dev d, int slot, const int32_t *toks, int n, int rng_draws) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  bl_slot_dev &sp = d.slots[slot];
+  const int V = d.vocab;
+  const int64_t so = (int64_t)slot * V;
+  uint32_t *tw = d.touched + (int64_t)slot * d.words;
+  for (int i = 0; i < n; i++) {
+    int32_t tok = toks[i];
+    if (tok < 0 || tok >= V) continue;
+    bool is_eog = false;
+    for (int k = 0; k < d.n_eog; k++) is_eog |= d.eog[k] == tok;
+    sp.n_tokens += 1;
+    if (sp.rep_on) {
+      int rl = sp.repeat_last_n;
+      if (rl > 0) {
+        int32_t *ring = d.ring + (int64_t)slot * BL_WCAP;
+        if (sp.win_len == rl) {
+          int32_t old = ring[sp.win_head];
+          d.wcnt[so + old] -= 1;
+          ring[sp.win_head] = tok;
+          sp.win_head = (sp.win_head + 1) % rl;
+        } else {
+          ring[(sp.win_head + sp.win_len) % rl] = tok;
+          sp.win_len += 1;
+        }
+      }
+      d.wcnt[so + tok] += 1;
+      tw[tok >> 5] |= 1u << (tok & 31);
+    }
+    if (!is_eog) {
+      sp.n_reply += 1;
+      if (sp.fp_on) {
+        d.cnt[so + tok] += 1;
+        tw[tok >> 5] |= 1u << (tok & 31);
+      }
+    }
+  }
+  for (int k = 0; k < rng_draws; k++) sp.rng = bl_xorshift(sp.rng);
+}
+
+__global__ void bl_k_bump(float *out, const int32_t *ids, int n, float add) {
+  int i = threadIdx.x;
+  if (i < n) out[ids[i]] = out[ids[i]] + add;
+}
+
+extern "C" {
+
+const char *bl_last_error(void) { return g_err.c_str(); }
+
+void bl_params_default(bl_params *p) {
+  memset(p, 0, sizeof *p);
+  p->temperature = 0.0f;
+  p->dynatemp_range = 0.0f;
+  p->dynatemp_exponent = 1.0f;
+  p->top_n_sigma = -1.0f;
+  p->top_k = 0;
+  p->typical_p = 1.0f;
+  p->top_p = 1.0f;
+  p->min_p = 0.0f;
+  p->xtc_probability = 0.0f;
+  p->xtc_threshold = 0.1f;
+  p->min_keep = 0;
+  p->repeat_penalty = 1.0f;
+  p->repeat_last_n = 64;
+  p->dry_multiplier = 0.0f;
+  p->dry_base = 1.75f;
+  p->dry_allowed_length = 2;
+  p->dry_penalty_last_n = 64;
+  p->final_softcap = 0.0f;
+  p->logit_mul = 1.0f;
+}
+
+int bl_create(int device, int max_slots, int max_rows, int vocab, bl_ctx **out) {
+  if (!out || max_slots <= 0 || max_rows <= 0 || vocab <= 0)
+    return fail(BL_EPARAM, "bl_create: invalid sizes (slots %d, rows %d, vocab %d)", max_slots, max_rows, vocab);
+  bl_ctx *c = new bl_ctx;
+  c->device = device;
+  hipError_t e = hipSetDevice(device);
+  if (e != hipSuccess) {
+    delete c;
+    return fail(BL_EDEVICE, "hipSetDevice(%d): %s", device, hipGetErrorString(e));
+  }
+  bl_dev &d = c->d;
+  d.vocab = vocab;
+  d.nc = (vocab + BL_CH - 1) / BL_CH;
+  d.max_slots = max_slots;
+  d.max_rows = max_rows;
+  d.words = (vocab + 31) / 32;
+  const size_t V = (size_t)vocab, S = (size_t)max_slots, R = (size_t)max_rows;
+  size_t P2 = 1;
+  while (P2 < V) P2 <<= 1;
+  const size_t G = V / 64 + 64;
+#define ALLOC(p, n)                                   \
+  do {                                                \
+    if (dalloc(c, &(p), (n)) != hipSuccess) {         \
+      bl_destroy(c);                                  \
+      return fail(BL_EDEVICE, "hipMalloc failed (%s)", #p); \
+    }                                                 \
+  } while (0)
+  ALLOC(d.slots, S);
+  ALLOC(d.touched, S * d.words);
+  ALLOC(d.flags, S * V);
+  ALLOC(d.bias, S * V);
+  ALLOC(d.cnt, S * V);
+  ALLOC(d.wcnt, S * V);
+  ALLOC(d.ring, S * BL_WCAP);
+  ALLOC(d.eog, 1024);
+  ALLOC(d.eff, R * V);
+  ALLOC(d.c_max, R * d.nc);
+  ALLOC(d.c_arg, R * d.nc);
+  ALLOC(d.c_sum, R * d.nc);
+  ALLOC(d.cand_v, R * d.nc * BL_KSEL_MAX);
+  ALLOC(d.cand_i, R * d.nc * BL_KSEL_MAX);
+  {
+    char *g = nullptr;
+    ALLOC(g, R * 2 * G * 32);
+    d.grec = g;
+  }
+  ALLOC(d.full_v, R * V);
+  ALLOC(d.full_i, R * V);
+  ALLOC(d.full_n, R);
+  ALLOC(d.sortk, R * std::max(P2, 2 * V));
+  ALLOC(d.gsum, R * G);
+  ALLOC(c->d_slot, R);
+  ALLOC(c->d_skip, R);
+  ALLOC(c->d_tok, R);
+  ALLOC(c->d_status, R);
+  ALLOC(c->d_lp, R);
+  ALLOC(c->d_top_ids, R * 256);
+  ALLOC(c->d_top_lp, R * 256);
+  ALLOC(c->d_commit_toks, 4096);
+#undef ALLOC
+  d.n_eog = 0;
+  if (hipHostMalloc((void **)&c->h_slot, R * sizeof(int32_t)) != hipSuccess ||
+      hipHostMalloc((void **)&c->h_skip, R * sizeof(int32_t)) != hipSuccess ||
+      hipHostMalloc((void **)&c->h_tok, R * sizeof(int32_t)) != hipSuccess ||
+      hipHostMalloc((void **)&c->h_status, R * sizeof(int32_t)) != hipSuccess ||
+      hipHostMalloc((void **)&c->h_lp, R * sizeof(float)) != hipSuccess ||
+      hipHostMalloc((void **)&c->h_top_ids, R * 256 * sizeof(int32_t)) != hipSuccess ||
+      hipHostMalloc((void **)&c->h_top_lp, R * 256 * sizeof(float)) != hipSuccess) {
+    bl_destroy(c);
+    return fail(BL_EDEVICE, "hipHostMalloc failed");
+  }
+  if (hipStreamCreateWithFlags(&c->own, hipStreamNonBlocking) != hipSuccess) {
+    bl_destroy(c);
+    return fail(BL_EDEVICE, "hipStreamCreate failed");
+  }
+  c->stream = c->own;
+  c->host_slots.assign(S, bl_slot_dev{});
+  c->slot_ready.assign(S, false);
+  *out = c;
+  return BL_OK;
+}
+
+void bl_destroy(bl_ctx *c) {
+  if (!c) return;
+  hipSetDevice(c->device);
+  if (c->stream) hipStreamSynchronize(c->stream);
+  for (void *p : c->allocs) hipFree(p);
+  void *hp[] = {c->h_slot, c->h_skip, c->h_tok, c->h_status, c->h_lp, c->h_top_ids, c->h_top_lp};
+  for (void *p : hp)
+    if (p) hipHostFree(p);
+  if (c->own) hipStreamDestroy(c->own);
+  delete c;
+}
+
+int bl_set_stream(bl_ctx *c, void *stream) {
+  if (!c) return fail(BL_EPARAM, "null context");
+  c->stream = stream ? (hipStream_t)stream : c->own;
+  return BL_OK;
+}
+
+int bl_set_eog(bl_ctx *c, int32_t eos_id, const int32_t *eog_ids, int n_eog) {
+  if (!c || n_eog < 0 || n_eog > 1000) return fail(BL_EPARAM, "bl_set_eog: invalid arguments");
+  std::vector<int32_t> ids;
+  if (eos_id >= 0) ids.push_back(eos_id);
+  for (int i = 0; i < n_eog; i++) ids.push_back(eog_ids[i]);
+  hipSetDevice(c->device);
+  if (!ids.empty()) HIPCHK(hipMemcpy(c->d.eog, ids.data(), ids.size() * sizeof(int32_t), hipMemcpyHostToDevice));
+  c->d.n_eog = (int32_t)ids.size();
+  return BL_OK;
+}
+
+/* mode and unsupported-stage checks for one slot's parameters */
+static int configure(const bl_ctx *c, const bl_params *p, bl_slot_dev &s) {
+  const int V = c->d.vocab;
+  if (p->temperature != p->temperature || p->top_p != p->top_p) return fail(BL_EPARAM, "NaN sampling parameter");
+  if (p->n_probs < 0 || p->n_probs > 256) return fail(BL_EPARAM, "n_probs must be in 0..256 (got %d)", p->n_probs);
+  s.temperature = p->temperature;
+  s.dynatemp_range = p->dynatemp_range;
+  s.dynatemp_exponent = p->dynatemp_exponent;
+  s.top_n_sigma = p->top_n_sigma;
+  s.typical_p = p->typical_p;
+  s.top_p = p->top_p;
+  s.min_p = p->min_p;
+  s.xtc_probability = p->xtc_probability;
+  s.xtc_threshold = p->xtc_threshold;
+  s.repeat_penalty = p->repeat_penalty;
+  s.frequency_penalty = p->frequency_penalty;
+  s.presence_penalty = p->presence_penalty;
+  s.final_softcap = p->final_softcap;
+  s.logit_mul = p->logit_mul;
+  s.top_k = p->top_k;
+  s.min_keep = p->min_keep;
+  s.repeat_last_n = p->repeat_last_n;
+  s.n_probs = p->logprobs ? p->n_probs : 0;
+  s.ignore_eos = p->ignore_eos;
+  s.post_sampling_probs = p->post_sampling_probs;
+  s.fp_on = !(p->frequency_penalty == 0.0f && p->presence_penalty == 0.0f);
+  s.rep_on = !(p->repeat_penalty == 1.0f || p->repeat_last_n == 0);
+  int mode = 0;
+  if (p->temperature <= 0.0f) mode |= BL_M_GREEDY;
+  else if (p->top_k > 0 && p->top_k < V) mode |= BL_M_TOPK;
+  else mode |= BL_M_FULL;
+  if (p->logprobs) mode |= BL_M_LOGPROBS;
+  s.mode = mode;
+  int k = 0;
+  if (mode & BL_M_TOPK) k = p->top_k;
+  if ((mode & BL_M_LOGPROBS) && p->n_probs > k) k = p->n_probs;
+  s.k_sel = k;
+  /* stages without a device path yet */
+  if (p->temperature > 0.0f && p->top_n_sigma > 0.0f) return fail(BL_EUNSUPPORTED, "top_n_sigma is not supported on the device");
+  if (p->dry_multiplier != 0.0f && p->dry_base >= 1.0f && p->dry_penalty_last_n != 0)
+    return fail(BL_EUNSUPPORTED, "DRY is not supported on the device");
+  if (p->temperature > 0.0f && p->typical_p < 1.0f) return fail(BL_EUNSUPPORTED, "typical_p is not supported on the device");
+  if (p->temperature > 0.0f && p->xtc_probability > 0.0f && p->xtc_threshold <= 0.5f)
+    return fail(BL_EUNSUPPORTED, "XTC is not supported on the device");
+  if (p->temperature > 0.0f && p->dynatemp_range > 0.0f)
+    return fail(BL_EUNSUPPORTED, "dynamic temperature is not supported on the device");
+  if (p->post_sampling_probs) return fail(BL_EUNSUPPORTED, "post_sampling_probs is not supported on the device");
+  if (k > BL_KSEL_MAX || c->d.nc * k > BL_LDS_SORT)
+    return fail(BL_EUNSUPPORTED, "top_k/n_probs of %d exceeds the device selection limit", k);
+  if (p->repeat_last_n > BL_WCAP) return fail(BL_EUNSUPPORTED, "repeat_last_n above %d", BL_WCAP);
+  return BL_OK;
+}
+
+int bl_slot_reset(bl_ctx *c, int slot, const bl_params *p, uint64_t rng_state, const int32_t *history, int n_hist,
+                  const int32_t *reply, int n_reply, const int32_t *bias_ids, const float *bias_vals, int n_bias) {
+  if (!c || !p || slot < 0 || slot >= c->d.max_slots || n_hist < 0 || n_reply < 0 || n_bias < 0)
+    return fail(BL_EPARAM, "bl_slot_reset: invalid arguments");
+  const int V = c->d.vocab;
+  bl_slot_dev s{};
+  int rc = configure(c, p, s);
+  if (rc) return rc;
+  for (int i = 0; i < n_hist; i++)
+    if (history[i] < 0 || history[i] >= V) return fail(BL_EPARAM, "history token %d outside the vocabulary", history[i]);
+  for (int i = 0; i < n_reply; i++)
+    if (reply[i] < 0 || reply[i] >= V) return fail(BL_EPARAM, "reply token %d outside the vocabulary", reply[i]);
+  for (int i = 0; i < n_bias; i++)
+    if (bias_ids[i] < 0 || bias_ids[i] >= V)
+      return fail(BL_EPARAM, "logit_bias token id %d is outside the vocabulary", bias_ids[i]);
+  std::vector<uint32_t> touched(c->d.words, 0u);
+  std::vector<uint8_t> flags(V, 0);
+  std::vector<float> bias(V, 0.0f);
+  std::vector<int32_t> cnt(V, 0), wcnt(V, 0), ring(BL_WCAP, 0);
+  auto touch = [&](int32_t id) { touched[id >> 5] |= 1u << (id & 31); };
+  for (int i = 0; i < n_bias; i++) {
+    flags[bias_ids[i]] |= BL_TF_BIAS;
+    bias[bias_ids[i]] = bias_vals[i]; /* a repeated id keeps the last value, as a JSON object would */
+    touch(bias_ids[i]);
+  }
+  if (p->ignore_eos) {
+    std::vector<int32_t> eog(c->d.n_eog);
+    if (c->d.n_eog) HIPCHK(hipMemcpy(eog.data(), c->d.eog, eog.size() * sizeof(int32_t), hipMemcpyDeviceToHost));
+    for (int32_t id : eog)
+      if (id >= 0 && id < V) {
+        flags[id] |= BL_TF_SUPPRESS;
+        touch(id);
+      }
+  }
+  if (s.fp_on)
+    for (int i = 0; i < n_reply; i++) {
+      cnt[reply[i]] += 1;
+      touch(reply[i]);
+    }
+  if (s.rep_on) {
+    int rl = p->repeat_last_n;
+    int win = (rl > 0 && n_hist > rl) ? rl : n_hist;
+    for (int i = n_hist - win; i < n_hist; i++) {
+      wcnt[history[i]] += 1;
+      touch(history[i]);
+    }
+    if (rl > 0) {
+      for (int i = 0; i < win; i++) ring[i] = history[n_hist - win + i];
+      s.win_len = win;
+      s.win_head = 0;
+    }
+  }
+  s.rng = rng_state;
+  s.n_tokens = n_hist;
+  s.n_reply = n_reply;
+  hipSetDevice(c->device);
+  const size_t so = (size_t)slot * V;
+  HIPCHK(hipStreamSynchronize(c->stream));
+  HIPCHK(hipMemcpy(c->d.touched + (size_t)slot * c->d.words, touched.data(), touched.size() * 4, hipMemcpyHostToDevice));
+  HIPCHK(hipMemcpy(c->d.flags + so, flags.data(), V, hipMemcpyHostToDevice));
+  HIPCHK(hipMemcpy(c->d.bias + so, bias.data(), (size_t)V * 4, hipMemcpyHostToDevice));
+  HIPCHK(hipMemcpy(c->d.cnt + so, cnt.data(), (size_t)V * 4, hipMemcpyHostToDevice));
+  HIPCHK(hipMemcpy(c->d.wcnt + so, wcnt.data(), (size_t)V * 4, hipMemcpyHostToDevice));
+  HIPCHK(hipMemcpy(c->d.ring + (size_t)slot * BL_WCAP, ring.data(), BL_WCAP * 4, hipMemcpyHostToDevice));
+  HIPCHK(hipMemcpy(c->d.slots + slot, &s, sizeof s, hipMemcpyHostToDevice));
+  c->host_slots[slot] = s;
+  c->slot_ready[slot] = true;
+  return BL_OK;
+}
+
+int bl_slot_rng(bl_ctx *c, int slot, uint64_t *state) {
+  if (!c || slot < 0 || slot >= c->d.max_slots || !state) return fail(BL_EPARAM, "bl_slot_rng: invalid arguments");
+  hipSetDevice(c->device);
+  bl_slot_dev s;
+  HIPCHK(hipStreamSynchronize(c->stream));
+  HIPCHK(hipMemcpy(&s, c->d.slots + slot, sizeof s, hipMemcpyDeviceToHost));
+  *state = s.rng;
+  return BL_OK;
+}
+
+int bl_slot_commit(bl_ctx *c, int slot, const int32_t *toks, int n) {
+  if (!c || slot < 0 || slot >= c->d.max_slots || n < 0 || n > 4096) return fail(BL_EPARAM, "bl_slot_commit: invalid arguments");
+  if (n == 0) return BL_OK;
+  hipSetDevice(c->device);
+  HIPCHK(hipMemcpyAsync(c->d_commit_toks, toks, n * sizeof(int32_t), hipMemcpyHostToDevice, c->stream));
+  hipLaunchKernelGGL(bl_k_commit, dim3(1), dim3(64), 0, c->stream, c->d, slot, c->d_commit_toks, n, 0);
+  HIPCHK(hipGetLastError());
+  HIPCHK(hipStreamSynchronize(c->stream));
+  return BL_OK;
+}
+
+static int check_rows(bl_ctx *c, const int32_t *slots, int B) {
+  if (!c || !slots || B <= 0 || B > c->d.max_rows) return fail(BL_EPARAM, "invalid row count %d", B);
+  std::vector<char> seen(c->d.max_slots, 0);
+  for (int i = 0; i < B; i++) {
+    int s = slots[i];
+    if (s < 0 || s >= c->d.max_slots || !c->slot_ready[s]) return fail(BL_EPARAM, "slot %d is not set up", s);
+    if (seen[s]) return fail(BL_EPARAM, "slot %d appears twice in one step", s);
+    seen[s] = 1;
+  }
+  return BL_OK;
+}
+
+static bool needs_exp(bl_ctx *c, const int32_t *slots, int B) {
+  for (int i = 0; i < B; i++)
+    if (c->host_slots[slots[i]].mode & (BL_M_LOGPROBS | BL_M_FULL)) return true;
+  return false;
+}
+
+static int status_error(int st) {
+  if (st & BL_SE_UNSUPPORTED) return fail(BL_EUNSUPPORTED, "a sampler stage outside the device path was reached");
+  if (st & BL_SE_TIE) return fail(BL_ETIE, "the full-vocabulary draw landed on equal logits; heap order is not reproduced");
+  if (st & BL_SE_CAND_FULL) return fail(BL_EDEVICE, "candidate buffer overflow");
+  if (st & BL_SE_EMPTY) return fail(BL_EEMPTY, "sample_candidates: empty or mismatched candidates");
+  return BL_OK;
+}
+
+static bl_rows make_rows(bl_ctx *c, bool with_skip, int commit, int top_stride) {
+  bl_rows r{};
+  r.slot = c->d_slot;
+  r.rng_skip = with_skip ? c->d_skip : nullptr;
+  r.commit = commit;
+  r.tok = c->d_tok;
+  r.lp = c->d_lp;
+  r.top_ids = c->d_top_ids;
+  r.top_lp = c->d_top_lp;
+  r.top_stride = top_stride;
+  r.status = c->d_status;
+  return r;
+}
+
+int bl_sample_step(bl_ctx *c, const int32_t *slots, int B, const float *d_logits, int64_t ld, int32_t *tokens,
+                   float *logprobs, int32_t *top_ids, float *top_logprobs, int top_stride) {
+  int rc = check_rows(c, slots, B);
+  if (rc) return rc;
+  if (!tokens || !d_logits || ld < c->d.vocab) return fail(BL_EPARAM, "bl_sample_step: invalid buffers");
+  if (top_stride < 0 || top_stride > 256) return fail(BL_EPARAM, "top_stride must be in 0..256");
+  hipSetDevice(c->device);
+  memcpy(c->h_slot, slots, B * sizeof(int32_t));
+  HIPCHK(hipMemcpyAsync(c->d_slot, c->h_slot, B * sizeof(int32_t), hipMemcpyHostToDevice, c->stream));
+  bl_rows rows = make_rows(c, false, 1, top_stride > 0 ? top_stride : 1);
+  bl_launch_step(c->d, d_logits, ld, rows, B, needs_exp(c, slots, B), c->stream);
+  HIPCHK(hipGetLastError());
+  HIPCHK(hipMemcpyAsync(c->h_tok, c->d_tok, B * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(hipMemcpyAsync(c->h_status, c->d_status, B * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(hipMemcpyAsync(c->h_lp, c->d_lp, B * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+  if (top_stride > 0) {
+    HIPCHK(hipMemcpyAsync(c->h_top_ids, c->d_top_ids, (size_t)B * top_stride * 4, hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(hipMemcpyAsync(c->h_top_lp, c->d_top_lp, (size_t)B * top_stride * 4, hipMemcpyDeviceToHost, c->stream));
+  }
+  HIPCHK(hipStreamSynchronize(c->stream));
+  int st = 0;
+  for (int i = 0; i < B; i++) st |= c->h_status[i];
+  memcpy(tokens, c->h_tok, B * sizeof(int32_t));
+  if (logprobs) memcpy(logprobs, c->h_lp, B * sizeof(float));
+  if (top_ids && top_stride > 0) memcpy(top_ids, c->h_top_ids, (size_t)B * top_stride * 4);
+  if (top_logprobs && top_stride > 0) memcpy(top_logprobs, c->h_top_lp, (size_t)B * top_stride * 4);
+  return status_error(st);
+}
+
+int bl_bind_rows(bl_ctx *c, const int32_t *slots, int B) {
+  int rc = check_rows(c, slots, B);
+  if (rc) return rc;
+  hipSetDevice(c->device);
+  HIPCHK(hipMemcpy(c->d_slot, slots, B * sizeof(int32_t), hipMemcpyHostToDevice));
+  memcpy(c->h_slot, slots, B * sizeof(int32_t));
+  c->bound_B = B;
+  return BL_OK;
+}
+
+int bl_sample_step_async(bl_ctx *c, int B, const float *d_logits, int64_t ld, int32_t *d_tokens, float *d_logprobs,
+                         int32_t *d_top_ids, float *d_top_logprobs, int top_stride) {
+  if (!c || B != c->bound_B || B <= 0) return fail(BL_EPARAM, "bl_sample_step_async: rows not bound (bl_bind_rows)");
+  if (!d_logits || !d_tokens || ld < c->d.vocab || top_stride < 0 || top_stride > 256)
+    return fail(BL_EPARAM, "bl_sample_step_async: invalid buffers");
+  bl_rows rows = make_rows(c, false, 1, top_stride > 0 ? top_stride : 1);
+  rows.tok = d_tokens;
+  rows.lp = d_logprobs;
+  rows.top_ids = d_top_ids ? d_top_ids : c->d_top_ids;
+  rows.top_lp = d_top_logprobs ? d_top_logprobs : c->d_top_lp;
+  bl_launch_step(c->d, d_logits, ld, rows, B, needs_exp(c, c->h_slot, B), c->stream);
+  HIPCHK(hipGetLastError());
+  return BL_OK;
+}
+
+int bl_spec_verify(bl_ctx *c, const int32_t *slots, int B, int k, const float *d_rows, int64_t ld,
+                   const int32_t *drafts, int32_t *tokens, int32_t *accepted) {
+  int rc = check_rows(c, slots, B);
+  if (rc) return rc;
+  const int R = B * (k + 1);
+  if (k < 0 || R > c->d.max_rows || !d_rows || !tokens || !accepted || ld < c->d.vocab)
+    return fail(BL_EPARAM, "bl_spec_verify: invalid arguments (B %d, k %d)", B, k);
+  for (int b = 0; b < B; b++) {
+    const bl_slot_dev &s = c->host_slots[slots[b]];
+    if (k > 0 && (s.fp_on || s.rep_on))
+      return fail(BL_EUNSUPPORTED, "speculative rows with history-dependent penalties are not supported on the device");
+  }
+  hipSetDevice(c->device);
+  for (int b = 0; b < B; b++)
+    for (int i = 0; i <= k; i++) {
+      c->h_slot[b * (k + 1) + i] = slots[b];
+      c->h_skip[b * (k + 1) + i] = i;
+    }
+  HIPCHK(hipMemcpyAsync(c->d_slot, c->h_slot, R * sizeof(int32_t), hipMemcpyHostToDevice, c->stream));
+  HIPCHK(hipMemcpyAsync(c->d_skip, c->h_skip, R * sizeof(int32_t), hipMemcpyHostToDevice, c->stream));
+  bl_rows rows = make_rows(c, true, 0, 1);
+  bool ne = false;
+  for (int b = 0; b < B; b++) ne |= (c->host_slots[slots[b]].mode & (BL_M_LOGPROBS | BL_M_FULL)) != 0;
+  bl_launch_step(c->d, d_rows, ld, rows, R, ne, c->stream);
+  HIPCHK(hipGetLastError());
+  HIPCHK(hipMemcpyAsync(c->h_tok, c->d_tok, R * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(hipMemcpyAsync(c->h_status, c->d_status, R * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(hipStreamSynchronize(c->stream));
+  int st = 0;
+  for (int i = 0; i < R; i++) st |= c->h_status[i];
+  memcpy(tokens, c->h_tok, R * sizeof(int32_t));
+  if ((rc = status_error(st))) return rc;
+  std::vector<int32_t> eog(c->d.n_eog);
+  if (c->d.n_eog) HIPCHK(hipMemcpy(eog.data(), c->d.eog, eog.size() * 4, hipMemcpyDeviceToHost));
+  for (int b = 0; b < B; b++) {
+    int a = 0;
+    while (a < k && tokens[b * (k + 1) + a] == drafts[b * k + a] &&
+           std::find(eog.begin(), eog.end(), tokens[b * (k + 1) + a]) == eog.end())
+      a++;
+    accepted[b] = a;
+    std::vector<int32_t> commit(drafts + b * k, drafts + b * k + a);
+    commit.push_back(tokens[b * (k + 1) + a]);
+    HIPCHK(hipMemcpyAsync(c->d_commit_toks, commit.data(), commit.size() * 4, hipMemcpyHostToDevice, c->stream));
+    int draws = c->host_slots[slots[b]].temperature > 0.0f ? a + 1 : 0;
+    hipLaunchKernelGGL(bl_k_commit, dim3(1), dim3(64), 0, c->stream, c->d, slots[b], c->d_commit_toks,
+                       (int)commit.size(), draws);
+    HIPCHK(hipGetLastError());
+    HIPCHK(hipStreamSynchronize(c->stream));
+  }
+  return BL_OK;
+}
+
+int bl_synth_logits(bl_ctx *c, float *d_out, int64_t ld, int cfg, int64_t seed, int64_t step, int rows, int vocab) {
+  if (!c || !d_out || rows <= 0 || vocab <= 0 || ld < vocab) return fail(BL_EPARAM, "bl_synth_logits: invalid arguments");
+  hipSetDevice(c->device);
+  bl_launch_synth(d_out, ld, cfg, seed, step, rows, vocab, c->stream);
+  HIPCHK(hipGetLastError());
+  if (cfg == 1) {
+    std::vector<int32_t> ids = blw::c1_bump_ids(seed, step, vocab);
+    for (int r = 0; r < rows; r++) {
+      HIPCHK(hipMemcpyAsync(c->d_commit_toks, ids.data(), ids.size() * 4, hipMemcpyHostToDevice, c->stream));
+      hipLaunchKernelGGL(bl_k_bump, dim3(1), dim3(64), 0, c->stream, d_out + (int64_t)r * ld, c->d_commit_toks,
+                         (int)ids.size(), 8.0f);
+      HIPCHK(hipStreamSynchronize(c->stream));
+    }
+  }
+  HIPCHK(hipStreamSynchronize(c->stream));
+  return BL_OK;
+}
+
+int bl_workload_ids(int kind, int cfg, int64_t seed, int row, int n, int vocab, int32_t *out) {
+  if (n < 0 || vocab <= 0 || !out || (kind != 0 && kind != 1)) return fail(BL_EPARAM, "bl_workload_ids: invalid arguments");
+  std::vector<int32_t> v = kind == 0 ? blw::uniform_ids(cfg, seed, row, n, vocab) : blw::zipf_ids(cfg, seed, row, n, vocab, 1.1);
+  memcpy(out, v.data(), v.size() * sizeof(int32_t));
+  return BL_OK;
+}
+
+int bl_workload_bias(int cfg, int64_t seed, int row, int n, int vocab, float lo, float hi, int32_t *ids, float *vals) {
+  if (n < 0 || n > vocab || !ids || !vals) return fail(BL_EPARAM, "bl_workload_bias: invalid arguments");
+  std::vector<int32_t> i;
+  std::vector<float> v;
+  blw::bias_list(cfg, seed, row, n, vocab, lo, hi, i, v);
+  memcpy(ids, i.data(), i.size() * sizeof(int32_t));
+  memcpy(vals, v.data(), v.size() * sizeof(float));
+  return BL_OK;
+}
+
+int bl_workload_drafts(int64_t seed, int64_t step, int seq, const int32_t *argmax, int k, int vocab, int32_t *out) {
+  if (k < 0 || !argmax || !out) return fail(BL_EPARAM, "bl_workload_drafts: invalid arguments");
+  std::vector<int32_t> d = blw::c5_drafts(seed, step, seq, argmax, k, vocab);
+  memcpy(out, d.data(), d.size() * sizeof(int32_t));
+  return BL_OK;
+}
+
+int bl_math_digest(bl_ctx *c, int fn, uint32_t first_block, int n_blocks, uint64_t *out) {
+  if (!c || (fn != 0 && fn != 1) || n_blocks <= 0 || (uint64_t)first_block + n_blocks > 4096 || !out)
+    return fail(BL_EPARAM, "bl_math_digest: invalid arguments");
+  hipSetDevice(c->device);
+  unsigned long long *d = nullptr;
+  HIPCHK(hipMalloc((void **)&d, n_blocks * sizeof(unsigned long long)));
+  bl_launch_math_digest(fn, first_block, n_blocks, d, c->stream);
+  hipError_t e = hipGetLastError();
+  if (e == hipSuccess) e = hipMemcpyAsync(out, d, n_blocks * sizeof(uint64_t), hipMemcpyDeviceToHost, c->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  (void)hipFree(d);
+  if (e != hipSuccess) return fail(BL_EDEVICE, "bl_math_digest: %s", hipGetErrorString(e));
+  return BL_OK;
+}
+
+} /* extern "C" */

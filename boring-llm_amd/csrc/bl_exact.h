@@ -1,0 +1,243 @@
+/*
+ * bl_exact.h — exact, parallel emulation of a sequential float32 sum of non-negative terms.
+ *
+ * The reference sums softmax terms one at a time in float32 (src/sampling.br:255-265 in index order;
+ * :506-598 in rank order), and logprobs/draws depend on the exact rounded result. A tree reduction
+ * does not reproduce it, so the sum is re-derived as integer arithmetic:
+ *
+ *   While the running sum S stays in one binade [2^e, 2^(e+1)), S = N*u with u = 2^(e-23) and N an
+ *   integer in [2^23, 2^24) (the bottom segment e = -126 covers [0, 2^-125) with N in [0, 2^24)).
+ *   Adding a term a rounds a/u = q + f to an integer ulps count: q, q+1 when f > 1/2, and on a tie
+ *   (f == 1/2) whichever makes N even. The increment therefore depends only on the parity of N, so a
+ *   term is a pair (d0, d1) = (increment from even N, increment from odd N) and consecutive terms
+ *   compose associatively (an automaton over parity). Sums of 64-term groups are wave reductions;
+ *   prefixes are wave scans.
+ *   When N would reach 2^24 the sum leaves the binade; that one step is done as a real float add and
+ *   the walk continues in the new binade.
+ *
+ * The walk is split in two phases:
+ *   Phase A (many threads): per 64-term group, the composed pair for three binades around the one an
+ *            approximate (double) prefix predicts.
+ *   Phase B (one wavefront): walks the groups 64 at a time with a composed scan, and drops to
+ *            element level only in a group that crosses a binade, lacks the needed binade, or contains
+ *            the element a threshold search is looking for.
+ */
+#ifndef BL_EXACT_H
+#define BL_EXACT_H
+
+#include <stdint.h>
+
+#include "bl_math.h"
+
+#if defined(__HIPCC__)
+#include <hip/hip_runtime.h>
+#define BL_SD __host__ __device__ __forceinline__
+#else
+#define BL_SD static inline
+#endif
+
+#define BL_N_TOP (1u << 24)
+#define BL_SAT (1u << 25)
+#define BL_E_MIN (-126)
+
+struct bl_inc {
+  uint32_t d0, d1;
+};
+
+/* group record: composed pairs for binades E-1, E, E+1 (a variant below BL_E_MIN is unused) */
+struct bl_grec {
+  int32_t E;
+  uint32_t pad;
+  bl_inc v[3];
+};
+
+BL_SD bl_inc bl_inc_ident() { return bl_inc{0u, 0u}; }
+
+/* f then g */
+BL_SD bl_inc bl_compose(bl_inc f, bl_inc g) {
+  uint32_t a = f.d0 + ((f.d0 & 1u) ? g.d1 : g.d0);
+  uint32_t b = f.d1 + (((f.d1 + 1u) & 1u) ? g.d1 : g.d0);
+  return bl_inc{a < BL_SAT ? a : BL_SAT, b < BL_SAT ? b : BL_SAT};
+}
+
+BL_SD uint32_t bl_apply(bl_inc f, uint32_t N) { return N + ((N & 1u) ? f.d1 : f.d0); }
+
+/* increment of a term a >= 0 at binade e (units of 2^(e-23)) */
+BL_SD bl_inc bl_term_inc(float a, int e) {
+  uint32_t b = bl_f2u(a) & 0x7fffffffu;
+  uint32_t ex = b >> 23, m = b & 0x7fffffu;
+  if (b == 0u) return bl_inc{0u, 0u};
+  if (ex == 0xffu) return bl_inc{BL_SAT, BL_SAT};
+  int ea = ex ? (int)ex - 127 : -126;
+  uint32_t M = ex ? (m | 0x800000u) : m;
+  int s = e - ea;
+  if (s < 0) return bl_inc{BL_SAT, BL_SAT};
+  if (s == 0) return bl_inc{M, M};
+  if (s >= 25) return bl_inc{0u, 0u};
+  uint32_t q = M >> s, rem = M & ((1u << s) - 1u), half = 1u << (s - 1);
+  if (rem > half) return bl_inc{q + 1u, q + 1u};
+  if (rem < half) return bl_inc{q, q};
+  return bl_inc{q + (q & 1u), q + ((q & 1u) ^ 1u)};
+}
+
+/* S (>= 0, finite) -> (e, N) */
+BL_SD void bl_split(float S, int &e, uint32_t &N) {
+  uint32_t b = bl_f2u(S) & 0x7fffffffu;
+  uint32_t ex = b >> 23;
+  if (ex == 0u) {
+    e = BL_E_MIN;
+    N = b;
+  } else {
+    e = (int)ex - 127;
+    N = (b & 0x7fffffu) | 0x800000u;
+  }
+}
+
+/* (e, N) with N < 2^24 -> S, exact */
+BL_SD float bl_make(int e, uint32_t N) {
+  if (N < 0x800000u) return bl_u2f(N); /* only reachable at e == BL_E_MIN: subnormal or zero */
+  return bl_u2f(((uint32_t)(e + 127) << 23) | (N & 0x7fffffu));
+}
+
+/* binade index predicted from an approximate sum */
+BL_SD int bl_binade_of(double s) {
+  float f = (float)s;
+  int e;
+  uint32_t N;
+  bl_split(f < 0.0f ? 0.0f : f, e, N);
+  return e;
+}
+
+#if defined(__HIPCC__)
+/* ---- wave primitives (wavefront of 64) ---- */
+__device__ __forceinline__ bl_inc bl_shfl_up(bl_inc v, int k) {
+  return bl_inc{(uint32_t)__shfl_up((int)v.d0, k, 64), (uint32_t)__shfl_up((int)v.d1, k, 64)};
+}
+__device__ __forceinline__ bl_inc bl_shfl(bl_inc v, int l) {
+  return bl_inc{(uint32_t)__shfl((int)v.d0, l, 64), (uint32_t)__shfl((int)v.d1, l, 64)};
+}
+/* inclusive ordered scan of composition across the wavefront */
+__device__ __forceinline__ bl_inc bl_wave_scan(bl_inc f, int lane) {
+#pragma unroll
+  for (int k = 1; k < 64; k <<= 1) {
+    bl_inc o = bl_shfl_up(f, k);
+    if (lane >= k) f = bl_compose(o, f);
+  }
+  return f;
+}
+/* ordered reduction; result valid in every lane */
+__device__ __forceinline__ bl_inc bl_wave_reduce(bl_inc f, int lane) { return bl_shfl(bl_wave_scan(f, lane), 63); }
+
+__device__ __forceinline__ double bl_wave_sum_d(double x) {
+#pragma unroll
+  for (int k = 32; k >= 1; k >>= 1) x += __shfl_xor(x, k, 64);
+  return x;
+}
+__device__ __forceinline__ double bl_wave_excl_scan_d(double x, int lane) {
+  double inc = x;
+#pragma unroll
+  for (int k = 1; k < 64; k <<= 1) {
+    double o = __shfl_up(inc, k, 64);
+    if (lane >= k) inc += o;
+  }
+  return inc - x;
+}
+
+/*
+ * Phase A for one group, executed by a whole wavefront: `a` is this lane's term (0 beyond the end),
+ * `approx_start` the approximate sum before the group. Returns the record (valid in every lane).
+ */
+__device__ __forceinline__ bl_grec bl_group_record(float a, double approx_start, int lane) {
+  bl_grec r;
+  r.E = bl_binade_of(approx_start);
+  r.pad = 0;
+#pragma unroll
+  for (int k = 0; k < 3; k++) {
+    int e = r.E - 1 + k;
+    bl_inc f = e >= BL_E_MIN ? bl_term_inc(a, e) : bl_inc{BL_SAT, BL_SAT};
+    r.v[k] = bl_wave_reduce(f, lane);
+  }
+  return r;
+}
+
+/*
+ * Phase B: sequential-sum walk over n terms in groups of 64, by one wavefront.
+ *   term(j)   -> float term j (only called for j < n)
+ *   rec(g)    -> bl_grec of group g
+ * Search mode (thr_on): stops at the first index j >= min_idx whose inclusive sum S_j >= thr and
+ * returns j (S holds S_j); otherwise returns -1 with S the full sum. All lanes return the same.
+ */
+template <class TermF, class RecF>
+__device__ int bl_seq_walk(int64_t n, TermF term, RecF rec, bool thr_on, float thr, int64_t min_idx, float &S_out,
+                           int lane) {
+  int e = BL_E_MIN;
+  uint32_t N = 0u;
+  int64_t G = (n + 63) / 64;
+  int64_t g = 0;
+  while (g < G) {
+    /* ---- group level over groups g .. g+63 ---- */
+    int64_t gl = g + lane;
+    bool valid = gl < G;
+    bl_inc f = bl_inc_ident();
+    if (valid) {
+      bl_grec r = rec(gl);
+      int k = e - (r.E - 1);
+      if (k >= 0 && k <= 2 && e >= BL_E_MIN) f = r.v[k];
+      else valid = false;
+    }
+    bl_inc sc = bl_wave_scan(f, lane);
+    uint32_t Nend = bl_apply(sc, N);
+    bool bad = !valid || Nend >= BL_N_TOP;
+    if (!bad && thr_on) bad = bl_make(e, Nend) >= thr; /* reaching the threshold: resolve at element level */
+    unsigned long long m = __ballot(bad);
+    int first = m ? __ffsll((long long)m) - 1 : 64;
+    if (first > 0) {
+      N = (uint32_t)__shfl((int)Nend, first - 1, 64);
+      g += first;
+    }
+    if (g >= G) break;
+    if (first == 64) continue;
+    /* ---- element level in group g ---- */
+    int64_t j0 = g * 64;
+    int64_t j = j0 + lane;
+    float a = j < n ? term(j) : 0.0f;
+    bool in = j < n;
+    int start = 0;
+    while (true) {
+      bl_inc fe = (in && lane >= start) ? bl_term_inc(a, e) : bl_inc_ident();
+      bl_inc se = bl_wave_scan(fe, lane);
+      uint32_t Ne = bl_apply(se, N);
+      bool act = in && lane >= start;
+      bool cross = act && Ne >= BL_N_TOP;
+      bool reach = act && !cross && thr_on && j >= min_idx && bl_make(e, Ne) >= thr;
+      unsigned long long ms = __ballot(cross || reach);
+      if (!ms) {
+        N = (uint32_t)__shfl((int)Ne, 63, 64);
+        break;
+      }
+      int c = __ffsll((long long)ms) - 1;
+      uint32_t Nbefore = c > start ? (uint32_t)__shfl((int)Ne, c - 1, 64) : N;
+      bool c_reach = __shfl((int)reach, c, 64) != 0;
+      if (c_reach) {
+        S_out = bl_make(e, (uint32_t)__shfl((int)Ne, c, 64));
+        return (int)(j0 + c);
+      }
+      float ac = __shfl(a, c, 64);
+      float Sn = bl_make(e, Nbefore) + ac; /* the one real float add at a binade crossing */
+      bl_split(Sn, e, N);
+      if (thr_on && j0 + c >= min_idx && Sn >= thr) {
+        S_out = Sn;
+        return (int)(j0 + c);
+      }
+      start = c + 1;
+      if (start >= 64) break;
+    }
+    g += 1;
+  }
+  S_out = bl_make(e, N);
+  return -1;
+}
+
+#endif /* __HIPCC__ */
+
+#endif /* BL_EXACT_H */

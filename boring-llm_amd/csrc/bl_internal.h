@@ -1,0 +1,99 @@
+/*
+ * bl_internal.h — device data layout shared by the kernels and the host side of libbl_select.
+ *
+ * Per slot (one request's sampler state, all in HBM, owned by the context):
+ *   bl_slot_dev            sampling parameters + scalar state (RNG, history lengths, window ring head)
+ *   touched[V/32]          bit t set when token t's logit is modified by the step (logit_bias,
+ *                          ignore_eos suppression, a reply count, a repeat-window count)
+ *   flags[V] u8, bias[V]   logit_bias presence/value and suppression, per token
+ *   cnt[V]                 occurrences of the token in the reply (frequency / presence penalties)
+ *   wcnt[V]                occurrences of the token in the repeat window
+ *   ring[WCAP]             the last repeat_last_n tokens, for window eviction
+ * The row pass reads `touched` densely (V/8 bytes per row, ~3% of the logits traffic) and the other
+ * tables only at set bits. Committing a token is O(1) writes.
+ *
+ * Per step workspace, rows = B: transformed rows, per-chunk statistics and top-K candidates,
+ * sequential-sum group records, full-vocabulary candidate lists and sort scratch.
+ */
+#ifndef BL_INTERNAL_H
+#define BL_INTERNAL_H
+
+#include <stdint.h>
+
+#define BL_CH 4096          /* vocabulary chunk per workgroup in the row passes */
+#define BL_RP_THREADS 256   /* row-pass workgroup */
+#define BL_SEL_THREADS 1024 /* per-row selection workgroup */
+#define BL_KSEL_MAX 256     /* largest per-chunk candidate count (top_k / n_probs) */
+#define BL_WCAP 8192        /* repeat window ring capacity */
+#define BL_LDS_SORT 4096    /* candidate lists sorted in LDS up to this size */
+
+/* per-token flags */
+#define BL_TF_BIAS 1u
+#define BL_TF_SUPPRESS 2u
+
+/* row modes */
+#define BL_M_GREEDY 1
+#define BL_M_TOPK 2
+#define BL_M_FULL 4
+#define BL_M_LOGPROBS 8
+
+/* per-row status bits (also sticky in the slot) */
+#define BL_SE_UNSUPPORTED 1
+#define BL_SE_TIE 2
+#define BL_SE_CAND_FULL 4
+#define BL_SE_EMPTY 8
+
+struct bl_slot_dev {
+  /* parameters (SamplingParams, src/model.br:1565-1584, and server extras) */
+  float temperature, dynatemp_range, dynatemp_exponent, top_n_sigma;
+  float typical_p, top_p, min_p, xtc_probability, xtc_threshold;
+  float repeat_penalty, frequency_penalty, presence_penalty, final_softcap, logit_mul;
+  int32_t top_k, min_keep, repeat_last_n, n_probs, ignore_eos, post_sampling_probs;
+  /* derived at configuration */
+  int32_t mode, k_sel, fp_on, rep_on;
+  /* state */
+  uint64_t rng;
+  int32_t n_tokens, n_reply, win_len, win_head, err, pad;
+};
+
+struct bl_dev {
+  int vocab, nc, max_slots, max_rows;
+  int64_t words; /* V/32 rounded up */
+  bl_slot_dev *slots;
+  uint32_t *touched; /* [slots][words] */
+  uint8_t *flags;    /* [slots][V] */
+  float *bias;       /* [slots][V] */
+  int32_t *cnt;      /* [slots][V] */
+  int32_t *wcnt;     /* [slots][V] */
+  int32_t *ring;     /* [slots][WCAP] */
+  int32_t *eog;      /* [n_eog] end-of-generation ids */
+  int32_t n_eog;
+  /* workspace for up to max_rows rows */
+  float *eff;       /* [rows][V] transformed row */
+  float *c_max;     /* [rows][nc] */
+  int32_t *c_arg;   /* [rows][nc] */
+  float *c_sum;     /* [rows][nc] approximate sum of exp(x - c_max) */
+  float *cand_v;    /* [rows][nc][KSEL_MAX] */
+  int32_t *cand_i;
+  void *grec;       /* [rows][2 * (V/64 + 64)] bl_grec: index-order records, then sorted-list records */
+  float *full_v;    /* [rows][V] full-vocabulary candidates */
+  int32_t *full_i;
+  int32_t *full_n;  /* [rows] */
+  uint64_t *sortk;  /* [rows][2^ceil(log2 V)] global sort scratch */
+  double *gsum;     /* [rows][V/64 + 64] */
+};
+
+/* one step's row table (device pointers) */
+struct bl_rows {
+  const int32_t *slot;     /* [B] */
+  const int32_t *rng_skip; /* [B] draws consumed before this row's draw (speculative rows), or null */
+  int32_t commit;          /* append the chosen token to the slot history */
+  int32_t *tok;            /* [B] */
+  float *lp;               /* [B] */
+  int32_t *top_ids;        /* [B][top_stride] */
+  float *top_lp;
+  int32_t top_stride;
+  int32_t *status;         /* [B] */
+};
+
+#endif /* BL_INTERNAL_H */

@@ -1,0 +1,748 @@
+/*
+ * bl_kernels.hip — HIP kernels of one token-selection step for B slots (gfx950, wave64).
+ *
+ *   bl_k_rowpass  grid (chunks, B) x 256: reads each logits row once (float4), applies the model tail
+ *                 (logit_mul, soft-cap), then the server's per-token stages at the touched bits
+ *                 (logit_bias -> ignore_eos suppression -> frequency/presence -> repeat penalty,
+ *                 src/server.br:940-944, src/sampling.br:65-107,175-237), writes the transformed
+ *                 row, and per chunk: max + first argmax, an approximate exp-sum, and the chunk's
+ *                 top-K by (value desc, index asc) via a three-pass LDS radix select.
+ *   bl_k_exppass  grid (chunks, B) x 256, rows with logprobs or full-vocabulary sampling: exact
+ *                 exp(x - max) terms (glibc-identical expf), the sequential-sum group records of the
+ *                 index-order normaliser (src/sampling.br:254-266), and the candidates of a
+ *                 full-vocabulary rank (every token within 17.5*max(T,1) of the max; the rest cannot
+ *                 change any float32 sum of the chain).
+ *   bl_k_select   grid (B) x 1024: greedy / top-k / full-vocabulary candidate sampling with exact
+ *                 sequential sums (src/sampling.br:490-607), the draw from the slot's xorshift stream,
+ *                 logprobs + alternatives (src/server.br:1027-1035), and the history commit
+ *                 (src/server.br:1004, :1037).
+ * No MFMA: the work is bandwidth- and latency-bound scanning, selection and integer arithmetic.
+ */
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "bl_exact.h"
+#include "bl_internal.h"
+#include "bl_math.h"
+#include "bl_synth.h"
+
+#define BL_NEG_INF (-__builtin_inff())
+
+__device__ __forceinline__ const bl_slot_dev &slot_of(const bl_dev &d, int s) { return d.slots[s]; }
+
+/* ------------------------------------------------------------------ block reductions (256 threads) */
+__device__ __forceinline__ void argmax_merge(float &m, int &mi, float m2, int mi2) {
+  if (m2 > m || (m2 == m && mi2 < mi)) {
+    m = m2;
+    mi = mi2;
+  }
+}
+
+template <int NT>
+__device__ void block_argmax(float &m, int &mi, float *sm, int *si) {
+  int t = threadIdx.x, lane = t & 63, w = t >> 6;
+#pragma unroll
+  for (int k = 32; k >= 1; k >>= 1) {
+    float m2 = __shfl_xor(m, k, 64);
+    int i2 = __shfl_xor(mi, k, 64);
+    argmax_merge(m, mi, m2, i2);
+  }
+  if (lane == 0) {
+    sm[w] = m;
+    si[w] = mi;
+  }
+  __syncthreads();
+  if (t == 0) {
+    for (int k = 1; k < NT / 64; k++) argmax_merge(m, mi, sm[k], si[k]);
+    sm[0] = m;
+    si[0] = mi;
+  }
+  __syncthreads();
+  m = sm[0];
+  mi = si[0];
+  __syncthreads();
+}
+
+template <int NT>
+__device__ double block_sum_d(double x, double *sd) {
+  int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  x = bl_wave_sum_d(x);
+  if (lane == 0) sd[w] = x;
+  __syncthreads();
+  double r = 0.0;
+  for (int k = 0; k < NT / 64; k++) r += sd[k];
+  __syncthreads();
+  return r;
+}
+
+/* ------------------------------------------------------------------ K1: row pass */
+__global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass(bl_dev d, const float *__restrict__ logits, int64_t ld,
+                                                              bl_rows rows) {
+  const int V = d.vocab, nc = d.nc;
+  const int c = blockIdx.x, row = blockIdx.y, t = threadIdx.x;
+  const int slot = rows.slot[row];
+  const bl_slot_dev &sp = slot_of(d, slot);
+  __shared__ float xs[BL_CH];
+  __shared__ uint32_t hist[2048];
+  __shared__ float red_m[4];
+  __shared__ int red_i[4];
+  __shared__ double red_d[4];
+  __shared__ uint32_t sel[4];
+  __shared__ int out_n;
+
+  const int i0 = c * BL_CH;
+  const int cnt = min(BL_CH, V - i0);
+  const float *src = logits + (int64_t)row * ld + i0;
+  if (c == 0 && t == 0) d.full_n[row] = 0; /* consumed by the exponent pass, which runs after this kernel */
+  if (cnt == BL_CH && (((uintptr_t)src) & 15) == 0) {
+#pragma unroll
+    for (int j = 0; j < BL_CH / (4 * BL_RP_THREADS); j++) {
+      float4 v = reinterpret_cast<const float4 *>(src)[j * BL_RP_THREADS + t];
+      reinterpret_cast<float4 *>(xs)[j * BL_RP_THREADS + t] = v;
+    }
+  } else {
+    for (int i = t; i < cnt; i += BL_RP_THREADS) xs[i] = src[i];
+  }
+  const float lmul = sp.logit_mul, cap = sp.final_softcap;
+  if (lmul != 1.0f || cap > 0.0f) {
+    for (int i = t; i < cnt; i += BL_RP_THREADS) {
+      float x = xs[i];
+      if (lmul != 1.0f) x = x * lmul;
+      if (cap > 0.0f) {
+        float q = x / cap;
+        x = cap * bl_tanhf(q);
+      }
+      xs[i] = x;
+    }
+  }
+  __syncthreads();
+  /* server stages at the touched tokens of this chunk */
+  {
+    const uint32_t *tw = d.touched + (int64_t)slot * d.words + (i0 >> 5);
+    const int nwords = (cnt + 31) >> 5;
+    const int64_t so = (int64_t)slot * V;
+    const bool fp = sp.fp_on && sp.n_reply > 0;
+    const bool rp = sp.rep_on && sp.n_tokens > 0;
+    for (int w = t; w < nwords; w += BL_RP_THREADS) {
+      uint32_t bits = tw[w];
+      while (bits) {
+        int b = __ffs(bits) - 1;
+        bits &= bits - 1;
+        int li = w * 32 + b;
+        if (li >= cnt) break;
+        int64_t id = so + i0 + li;
+        float x = xs[li];
+        uint32_t f = d.flags[id];
+        if (f & BL_TF_BIAS) x = x + d.bias[id];
+        if (f & BL_TF_SUPPRESS) x = -1000000000.0f;
+        if (fp) {
+          int cc = d.cnt[id];
+          if (cc > 0) {
+            float tcf = (float)cc * sp.frequency_penalty;
+            x = x - tcf;
+            x = x - sp.presence_penalty;
+          }
+        }
+        if (rp && d.wcnt[id] > 0) x = x > 0.0f ? x / sp.repeat_penalty : x * sp.repeat_penalty;
+        xs[li] = x;
+      }
+    }
+  }
+  __syncthreads();
+  /* transformed row */
+  {
+    float *dst = d.eff + (int64_t)row * V + i0;
+    if (cnt == BL_CH) {
+#pragma unroll
+      for (int j = 0; j < BL_CH / (4 * BL_RP_THREADS); j++)
+        reinterpret_cast<float4 *>(dst)[j * BL_RP_THREADS + t] = reinterpret_cast<float4 *>(xs)[j * BL_RP_THREADS + t];
+    } else {
+      for (int i = t; i < cnt; i += BL_RP_THREADS) dst[i] = xs[i];
+    }
+  }
+  /* max, first argmax, approximate exp-sum */
+  float m = BL_NEG_INF;
+  int mi = 0x7fffffff;
+  for (int i = t; i < cnt; i += BL_RP_THREADS) {
+    float x = xs[i];
+    if (x > m) {
+      m = x;
+      mi = i;
+    }
+  }
+  block_argmax<BL_RP_THREADS>(m, mi, red_m, red_i);
+  double s = 0.0;
+  if (m > BL_NEG_INF)
+    for (int i = t; i < cnt; i += BL_RP_THREADS) s += (double)__expf(xs[i] - m);
+  s = block_sum_d<BL_RP_THREADS>(s, red_d);
+  if (t == 0) {
+    int64_t o = (int64_t)row * nc + c;
+    d.c_max[o] = m;
+    d.c_arg[o] = mi == 0x7fffffff ? i0 : i0 + mi;
+    d.c_sum[o] = (float)s;
+  }
+
+  /* chunk top-K by (value desc, index asc) over values > -1e30 (src/sampling.br:280-296) */
+  const int K = sp.k_sel;
+  if (K <= 0) return;
+  uint32_t prefix = 0u, pmask = 0u;
+  int need = K;
+  bool take_all = false;
+  for (int pass = 0; pass < 3; pass++) {
+    const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
+    const int nb = pass == 2 ? 1024 : 2048;
+    for (int b = t; b < nb; b += BL_RP_THREADS) hist[b] = 0u;
+    __syncthreads();
+    for (int i = t; i < cnt; i += BL_RP_THREADS) {
+      float x = xs[i];
+      if (x > -1.0e30f) {
+        uint32_t k = bl_fkey(x);
+        if ((k & pmask) == prefix) atomicAdd(&hist[(k >> shift) & (nb - 1)], 1u);
+      }
+    }
+    __syncthreads();
+    /* bins from the top: thread t owns [nb - (t+1)*per, nb - t*per) */
+    const int per = nb / BL_RP_THREADS;
+    uint32_t local = 0u;
+    for (int q = 0; q < per; q++) local += hist[nb - 1 - (t * per + q)];
+    /* exclusive scan of `local` over threads 0..255 */
+    uint32_t inc = local;
+    int lane = t & 63, w = t >> 6;
+#pragma unroll
+    for (int k = 1; k < 64; k <<= 1) {
+      uint32_t o = __shfl_up(inc, k, 64);
+      if (lane >= k) inc += o;
+    }
+    __shared__ uint32_t wsum[4];
+    if (lane == 63) wsum[w] = inc;
+    __syncthreads();
+    uint32_t above = inc - local;
+    for (int k = 0; k < w; k++) above += wsum[k];
+    uint32_t total = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+    if (pass == 0 && total <= (uint32_t)need) {
+      take_all = true;
+    } else if (above < (uint32_t)need && above + local >= (uint32_t)need) {
+      uint32_t acc = above;
+      for (int q = 0; q < per; q++) {
+        int b = nb - 1 - (t * per + q);
+        uint32_t h = hist[b];
+        if (acc + h >= (uint32_t)need) {
+          sel[0] = (uint32_t)b;
+          sel[1] = acc;
+          sel[2] = h;
+          break;
+        }
+        acc += h;
+      }
+    }
+    __syncthreads();
+    if (take_all) break;
+    prefix |= sel[0] << shift;
+    pmask |= (uint32_t)(nb - 1) << shift;
+    need -= (int)sel[1];
+    __syncthreads();
+  }
+  /* take_all is uniform: every thread saw the same total */
+  if (t == 0) out_n = 0;
+  __syncthreads();
+  const int64_t cbase = ((int64_t)row * nc + c) * BL_KSEL_MAX;
+  const uint32_t kth = prefix;
+  const bool cut_ties = !take_all && (int)sel[2] > need;
+  int eq_before = 0; /* ties of kth at smaller indices, for the index-order cut */
+  for (int s0 = 0; s0 < cnt; s0 += BL_RP_THREADS) {
+    int i = s0 + t;
+    bool ok = false;
+    bool eq = false;
+    if (i < cnt) {
+      float x = xs[i];
+      if (x > -1.0e30f) {
+        uint32_t k = bl_fkey(x);
+        if (take_all || k > kth) ok = true;
+        else if (k == kth) eq = true;
+      }
+    }
+    if (cut_ties) {
+      unsigned long long bm = __ballot(eq);
+      int lane = t & 63, w = t >> 6;
+      __shared__ int wcnt_eq[4];
+      if (lane == 0) wcnt_eq[w] = __popcll(bm);
+      __syncthreads();
+      int before = eq_before + __popcll(bm & ((1ull << lane) - 1ull));
+      for (int k = 0; k < w; k++) before += wcnt_eq[k];
+      if (eq && before < need) ok = true;
+      eq_before += wcnt_eq[0] + wcnt_eq[1] + wcnt_eq[2] + wcnt_eq[3];
+      __syncthreads();
+    } else if (eq) {
+      ok = true;
+    }
+    if (ok) {
+      int pos = atomicAdd(&out_n, 1);
+      if (pos < K) {
+        d.cand_v[cbase + pos] = xs[i];
+        d.cand_i[cbase + pos] = i0 + i;
+      }
+    }
+  }
+  __syncthreads();
+  for (int p = min(out_n, K) + t; p < K; p += BL_RP_THREADS) {
+    d.cand_v[cbase + p] = BL_NEG_INF;
+    d.cand_i[cbase + p] = -1;
+  }
+}
+
+/* ------------------------------------------------------------------ K2: exponent pass */
+__device__ float row_max(const bl_dev &d, int row, float *sm, int *si) {
+  float m = BL_NEG_INF;
+  int mi = 0x7fffffff;
+  for (int k = threadIdx.x; k < d.nc; k += blockDim.x) argmax_merge(m, mi, d.c_max[(int64_t)row * d.nc + k], k);
+  block_argmax<BL_RP_THREADS>(m, mi, sm, si);
+  return m;
+}
+
+__global__ __launch_bounds__(BL_RP_THREADS) void bl_k_exppass(bl_dev d, bl_rows rows) {
+  const int V = d.vocab, nc = d.nc;
+  const int c = blockIdx.x, row = blockIdx.y, t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int slot = rows.slot[row];
+  const bl_slot_dev &sp = slot_of(d, slot);
+  const int mode = sp.mode;
+  if (!(mode & (BL_M_LOGPROBS | BL_M_FULL))) return;
+  __shared__ float xs[BL_CH];
+  __shared__ double gs[64];
+  __shared__ float red_m[4];
+  __shared__ int red_i[4];
+  const int i0 = c * BL_CH;
+  const int cnt = min(BL_CH, V - i0);
+  const float *src = d.eff + (int64_t)row * V + i0;
+  for (int i = t; i < BL_CH; i += BL_RP_THREADS) xs[i] = i < cnt ? src[i] : BL_NEG_INF;
+  const float M = row_max(d, row, red_m, red_i); /* includes the barrier that publishes xs */
+
+  if (mode & BL_M_LOGPROBS) {
+    /* approximate sum before this chunk, from the row pass statistics */
+    double S0 = 0.0;
+    if (t == 0)
+      for (int k = 0; k < c; k++) {
+        float cm = d.c_max[(int64_t)row * nc + k];
+        if (cm > BL_NEG_INF) S0 += (double)d.c_sum[(int64_t)row * nc + k] * exp((double)cm - (double)M);
+      }
+    /* group sums (approximate) */
+    for (int g = w; g < 64; g += BL_RP_THREADS / 64) {
+      int i = g * 64 + lane;
+      float a = i < cnt ? bl_expf(xs[i] - M) : 0.0f;
+      double sg = bl_wave_sum_d((double)a);
+      if (lane == 0) gs[g] = sg;
+    }
+    __shared__ double s0s;
+    if (t == 0) s0s = S0;
+    __syncthreads();
+    if (w == 0) {
+      double v = gs[lane];
+      double ex = bl_wave_excl_scan_d(v, lane);
+      gs[lane] = s0s + ex;
+    }
+    __syncthreads();
+    bl_grec *rec = reinterpret_cast<bl_grec *>(d.grec) + (int64_t)row * 2 * (V / 64 + 64) + (int64_t)c * 64;
+    for (int g = w; g < 64; g += BL_RP_THREADS / 64) {
+      if (i0 + g * 64 >= V) break;
+      int i = g * 64 + lane;
+      float a = i < cnt ? bl_expf(xs[i] - M) : 0.0f;
+      bl_grec r = bl_group_record(a, gs[g], lane);
+      if (lane == 0) rec[g] = r;
+    }
+  }
+  if (mode & BL_M_FULL) {
+    float T = sp.temperature;
+    float span = 17.5f * (T > 1.0f ? T : 1.0f);
+    float thr = M - span;
+    for (int i = t; i < cnt; i += BL_RP_THREADS) {
+      float x = xs[i];
+      if (x >= thr) {
+        int pos = atomicAdd(&d.full_n[row], 1);
+        if (pos < V) {
+          d.full_v[(int64_t)row * V + pos] = x;
+          d.full_i[(int64_t)row * V + pos] = i0 + i;
+        }
+      }
+    }
+  }
+}
+
+/* ------------------------------------------------------------------ K3: per-row selection */
+#define SEL_NW (BL_SEL_THREADS / 64)
+
+/* LDS-resident candidate list as composite keys: (fkey(value) << 32) | ~index, descending order */
+__device__ __forceinline__ uint64_t ckey(float v, int32_t id) {
+  return ((uint64_t)bl_fkey(v) << 32) | (uint64_t)(0xffffffffu - (uint32_t)id);
+}
+__device__ __forceinline__ float ckey_v(uint64_t k) { return bl_fkey_inv((uint32_t)(k >> 32)); }
+__device__ __forceinline__ int32_t ckey_i(uint64_t k) { return (int32_t)(0xffffffffu - (uint32_t)k); }
+
+__device__ void bitonic_desc(uint64_t *s, int P) {
+  for (int k = 2; k <= P; k <<= 1)
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = threadIdx.x; i < P; i += blockDim.x) {
+        int ixj = i ^ j;
+        if (ixj > i) {
+          uint64_t a = s[i], b = s[ixj];
+          bool desc = (i & k) == 0;
+          if (desc ? (a < b) : (a > b)) {
+            s[i] = b;
+            s[ixj] = a;
+          }
+        }
+      }
+      __syncthreads();
+    }
+}
+
+/* Phase A over a list of n terms, records into `recs`, approximate sums through `gsum` */
+template <class TermF>
+__device__ void block_records(int64_t n, TermF term, bl_grec *recs, double *gsum) {
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int64_t G = (n + 63) / 64;
+  for (int64_t g = w; g < G; g += SEL_NW) {
+    int64_t j = g * 64 + lane;
+    float a = j < n ? term(j) : 0.0f;
+    double sg = bl_wave_sum_d((double)a);
+    if (lane == 0) gsum[g] = sg;
+  }
+  __syncthreads();
+  if (w == 0) {
+    double run = 0.0;
+    for (int64_t g0 = 0; g0 < G; g0 += 64) {
+      int64_t g = g0 + lane;
+      double v = g < G ? gsum[g] : 0.0;
+      double ex = bl_wave_excl_scan_d(v, lane);
+      double tot = __shfl(ex + v, 63, 64);
+      if (g < G) gsum[g] = run + ex;
+      run += tot;
+    }
+  }
+  __syncthreads();
+  for (int64_t g = w; g < G; g += SEL_NW) {
+    int64_t j = g * 64 + lane;
+    float a = j < n ? term(j) : 0.0f;
+    bl_grec r = bl_group_record(a, gsum[g], lane);
+    if (lane == 0) recs[g] = r;
+  }
+  __syncthreads();
+}
+
+struct sel_shared {
+  uint64_t keys[BL_LDS_SORT];
+  bl_grec recs[BL_LDS_SORT / 64];
+  double gsum[BL_LDS_SORT / 64];
+  float fres[8];
+  int ires[8];
+  float red_m[SEL_NW];
+  int red_i[SEL_NW];
+};
+
+/*
+ * sample_candidates_with_probs (src/sampling.br:490-607) for T > 0 on the ranked list `vals/ids`
+ * (n_list entries materialised; n_logical >= n_list is the reference's candidate count, the
+ * entries past n_list being too small to change any float32 sum). Returns the chosen position,
+ * or -1 with `status` set.
+ */
+template <class ValF>
+__device__ int sample_ranked(const bl_slot_dev &sp, ValF val, int64_t n_list, int64_t n_logical, uint64_t &rng,
+                             int rng_skip, bl_grec *recs, double *gsum, sel_shared &sh, int &status) {
+  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+  const float T = sp.temperature;
+  int64_t keep = sp.min_keep > 1 ? sp.min_keep : 1;
+  if (keep > n_logical) keep = n_logical;
+  if (sp.typical_p < 1.0f || (sp.xtc_probability > 0.0f && sp.xtc_threshold <= 0.5f) || sp.dynatemp_range > 0.0f ||
+      keep > n_list) {
+    status |= BL_SE_UNSUPPORTED;
+    return -1;
+  }
+  const float v0 = val(0);
+  int64_t cutoff = n_logical;
+  if (sp.top_p < 1.0f || sp.min_p > 0.0f) {
+    auto termE = [&](int64_t j) { return bl_expf(val(j) - v0); };
+    block_records(n_list, termE, recs, gsum);
+    if (w == 0) {
+      float S;
+      bl_seq_walk(n_list, termE, [&](int64_t g) { return recs[g]; }, false, 0.0f, 0, S, lane);
+      if (lane == 0) sh.fres[0] = S;
+    }
+    __syncthreads();
+    const float sum_exp = sh.fres[0];
+    __syncthreads();
+    auto termP = [&](int64_t j) { return bl_expf(val(j) - v0) / sum_exp; };
+    if (sp.top_p < 1.0f) {
+      block_records(n_list, termP, recs, gsum);
+      if (w == 0) {
+        float S;
+        int f = bl_seq_walk(n_list, termP, [&](int64_t g) { return recs[g]; }, true, sp.top_p, keep - 1, S, lane);
+        if (lane == 0) sh.ires[0] = f;
+      }
+      __syncthreads();
+      if (sh.ires[0] >= 0) cutoff = sh.ires[0] + 1;
+      __syncthreads();
+    }
+    if (sp.min_p > 0.0f) {
+      const float p0 = termP(0);
+      const float threshold = p0 * sp.min_p;
+      /* first j in [keep, cutoff) with probs[j] < threshold */
+      if (t == 0) sh.ires[1] = 0x7fffffff;
+      __syncthreads();
+      int64_t lim = cutoff < n_list ? cutoff : n_list;
+      for (int64_t j = keep + t; j < lim; j += blockDim.x)
+        if (termP(j) < threshold) atomicMin(&sh.ires[1], (int)j);
+      __syncthreads();
+      int64_t first_small = sh.ires[1];
+      if (first_small == 0x7fffffff) {
+        if (lim < cutoff) {
+          /* the next, unmaterialised candidate is below 2^-25 of the top one */
+          if (threshold <= p0 * 5.9604645e-8f) status |= BL_SE_UNSUPPORTED;
+          first_small = lim;
+        } else {
+          first_small = cutoff;
+        }
+      }
+      cutoff = keep > first_small ? keep : first_small;
+      __syncthreads();
+    }
+  }
+  if (status) return -1;
+  const int64_t n_eff = cutoff < n_list ? cutoff : n_list;
+  auto termR = [&](int64_t j) {
+    float dd = val(j) - v0;
+    float q = dd / T;
+    return bl_expf(q);
+  };
+  block_records(n_eff, termR, recs, gsum);
+  if (w == 0) {
+    float S;
+    bl_seq_walk(n_eff, termR, [&](int64_t g) { return recs[g]; }, false, 0.0f, 0, S, lane);
+    uint64_t st = rng;
+    for (int k = 0; k < rng_skip; k++) st = bl_xorshift(st);
+    float r01 = bl_rng_f32(&st);
+    float target = r01 * S;
+    float S2;
+    int f = bl_seq_walk(n_eff, termR, [&](int64_t g) { return recs[g]; }, true, target, 0, S2, lane);
+    if (lane == 0) {
+      sh.ires[2] = f >= 0 ? f : (int)(cutoff - 1);
+      sh.fres[1] = S;
+      *reinterpret_cast<uint64_t *>(&sh.fres[2]) = st;
+    }
+  }
+  __syncthreads();
+  int chosen = sh.ires[2];
+  rng = *reinterpret_cast<uint64_t *>(&sh.fres[2]);
+  __syncthreads();
+  if (chosen >= n_list) {
+    status |= BL_SE_UNSUPPORTED;
+    return -1;
+  }
+  return chosen;
+}
+
+__global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows rows) {
+  const int V = d.vocab, nc = d.nc;
+  const int row = blockIdx.x, t = threadIdx.x, w = t >> 6, lane = t & 63;
+  const int slot = rows.slot[row];
+  bl_slot_dev &sp = d.slots[slot];
+  const int mode = sp.mode;
+  __shared__ sel_shared sh;
+  int status = 0;
+
+  /* row max and first argmax from the chunk statistics */
+  float M = BL_NEG_INF;
+  int Mi = 0x7fffffff;
+  for (int k = t; k < nc; k += BL_SEL_THREADS) {
+    float cm = d.c_max[(int64_t)row * nc + k];
+    argmax_merge(M, Mi, cm, d.c_arg[(int64_t)row * nc + k]);
+  }
+  block_argmax<BL_SEL_THREADS>(M, Mi, sh.red_m, sh.red_i);
+  if (Mi == 0x7fffffff) Mi = 0;
+
+  /* exact index-order normaliser (wave 0 walks the records written by the exponent pass) */
+  const float *eff = d.eff + (int64_t)row * V;
+  float lse = 0.0f;
+  if (mode & BL_M_LOGPROBS) {
+    if (w == 0) {
+      const bl_grec *rec = reinterpret_cast<const bl_grec *>(d.grec) + (int64_t)row * 2 * (V / 64 + 64);
+      float S;
+      bl_seq_walk((int64_t)V, [&](int64_t j) { return bl_expf(eff[j] - M); }, [&](int64_t g) { return rec[g]; },
+                  false, 0.0f, 0, S, lane);
+      if (lane == 0) sh.fres[4] = (float)log((double)S);
+    }
+    __syncthreads();
+    lse = sh.fres[4];
+    __syncthreads();
+  }
+
+  /* merged top-K candidates of the row pass: sorted (value desc, index asc) in sh.keys */
+  int n_top = 0;
+  const int K = sp.k_sel;
+  if (K > 0) {
+    int total = nc * K;
+    int P = 1;
+    while (P < total) P <<= 1;
+    for (int i = t; i < P; i += BL_SEL_THREADS) {
+      uint64_t k = 0ull;
+      if (i < total) {
+        int ch = i / K, q = i % K;
+        int64_t o = ((int64_t)row * nc + ch) * BL_KSEL_MAX + q;
+        int32_t id = d.cand_i[o];
+        if (id >= 0) k = ckey(d.cand_v[o], id);
+      }
+      sh.keys[i] = k;
+    }
+    __syncthreads();
+    bitonic_desc(sh.keys, P);
+    n_top = K;
+  }
+
+  uint64_t rng = sp.rng;
+  const int skip = rows.rng_skip ? rows.rng_skip[row] : 0;
+  int32_t tok = Mi;
+  const float T = sp.temperature;
+  if (T <= 0.0f) {
+    tok = Mi; /* sample_greedy over the full penalised row (src/sampling.br:752-754) */
+  } else if (mode & BL_M_TOPK) {
+    /* top_k_select list: kk = min(top_k, V) entries, unfilled slots are (-1e30, 0) */
+    int64_t kk = sp.top_k < V ? sp.top_k : V;
+    auto val = [&](int64_t j) -> float { return sh.keys[j] ? ckey_v(sh.keys[j]) : -1.0e30f; };
+    int pos = sample_ranked(sp, val, kk, kk, rng, skip, sh.recs, sh.gsum, sh, status);
+    if (pos >= 0) tok = sh.keys[pos] ? ckey_i(sh.keys[pos]) : 0;
+  } else {
+    /* full-vocabulary rank (src/sampling.br:301-365): candidates from the exponent pass */
+    int nf = d.full_n[row];
+    if (nf > V) {
+      nf = V;
+      status |= BL_SE_CAND_FULL;
+    }
+    int P = 1;
+    while (P < nf) P <<= 1;
+    uint64_t *keys = P <= BL_LDS_SORT ? sh.keys : d.sortk + (int64_t)row * (2 * (int64_t)V);
+    /* when the LDS holds the merged top-K list (logprob alternatives) keep it: sort the full list in global */
+    if (K > 0 && keys == sh.keys) keys = d.sortk + (int64_t)row * (2 * (int64_t)V);
+    for (int i = t; i < P; i += BL_SEL_THREADS)
+      keys[i] = i < nf ? ckey(d.full_v[(int64_t)row * V + i], d.full_i[(int64_t)row * V + i]) : 0ull;
+    __syncthreads();
+    bitonic_desc(keys, P);
+    bl_grec *recs = sh.recs;
+    double *gsum = sh.gsum;
+    if ((nf + 63) / 64 > BL_LDS_SORT / 64) {
+      recs = reinterpret_cast<bl_grec *>(d.grec) + (int64_t)row * 2 * (V / 64 + 64) + (V / 64 + 64);
+      gsum = d.gsum + (int64_t)row * (V / 64 + 64);
+    }
+    auto val = [&](int64_t j) -> float { return ckey_v(keys[j]); };
+    int pos = sample_ranked(sp, val, nf, (int64_t)V, rng, skip, recs, gsum, sh, status);
+    if (pos >= 0) {
+      tok = ckey_i(keys[pos]);
+      /* the heap rank orders equal values its own way (src/sampling.br:310-364): a tie at the chosen
+       * position is reported instead of guessing */
+      float vp = val(pos);
+      if ((pos > 0 && val(pos - 1) == vp) || (pos + 1 < nf && val(pos + 1) == vp)) status |= BL_SE_TIE;
+    }
+  }
+
+  /* outputs, logprobs (src/server.br:1027-1035) */
+  if (t == 0) {
+    rows.tok[row] = tok;
+    if (rows.status) rows.status[row] = status;
+    bool is_eog = false;
+    for (int k = 0; k < d.n_eog; k++) is_eog |= d.eog[k] == tok;
+    if ((mode & BL_M_LOGPROBS) && rows.lp) {
+      float a = eff[tok] - M;
+      rows.lp[row] = a - lse;
+      for (int q = 0; q < sp.n_probs && q < rows.top_stride; q++) {
+        uint64_t k = q < n_top ? sh.keys[q] : 0ull;
+        int32_t id = k ? ckey_i(k) : 0;
+        float v = k ? ckey_v(k) : -1.0e30f;
+        rows.top_ids[(int64_t)row * rows.top_stride + q] = id;
+        float b = v - M;
+        rows.top_lp[(int64_t)row * rows.top_stride + q] = b - lse;
+      }
+    }
+    if (rows.commit && status == 0) {
+      /* tokens.push (src/server.br:1004): repeat window; reply_tokens.push unless EOG (:1037) */
+      const int64_t so = (int64_t)slot * V;
+      uint32_t *tw = d.touched + (int64_t)slot * d.words;
+      sp.n_tokens += 1;
+      if (sp.rep_on) {
+        int rl = sp.repeat_last_n;
+        if (rl > 0) {
+          int32_t *ring = d.ring + (int64_t)slot * BL_WCAP;
+          if (sp.win_len == rl) {
+            int32_t old = ring[sp.win_head];
+            d.wcnt[so + old] -= 1;
+            ring[sp.win_head] = tok;
+            sp.win_head = (sp.win_head + 1) % rl;
+          } else {
+            ring[(sp.win_head + sp.win_len) % rl] = tok;
+            sp.win_len += 1;
+          }
+        }
+        d.wcnt[so + tok] += 1;
+        tw[tok >> 5] |= 1u << (tok & 31);
+      }
+      if (!is_eog) {
+        sp.n_reply += 1;
+        if (sp.fp_on) {
+          d.cnt[so + tok] += 1;
+          tw[tok >> 5] |= 1u << (tok & 31);
+        }
+      }
+      sp.rng = rng;
+    }
+    if (status) sp.err |= status;
+  }
+}
+
+/* ------------------------------------------------------------------ synthetic inputs for the benchmark */
+__global__ void bl_k_synth(float *out, int64_t ld, int cfg, int64_t seed, int64_t step0, int rows, int V) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int r = blockIdx.y;
+  if (i >= V) return;
+  int64_t step = step0;
+  uint64_t st = bl_stream((uint32_t)cfg, seed, step, r, BL_P_LOGIT);
+  out[(int64_t)r * ld + i] = bl_normal(st, (uint64_t)i, bl_cfg_sigma(cfg));
+}
+
+/* ------------------------------------------------------------------ host-side launchers */
+void bl_launch_step(const bl_dev &d, const float *logits, int64_t ld, const bl_rows &rows, int B, bool need_exp,
+                    hipStream_t s) {
+  dim3 g1(d.nc, B);
+  hipLaunchKernelGGL(bl_k_rowpass, g1, dim3(BL_RP_THREADS), 0, s, d, logits, ld, rows);
+  if (need_exp) {
+    hipLaunchKernelGGL(bl_k_exppass, g1, dim3(BL_RP_THREADS), 0, s, d, rows);
+  }
+  hipLaunchKernelGGL(bl_k_select, dim3(B), dim3(BL_SEL_THREADS), 0, s, d, rows);
+}
+
+void bl_launch_synth(float *out, int64_t ld, int cfg, int64_t seed, int64_t step, int rows, int V, hipStream_t s) {
+  dim3 g((V + 255) / 256, rows);
+  hipLaunchKernelGGL(bl_k_synth, g, dim3(256), 0, s, out, ld, cfg, seed, step, rows, V);
+}
+
+/* ------------------------------------------------------------------ math self-test */
+/* Digest of f over input bit patterns [b*2^20, (b+1)*2^20): sum of splitmix(u << 32 | bits(f(u))). */
+__global__ void bl_k_math_digest(int fn, uint32_t first_block, unsigned long long *out) {
+  const uint32_t blk = first_block + blockIdx.y;
+  const uint32_t base = blk << 20;
+  uint64_t h = 0;
+  for (int k = 0; k < 16; k++) {
+    uint32_t u = base + (uint32_t)(blockIdx.x * 4096 + k * 256 + threadIdx.x);
+    float x = bl_u2f(u);
+    float y = fn == 0 ? bl_expf(x) : bl_tanhf(x);
+    uint32_t yb = y != y ? 0x7fc00000u : bl_f2u(y); /* NaN payloads are not part of the path */
+    h += bl_splitmix(((uint64_t)u << 32) | yb);
+  }
+#pragma unroll
+  for (int k = 32; k >= 1; k >>= 1) h += (uint64_t)__shfl_xor((long long)h, k, 64);
+  if ((threadIdx.x & 63) == 0) atomicAdd(out + blockIdx.y, (unsigned long long)h);
+}
+
+__global__ void bl_k_zero_u64(unsigned long long *p, int n) {
+  int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0ull;
+}
+
+void bl_launch_math_digest(int fn, uint32_t first_block, int n_blocks, unsigned long long *out, hipStream_t s) {
+  hipLaunchKernelGGL(bl_k_zero_u64, dim3((n_blocks + 255) / 256), dim3(256), 0, s, out, n_blocks);
+  hipLaunchKernelGGL(bl_k_math_digest, dim3(256, n_blocks), dim3(256), 0, s, fn, first_block, out);
+}

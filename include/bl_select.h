@@ -1,0 +1,135 @@
+/*
+ * bl_select.h — C ABI of boring-llm's per-step token selection on MI355X (libbl_select.so).
+ *
+ * The reference runs this path as Boring functions on host rows (src/sampling.br, src/grammar.br,
+ * src/server.br:939-1231); its generated Rust target would declare these functions in an
+ * `extern "C"` block and keep the Boring-level API unchanged. Every entry point below names the
+ * reference function(s) it replaces. Plain C types only; logits are borrowed device pointers.
+ *
+ * Threading: a context is used by one host thread at a time; contexts are independent. Calls are
+ * ordered on the context's stream; the synchronous entry points return once results are in host
+ * memory. Errors: a negative BL_E* code, with the reference's message from bl_last_error().
+ */
+#ifndef BL_SELECT_H
+#define BL_SELECT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct bl_ctx bl_ctx;
+
+enum {
+  BL_OK = 0,
+  BL_EPARAM = -1,          /* a value outside the request validation ranges (src/openai.br:1652-1890) */
+  BL_EDEVICE = -2,         /* HIP runtime failure */
+  BL_EEMPTY = -3,          /* "sample_candidates: empty or mismatched candidates" (src/sampling.br:495) */
+  BL_EGRAMMAR = -4,        /* GBNF parse error (src/grammar.br:57-323) */
+  BL_EGRAMMAR_DEAD = -5,   /* "the reply no longer matches the grammar" (src/server.br:320) */
+  BL_EGRAMMAR_REJECT = -6, /* "the grammar rejected every vocabulary token" (src/server.br:361) */
+  BL_EGRAMMAR_AMBIG = -7,  /* "grammar is left-recursive or too ambiguous to match" (src/grammar.br:354) */
+  BL_EUNSUPPORTED = -8,    /* a sampler stage this library does not run on the device yet */
+  BL_ETIE = -9             /* full-vocabulary draw landed on equal logits (heap order needed) */
+};
+
+/* SamplingParams (src/model.br:1565-1584) + the per-request server fields (src/server.br:665-760).
+ * Defaults are greedy_params() (src/model.br:1586-1589). */
+typedef struct {
+  float temperature;       /* <= 0: greedy */
+  float dynatemp_range;
+  float dynatemp_exponent;
+  float top_n_sigma;       /* <= 0: off */
+  int32_t top_k;           /* <= 0 or >= vocab: full-vocabulary rank */
+  float typical_p;
+  float top_p;
+  float min_p;
+  float xtc_probability;
+  float xtc_threshold;
+  int32_t min_keep;
+  float repeat_penalty;    /* 1: off */
+  int32_t repeat_last_n;   /* 0: off, -1: whole history */
+  float dry_multiplier;    /* 0: off */
+  float dry_base;
+  int32_t dry_allowed_length;
+  int32_t dry_penalty_last_n;
+  float frequency_penalty; /* server extras */
+  float presence_penalty;
+  int32_t logprobs;        /* 1: return the chosen token's logprob (wants_logprobs) */
+  int32_t n_probs;         /* alternatives returned with logprobs (0..256) */
+  int32_t post_sampling_probs;
+  int32_t ignore_eos;
+  float final_softcap;     /* model tail (src/model.br:973-984): 0 = off */
+  float logit_mul;         /* model tail: 1 = off */
+} bl_params;
+
+void bl_params_default(bl_params *p);
+
+/* Context on `device` for up to `max_slots` concurrent requests and `max_rows` rows per call, over a
+ * vocabulary of `vocab` tokens. Replaces nothing in the reference (it holds no device state). */
+int bl_create(int device, int max_slots, int max_rows, int vocab, bl_ctx **out);
+void bl_destroy(bl_ctx *ctx);
+const char *bl_last_error(void);
+/* The HIP stream the context's work is ordered on (hipStream_t); NULL selects the context's own. */
+int bl_set_stream(bl_ctx *ctx, void *stream);
+
+/* End-of-generation registry: src/sampling.br:200-237 (set_eog_tokens / is_eog_token). */
+int bl_set_eog(bl_ctx *ctx, int32_t eos_id, const int32_t *eog_ids, int n_eog);
+
+/* A new request on `slot`: seed_rng (src/sampling.br:35-40) is the caller's rng_state; history =
+ * prompt + reply tokens (repeat penalty / DRY, src/sampling.br:65-85), reply = reply tokens
+ * (frequency / presence, :91-107), logit_bias as parallel arrays (src/server.br:150-185, :940). */
+int bl_slot_reset(bl_ctx *ctx, int slot, const bl_params *p, uint64_t rng_state, const int32_t *history, int n_hist,
+                  const int32_t *reply, int n_reply, const int32_t *bias_ids, const float *bias_vals, int n_bias);
+/* The slot's current xorshift64 state (Rng.state, src/sampling.br:18-19). */
+int bl_slot_rng(bl_ctx *ctx, int slot, uint64_t *state);
+/* Append tokens chosen elsewhere to the slot history (tokens.push / reply_tokens.push,
+ * src/server.br:1004, :1037). */
+int bl_slot_commit(bl_ctx *ctx, int slot, const int32_t *toks, int n);
+
+/* One decode-loop sampling block for B slots (src/server.br:940-1037: logit_bias, ignore_eos,
+ * frequency/presence, then sample() = sampling_logits + greedy | rank + sample_candidates, then
+ * logprob_normalizer + top_k_select for logprobs). `d_logits` is a device pointer to B rows of
+ * `ld` floats. The chosen tokens are appended to each slot's history. Host outputs; `logprobs`,
+ * `top_ids`, `top_logprobs` may be NULL; `top_stride` entries per row. */
+int bl_sample_step(bl_ctx *ctx, const int32_t *slots, int B, const float *d_logits, int64_t ld, int32_t *tokens,
+                   float *logprobs, int32_t *top_ids, float *top_logprobs, int top_stride);
+
+/* The same step with device-memory outputs and no host synchronisation, on the context stream
+ * (capturable in a HIP graph once bl_bind_rows has fixed the row table). */
+int bl_bind_rows(bl_ctx *ctx, const int32_t *slots, int B);
+int bl_sample_step_async(bl_ctx *ctx, int B, const float *d_logits, int64_t ld, int32_t *d_tokens, float *d_logprobs,
+                         int32_t *d_top_ids, float *d_top_logprobs, int top_stride);
+
+/* Speculative verification (src/server.br:1173-1216): for each of the B slots, rows
+ * d_rows[b*(k+1) + i] (i = 0..k) are the target logits after feeding drafts[b*k .. b*k+i). Row i is
+ * sampled with the slot's RNG advanced by i draws; accepted[b] = number of leading rows whose token
+ * equals its draft; the slot commits drafts[0..accepted) and tokens[b*(k+1)+accepted].
+ * `tokens` receives every row's token (row i as if drafts[0..i) were accepted). */
+int bl_spec_verify(bl_ctx *ctx, const int32_t *slots, int B, int k, const float *d_rows, int64_t ld,
+                   const int32_t *drafts, int32_t *tokens, int32_t *accepted);
+
+/* Benchmark/test input generation (no reference counterpart): fills `rows` rows of `ld` floats with
+ * the synthetic logits of workload `cfg` (integer-only generator, identical on host and device). */
+int bl_synth_logits(bl_ctx *ctx, float *d_out, int64_t ld, int cfg, int64_t seed, int64_t step, int rows, int vocab);
+
+/* Sparse inputs of the benchmark workloads (no reference counterpart; host only): kind 0 = uniform
+ * ids, kind 1 = Zipf(1.1) ids; logit_bias lists of n distinct ids with values in [lo, hi); speculative
+ * drafts (argmax with probability 0.7, else uniform). Deterministic in (cfg, seed, row/step). */
+int bl_workload_ids(int kind, int cfg, int64_t seed, int row, int n, int vocab, int32_t *out);
+int bl_workload_bias(int cfg, int64_t seed, int row, int n, int vocab, float lo, float hi, int32_t *ids, float *vals);
+int bl_workload_drafts(int64_t seed, int64_t step, int seq, const int32_t *argmax, int k, int vocab, int32_t *out);
+
+/* Self-test (no reference counterpart): digests of the device expf (fn 0) / tanhf (fn 1) over
+ * input bit-pattern blocks [b*2^20, (b+1)*2^20), b = first_block .. first_block+n_blocks-1; each digest
+ * is the wrapping sum of splitmix64(u << 32 | bits(f(u))) with NaN results canonicalised to 0x7fc00000.
+ * Compared with host-glibc fixtures. */
+int bl_math_digest(bl_ctx *ctx, int fn, uint32_t first_block, int n_blocks, uint64_t *out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BL_SELECT_H */

@@ -1,0 +1,51 @@
+"""The C-ABI library loads and exports every function include/*.h declares (no GPU needed: no
+compute call is made)."""
+import ctypes
+import glob
+import os
+import re
+
+import bl_select as BL
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared():
+    names = set()
+    for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        names |= set(re.findall(r"^\s*[A-Za-z_][\w\s\*]*?\b(bl_\w+)\s*\(", text, flags=re.M))
+    return names
+
+
+def test_header_declares_the_boundary():
+    names = declared()
+    for must in ("bl_create", "bl_slot_reset", "bl_sample_step", "bl_spec_verify", "bl_last_error"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(BL.LIB_PATH)
+    missing = [n for n in sorted(declared()) if not hasattr(lib, n)]
+    assert not missing, missing
+    assert set(BL.EXPORTS) <= declared()
+
+
+def test_params_layout_matches_header():
+    # bl_params is 25 4-byte fields in the header's order
+    assert ctypes.sizeof(BL.Params) == 25 * 4
+    p = BL.Params()
+    assert p.temperature == 0.0 and p.top_p == 1.0 and p.repeat_last_n == 64 and p.dynatemp_exponent == 1.0
+
+
+def test_seed_fold():
+    # seed_rng (src/sampling.br:35-40)
+    assert BL.seed_rng(0) == 88172645463325252
+    assert BL.seed_rng(5) == 5 ^ 88172645463325252
+
+
+def test_workload_generators_are_deterministic():
+    a = BL.workload_ids(1, 2, 2, 0, 64, 151936)
+    assert a == BL.workload_ids(1, 2, 2, 0, 64, 151936) and min(a) >= 0 and max(a) < 151936
+    b = BL.workload_bias(2, 2, 0, 300, 151936, -100.0, 100.0)
+    assert len(b) == 300 and all(-100.0 <= v < 100.0 for v in b.values())
