@@ -94,26 +94,31 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass(bl_dev d, const fl
   const int cnt = min(BL_CH, V - i0);
   const float *src = logits + (int64_t)row * ld + i0;
   if (c == 0 && t == 0) d.full_n[row] = 0; /* consumed by the exponent pass, which runs after this kernel */
+  /* model tail (src/model.br:973-984), applied in registers by the thread that loads the value */
+  const float lmul = sp.logit_mul, cap = sp.final_softcap;
+  const bool tail = lmul != 1.0f || cap > 0.0f;
+  auto finish = [&](float x) {
+    if (lmul != 1.0f) x = x * lmul;
+    if (cap > 0.0f) {
+      float q = x / cap;
+      x = cap * bl_tanhf(q);
+    }
+    return x;
+  };
   if (cnt == BL_CH && (((uintptr_t)src) & 15) == 0) {
 #pragma unroll
     for (int j = 0; j < BL_CH / (4 * BL_RP_THREADS); j++) {
       float4 v = reinterpret_cast<const float4 *>(src)[j * BL_RP_THREADS + t];
+      if (tail) {
+        v.x = finish(v.x);
+        v.y = finish(v.y);
+        v.z = finish(v.z);
+        v.w = finish(v.w);
+      }
       reinterpret_cast<float4 *>(xs)[j * BL_RP_THREADS + t] = v;
     }
   } else {
-    for (int i = t; i < cnt; i += BL_RP_THREADS) xs[i] = src[i];
-  }
-  const float lmul = sp.logit_mul, cap = sp.final_softcap;
-  if (lmul != 1.0f || cap > 0.0f) {
-    for (int i = t; i < cnt; i += BL_RP_THREADS) {
-      float x = xs[i];
-      if (lmul != 1.0f) x = x * lmul;
-      if (cap > 0.0f) {
-        float q = x / cap;
-        x = cap * bl_tanhf(q);
-      }
-      xs[i] = x;
-    }
+    for (int i = t; i < cnt; i += BL_RP_THREADS) xs[i] = tail ? finish(src[i]) : src[i];
   }
   __syncthreads();
   /* server stages at the touched tokens of this chunk */

@@ -149,7 +149,8 @@ def test_workload4_softcap_topk(cuda):
             assert tok[r] == wt[a], f"step {t} row {r}"
             assert lp_close(lp[r], wl[a]), f"step {t} row {r}: {lp[r]!r} vs {wl[a]!r}"
             assert ti[r] == list(wi[a * 20:(a + 1) * 20])
-            assert all(lp_close(tl[r][q], wp[a * 20 + q]) for q in range(20))
+            for q in range(20):
+                assert lp_close(tl[r][q], wp[a * 20 + q]), (t, r, q, ti[r][q], tl[r][q], float(wp[a * 20 + q]), lp[r])
     ctx.close()
 
 
