@@ -47,7 +47,7 @@ EXPORTS = [
     "bl_params_default", "bl_create", "bl_destroy", "bl_last_error", "bl_set_stream", "bl_set_eog",
     "bl_slot_reset", "bl_slot_rng", "bl_slot_commit", "bl_sample_step", "bl_bind_rows", "bl_sample_step_async",
     "bl_spec_verify", "bl_synth_logits", "bl_math_digest", "bl_workload_ids", "bl_workload_bias",
-    "bl_workload_drafts",
+    "bl_workload_drafts", "bl_set_timing", "bl_get_timing",
 ]
 
 _lib = None
@@ -81,6 +81,8 @@ def lib():
         L.bl_synth_logits.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_int, C.c_int64, C.c_int64, C.c_int,
                                       C.c_int]
         L.bl_math_digest.argtypes = [C.c_void_p, C.c_int, C.c_uint32, C.c_int, u64p]
+        L.bl_set_timing.argtypes = [C.c_void_p, C.c_int]
+        L.bl_get_timing.argtypes = [C.c_void_p, C.POINTER(C.c_double), C.POINTER(C.c_int64)]
         L.bl_workload_ids.argtypes = [C.c_int, C.c_int, C.c_int64, C.c_int, C.c_int, C.c_int, i32p]
         L.bl_workload_bias.argtypes = [C.c_int, C.c_int64, C.c_int, C.c_int, C.c_int, C.c_float, C.c_float, i32p,
                                        f32p]
@@ -117,6 +119,21 @@ class Context:
             self.close()
         except Exception:
             pass
+
+    def set_stream(self, stream_ptr):
+        """Order the context's work on an existing HIP stream (0 = the context's own)."""
+        _check(lib().bl_set_stream(self.h, C.c_void_p(stream_ptr)))
+
+    def set_timing(self, enable):
+        _check(lib().bl_set_timing(self.h, 1 if enable else 0))
+
+    def get_timing(self):
+        """(ms per step of the row pass, exponent pass, selection kernel; timed steps)"""
+        ms = (C.c_double * 3)()
+        n = C.c_int64()
+        _check(lib().bl_get_timing(self.h, ms, C.byref(n)))
+        k = max(n.value, 1)
+        return [ms[i] / k for i in range(3)], n.value
 
     def set_eog(self, eos_id, eog_ids=()):
         a, n = _arr(C.c_int32, eog_ids)

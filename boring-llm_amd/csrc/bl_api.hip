@@ -18,7 +18,7 @@
 #include "bl_workload.h"
 
 void bl_launch_step(const bl_dev &d, const float *logits, int64_t ld, const bl_rows &rows, int B, bool need_exp,
-                    hipStream_t s);
+                    hipStream_t s, hipEvent_t *ev);
 void bl_launch_synth(float *out, int64_t ld, int cfg, int64_t seed, int64_t step, int rows, int V, hipStream_t s);
 void bl_launch_math_digest(int fn, uint32_t first_block, int n_blocks, unsigned long long *out, hipStream_t s);
 
@@ -54,6 +54,10 @@ struct bl_ctx {
   int32_t *d_commit_toks = nullptr;
   int bound_B = 0;
   std::vector<void *> allocs;
+  bool timing = false;
+  hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};
+  double kernel_ms[3] = {0.0, 0.0, 0.0};
+  int64_t timed_steps = 0;
 };
 
 template <class T>
@@ -227,6 +231,8 @@ void bl_destroy(bl_ctx *c) {
   void *hp[] = {c->h_slot, c->h_skip, c->h_tok, c->h_status, c->h_lp, c->h_top_ids, c->h_top_lp};
   for (void *p : hp)
     if (p) hipHostFree(p);
+  for (hipEvent_t e : c->ev)
+    if (e) hipEventDestroy(e);
   if (c->own) hipStreamDestroy(c->own);
   delete c;
 }
@@ -442,7 +448,7 @@ int bl_sample_step(bl_ctx *c, const int32_t *slots, int B, const float *d_logits
   memcpy(c->h_slot, slots, B * sizeof(int32_t));
   HIPCHK(hipMemcpyAsync(c->d_slot, c->h_slot, B * sizeof(int32_t), hipMemcpyHostToDevice, c->stream));
   bl_rows rows = make_rows(c, false, 1, top_stride > 0 ? top_stride : 1);
-  bl_launch_step(c->d, d_logits, ld, rows, B, needs_exp(c, slots, B), c->stream);
+  bl_launch_step(c->d, d_logits, ld, rows, B, needs_exp(c, slots, B), c->stream, nullptr);
   HIPCHK(hipGetLastError());
   HIPCHK(hipMemcpyAsync(c->h_tok, c->d_tok, B * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));
   HIPCHK(hipMemcpyAsync(c->h_status, c->d_status, B * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));
@@ -481,8 +487,39 @@ int bl_sample_step_async(bl_ctx *c, int B, const float *d_logits, int64_t ld, in
   rows.lp = d_logprobs;
   rows.top_ids = d_top_ids ? d_top_ids : c->d_top_ids;
   rows.top_lp = d_top_logprobs ? d_top_logprobs : c->d_top_lp;
-  bl_launch_step(c->d, d_logits, ld, rows, B, needs_exp(c, c->h_slot, B), c->stream);
+  hipEvent_t *ev = nullptr;
+  if (c->timing) {
+    if (!c->ev[0])
+      for (int k = 0; k < 4; k++) HIPCHK(hipEventCreate(&c->ev[k]));
+    ev = c->ev;
+  }
+  bl_launch_step(c->d, d_logits, ld, rows, B, needs_exp(c, c->h_slot, B), c->stream, ev);
   HIPCHK(hipGetLastError());
+  if (ev) {
+    /* per-kernel durations of this step, accumulated (the caller asked for timing: synchronous) */
+    HIPCHK(hipEventSynchronize(ev[3]));
+    for (int k = 0; k < 3; k++) {
+      float ms = 0.0f;
+      HIPCHK(hipEventElapsedTime(&ms, ev[k], ev[k + 1]));
+      c->kernel_ms[k] += ms;
+    }
+    c->timed_steps += 1;
+  }
+  return BL_OK;
+}
+
+int bl_set_timing(bl_ctx *c, int enable) {
+  if (!c) return fail(BL_EPARAM, "null context");
+  c->timing = enable != 0;
+  for (int k = 0; k < 3; k++) c->kernel_ms[k] = 0.0;
+  c->timed_steps = 0;
+  return BL_OK;
+}
+
+int bl_get_timing(bl_ctx *c, double *ms_total3, int64_t *steps) {
+  if (!c || !ms_total3 || !steps) return fail(BL_EPARAM, "bl_get_timing: invalid arguments");
+  for (int k = 0; k < 3; k++) ms_total3[k] = c->kernel_ms[k];
+  *steps = c->timed_steps;
   return BL_OK;
 }
 
@@ -509,7 +546,7 @@ int bl_spec_verify(bl_ctx *c, const int32_t *slots, int B, int k, const float *d
   bl_rows rows = make_rows(c, true, 0, 1);
   bool ne = false;
   for (int b = 0; b < B; b++) ne |= (c->host_slots[slots[b]].mode & (BL_M_LOGPROBS | BL_M_FULL)) != 0;
-  bl_launch_step(c->d, d_rows, ld, rows, R, ne, c->stream);
+  bl_launch_step(c->d, d_rows, ld, rows, R, ne, c->stream, nullptr);
   HIPCHK(hipGetLastError());
   HIPCHK(hipMemcpyAsync(c->h_tok, c->d_tok, R * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));
   HIPCHK(hipMemcpyAsync(c->h_status, c->d_status, R * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));

@@ -709,14 +709,19 @@ __global__ void bl_k_synth(float *out, int64_t ld, int cfg, int64_t seed, int64_
 }
 
 /* ------------------------------------------------------------------ host-side launchers */
+/* ev: optional 4 events recorded before/after the three kernels (kernel timing for the benchmark) */
 void bl_launch_step(const bl_dev &d, const float *logits, int64_t ld, const bl_rows &rows, int B, bool need_exp,
-                    hipStream_t s) {
+                    hipStream_t s, hipEvent_t *ev) {
   dim3 g1(d.nc, B);
+  if (ev) (void)hipEventRecord(ev[0], s);
   hipLaunchKernelGGL(bl_k_rowpass, g1, dim3(BL_RP_THREADS), 0, s, d, logits, ld, rows);
+  if (ev) (void)hipEventRecord(ev[1], s);
   if (need_exp) {
     hipLaunchKernelGGL(bl_k_exppass, g1, dim3(BL_RP_THREADS), 0, s, d, rows);
   }
+  if (ev) (void)hipEventRecord(ev[2], s);
   hipLaunchKernelGGL(bl_k_select, dim3(B), dim3(BL_SEL_THREADS), 0, s, d, rows);
+  if (ev) (void)hipEventRecord(ev[3], s);
 }
 
 void bl_launch_synth(float *out, int64_t ld, int cfg, int64_t seed, int64_t step, int rows, int V, hipStream_t s) {

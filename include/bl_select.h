@@ -103,6 +103,13 @@ int bl_bind_rows(bl_ctx *ctx, const int32_t *slots, int B);
 int bl_sample_step_async(bl_ctx *ctx, int B, const float *d_logits, int64_t ld, int32_t *d_tokens, float *d_logprobs,
                          int32_t *d_top_ids, float *d_top_logprobs, int top_stride);
 
+/* Kernel timing for measurement (no reference counterpart): while enabled, bl_sample_step_async records
+ * HIP events around its three kernels (row pass, exponent pass, selection) on the context stream,
+ * waits for them, and accumulates the durations; bl_get_timing returns the totals in ms and the
+ * number of timed steps. Enabling resets the totals. */
+int bl_set_timing(bl_ctx *ctx, int enable);
+int bl_get_timing(bl_ctx *ctx, double *ms_total3, int64_t *steps);
+
 /* Speculative verification (src/server.br:1173-1216): for each of the B slots, rows
  * d_rows[b*(k+1) + i] (i = 0..k) are the target logits after feeding drafts[b*k .. b*k+i). Row i is
  * sampled with the slot's RNG advanced by i draws; accepted[b] = number of leading rows whose token
