@@ -13,7 +13,6 @@
 #include <vector>
 
 #include "../../include/bl_select.h"
-#include "bl_exact.h"
 #include "bl_internal.h"
 #include "bl_math.h"
 #include "bl_workload.h"
@@ -181,19 +180,12 @@ int bl_create(int device, int max_slots, int max_rows, int vocab, bl_ctx **out) 
   ALLOC(d.c_max, R * d.nc);
   ALLOC(d.c_arg, R * d.nc);
   ALLOC(d.c_sum, R * d.nc);
-  ALLOC(d.cand_v, R * d.nc * BL_CCAP);
-  ALLOC(d.cand_i, R * d.nc * BL_CCAP);
-  ALLOC(d.c_cnt, R * d.nc);
-  ALLOC(d.c_edge, R * d.nc);
-  ALLOC(d.lse, R);
-  ALLOC(d.done, R);
+  ALLOC(d.cand_v, R * d.nc * BL_KSEL_MAX);
+  ALLOC(d.cand_i, R * d.nc * BL_KSEL_MAX);
   {
-    bl_grec *g = nullptr;
-    ALLOC(g, R * 2 * G);
+    char *g = nullptr;
+    ALLOC(g, R * 2 * G * 32);
     d.grec = g;
-    bl_grec *cr = nullptr;
-    ALLOC(cr, R * d.nc);
-    d.crec = cr;
   }
   ALLOC(d.full_v, R * V);
   ALLOC(d.full_i, R * V);
@@ -309,7 +301,8 @@ static int configure(const bl_ctx *c, const bl_params *p, bl_slot_dev &s) {
   if (p->temperature > 0.0f && p->dynatemp_range > 0.0f)
     return fail(BL_EUNSUPPORTED, "dynamic temperature is not supported on the device");
   if (p->post_sampling_probs) return fail(BL_EUNSUPPORTED, "post_sampling_probs is not supported on the device");
-  if (k > BL_KSEL_MAX) return fail(BL_EUNSUPPORTED, "top_k/n_probs of %d exceeds the device selection limit", k);
+  if (k > BL_KSEL_MAX || c->d.nc * k > BL_LDS_SORT)
+    return fail(BL_EUNSUPPORTED, "top_k/n_probs of %d exceeds the device selection limit", k);
   if (p->repeat_last_n > BL_WCAP) return fail(BL_EUNSUPPORTED, "repeat_last_n above %d", BL_WCAP);
   return BL_OK;
 }

@@ -44,19 +44,12 @@ struct bl_inc {
   uint32_t d0, d1;
 };
 
-/*
- * Record of a run of terms (a 64-term group, or a 4096-term chunk): the composed pairs at binade E
- * (v[0]) and E+1 (v[1]); `mask` bit k says v[k] was computed. E is chosen from an approximate sum
- * before the run: one binade when the approximation sits well inside it, two when it lies within
- * 2^-8 of a binade edge. A walk that finds neither variant usable drops to the next level down,
- * so the choice affects speed only, never the result.
- */
+/* group record: composed pairs for binades E-1, E, E+1 (a variant below BL_E_MIN is unused) */
 struct bl_grec {
   int32_t E;
-  uint32_t mask;
-  bl_inc v[2];
+  uint32_t pad;
+  bl_inc v[3];
 };
-#define BL_E_NONE (-100000)
 
 BL_SD bl_inc bl_inc_ident() { return bl_inc{0u, 0u}; }
 
@@ -106,25 +99,12 @@ BL_SD float bl_make(int e, uint32_t N) {
   return bl_u2f(((uint32_t)(e + 127) << 23) | (N & 0x7fffffu));
 }
 
-/* variants for a run starting at an approximate sum s: returns E, sets *mask */
-BL_SD int bl_choose_binades(double s, uint32_t *mask) {
-  float f = (float)(s > 0.0 ? s : 0.0);
+/* binade index predicted from an approximate sum */
+BL_SD int bl_binade_of(double s) {
+  float f = (float)s;
   int e;
   uint32_t N;
-  bl_split(f, e, N);
-  if (e == BL_E_MIN) {
-    *mask = 3u;
-    return BL_E_MIN;
-  }
-  if (N < 0x808000u) { /* within 2^-8 above 2^e: the exact sum may still be below */
-    *mask = 3u;
-    return e - 1;
-  }
-  if (N > 0xff0000u) { /* within 2^-8 below 2^(e+1) */
-    *mask = 3u;
-    return e;
-  }
-  *mask = 1u;
+  bl_split(f < 0.0f ? 0.0f : f, e, N);
   return e;
 }
 
@@ -163,123 +143,96 @@ __device__ __forceinline__ double bl_wave_excl_scan_d(double x, int lane) {
   return inc - x;
 }
 
-/* pair of a run of terms at binade e, composed in order by one thread */
-template <int NT>
-__device__ __forceinline__ bl_inc bl_thread_compose(const float *a, int e) {
-  bl_inc f = bl_inc_ident();
+/*
+ * Phase A for one group, executed by a whole wavefront: `a` is this lane's term (0 beyond the end),
+ * `approx_start` the approximate sum before the group. Returns the record (valid in every lane).
+ */
+__device__ __forceinline__ bl_grec bl_group_record(float a, double approx_start, int lane) {
+  bl_grec r;
+  r.E = bl_binade_of(approx_start);
+  r.pad = 0;
 #pragma unroll
-  for (int k = 0; k < NT; k++) f = bl_compose(f, bl_term_inc(a[k], e));
-  return f;
-}
-
-/* ordered composition across the 4 lanes of a quad (lanes 4q..4q+3 hold consecutive runs) */
-__device__ __forceinline__ bl_inc bl_quad_compose(bl_inc f, int lane) {
-  bl_inc o = bl_inc{(uint32_t)__shfl_xor((int)f.d0, 1, 64), (uint32_t)__shfl_xor((int)f.d1, 1, 64)};
-  f = (lane & 1) ? bl_compose(o, f) : bl_compose(f, o);
-  o = bl_inc{(uint32_t)__shfl_xor((int)f.d0, 2, 64), (uint32_t)__shfl_xor((int)f.d1, 2, 64)};
-  f = (lane & 2) ? bl_compose(o, f) : bl_compose(f, o);
-  return f;
+  for (int k = 0; k < 3; k++) {
+    int e = r.E - 1 + k;
+    bl_inc f = e >= BL_E_MIN ? bl_term_inc(a, e) : bl_inc{BL_SAT, BL_SAT};
+    r.v[k] = bl_wave_reduce(f, lane);
+  }
+  return r;
 }
 
 /*
- * Phase B, run by one wavefront. Units of one level (chunks of 64 groups, groups of 64 terms) are
- * taken 64 at a time: each lane loads one unit's record, picks the variant of the current binade,
- * and an ordered scan gives the running N after every unit. Units up to the first one that crosses
- * the binade, has no usable variant, or reaches the search threshold are committed at once; that
- * unit is then resolved one level down (at element level: one real float add per crossing).
- * Returns the number of leading units committed; N is updated.
+ * Phase B: sequential-sum walk over n terms in groups of 64, by one wavefront.
+ *   term(j)   -> float term j (only called for j < n)
+ *   rec(g)    -> bl_grec of group g
+ * Search mode (thr_on): stops at the first index j >= min_idx whose inclusive sum S_j >= thr and
+ * returns j (S holds S_j); otherwise returns -1 with S the full sum. All lanes return the same.
  */
-template <class RecF>
-__device__ __forceinline__ int bl_unit_scan(int64_t u0, int64_t u_end, RecF rec, int e, uint32_t &N, bool thr_on,
-                                            float thr, int lane) {
-  int64_t ul = u0 + lane;
-  bool valid = ul < u_end;
-  bl_inc f = bl_inc_ident();
-  if (valid) {
-    bl_grec r = rec(ul);
-    int k = e - r.E;
-    if (k >= 0 && k <= 1 && ((r.mask >> k) & 1u)) f = r.v[k];
-    else valid = false;
-  }
-  bl_inc sc = bl_wave_scan(f, lane);
-  uint32_t Nend = bl_apply(sc, N);
-  bool bad = !valid || Nend >= BL_N_TOP;
-  if (!bad && thr_on) bad = bl_make(e, Nend) >= thr;
-  unsigned long long m = __ballot(bad);
-  int first = m ? __ffsll((long long)m) - 1 : 64;
-  if (first > 0) N = (uint32_t)__shfl((int)Nend, first - 1, 64);
-  return first;
-}
-
-/* element level over terms [j0, min(j0+64, n)); returns the found index or -1 */
-template <class TermF>
-__device__ int bl_elem_walk(int64_t j0, int64_t n, TermF term, int &e, uint32_t &N, bool thr_on, float thr,
-                            int64_t min_idx, float &S_out, int lane) {
-  int64_t j = j0 + lane;
-  bool in = j < n;
-  float a = in ? term(j) : 0.0f;
-  int start = 0;
-  while (true) {
-    bool act = in && lane >= start;
-    bl_inc fe = act ? bl_term_inc(a, e) : bl_inc_ident();
-    bl_inc se = bl_wave_scan(fe, lane);
-    uint32_t Ne = bl_apply(se, N);
-    bool cross = act && Ne >= BL_N_TOP;
-    bool reach = act && !cross && thr_on && j >= min_idx && bl_make(e, Ne) >= thr;
-    unsigned long long ms = __ballot(cross || reach);
-    if (!ms) {
-      N = (uint32_t)__shfl((int)Ne, 63, 64);
-      return -1;
-    }
-    int c = __ffsll((long long)ms) - 1;
-    uint32_t Nbefore = c > start ? (uint32_t)__shfl((int)Ne, c - 1, 64) : N;
-    if (__shfl((int)reach, c, 64)) {
-      N = (uint32_t)__shfl((int)Ne, c, 64);
-      S_out = bl_make(e, N);
-      return (int)(j0 + c);
-    }
-    float ac = __shfl(a, c, 64);
-    float Sn = bl_make(e, Nbefore) + ac; /* the one real float add at a binade crossing */
-    bl_split(Sn, e, N);
-    if (thr_on && j0 + c >= min_idx && Sn >= thr) {
-      S_out = Sn;
-      return (int)(j0 + c);
-    }
-    start = c + 1;
-    if (start >= 64) return -1;
-  }
-}
-
-/*
- * Sequential-sum walk over n terms: chunk records crec(c) (4096 terms; pass have_crec = false to
- * skip that level), group records grec(g) (64 terms; a record with E = BL_E_NONE sends every group to
- * element level), terms term(j). Search mode (thr_on): stops at the first index j >= min_idx whose
- * inclusive sum S_j >= thr and returns j with S_out = S_j; otherwise returns -1, S_out = the sum.
- */
-template <class TermF, class GRecF, class CRecF>
-__device__ int bl_seq_walk(int64_t n, TermF term, GRecF grec, CRecF crec, bool have_crec, bool thr_on, float thr,
-                           int64_t min_idx, float &S_out, int lane) {
+template <class TermF, class RecF>
+__device__ int bl_seq_walk(int64_t n, TermF term, RecF rec, bool thr_on, float thr, int64_t min_idx, float &S_out,
+                           int lane) {
   int e = BL_E_MIN;
   uint32_t N = 0u;
-  const int64_t G = (n + 63) / 64, C = (G + 63) / 64;
-  int64_t c = 0;
-  while (c < C) {
-    if (have_crec) {
-      int fc = bl_unit_scan(c, C, crec, e, N, thr_on, thr, lane);
-      c += fc;
-      if (c >= C) break;
-      if (fc == 64) continue;
+  int64_t G = (n + 63) / 64;
+  int64_t g = 0;
+  while (g < G) {
+    /* ---- group level over groups g .. g+63 ---- */
+    int64_t gl = g + lane;
+    bool valid = gl < G;
+    bl_inc f = bl_inc_ident();
+    if (valid) {
+      bl_grec r = rec(gl);
+      int k = e - (r.E - 1);
+      if (k >= 0 && k <= 2 && e >= BL_E_MIN) f = r.v[k];
+      else valid = false;
     }
-    int64_t g = c * 64, gend = g + 64 < G ? g + 64 : G;
-    while (g < gend) {
-      int fg = bl_unit_scan(g, gend, grec, e, N, thr_on, thr, lane);
-      g += fg;
-      if (g >= gend) break;
-      int f = bl_elem_walk(g * 64, n, term, e, N, thr_on, thr, min_idx, S_out, lane);
-      if (f >= 0) return f;
-      g += 1;
+    bl_inc sc = bl_wave_scan(f, lane);
+    uint32_t Nend = bl_apply(sc, N);
+    bool bad = !valid || Nend >= BL_N_TOP;
+    if (!bad && thr_on) bad = bl_make(e, Nend) >= thr; /* reaching the threshold: resolve at element level */
+    unsigned long long m = __ballot(bad);
+    int first = m ? __ffsll((long long)m) - 1 : 64;
+    if (first > 0) {
+      N = (uint32_t)__shfl((int)Nend, first - 1, 64);
+      g += first;
     }
-    c += 1;
+    if (g >= G) break;
+    if (first == 64) continue;
+    /* ---- element level in group g ---- */
+    int64_t j0 = g * 64;
+    int64_t j = j0 + lane;
+    float a = j < n ? term(j) : 0.0f;
+    bool in = j < n;
+    int start = 0;
+    while (true) {
+      bl_inc fe = (in && lane >= start) ? bl_term_inc(a, e) : bl_inc_ident();
+      bl_inc se = bl_wave_scan(fe, lane);
+      uint32_t Ne = bl_apply(se, N);
+      bool act = in && lane >= start;
+      bool cross = act && Ne >= BL_N_TOP;
+      bool reach = act && !cross && thr_on && j >= min_idx && bl_make(e, Ne) >= thr;
+      unsigned long long ms = __ballot(cross || reach);
+      if (!ms) {
+        N = (uint32_t)__shfl((int)Ne, 63, 64);
+        break;
+      }
+      int c = __ffsll((long long)ms) - 1;
+      uint32_t Nbefore = c > start ? (uint32_t)__shfl((int)Ne, c - 1, 64) : N;
+      bool c_reach = __shfl((int)reach, c, 64) != 0;
+      if (c_reach) {
+        S_out = bl_make(e, (uint32_t)__shfl((int)Ne, c, 64));
+        return (int)(j0 + c);
+      }
+      float ac = __shfl(a, c, 64);
+      float Sn = bl_make(e, Nbefore) + ac; /* the one real float add at a binade crossing */
+      bl_split(Sn, e, N);
+      if (thr_on && j0 + c >= min_idx && Sn >= thr) {
+        S_out = Sn;
+        return (int)(j0 + c);
+      }
+      start = c + 1;
+      if (start >= 64) break;
+    }
+    g += 1;
   }
   S_out = bl_make(e, N);
   return -1;

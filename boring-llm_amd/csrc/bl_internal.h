@@ -23,8 +23,7 @@
 #define BL_CH 4096          /* vocabulary chunk per workgroup in the row passes */
 #define BL_RP_THREADS 256   /* row-pass workgroup */
 #define BL_SEL_THREADS 1024 /* per-row selection workgroup */
-#define BL_KSEL_MAX 256     /* largest top_k / n_probs served by the candidate path */
-#define BL_CCAP (BL_KSEL_MAX + 32) /* candidates one chunk may emit */
+#define BL_KSEL_MAX 256     /* largest per-chunk candidate count (top_k / n_probs) */
 #define BL_WCAP 8192        /* repeat window ring capacity */
 #define BL_LDS_SORT 4096    /* candidate lists sorted in LDS up to this size */
 
@@ -74,14 +73,9 @@ struct bl_dev {
   float *c_max;     /* [rows][nc] */
   int32_t *c_arg;   /* [rows][nc] */
   float *c_sum;     /* [rows][nc] approximate sum of exp(x - c_max) */
-  float *cand_v;    /* [rows][nc][CCAP] chunk candidates: a superset of the chunk's top-K */
+  float *cand_v;    /* [rows][nc][KSEL_MAX] */
   int32_t *cand_i;
-  int32_t *c_cnt;   /* [rows][nc] candidates emitted */
-  uint32_t *c_edge; /* [rows][nc] order key every emitted candidate reaches (>= K of them do) */
   void *grec;       /* [rows][2 * (V/64 + 64)] bl_grec: index-order records, then sorted-list records */
-  void *crec;       /* [rows][nc] bl_grec per 4096-term chunk of the index-order normaliser */
-  float *lse;       /* [rows] log of the normaliser */
-  int32_t *done;    /* [rows] hand-off counter between the sampling and logprob workgroups */
   float *full_v;    /* [rows][V] full-vocabulary candidates */
   int32_t *full_i;
   int32_t *full_n;  /* [rows] */

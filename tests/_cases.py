@@ -1,0 +1,39 @@
+"""Parameter sets of the small-vocabulary parity cases, shared by the GPU tests and the CPU emulator runs.
+
+Each case is one bl_params / oracle Params configuration; the inputs (history, reply, logit_bias, planted
+ties) are drawn from numpy's default_rng(case) in `small_case_inputs`.
+"""
+import numpy as np
+
+CASES = [
+    dict(temperature=0.0),
+    dict(temperature=0.9, top_k=5),
+    dict(temperature=1.3, top_k=0),
+    dict(temperature=0.5, top_k=0, top_p=0.8, min_p=0.02),
+    dict(temperature=0.7, top_k=50, top_p=0.9, min_p=0.1, min_keep=3),
+    dict(temperature=1.0, top_k=200, repeat_penalty=1.3, repeat_last_n=16),
+    dict(temperature=0.8, top_k=0, repeat_penalty=0.9, repeat_last_n=-1, frequency_penalty=0.4, presence_penalty=-0.2),
+    dict(temperature=0.0, repeat_penalty=1.5, repeat_last_n=8, logprobs=1, n_probs=5),
+    dict(temperature=1.0, top_k=10, logprobs=1, n_probs=12, ignore_eos=1),
+    dict(temperature=2.0, top_k=0, logprobs=1, n_probs=3, final_softcap=5.0),
+    dict(temperature=0.6, top_k=30, logit_mul=0.5, logprobs=1, n_probs=1),
+]
+SMALL_V = 5003
+EOS, EOGS = 7, [11, 13]
+
+
+def small_case_inputs(case):
+    """(rng, history, reply, bias) of a small case; the rng then draws the per-step logits."""
+    rng = np.random.default_rng(case)
+    hist = [int(x) for x in rng.integers(0, SMALL_V, 40)]
+    reply = hist[-15:]
+    bias = {int(i): float(np.float32(v)) for i, v in zip(rng.integers(0, SMALL_V, 20), rng.uniform(-5, 5, 20))}
+    return rng, hist, reply, bias
+
+
+def small_case_logits(rng):
+    """One step's logits: N(0, 2.5^2), 30 bumped ids and 5 planted equal values."""
+    x = (rng.standard_normal(SMALL_V) * 2.5).astype(np.float32)
+    x[rng.integers(0, SMALL_V, 30)] += 6.0
+    x[rng.integers(0, SMALL_V, 5)] = x[int(rng.integers(0, SMALL_V))]
+    return x

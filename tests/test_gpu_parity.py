@@ -16,6 +16,7 @@ pytestmark = pytest.mark.gpu
 torch = pytest.importorskip("torch")
 import bl_select as BL  # noqa: E402
 import _oracle as O  # noqa: E402
+from _cases import CASES, EOGS, EOS, SMALL_V, small_case_inputs, small_case_logits  # noqa: E402
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
 LP_RTOL = 1e-5
@@ -187,30 +188,13 @@ def test_workload5_spec_verify(cuda):
 
 
 # ------------------------------------------------------------------ many small configurations
-CASES = [
-    dict(temperature=0.0),
-    dict(temperature=0.9, top_k=5),
-    dict(temperature=1.3, top_k=0),
-    dict(temperature=0.5, top_k=0, top_p=0.8, min_p=0.02),
-    dict(temperature=0.7, top_k=50, top_p=0.9, min_p=0.1, min_keep=3),
-    dict(temperature=1.0, top_k=200, repeat_penalty=1.3, repeat_last_n=16),
-    dict(temperature=0.8, top_k=0, repeat_penalty=0.9, repeat_last_n=-1, frequency_penalty=0.4, presence_penalty=-0.2),
-    dict(temperature=0.0, repeat_penalty=1.5, repeat_last_n=8, logprobs=1, n_probs=5),
-    dict(temperature=1.0, top_k=10, logprobs=1, n_probs=12, ignore_eos=1),
-    dict(temperature=2.0, top_k=0, logprobs=1, n_probs=3, final_softcap=5.0),
-    dict(temperature=0.6, top_k=30, logit_mul=0.5, logprobs=1, n_probs=1),
-]
-
-
 @pytest.mark.parametrize("case", range(len(CASES)))
 def test_small_vocab_cases(cuda, case):
-    V, steps = 5003, 25
+    V, steps = SMALL_V, 25
     kw = CASES[case]
-    rng = np.random.default_rng(case)
-    hist = [int(x) for x in rng.integers(0, V, 40)]
-    reply = hist[-15:]
-    bias = {int(i): float(np.float32(v)) for i, v in zip(rng.integers(0, V, 20), rng.uniform(-5, 5, 20))}
-    eos, eogs = 7, [11, 13]
+    say(f"small case {case}: {kw}")
+    rng, hist, reply, bias = small_case_inputs(case)
+    eos, eogs = EOS, EOGS
     ctx = BL.Context(V, 2, 2)
     ctx.set_eog(eos, eogs)
     p = BL.Params(**kw)
@@ -228,9 +212,7 @@ def test_small_vocab_cases(cuda, case):
     n_probs = kw.get("n_probs", 0)
     try:
         for t in range(steps):
-            x = (rng.standard_normal(V) * 2.5).astype(np.float32)
-            x[rng.integers(0, V, 30)] += 6.0
-            x[rng.integers(0, V, 5)] = x[int(rng.integers(0, V))]  # planted ties
+            x = small_case_logits(rng)
             buf.copy_(torch.from_numpy(x))
             torch.cuda.synchronize()
             tok, lp, ti, tl = ctx.sample_step([1], buf.data_ptr(), V, top_stride=max(n_probs, 1))

@@ -1,0 +1,64 @@
+"""The library's kernels on the CPU: the HIP sources built for the SIMT emulator (tests/cpu/simt) and
+checked against the oracle.
+
+No GPU is involved: every GPU thread is a fiber, workgroup barriers and wavefront shuffles/ballots are
+rendezvous of those fibers, and LDS is filled with a stale-data pattern before each workgroup. The
+emulator aborts on a barrier or wave operation reached from divergent code. Threads run in a random
+order between barriers (SIMT_ORDER=rand), so a result that depends on the order of two threads'
+unsynchronised accesses shows up as a parity failure. The AddressSanitizer/UBSan build turns any
+out-of-bounds device-memory, LDS or private-array access into a failure. This runs the same code as
+the GPU parity tests, on the same inputs, at reduced step counts.
+"""
+import os
+import subprocess
+import sys
+
+import pytest
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+SIMT = os.path.join(HERE, "cpu", "simt")
+
+
+def _build(target):
+    r = subprocess.run(["make", "-s", "-C", SIMT, target], capture_output=True, text=True)
+    assert r.returncode == 0, r.stdout + r.stderr
+
+
+@pytest.fixture(scope="module")
+def simt_lib():
+    _build("all")
+    return os.path.join(SIMT, "_build", "libbl_simt.so")
+
+
+def _run(lib, items, env_extra=None, timeout=600):
+    env = dict(os.environ)
+    env.update(env_extra or {})
+    r = subprocess.run([sys.executable, os.path.join(SIMT, "run_parity.py"), "--lib", lib] + items,
+                       capture_output=True, text=True, env=env, timeout=timeout)
+    out = r.stdout + r.stderr
+    assert r.returncode == 0, out[-4000:]
+    return out
+
+
+def test_small_cases_random_thread_order(simt_lib):
+    out = _run(simt_lib, ["small:0-10:4"], {"SIMT_ORDER": "rand"})
+    assert out.count("ok   small case") == 11
+
+
+def test_full_vocabulary_workloads(simt_lib):
+    """Workload 2 (the benchmark step), workload 4 (soft-cap, V=262144, top-64 + 20 logprobs) on 2 rows, and
+    the bound-rows asynchronous step against the synchronous one."""
+    out = _run(simt_lib, ["w2:1", "w4:1:2", "async:1"], {"SIMT_ORDER": "rev"})
+    assert "ok   workload 2" in out and "ok   workload 4" in out and "ok   asynchronous step" in out
+
+
+def test_small_cases_address_sanitizer():
+    _build("asan")
+    pre = []
+    for rt in ("libasan.so", "libubsan.so"):
+        p = subprocess.run(["gcc", f"-print-file-name={rt}"], capture_output=True, text=True).stdout.strip()
+        assert os.path.isabs(p) and os.path.exists(p), f"{rt} not found"
+        pre.append(p)
+    env = {"LD_PRELOAD": " ".join(pre), "ASAN_OPTIONS": "detect_leaks=0", "UBSAN_OPTIONS": "print_stacktrace=1"}
+    out = _run(os.path.join(SIMT, "_build", "libbl_simt_asan.so"), ["small:0-10:3"], env)
+    assert "ERROR: AddressSanitizer" not in out and "runtime error" not in out
