@@ -21,6 +21,28 @@
  * round-to-nearest-even and no contraction (build with -ffp-contract=off), Rust f32::{exp,ln,tanh,
  * powf} -> the host glibc expf/logf/tanhf/powf, `as float32` from integers -> round to nearest even.
  * That lowering is an assumption about the external `boring` compiler, which is not vendored.
+ *
+ * What pins each part (tests/test_oracle_*.py, tests/test_device_math.py):
+ *   RNG, seed fold, u64->f32      closed form with exact integer/Fraction arithmetic; the reference's
+ *                                 determinism tests (test/test_sampling.br:7-13, :29-39)
+ *   bias, penalties, greedy,      the reference's known answers (test/test_sampling.br:16, :42-61,
+ *   top-k, heap rank (distinct)   :187-264) and lexsort/brute-force rankings on random rows
+ *   candidate sampling            known answers typical->8, XTC->9, min_p=1 (:112-122, :163-167,
+ *                                 :268-272), min_keep/top-p cut properties, a chi-square check of the
+ *                                 draw distribution against the float64 softmax
+ *   logprobs                      the reference's approximate known answers (:19-26) and a float64
+ *                                 log-sum-exp within float32 rounding
+ *   soft-cap                      float64 closed form within float32 rounding (test/test_arch.br)
+ *   grammar, schema, UTF-8,       transliterations of test/test_grammar.br, test_schema_grammar.br,
+ *   n-gram drafts                 test_tokenizer.br:52-58, test_speculative.br; the workload-3 GBNF
+ *                                 against its hand derivation; the carry form of a candidate piece
+ *                                 against the literal whole-reply re-decode
+ *   speculative verification      sequential decoding of the same rows (CHANGELOG.md:92's invariant)
+ * Parity unpinned (the restatement is the only authority, no reference vector or closed form fixes it):
+ *   - the order of equal values in the heap rank (all_candidates_sorted, src/sampling.br:301-365);
+ *   - the float32 bits of the sequential sums and of expf/logf/tanhf beyond the glibc the oracle links
+ *     (the Boring compiler's lowering to Rust f32 -> glibc is assumed, not vendored);
+ *   - full-vocabulary grammar masks beyond the language tests above.
  */
 #ifndef BL_ORACLE_H
 #define BL_ORACLE_H

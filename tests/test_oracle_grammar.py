@@ -230,3 +230,50 @@ def test_carry_piece_equals_literal(gbnf):
             assert np.array_equal(m1, m2) and a.value == b.value
             agree += 1
     assert agree > 5
+
+
+# ------------------------------------------------------------ speculative verification (src/server.br:1173-1216)
+
+@pytest.mark.parametrize("temperature", [0.0, 0.7])
+def test_spec_verify_equals_sequential_decoding(temperature):
+    """The invariant the reference states for speculation (CHANGELOG.md:92, "greedy output with spec ==
+    without spec"), extended to sampled rows: spec_verify's per-row tokens equal plain sequential
+    decode steps on those rows with the drafts appended to the history, its accepted length is the
+    first mismatch, and the slot ends in the sequential run's RNG state (accepted + 1 draws)."""
+    V, K = 997, 6
+    rng = np.random.default_rng(11)
+    L = O.lib()
+    p = O.params(temperature=temperature, top_k=0, repeat_penalty=1.2, repeat_last_n=8,
+                 frequency_penalty=0.3, presence_penalty=0.1)
+    hist = O.i32(rng.integers(0, V, 12))
+    for trial in range(6):
+        rows = (rng.standard_normal((K + 1) * V) * 3.0).astype(np.float32)
+        spec = L.orc_slot_new(O.C.byref(p), 1000 + trial, O.ip(hist), len(hist), O.ip(hist), len(hist), None, None, 0)
+        seq = L.orc_slot_new(O.C.byref(p), 1000 + trial, O.ip(hist), len(hist), O.ip(hist), len(hist), None, None, 0)
+        ref = L.orc_slot_new(O.C.byref(p), 1000 + trial, O.ip(hist), len(hist), O.ip(hist), len(hist), None, None, 0)
+        try:
+            # the sequential tokens when every draft is accepted (history grows with the drafts)
+            want = []
+            for i in range(K + 1):
+                t = np.zeros(1, np.int32)
+                assert L.orc_slot_step(ref, O.fp(rows[i * V:(i + 1) * V]), V, 0, 1, O.ip(t), None, None, None, None) == 0
+                want.append(int(t[0]))
+            cut = trial % (K + 1)  # drafts agree with the sequential tokens up to `cut`
+            drafts = want[:K]
+            if cut < K:
+                drafts[cut] = (drafts[cut] + 1) % V
+            toks = np.zeros(K + 1, np.int32)
+            acc = O.C.c_int32()
+            assert L.orc_slot_spec_verify(spec, O.fp(rows), V, O.ip(O.i32(drafts)), K, O.ip(toks),
+                                          O.C.byref(acc)) == 0
+            assert acc.value == cut
+            assert list(toks[:cut + 1]) == want[:cut + 1]
+            # the slot continues exactly as a sequential run of cut + 1 steps
+            for i in range(cut + 1):
+                t = np.zeros(1, np.int32)
+                assert L.orc_slot_step(seq, O.fp(rows[i * V:(i + 1) * V]), V, 0, 1, O.ip(t), None, None, None, None) == 0
+                assert int(t[0]) == want[i]
+            assert L.orc_slot_rng(spec) == L.orc_slot_rng(seq)
+        finally:
+            for h in (spec, seq, ref):
+                L.orc_slot_free(h)
