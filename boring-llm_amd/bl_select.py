@@ -47,7 +47,8 @@ EXPORTS = [
     "bl_params_default", "bl_create", "bl_destroy", "bl_last_error", "bl_set_stream", "bl_set_eog",
     "bl_slot_reset", "bl_slot_rng", "bl_slot_commit", "bl_sample_step", "bl_bind_rows", "bl_sample_step_async",
     "bl_spec_verify", "bl_synth_logits", "bl_math_digest", "bl_workload_ids", "bl_workload_bias",
-    "bl_workload_drafts", "bl_set_timing", "bl_get_timing",
+    "bl_workload_drafts", "bl_set_timing", "bl_get_timing", "bl_set_vocab", "bl_slot_grammar", "bl_grammar_mask",
+    "bl_workload_c3_vocab",
 ]
 
 _lib = None
@@ -87,6 +88,10 @@ def lib():
         L.bl_workload_bias.argtypes = [C.c_int, C.c_int64, C.c_int, C.c_int, C.c_int, C.c_float, C.c_float, i32p,
                                        f32p]
         L.bl_workload_drafts.argtypes = [C.c_int64, C.c_int64, C.c_int, i32p, C.c_int, C.c_int, i32p]
+        L.bl_set_vocab.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int]
+        L.bl_slot_grammar.argtypes = [C.c_void_p, C.c_int, C.c_char_p, C.c_size_t]
+        L.bl_grammar_mask.argtypes = [C.c_void_p, C.c_int, C.c_void_p, i32p]
+        L.bl_workload_c3_vocab.argtypes = [C.c_int64, C.c_int, C.c_void_p, C.c_size_t, C.c_void_p, i32p]
         _lib = L
     return _lib
 
@@ -186,6 +191,27 @@ class Context:
         _check(lib().bl_spec_verify(self.h, s, B, k, C.c_void_p(d_rows_ptr), ld, d, tok, acc))
         return list(tok), list(acc)
 
+    def set_vocab(self, blob, offsets):
+        """Token pieces: `blob` (bytes or uint8 array) and `offsets` (len vocab + 1, uint32)."""
+        b = bytes(blob)
+        o = (C.c_uint32 * len(offsets))(*[int(x) for x in offsets])
+        bb = C.create_string_buffer(b, max(len(b), 1))
+        _check(lib().bl_set_vocab(self.h, bb, o, len(offsets) - 1))
+
+    def slot_grammar(self, slot, gbnf):
+        """Attach a GBNF grammar to `slot` (None detaches)."""
+        if gbnf is None:
+            _check(lib().bl_slot_grammar(self.h, slot, None, 0))
+        else:
+            t = gbnf.encode() if isinstance(gbnf, str) else bytes(gbnf)
+            _check(lib().bl_slot_grammar(self.h, slot, t, len(t)))
+
+    def grammar_mask(self, slot, d_mask_ptr):
+        """Writes ceil(V/32) mask words to device memory; returns forced_eos."""
+        f = C.c_int32()
+        _check(lib().bl_grammar_mask(self.h, slot, C.c_void_p(d_mask_ptr), C.byref(f)))
+        return bool(f.value)
+
     def synth_logits(self, d_out_ptr, ld, cfg, seed, step, rows, vocab):
         _check(lib().bl_synth_logits(self.h, C.c_void_p(d_out_ptr), ld, cfg, seed, step, rows, vocab))
 
@@ -214,6 +240,18 @@ def workload_drafts(seed, step, seq, argmax, vocab):
     out = (C.c_int32 * max(k, 1))()
     _check(lib().bl_workload_drafts(seed, step, seq, a, k, vocab, out))
     return list(out[:k])
+
+
+def workload_c3_vocab(seed, vocab):
+    """(blob bytes, offsets list, eos_id) of the workload-3 synthetic vocabulary."""
+    cap = vocab * 64 + 4096
+    blob = (C.c_uint8 * cap)()
+    off = (C.c_uint32 * (vocab + 1))()
+    eos = C.c_int32()
+    n = lib().bl_workload_c3_vocab(seed, vocab, blob, cap, off, C.byref(eos))
+    if n < 0:
+        _check(n)
+    return bytes(blob[:n]), list(off), eos.value
 
 
 def seed_rng(seed):

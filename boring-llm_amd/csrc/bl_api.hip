@@ -13,12 +13,14 @@
 #include <vector>
 
 #include "../../include/bl_select.h"
+#include "bl_grammar.h"
 #include "bl_internal.h"
 #include "bl_math.h"
 #include "bl_workload.h"
 
 void bl_launch_step(const bl_dev &d, const float *logits, int64_t ld, const bl_rows &rows, int B, bool need_exp,
-                    hipStream_t s, hipEvent_t *ev);
+                    bool need_gram, hipStream_t s, hipEvent_t *ev);
+void bl_launch_gmask(const bl_dev &d, const bl_rows &rows, hipStream_t s);
 void bl_launch_synth(float *out, int64_t ld, int cfg, int64_t seed, int64_t step, int rows, int V, hipStream_t s);
 void bl_launch_math_digest(int fn, uint32_t first_block, int n_blocks, unsigned long long *out, hipStream_t s);
 
@@ -52,12 +54,27 @@ struct bl_ctx {
   int32_t *h_slot = nullptr, *h_tok = nullptr, *h_status = nullptr, *h_top_ids = nullptr, *h_skip = nullptr;
   float *h_lp = nullptr, *h_top_lp = nullptr;
   int32_t *d_commit_toks = nullptr;
+  int32_t *d_mslot = nullptr; /* row table of bl_grammar_mask */
   int bound_B = 0;
   std::vector<void *> allocs;
   bool timing = false;
   hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};
   double kernel_ms[3] = {0.0, 0.0, 0.0};
   int64_t timed_steps = 0;
+  /* grammar: host copies of the vocabulary and of each slot's reply, compiled grammars by text */
+  std::vector<uint8_t> vblob;
+  std::vector<uint32_t> voff;
+  uint8_t *d_vblob = nullptr;
+  uint32_t *d_voff = nullptr;
+  std::vector<std::vector<int32_t>> reply;
+  struct gram_entry {
+    bl_gram_tables tab;
+    bl_gram_view dev{}, host{};
+    std::vector<void *> mem;
+  };
+  std::unordered_map<std::string, gram_entry *> grammars;
+  std::vector<char> stepped; /* the slot took part in a step since its reset */
+  std::vector<int32_t> eog_ids; /* host copy of the end-of-generation registry */
 };
 
 template <class T>
@@ -104,6 +121,7 @@ __global__ void bl_k_commit(bl_dev d, int slot, const int32_t *toks, int n, int 
         d.cnt[so + tok] += 1;
         tw[tok >> 5] |= 1u << (tok & 31);
       }
+      if (sp.g_on) grammar_commit(d, sp, d.gram[slot], tok);
     }
   }
   for (int k = 0; k < rng_draws; k++) sp.rng = bl_xorshift(sp.rng);
@@ -192,6 +210,15 @@ int bl_create(int device, int max_slots, int max_rows, int vocab, bl_ctx **out) 
   ALLOC(d.full_n, R);
   ALLOC(d.sortk, R * std::max(P2, 2 * V));
   ALLOC(d.gsum, R * G);
+  d.gm_blocks = (vocab + BL_GM_THREADS - 1) / BL_GM_THREADS;
+  ALLOC(d.gram, S);
+  ALLOC(d.gmask, R * 2 * ((V + 63) / 64));
+  ALLOC(d.gstat, R);
+  ALLOC(d.gamb, R);
+  ALLOC(d.gm_max, R * d.gm_blocks);
+  ALLOC(d.gm_arg, R * d.gm_blocks);
+  ALLOC(d.gm_eq, R * d.gm_blocks);
+  d.eos_id = -1;
   ALLOC(c->d_slot, R);
   ALLOC(c->d_skip, R);
   ALLOC(c->d_tok, R);
@@ -200,6 +227,7 @@ int bl_create(int device, int max_slots, int max_rows, int vocab, bl_ctx **out) 
   ALLOC(c->d_top_ids, R * 256);
   ALLOC(c->d_top_lp, R * 256);
   ALLOC(c->d_commit_toks, 4096);
+  ALLOC(c->d_mslot, 1);
 #undef ALLOC
   d.n_eog = 0;
   if (hipHostMalloc((void **)&c->h_slot, R * sizeof(int32_t)) != hipSuccess ||
@@ -219,6 +247,8 @@ int bl_create(int device, int max_slots, int max_rows, int vocab, bl_ctx **out) 
   c->stream = c->own;
   c->host_slots.assign(S, bl_slot_dev{});
   c->slot_ready.assign(S, false);
+  c->reply.assign(S, {});
+  c->stepped.assign(S, 0);
   *out = c;
   return BL_OK;
 }
@@ -228,6 +258,12 @@ void bl_destroy(bl_ctx *c) {
   hipSetDevice(c->device);
   if (c->stream) hipStreamSynchronize(c->stream);
   for (void *p : c->allocs) hipFree(p);
+  for (auto &kv : c->grammars) {
+    for (void *p : kv.second->mem) hipFree(p);
+    delete kv.second;
+  }
+  if (c->d_vblob) hipFree(c->d_vblob);
+  if (c->d_voff) hipFree(c->d_voff);
   void *hp[] = {c->h_slot, c->h_skip, c->h_tok, c->h_status, c->h_lp, c->h_top_ids, c->h_top_lp};
   for (void *p : hp)
     if (p) hipHostFree(p);
@@ -251,6 +287,8 @@ int bl_set_eog(bl_ctx *c, int32_t eos_id, const int32_t *eog_ids, int n_eog) {
   hipSetDevice(c->device);
   if (!ids.empty()) HIPCHK(hipMemcpy(c->d.eog, ids.data(), ids.size() * sizeof(int32_t), hipMemcpyHostToDevice));
   c->d.n_eog = (int32_t)ids.size();
+  c->d.eos_id = eos_id;
+  c->eog_ids = ids;
   return BL_OK;
 }
 
@@ -362,6 +400,9 @@ int bl_slot_reset(bl_ctx *c, int slot, const bl_params *p, uint64_t rng_state, c
   s.rng = rng_state;
   s.n_tokens = n_hist;
   s.n_reply = n_reply;
+  s.g_on = 0; /* a grammar is attached by bl_slot_grammar */
+  c->reply[slot].assign(reply, reply + n_reply);
+  c->stepped[slot] = 0;
   hipSetDevice(c->device);
   const size_t so = (size_t)slot * V;
   HIPCHK(hipStreamSynchronize(c->stream));
@@ -390,11 +431,141 @@ int bl_slot_rng(bl_ctx *c, int slot, uint64_t *state) {
 int bl_slot_commit(bl_ctx *c, int slot, const int32_t *toks, int n) {
   if (!c || slot < 0 || slot >= c->d.max_slots || n < 0 || n > 4096) return fail(BL_EPARAM, "bl_slot_commit: invalid arguments");
   if (n == 0) return BL_OK;
+  for (int i = 0; i < n; i++)
+    if (toks[i] >= 0 && toks[i] < c->d.vocab) {
+      bool eog = false;
+      for (int32_t e : c->eog_ids) eog |= e == toks[i];
+      if (!eog) c->reply[slot].push_back(toks[i]);
+    }
   hipSetDevice(c->device);
   HIPCHK(hipMemcpyAsync(c->d_commit_toks, toks, n * sizeof(int32_t), hipMemcpyHostToDevice, c->stream));
   hipLaunchKernelGGL(bl_k_commit, dim3(1), dim3(64), 0, c->stream, c->d, slot, c->d_commit_toks, n, 0);
   HIPCHK(hipGetLastError());
   HIPCHK(hipStreamSynchronize(c->stream));
+  return BL_OK;
+}
+
+/* ------------------------------------------------------------------ grammar-constrained slots */
+int bl_set_vocab(bl_ctx *c, const uint8_t *blob, const uint32_t *offsets, int n_tokens) {
+  if (!c || !blob || !offsets || n_tokens != c->d.vocab)
+    return fail(BL_EPARAM, "bl_set_vocab: expected %d token pieces", c ? c->d.vocab : 0);
+  for (int i = 0; i < n_tokens; i++)
+    if (offsets[i + 1] < offsets[i]) return fail(BL_EPARAM, "bl_set_vocab: offsets must not decrease");
+  const size_t nb = offsets[n_tokens];
+  hipSetDevice(c->device);
+  HIPCHK(hipStreamSynchronize(c->stream));
+  if (c->d_vblob) HIPCHK(hipFree(c->d_vblob));
+  if (c->d_voff) HIPCHK(hipFree(c->d_voff));
+  c->d_vblob = nullptr;
+  c->d_voff = nullptr;
+  HIPCHK(hipMalloc((void **)&c->d_vblob, nb + 16));
+  HIPCHK(hipMalloc((void **)&c->d_voff, ((size_t)n_tokens + 1) * sizeof(uint32_t)));
+  if (nb) HIPCHK(hipMemcpy(c->d_vblob, blob, nb, hipMemcpyHostToDevice));
+  HIPCHK(hipMemcpy(c->d_voff, offsets, ((size_t)n_tokens + 1) * sizeof(uint32_t), hipMemcpyHostToDevice));
+  c->vblob.assign(blob, blob + nb);
+  c->voff.assign(offsets, offsets + n_tokens + 1);
+  c->d.vblob = c->d_vblob;
+  c->d.voff = c->d_voff;
+  return BL_OK;
+}
+
+static const int kMaxGrammarStates = 1 << 16;
+
+/* compiled tables of `text`, uploaded once per context */
+static int grammar_tables(bl_ctx *c, const std::string &text, bl_ctx::gram_entry **out) {
+  auto it = c->grammars.find(text);
+  if (it != c->grammars.end()) {
+    *out = it->second;
+    return BL_OK;
+  }
+  bl_ctx::gram_entry *e = new bl_ctx::gram_entry;
+  std::string err;
+  int rc = bl_gram_compile(text, kMaxGrammarStates, e->tab, err);
+  if (rc) {
+    delete e;
+    return fail(rc, "%s", err.c_str());
+  }
+  const bl_gram_tables &t = e->tab;
+  auto up = [&](const void *src, size_t bytes, void **dst) -> hipError_t {
+    hipError_t r = hipMalloc(dst, bytes + 16);
+    if (r != hipSuccess) return r;
+    e->mem.push_back(*dst);
+    return bytes ? hipMemcpy(*dst, src, bytes, hipMemcpyHostToDevice) : hipSuccess;
+  };
+  void *tr, *fl, *as, *il, *ic;
+  hipError_t r = up(t.trans.data(), t.trans.size() * 4, &tr);
+  if (r == hipSuccess) r = up(t.flags.data(), t.flags.size(), &fl);
+  if (r == hipSuccess) r = up(t.ascii.data(), t.ascii.size() * 2, &as);
+  if (r == hipSuccess) r = up(t.ivl_lo.data(), t.ivl_lo.size() * 4, &il);
+  if (r == hipSuccess) r = up(t.ivl_cls.data(), t.ivl_cls.size() * 2, &ic);
+  if (r != hipSuccess) {
+    for (void *p : e->mem) hipFree(p);
+    delete e;
+    return fail(BL_EDEVICE, "grammar tables: %s", hipGetErrorString(r));
+  }
+  e->dev = bl_gram_view{(const int32_t *)tr, (const uint8_t *)fl, (const uint16_t *)as, (const uint32_t *)il,
+                        (const uint16_t *)ic, (int32_t)t.ivl_lo.size(), t.n_classes, t.start, 0};
+  e->host = bl_gram_view{t.trans.data(), t.flags.data(), t.ascii.data(), t.ivl_lo.data(), t.ivl_cls.data(),
+                         (int32_t)t.ivl_lo.size(), t.n_classes, t.start, 0};
+  c->grammars[text] = e;
+  *out = e;
+  return BL_OK;
+}
+
+int bl_slot_grammar(bl_ctx *c, int slot, const char *gbnf, size_t len) {
+  if (!c || slot < 0 || slot >= c->d.max_slots || !c->slot_ready[slot])
+    return fail(BL_EPARAM, "bl_slot_grammar: slot %d is not set up", slot);
+  if (c->stepped[slot]) return fail(BL_EPARAM, "bl_slot_grammar: attach the grammar before the slot's first step");
+  bl_slot_dev s = c->host_slots[slot];
+  if (!gbnf || len == 0) {
+    s.g_on = 0;
+    s.mode &= ~BL_M_GRAMMAR;
+  } else {
+    if (c->voff.empty()) return fail(BL_EPARAM, "bl_slot_grammar: the vocabulary pieces are not set (bl_set_vocab)");
+    if (s.temperature > 0.0f)
+      return fail(BL_EUNSUPPORTED, "grammar-constrained sampling with temperature > 0 is not supported on the device");
+    bl_ctx::gram_entry *e = nullptr;
+    int rc = grammar_tables(c, std::string(gbnf, len), &e);
+    if (rc) return rc;
+    /* the slot's position after its reply (the reference re-decodes it every step) */
+    bl_gram_pos pos{e->tab.start, e->tab.start, BL_GW_NONE, 0u, 0};
+    for (int32_t id : c->reply[slot]) {
+      const uint8_t *b = c->vblob.data() + c->voff[id];
+      bl_gw_commit(e->host, pos, [&](int i) { return (uint32_t)b[i]; }, (int)(c->voff[id + 1] - c->voff[id]));
+    }
+    s.gpos = pos;
+    s.g_on = 1;
+    s.mode |= BL_M_GRAMMAR;
+    hipSetDevice(c->device);
+    HIPCHK(hipStreamSynchronize(c->stream));
+    HIPCHK(hipMemcpy(c->d.gram + slot, &e->dev, sizeof(bl_gram_view), hipMemcpyHostToDevice));
+  }
+  hipSetDevice(c->device);
+  HIPCHK(hipStreamSynchronize(c->stream));
+  HIPCHK(hipMemcpy(c->d.slots + slot, &s, sizeof s, hipMemcpyHostToDevice));
+  c->host_slots[slot] = s;
+  return BL_OK;
+}
+
+int bl_grammar_mask(bl_ctx *c, int slot, uint32_t *d_mask_out, int32_t *forced_eos) {
+  if (!c || slot < 0 || slot >= c->d.max_slots || !c->slot_ready[slot] || !c->host_slots[slot].g_on || !d_mask_out)
+    return fail(BL_EPARAM, "bl_grammar_mask: slot %d has no grammar", slot);
+  hipSetDevice(c->device);
+  HIPCHK(hipStreamSynchronize(c->stream));
+  HIPCHK(hipMemcpy(c->d_mslot, &slot, sizeof(int32_t), hipMemcpyHostToDevice));
+  bl_rows rows{};
+  rows.slot = c->d_mslot; /* its own row table: the bound rows of the asynchronous step stay intact */
+  bl_launch_gmask(c->d, rows, c->stream);
+  HIPCHK(hipGetLastError());
+  const size_t words = ((size_t)c->d.vocab + 31) / 32;
+  HIPCHK(hipMemcpyAsync(d_mask_out, c->d.gmask, words * 4, hipMemcpyDeviceToDevice, c->stream));
+  int32_t st[2] = {0, 0};
+  HIPCHK(hipMemcpyAsync(&st[0], c->d.gstat, 4, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(hipMemcpyAsync(&st[1], c->d.gamb, 4, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(hipStreamSynchronize(c->stream));
+  if (forced_eos) *forced_eos = (st[0] & BL_GR_FORCED) ? 1 : 0;
+  if ((st[0] & BL_GR_FAMBIG) || st[1]) return fail(BL_EGRAMMAR_AMBIG, "grammar is left-recursive or too ambiguous to match");
+  if (st[0] & BL_GR_DEAD) return fail(BL_EGRAMMAR_DEAD, "the reply no longer matches the grammar");
   return BL_OK;
 }
 
@@ -410,6 +581,16 @@ static int check_rows(bl_ctx *c, const int32_t *slots, int B) {
   return BL_OK;
 }
 
+static bool needs_gram(bl_ctx *c, const int32_t *slots, int B) {
+  for (int i = 0; i < B; i++)
+    if (c->host_slots[slots[i]].g_on) return true;
+  return false;
+}
+
+static void mark_stepped(bl_ctx *c, const int32_t *slots, int B) {
+  for (int i = 0; i < B; i++) c->stepped[slots[i]] = 1;
+}
+
 static bool needs_exp(bl_ctx *c, const int32_t *slots, int B) {
   for (int i = 0; i < B; i++)
     if (c->host_slots[slots[i]].mode & (BL_M_LOGPROBS | BL_M_FULL)) return true;
@@ -421,6 +602,9 @@ static int status_error(int st) {
   if (st & BL_SE_TIE) return fail(BL_ETIE, "the full-vocabulary draw landed on equal logits; heap order is not reproduced");
   if (st & BL_SE_CAND_FULL) return fail(BL_EDEVICE, "candidate buffer overflow");
   if (st & BL_SE_EMPTY) return fail(BL_EEMPTY, "sample_candidates: empty or mismatched candidates");
+  if (st & BL_SE_GDEAD) return fail(BL_EGRAMMAR_DEAD, "the reply no longer matches the grammar");
+  if (st & BL_SE_GAMBIG) return fail(BL_EGRAMMAR_AMBIG, "grammar is left-recursive or too ambiguous to match");
+  if (st & BL_SE_GREJECT) return fail(BL_EGRAMMAR_REJECT, "the grammar rejected every vocabulary token");
   return BL_OK;
 }
 
@@ -448,7 +632,8 @@ int bl_sample_step(bl_ctx *c, const int32_t *slots, int B, const float *d_logits
   memcpy(c->h_slot, slots, B * sizeof(int32_t));
   HIPCHK(hipMemcpyAsync(c->d_slot, c->h_slot, B * sizeof(int32_t), hipMemcpyHostToDevice, c->stream));
   bl_rows rows = make_rows(c, false, 1, top_stride > 0 ? top_stride : 1);
-  bl_launch_step(c->d, d_logits, ld, rows, B, needs_exp(c, slots, B), c->stream, nullptr);
+  mark_stepped(c, slots, B);
+  bl_launch_step(c->d, d_logits, ld, rows, B, needs_exp(c, slots, B), needs_gram(c, slots, B), c->stream, nullptr);
   HIPCHK(hipGetLastError());
   HIPCHK(hipMemcpyAsync(c->h_tok, c->d_tok, B * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));
   HIPCHK(hipMemcpyAsync(c->h_status, c->d_status, B * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));
@@ -474,6 +659,7 @@ int bl_bind_rows(bl_ctx *c, const int32_t *slots, int B) {
   HIPCHK(hipMemcpy(c->d_slot, slots, B * sizeof(int32_t), hipMemcpyHostToDevice));
   memcpy(c->h_slot, slots, B * sizeof(int32_t));
   c->bound_B = B;
+  mark_stepped(c, slots, B);
   return BL_OK;
 }
 
@@ -493,7 +679,7 @@ int bl_sample_step_async(bl_ctx *c, int B, const float *d_logits, int64_t ld, in
       for (int k = 0; k < 4; k++) HIPCHK(hipEventCreate(&c->ev[k]));
     ev = c->ev;
   }
-  bl_launch_step(c->d, d_logits, ld, rows, B, needs_exp(c, c->h_slot, B), c->stream, ev);
+  bl_launch_step(c->d, d_logits, ld, rows, B, needs_exp(c, c->h_slot, B), needs_gram(c, c->h_slot, B), c->stream, ev);
   HIPCHK(hipGetLastError());
   if (ev) {
     /* per-kernel durations of this step, accumulated (the caller asked for timing: synchronous) */
@@ -534,6 +720,7 @@ int bl_spec_verify(bl_ctx *c, const int32_t *slots, int B, int k, const float *d
     const bl_slot_dev &s = c->host_slots[slots[b]];
     if (k > 0 && (s.fp_on || s.rep_on))
       return fail(BL_EUNSUPPORTED, "speculative rows with history-dependent penalties are not supported on the device");
+    if (s.g_on) return fail(BL_EUNSUPPORTED, "speculative rows of a grammar-constrained slot are not supported on the device");
   }
   hipSetDevice(c->device);
   for (int b = 0; b < B; b++)
@@ -546,7 +733,8 @@ int bl_spec_verify(bl_ctx *c, const int32_t *slots, int B, int k, const float *d
   bl_rows rows = make_rows(c, true, 0, 1);
   bool ne = false;
   for (int b = 0; b < B; b++) ne |= (c->host_slots[slots[b]].mode & (BL_M_LOGPROBS | BL_M_FULL)) != 0;
-  bl_launch_step(c->d, d_rows, ld, rows, R, ne, c->stream, nullptr);
+  mark_stepped(c, slots, B);
+  bl_launch_step(c->d, d_rows, ld, rows, R, ne, false, c->stream, nullptr);
   HIPCHK(hipGetLastError());
   HIPCHK(hipMemcpyAsync(c->h_tok, c->d_tok, R * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));
   HIPCHK(hipMemcpyAsync(c->h_status, c->d_status, R * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));
@@ -608,6 +796,19 @@ int bl_workload_bias(int cfg, int64_t seed, int row, int n, int vocab, float lo,
   memcpy(ids, i.data(), i.size() * sizeof(int32_t));
   memcpy(vals, v.data(), v.size() * sizeof(float));
   return BL_OK;
+}
+
+int bl_workload_c3_vocab(int64_t seed, int vocab, uint8_t *blob, size_t blob_cap, uint32_t *offsets, int32_t *eos_id) {
+  if (vocab <= 257 || !offsets || !eos_id) return fail(BL_EPARAM, "bl_workload_c3_vocab: invalid arguments");
+  std::vector<uint8_t> b;
+  std::vector<uint32_t> off;
+  int32_t eos = -1;
+  blw::c3_vocab(seed, vocab, b, off, eos);
+  if (!blob || b.size() > blob_cap) return fail(BL_EPARAM, "bl_workload_c3_vocab: blob needs %zu bytes", b.size());
+  memcpy(blob, b.data(), b.size());
+  memcpy(offsets, off.data(), off.size() * sizeof(uint32_t));
+  *eos_id = eos;
+  return (int)b.size();
 }
 
 int bl_workload_drafts(int64_t seed, int64_t step, int seq, const int32_t *argmax, int k, int vocab, int32_t *out) {

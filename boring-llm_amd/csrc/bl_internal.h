@@ -20,6 +20,8 @@
 
 #include <stdint.h>
 
+#include "bl_gwalk.h"
+
 #define BL_CH 4096          /* vocabulary chunk per workgroup in the row passes */
 #define BL_RP_THREADS 256   /* row-pass workgroup */
 #define BL_SEL_THREADS 1024 /* per-row selection workgroup */
@@ -36,12 +38,24 @@
 #define BL_M_TOPK 2
 #define BL_M_FULL 4
 #define BL_M_LOGPROBS 8
+#define BL_M_GRAMMAR 16
+
+/* grammar mask kernel: tokens per workgroup */
+#define BL_GM_THREADS 256
+
+/* per-row grammar status (bl_dev.gstat) */
+#define BL_GR_FORCED 1  /* complete and cannot continue: the step returns EOS (src/server.br:319-321) */
+#define BL_GR_DEAD 2    /* the reply no longer matches the grammar (src/server.br:318) */
+#define BL_GR_FAMBIG 4  /* the reply's own walk hit the 20,000-stack guard (src/grammar.br:354) */
 
 /* per-row status bits (also sticky in the slot) */
 #define BL_SE_UNSUPPORTED 1
 #define BL_SE_TIE 2
 #define BL_SE_CAND_FULL 4
 #define BL_SE_EMPTY 8
+#define BL_SE_GDEAD 16
+#define BL_SE_GREJECT 32
+#define BL_SE_GAMBIG 64
 
 struct bl_slot_dev {
   /* parameters (SamplingParams, src/model.br:1565-1584, and server extras) */
@@ -54,6 +68,9 @@ struct bl_slot_dev {
   /* state */
   uint64_t rng;
   int32_t n_tokens, n_reply, win_len, win_head, err, pad;
+  /* grammar (src/server.br:309-362): position of the reply in the slot's automaton */
+  bl_gram_pos gpos;
+  int32_t g_on, pad2;
 };
 
 struct bl_dev {
@@ -81,6 +98,18 @@ struct bl_dev {
   int32_t *full_n;  /* [rows] */
   uint64_t *sortk;  /* [rows][2^ceil(log2 V)] global sort scratch */
   double *gsum;     /* [rows][V/64 + 64] */
+  /* grammar-constrained sampling */
+  bl_gram_view *gram; /* [slots] the slot's compiled grammar (device pointers) */
+  const uint8_t *vblob;   /* vocabulary piece bytes */
+  const uint32_t *voff;   /* [V+1] byte offsets of each token's piece */
+  int32_t eos_id;
+  int32_t gm_blocks;      /* ceil(V / BL_GM_THREADS) */
+  uint32_t *gmask;        /* [rows][2 * ceil(V/64)] allow-bitmask */
+  int32_t *gstat;         /* [rows] BL_GR_* of the frontier */
+  int32_t *gamb;          /* [rows] a candidate's walk hit the 20,000-stack guard */
+  float *gm_max;          /* [rows][gm_blocks] allowed maximum per block */
+  int32_t *gm_arg;        /* lowest index reaching it */
+  int32_t *gm_eq;         /* allowed tokens equal to it */
 };
 
 /* one step's row table (device pointers) */
@@ -95,5 +124,15 @@ struct bl_rows {
   int32_t top_stride;
   int32_t *status;         /* [B] */
 };
+
+#if defined(__HIPCC__)
+/* appends token `tok`'s bytes to the slot's grammar position (reply_tokens.push of a non-EOG token,
+ * src/server.br:1037); one thread */
+__device__ inline void grammar_commit(const bl_dev &d, bl_slot_dev &sp, const bl_gram_view &g, int32_t tok) {
+  const uint32_t o0 = d.voff[tok], o1 = d.voff[tok + 1];
+  const uint8_t *b = d.vblob + o0;
+  bl_gw_commit(g, sp.gpos, [&](int i) { return (uint32_t)b[i]; }, (int)(o1 - o0));
+}
+#endif
 
 #endif /* BL_INTERNAL_H */

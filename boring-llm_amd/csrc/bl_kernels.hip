@@ -93,7 +93,11 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass(bl_dev d, const fl
   const int i0 = c * BL_CH;
   const int cnt = min(BL_CH, V - i0);
   const float *src = logits + (int64_t)row * ld + i0;
-  if (c == 0 && t == 0) d.full_n[row] = 0; /* consumed by the exponent pass, which runs after this kernel */
+  if (c == 0 && t == 0) {
+    /* consumed by the kernels that run after this one */
+    d.full_n[row] = 0;
+    d.gamb[row] = 0;
+  }
   /* model tail (src/model.br:973-984), applied in registers by the thread that loads the value */
   const float lmul = sp.logit_mul, cap = sp.final_softcap;
   const bool tail = lmul != 1.0f || cap > 0.0f;
@@ -371,6 +375,85 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_exppass(bl_dev d, bl_rows 
   }
 }
 
+/* ------------------------------------------------------------------ K2g: grammar allow-mask */
+/*
+ * grid (ceil(V/256), B) x 256 over the rows of grammar slots; one lane per token. The allowed
+ * predicate of sample_grammar_token (src/server.br:334-350): an end-of-generation token when the
+ * frontier is complete and ignore_eos is off, any other token when grammar_advance_text(frontier,
+ * piece) is not empty. Writes the packed allow-bitmask (a __ballot per wavefront), the frontier's
+ * status (src/server.br:311-321), and, with `with_values`, each block's allowed maximum of the
+ * transformed row with its lowest index and the number of allowed tokens equal to it (the first
+ * allowed candidate in rank order of a greedy step, src/server.br:351-356).
+ */
+__global__ __launch_bounds__(BL_GM_THREADS) void bl_k_gmask(bl_dev d, bl_rows rows, int with_values) {
+  const int V = d.vocab, row = blockIdx.y, t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int slot = rows.slot[row];
+  const bl_slot_dev &sp = d.slots[slot];
+  if (!sp.g_on) return;
+  __shared__ float red_m[BL_GM_THREADS / 64];
+  __shared__ int red_i[BL_GM_THREADS / 64];
+  __shared__ int red_n[BL_GM_THREADS / 64];
+  const bl_gram_view g = d.gram[slot];
+  const bl_gram_pos pos = sp.gpos;
+  const int32_t front = bl_gw_frontier(g, pos);
+  const int64_t tok = (int64_t)blockIdx.x * BL_GM_THREADS + t;
+  bool allowed = false, ambig = false;
+  if (front >= 0 && tok < V) {
+    bool eog = false;
+    for (int k = 0; k < d.n_eog; k++) eog |= d.eog[k] == (int32_t)tok;
+    if (eog) {
+      allowed = (g.flags[front] & BL_GS_COMPLETE) && !sp.ignore_eos;
+    } else {
+      const uint32_t o0 = d.voff[tok], o1 = d.voff[tok + 1];
+      const uint8_t *b = d.vblob + o0;
+      int32_t st = bl_gw_walk(g, pos, front, [&](int i) { return (uint32_t)b[i]; }, (int)(o1 - o0));
+      allowed = st >= 0;
+      ambig = st == BL_GT_AMBIG;
+    }
+  }
+  const unsigned long long bm = __ballot(allowed);
+  const unsigned long long am = __ballot(ambig);
+  const int64_t words = 2 * (((int64_t)V + 63) / 64);
+  if (lane == 0) {
+    const int64_t wi = (tok >> 6) * 2; /* lane 0 holds a multiple of 64 */
+    if (wi < words) {
+      d.gmask[(int64_t)row * words + wi] = (uint32_t)bm;
+      d.gmask[(int64_t)row * words + wi + 1] = (uint32_t)(bm >> 32);
+    }
+    if (am) atomicOr(&d.gamb[row], 1);
+  }
+  if (blockIdx.x == 0 && t == 0) {
+    int st = 0;
+    if (front == BL_GT_AMBIG) st |= BL_GR_FAMBIG;
+    else if (front < 0) st |= BL_GR_DEAD;
+    else if ((g.flags[front] & BL_GS_COMPLETE) && !(g.flags[front] & BL_GS_CONTINUE) && !sp.ignore_eos)
+      st |= BL_GR_FORCED;
+    d.gstat[row] = st;
+  }
+  if (!with_values) return;
+  /* allowed maximum of this block, lowest index, and its multiplicity */
+  float m = BL_NEG_INF;
+  int mi = 0x7fffffff;
+  const float v = allowed ? d.eff[(int64_t)row * V + tok] : BL_NEG_INF;
+  if (allowed) {
+    m = v;
+    mi = (int)tok;
+  }
+  block_argmax<BL_GM_THREADS>(m, mi, red_m, red_i);
+  const bool eq = allowed && v == m;
+  int n_eq = __popcll(__ballot(eq));
+  if (lane == 0) red_n[w] = n_eq;
+  __syncthreads();
+  if (t == 0) {
+    int tot = 0;
+    for (int k = 0; k < BL_GM_THREADS / 64; k++) tot += red_n[k];
+    const int64_t o = (int64_t)row * d.gm_blocks + blockIdx.x;
+    d.gm_max[o] = m;
+    d.gm_arg[o] = mi;
+    d.gm_eq[o] = tot;
+  }
+}
+
 /* ------------------------------------------------------------------ K3: per-row selection */
 #define SEL_NW (BL_SEL_THREADS / 64)
 
@@ -604,7 +687,38 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
   const int skip = rows.rng_skip ? rows.rng_skip[row] : 0;
   int32_t tok = Mi;
   const float T = sp.temperature;
-  if (T <= 0.0f) {
+  if (mode & BL_M_GRAMMAR) {
+    /* sample_grammar_token, greedy (src/server.br:308-361): the frontier's status, then the first
+     * allowed candidate in rank order = the allowed maximum; the lowest index among equal allowed
+     * maxima is top_k_select's order but not the heap rank's, so a tie is reported */
+    const int gst = d.gstat[row];
+    if (gst & BL_GR_FAMBIG) {
+      status |= BL_SE_GAMBIG;
+    } else if (gst & BL_GR_DEAD) {
+      status |= BL_SE_GDEAD;
+    } else if (gst & BL_GR_FORCED) {
+      tok = d.eos_id;
+    } else if (d.gamb[row]) {
+      status |= BL_SE_GAMBIG;
+    } else {
+      float gm = BL_NEG_INF;
+      int gi = 0x7fffffff;
+      const int64_t go = (int64_t)row * d.gm_blocks;
+      for (int k = t; k < d.gm_blocks; k += BL_SEL_THREADS) argmax_merge(gm, gi, d.gm_max[go + k], d.gm_arg[go + k]);
+      block_argmax<BL_SEL_THREADS>(gm, gi, sh.red_m, sh.red_i);
+      double n_eq = 0.0;
+      if (gi != 0x7fffffff)
+        for (int k = t; k < d.gm_blocks; k += BL_SEL_THREADS)
+          if (d.gm_arg[go + k] != 0x7fffffff && d.gm_max[go + k] == gm) n_eq += (double)d.gm_eq[go + k];
+      n_eq = block_sum_d<BL_SEL_THREADS>(n_eq, sh.gsum);
+      if (gi == 0x7fffffff) {
+        status |= BL_SE_GREJECT;
+      } else {
+        tok = gi;
+        if (n_eq > 1.0) status |= BL_SE_TIE;
+      }
+    }
+  } else if (T <= 0.0f) {
     tok = Mi; /* sample_greedy over the full penalised row (src/sampling.br:752-754) */
   } else if (mode & BL_M_TOPK) {
     /* top_k_select list: kk = min(top_k, V) entries, unfilled slots are (-1e30, 0) */
@@ -691,6 +805,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
           d.cnt[so + tok] += 1;
           tw[tok >> 5] |= 1u << (tok & 31);
         }
+        if (sp.g_on) grammar_commit(d, sp, d.gram[slot], tok);
       }
       sp.rng = rng;
     }
@@ -711,17 +826,28 @@ __global__ void bl_k_synth(float *out, int64_t ld, int cfg, int64_t seed, int64_
 /* ------------------------------------------------------------------ host-side launchers */
 /* ev: optional 4 events recorded before/after the three kernels (kernel timing for the benchmark) */
 void bl_launch_step(const bl_dev &d, const float *logits, int64_t ld, const bl_rows &rows, int B, bool need_exp,
-                    hipStream_t s, hipEvent_t *ev) {
+                    bool need_gram, hipStream_t s, hipEvent_t *ev) {
   dim3 g1(d.nc, B);
   if (ev) (void)hipEventRecord(ev[0], s);
   hipLaunchKernelGGL(bl_k_rowpass, g1, dim3(BL_RP_THREADS), 0, s, d, logits, ld, rows);
   if (ev) (void)hipEventRecord(ev[1], s);
+  if (need_gram) hipLaunchKernelGGL(bl_k_gmask, dim3(d.gm_blocks, B), dim3(BL_GM_THREADS), 0, s, d, rows, 1);
   if (need_exp) {
     hipLaunchKernelGGL(bl_k_exppass, g1, dim3(BL_RP_THREADS), 0, s, d, rows);
   }
   if (ev) (void)hipEventRecord(ev[2], s);
   hipLaunchKernelGGL(bl_k_select, dim3(B), dim3(BL_SEL_THREADS), 0, s, d, rows);
   if (ev) (void)hipEventRecord(ev[3], s);
+}
+
+/* the allow-mask of one slot's current position, without a step (bl_grammar_mask); rows.slot[0] is
+ * the slot, row 0's mask and status are written */
+__global__ void bl_k_gclear(bl_dev d) {
+  if (threadIdx.x == 0) d.gamb[0] = 0;
+}
+void bl_launch_gmask(const bl_dev &d, const bl_rows &rows, hipStream_t s) {
+  hipLaunchKernelGGL(bl_k_gclear, dim3(1), dim3(64), 0, s, d);
+  hipLaunchKernelGGL(bl_k_gmask, dim3(d.gm_blocks, 1), dim3(BL_GM_THREADS), 0, s, d, rows, 0);
 }
 
 void bl_launch_synth(float *out, int64_t ld, int cfg, int64_t seed, int64_t step, int rows, int V, hipStream_t s) {

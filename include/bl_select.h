@@ -89,6 +89,27 @@ int bl_slot_rng(bl_ctx *ctx, int slot, uint64_t *state);
  * src/server.br:1004, :1037). */
 int bl_slot_commit(bl_ctx *ctx, int slot, const int32_t *toks, int n);
 
+/* Vocabulary pieces for grammar-constrained slots: token t's bytes are blob[offsets[t] .. offsets[t+1]),
+ * n_tokens = the context's vocabulary (Tokenizer.decode / piece_bytes, src/tokenizer.br:122-151,
+ * :227-240; special tokens as their literal UTF-8). The grammar's end-of-sequence token is the
+ * eos_id of bl_set_eog. */
+int bl_set_vocab(bl_ctx *ctx, const uint8_t *blob, const uint32_t *offsets, int n_tokens);
+
+/* Attach a GBNF grammar to a slot set up by bl_slot_reset, before its first step (the request's
+ * `grammar` field; parse_gbnf src/grammar.br:309-323). The slot's steps then follow
+ * sample_grammar_token (src/server.br:308-361): forced EOS when the reply is complete and cannot
+ * continue, otherwise the first allowed candidate in rank order (greedy: temperature <= 0 only on the
+ * device). gbnf = NULL detaches. Errors: BL_EGRAMMAR (parse, with the reference's message),
+ * BL_EGRAMMAR_AMBIG, BL_EUNSUPPORTED (temperature > 0, or a grammar whose reachable automaton exceeds
+ * 65536 states: a recursive one). */
+int bl_slot_grammar(bl_ctx *ctx, int slot, const char *gbnf, size_t len);
+
+/* The slot's allow-bitmask for the next token (the `allowed` predicate of src/server.br:334-350 over
+ * every vocabulary id, including the EOG rule): ceil(vocab/32) words into device memory, bit t of
+ * word t/32 set when token t is allowed; *forced_eos = the step would return EOS without sampling.
+ * BL_EGRAMMAR_DEAD when the reply no longer matches (src/server.br:318). */
+int bl_grammar_mask(bl_ctx *ctx, int slot, uint32_t *d_mask_out, int32_t *forced_eos);
+
 /* One decode-loop sampling block for B slots (src/server.br:940-1037: logit_bias, ignore_eos,
  * frequency/presence, then sample() = sampling_logits + greedy | rank + sample_candidates, then
  * logprob_normalizer + top_k_select for logprobs). `d_logits` is a device pointer to B rows of
@@ -123,10 +144,14 @@ int bl_spec_verify(bl_ctx *ctx, const int32_t *slots, int B, int k, const float 
 int bl_synth_logits(bl_ctx *ctx, float *d_out, int64_t ld, int cfg, int64_t seed, int64_t step, int rows, int vocab);
 
 /* Sparse inputs of the benchmark workloads (no reference counterpart; host only): kind 0 = uniform
- * ids, kind 1 = Zipf(1.1) ids; logit_bias lists of n distinct ids with values in [lo, hi); speculative
- * drafts (argmax with probability 0.7, else uniform). Deterministic in (cfg, seed, row/step). */
+ * ids, kind 1 = Zipf(1.1) ids; logit_bias lists of n distinct ids with values in [lo, hi); the
+ * workload-3 vocabulary (256 single-byte tokens, byte strings of Zipf lengths 1..16, 70% printable
+ * ASCII / 30% valid UTF-8, EOS "<|eos|>" = vocab-1; returns the blob size, BL_EPARAM when blob_cap is
+ * too small); speculative drafts (argmax with probability 0.7, else uniform). Deterministic in
+ * (cfg, seed, row/step). */
 int bl_workload_ids(int kind, int cfg, int64_t seed, int row, int n, int vocab, int32_t *out);
 int bl_workload_bias(int cfg, int64_t seed, int row, int n, int vocab, float lo, float hi, int32_t *ids, float *vals);
+int bl_workload_c3_vocab(int64_t seed, int vocab, uint8_t *blob, size_t blob_cap, uint32_t *offsets, int32_t *eos_id);
 int bl_workload_drafts(int64_t seed, int64_t step, int seq, const int32_t *argmax, int k, int vocab, int32_t *out);
 
 /* Self-test (no reference counterpart): digests of the device expf (fn 0) / tanhf (fn 1) over

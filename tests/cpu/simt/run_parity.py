@@ -7,7 +7,8 @@ alone) and checks the workloads the GPU parity tests check, at reduced step coun
 
     python run_parity.py --lib _build/libbl_simt.so small:0-10:25 w2:2 w4:1:8 w5:1 async:2
 
-Items: small:<cases>:<steps>, w2:<steps>, w4:<steps>:<rows>, w5:<steps>, async:<steps>.
+Items: small:<cases>:<steps>, w2:<steps>, w3:<steps>, w4:<steps>:<rows>, w5:<steps>, async:<steps>,
+grammar:<cases>:<steps>.
 Prints one line per item ("ok ..." / "FAIL ...") and exits 1 if any failed.
 """
 import argparse
@@ -24,6 +25,28 @@ import _oracle as O  # noqa: E402
 from _cases import CASES, EOGS, EOS, SMALL_V, small_case_inputs, small_case_logits  # noqa: E402
 
 LP_RTOL = 1e-5
+
+
+class HostMem:
+    """Device buffers of the emulator: host memory (numpy)."""
+
+    class Buf:
+        def __init__(self, n, dtype):
+            self.a = np.zeros(n, dtype)
+            self.ptr = self.a.ctypes.data
+
+        def upload(self, x):
+            self.a[:] = x
+
+        def host(self):
+            return self.a.copy()
+
+    def zeros(self, n, dtype):
+        return self.Buf(n, dtype)
+
+
+# where the harness allocates "device" buffers; the GPU tests replace it with torch device memory
+MEM = HostMem()
 
 
 def load_binding(lib_path):
@@ -55,12 +78,12 @@ def run_small(BL, case, steps):
                        O.ip(bi), O.fp(bv), len(bias))
     wants = 1 if kw.get("logprobs") else 0
     n_probs = kw.get("n_probs", 0)
-    buf = np.zeros(SMALL_V, np.float32)
+    buf = MEM.zeros(SMALL_V, np.float32)
     try:
         for t in range(steps):
             x = small_case_logits(rng)
-            buf[:] = x
-            tok, lp, ti, tl = ctx.sample_step([1], buf.ctypes.data, SMALL_V, top_stride=max(n_probs, 1))
+            buf.upload(x)
+            tok, lp, ti, tl = ctx.sample_step([1], buf.ptr, SMALL_V, top_stride=max(n_probs, 1))
             ot, olp = np.zeros(1, np.int32), np.zeros(1, np.float32)
             oti, otl = np.zeros(max(n_probs, 1), np.int32), np.zeros(max(n_probs, 1), np.float32)
             eog = O.C.c_int()
@@ -99,11 +122,11 @@ def run_w2(BL, steps):
     wi, wp = np.zeros(steps * B * 10, np.int32), np.zeros(steps * B * 10, np.float32)
     assert O.lib().orc_run_c2(seed, steps, B, O.ip(wt), O.fp(wl), O.ip(wi), O.fp(wp), None) == 0
     ctx = c2_context(BL, V, seed)
-    buf = np.zeros(B * V, np.float32)
+    buf = MEM.zeros(B * V, np.float32)
     try:
         for t in range(steps):
-            ctx.synth_logits(buf.ctypes.data, V, 2, seed, t, B, V)
-            tok, lp, ti, tl = ctx.sample_step(list(range(B)), buf.ctypes.data, V, top_stride=10)
+            ctx.synth_logits(buf.ptr, V, 2, seed, t, B, V)
+            tok, lp, ti, tl = ctx.sample_step(list(range(B)), buf.ptr, V, top_stride=10)
             for r in range(B):
                 a = t * B + r
                 if tok[r] != wt[a] or not lp_close(lp[r], wl[a]) or ti[r] != list(wi[a * 10:(a + 1) * 10]):
@@ -124,11 +147,11 @@ def run_w4(BL, steps, rows):
     for r in range(rows):
         ctx.slot_reset(r, BL.Params(temperature=1.0, top_k=64, top_p=0.95, logprobs=1, n_probs=20, final_softcap=30.0),
                        BL.seed_rng(seed + r))
-    buf = np.zeros(rows * V, np.float32)
+    buf = MEM.zeros(rows * V, np.float32)
     try:
         for t in range(steps):
-            ctx.synth_logits(buf.ctypes.data, V, 4, seed, t, rows, V)
-            tok, lp, ti, tl = ctx.sample_step(list(range(rows)), buf.ctypes.data, V, top_stride=20)
+            ctx.synth_logits(buf.ptr, V, 4, seed, t, rows, V)
+            tok, lp, ti, tl = ctx.sample_step(list(range(rows)), buf.ptr, V, top_stride=20)
             for r in range(rows):
                 a = t * B + r
                 if tok[r] != wt[a] or not lp_close(lp[r], wl[a]) or ti[r] != list(wi[a * 20:(a + 1) * 20]):
@@ -150,16 +173,16 @@ def run_w5(BL, steps):
     for b in range(S):
         g.slot_reset(b, BL.Params(), BL.seed_rng(seed + b))
         s.slot_reset(b, BL.Params(temperature=0.7), BL.seed_rng(seed + b))
-    buf = np.zeros(R * V, np.float32)
+    buf = MEM.zeros(R * V, np.float32)
     try:
         for t in range(steps):
-            g.synth_logits(buf.ctypes.data, V, 5, seed, t, R, V)
-            am = np.argmax(buf.reshape(R, V), axis=1)
+            g.synth_logits(buf.ptr, V, 5, seed, t, R, V)
+            am = np.argmax(buf.host().reshape(R, V), axis=1)
             drafts = []
             for b in range(S):
                 drafts += BL.workload_drafts(seed, t, b, [int(x) for x in am[b * (K + 1):b * (K + 1) + K]], V)
-            gt, ga = g.spec_verify(list(range(S)), K, buf.ctypes.data, V, drafts)
-            st, sa = s.spec_verify(list(range(S)), K, buf.ctypes.data, V, drafts)
+            gt, ga = g.spec_verify(list(range(S)), K, buf.ptr, V, drafts)
+            st, sa = s.spec_verify(list(range(S)), K, buf.ptr, V, drafts)
             if gt != list(wgt[t * R:(t + 1) * R]) or ga != list(wga[t * S:(t + 1) * S]):
                 return f"greedy step {t}"
             if st != list(wst[t * R:(t + 1) * R]) or sa != list(wsa[t * S:(t + 1) * S]):
@@ -173,23 +196,170 @@ def run_w5(BL, steps):
 def run_async(BL, steps):
     """bl_bind_rows + bl_sample_step_async into caller buffers equals the synchronous step."""
     V, seed, B = 151936, 2, 8
-    pool = np.zeros((steps, B * V), np.float32)
+    pool = [MEM.zeros(B * V, np.float32) for _ in range(steps)]
     eager = c2_context(BL, V, seed)
     for t in range(steps):
-        eager.synth_logits(pool[t].ctypes.data, V, 2, seed, t, B, V)
-    want = [eager.sample_step(list(range(B)), pool[t].ctypes.data, V, top_stride=10)[:2] for t in range(steps)]
+        eager.synth_logits(pool[t].ptr, V, 2, seed, t, B, V)
+    want = [eager.sample_step(list(range(B)), pool[t].ptr, V, top_stride=10)[:2] for t in range(steps)]
     eager.close()
     ctx = c2_context(BL, V, seed)
     ctx.bind_rows(list(range(B)))
-    tok, lp = np.zeros(B, np.int32), np.zeros(B, np.float32)
-    ti, tl = np.zeros(B * 10, np.int32), np.zeros(B * 10, np.float32)
+    tok, lp = MEM.zeros(B, np.int32), MEM.zeros(B, np.float32)
+    ti, tl = MEM.zeros(B * 10, np.int32), MEM.zeros(B * 10, np.float32)
     try:
         for t in range(steps):
-            ctx.sample_step_async(B, pool[t].ctypes.data, V, tok.ctypes.data, lp.ctypes.data, ti.ctypes.data,
-                                  tl.ctypes.data, 10)
-            if tok.tolist() != list(want[t][0]) or lp.tolist() != list(want[t][1]):
+            ctx.sample_step_async(B, pool[t].ptr, V, tok.ptr, lp.ptr, ti.ptr, tl.ptr, 10)
+            if tok.host().tolist() != list(want[t][0]) or lp.host().tolist() != list(want[t][1]):
                 return f"step {t}: asynchronous step differs from the synchronous one"
     finally:
+        ctx.close()
+    return None
+
+
+GOLDEN = os.path.join(ROOT, "tests", "golden")
+
+
+def run_w3(BL, steps, check_masks=True):
+    """Workload 3: greedy decode under the config-3 JSON-Schema grammar, masks and tokens per step."""
+    V, seed = 151936, 3
+    L = O.lib()
+    L.orc_set_eog_tokens(O.ip(O.i32([0])), 0, -1)
+    wt, wc, wf = np.zeros(steps, np.int32), np.zeros(steps, np.uint32), np.zeros(steps, np.int32)
+    assert L.orc_run_c3(seed, steps, 1, O.ip(wt), wc.ctypes.data_as(O.C.POINTER(O.C.c_uint32)), O.ip(wf), None) == 0, \
+        O.last_error()
+    blob, off, eos = BL.workload_c3_vocab(seed, V)
+    with open(os.path.join(GOLDEN, "c3_schema.gbnf")) as f:
+        gbnf = f.read()
+    ctx = BL.Context(V, 1, 1)
+    ctx.set_eog(eos, [])
+    ctx.set_vocab(blob, off)
+
+    def restart():
+        ctx.slot_reset(0, BL.Params(), BL.seed_rng(seed))
+        ctx.slot_grammar(0, gbnf)
+
+    restart()
+    buf = MEM.zeros(V, np.float32)
+    mask = MEM.zeros((V + 31) // 32, np.uint32)
+    try:
+        for t in range(steps):
+            ctx.synth_logits(buf.ptr, V, 3, seed, t, 1, V)
+            if check_masks:
+                forced = ctx.grammar_mask(0, mask.ptr)
+                m = mask.host()
+                crc = L.orc_crc32(m.ctypes.data, m.nbytes)
+                if crc != wc[t] or int(forced) != wf[t]:
+                    return f"step {t}: mask crc {crc:#x} vs {int(wc[t]):#x}, forced {forced} vs {wf[t]}"
+            tok = ctx.sample_step([0], buf.ptr, V)[0][0]
+            if tok != wt[t]:
+                return f"step {t}: token {tok} vs {wt[t]}"
+            if tok == eos:
+                restart()
+    finally:
+        ctx.close()
+    return None
+
+
+# byte-level vocabulary with every lone byte, UTF-8 fragments and whole characters, and a grammar whose
+# classes see non-ASCII text: exercises the carry of unfinished sequences and the trailing U+FFFD rule
+GRAMMAR_CASES = [
+    'root ::= "{" [^"}]* "}" "x"?\n',
+    'root ::= ([a-c] | [\\u00e0-\\u00ff] | "\\u20ac")+ ";"\n',
+    'root ::= "\\"" ( [^"\\\\] | "\\\\" ["\\\\n] )* "\\"" [ ]{0,3}\n',
+    'root ::= ("ab" | "a" [^b])* "!" | [0-9]{2,4}\n',
+    None,  # the workload-3 schema grammar (tests/golden/c3_schema.gbnf)
+    'root ::= [^\\x00-\\x7f]{1,6} ("." [^\\x00-\\x7f])* ";"\n',
+    'root ::= ("\\u00e9\\u20ac" | "\\U0001F600" | "a")+ "."\n',
+]
+
+
+def grammar_vocab(rng, n_extra):
+    pieces = [bytes([b]) for b in range(256)]
+    chars = ["a", "b", "c", "{", "}", '"', "\\", "!", ";", "x", " ", "é", "ÿ", "€", "\U0001F600", "�",
+             "n", "0", "7"]
+    for _ in range(n_extra):
+        k = int(rng.integers(1, 5))
+        s = "".join(chars[int(i)] for i in rng.integers(0, len(chars), k)).encode()
+        if rng.random() < 0.3:  # a fragment: cut inside a multi-byte sequence
+            cut = int(rng.integers(0, len(s) + 1))
+            s = s[cut:] if rng.random() < 0.5 else s[:cut]
+        if not s:
+            s = bytes([int(rng.integers(0, 256))])
+        pieces.append(s)
+    pieces.append(b"<|eos|>")
+    off = [0]
+    for pc in pieces:
+        off.append(off[-1] + len(pc))
+    return b"".join(pieces), off, len(pieces) - 1
+
+
+def run_grammar_case(BL, case, steps):
+    """Masks and greedy tokens of a small grammar against the oracle's slot on random rows."""
+    rng = np.random.default_rng(500 + case)
+    blob, off, eos = grammar_vocab(rng, 700)
+    V = len(off) - 1
+    gbnf = GRAMMAR_CASES[case]
+    if gbnf is None:
+        with open(os.path.join(GOLDEN, "c3_schema.gbnf")) as f:
+            gbnf = f.read()
+    L = O.lib()
+    L.orc_set_eog_tokens(O.ip(O.i32([0])), 0, -1)
+    op = O.params()
+    h = L.orc_slot_new(O.C.byref(op), 1, None, 0, None, 0, None, None, 0)
+    oo = np.array(off, np.uint32)
+    assert L.orc_slot_set_grammar(h, gbnf.encode(), blob, oo.ctypes.data_as(O.C.POINTER(O.C.c_uint32)), V,
+                                  eos) == 0, O.last_error()
+    ctx = BL.Context(V, 1, 1)
+    ctx.set_eog(eos, [])
+    ctx.set_vocab(blob, off)
+    ctx.slot_reset(0, BL.Params(), 1)
+    ctx.slot_grammar(0, gbnf)
+    words = (V + 31) // 32
+    mask, want = MEM.zeros(words, np.uint32), np.zeros(words, np.uint32)
+    buf = MEM.zeros(V, np.float32)
+    try:
+        for t in range(steps):
+            of = O.C.c_int()
+            ok = L.orc_slot_grammar_mask(h, V, want.ctypes.data_as(O.C.POINTER(O.C.c_uint32)), O.C.byref(of), 1)
+            try:
+                forced = ctx.grammar_mask(0, mask.ptr)
+            except BL.BLError as e:
+                if e.code != BL.BL_EGRAMMAR_DEAD or ok != 0:
+                    return f"step {t}: device '{e}', oracle mask status {ok}"
+                # both find the reply dead (a piece can be allowed and the re-decoded reply still fail,
+                # src/server.br:311-318): start a new reply
+                L.orc_slot_restart(h)
+                ctx.slot_reset(0, BL.Params(), 1)
+                ctx.slot_grammar(0, gbnf)
+                continue
+            if ok != 1:
+                return f"step {t}: the oracle's reply is dead ({ok}) but the device's is not"
+            got = mask.host()
+            if not np.array_equal(got, want) or bool(of.value) != forced:
+                bad = np.nonzero(got != want)[0]
+                return f"step {t}: mask differs in {len(bad)} words (first {bad[:4]}), forced {forced} vs {of.value}"
+            x = (rng.standard_normal(V) * 3.0).astype(np.float32)
+            buf.upload(x)
+            ot = np.zeros(1, np.int32)
+            eg = O.C.c_int()
+            orc = L.orc_slot_step(h, O.fp(x), V, 0, 1, O.ip(ot), None, None, None, O.C.byref(eg))
+            try:
+                tok = ctx.sample_step([0], buf.ptr, V)[0][0]
+            except BL.BLError as e:
+                # the reference's errors (dead reply, every token rejected) must be the same errors
+                if orc == 0 or O.last_error() not in str(e):
+                    return f"step {t}: device error '{e}', oracle {'token ' + str(ot[0]) if orc == 0 else O.last_error()}"
+                return None
+            if orc != 0:
+                return f"step {t}: oracle error '{O.last_error()}', device token {tok}"
+            if tok != ot[0]:
+                return f"step {t}: token {tok} vs {ot[0]}"
+            if tok == eos:
+                L.orc_slot_restart(h)
+                ctx.slot_reset(0, BL.Params(), 1)
+                ctx.slot_grammar(0, gbnf)
+    finally:
+        L.orc_slot_free(h)
         ctx.close()
     return None
 
@@ -227,6 +397,11 @@ def main():
             results.append(("workload 5", run_w5(BL, int(f[1]))))
         elif kind == "async":
             results.append(("asynchronous step", run_async(BL, int(f[1]))))
+        elif kind == "w3":
+            results.append(("workload 3", run_w3(BL, int(f[1]))))
+        elif kind == "grammar":
+            for c in parse_range(f[1]):
+                results.append((f"grammar case {c}", run_grammar_case(BL, c, int(f[2]) if len(f) > 2 else 30)))
         else:
             raise SystemExit(f"unknown item {item}")
         for name, err in results:

@@ -1,0 +1,117 @@
+"""GPU parity of the grammar-constrained path (libbl_select.so through its C ABI) against the oracle.
+
+Allow-bitmasks and tokens must be identical. Workload 3: greedy decode of 256
+steps over the synthetic 151936-token vocabulary under the JSON-Schema grammar of tests/golden, the
+mask's CRC32, the forced-EOS flag and the token compared at every step with the oracle's literal
+restatement of src/server.br:308-361. Seven small grammars over a byte-level vocabulary of lone bytes,
+UTF-8 fragments and whole characters check the carry of unfinished UTF-8 sequences, the
+trailing-U+FFFD rule and the reference's error outcomes. The same harness runs on the CPU emulator
+(tests/test_simt_kernels.py); here its buffers are device memory.
+"""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+import bl_select as BL  # noqa: E402
+import _oracle as O  # noqa: E402
+
+sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "cpu", "simt"))
+import run_parity as RP  # noqa: E402
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+class TorchMem:
+    """Harness buffers in device memory; transfers synchronise the device."""
+
+    _types = {np.float32: torch.float32, np.int32: torch.int32, np.uint32: torch.int32}
+
+    class Buf:
+        def __init__(self, n, dtype):
+            self.dtype = np.dtype(dtype)
+            self.t = torch.zeros(n, dtype=TorchMem._types[self.dtype.type], device="cuda:0")
+            self.ptr = self.t.data_ptr()
+
+        def upload(self, x):
+            a = np.ascontiguousarray(x, dtype=self.dtype)
+            if self.dtype == np.uint32:
+                a = a.view(np.int32)
+            self.t.copy_(torch.from_numpy(a))
+            torch.cuda.synchronize()
+
+        def host(self):
+            torch.cuda.synchronize()
+            return self.t.cpu().numpy().view(self.dtype)
+
+    def zeros(self, n, dtype):
+        return self.Buf(n, dtype)
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device_memory():
+    assert torch.cuda.is_available(), "a GPU test ran without a GPU"
+    old = RP.MEM
+    RP.MEM = TorchMem()
+    yield
+    RP.MEM = old
+
+
+def test_workload3_masks_and_tokens():
+    say("workload 3: 256 greedy grammar steps, masks and tokens")
+    err = RP.run_w3(BL, 256)
+    assert err is None, err
+
+
+@pytest.mark.parametrize("case", range(len(RP.GRAMMAR_CASES)))
+def test_grammar_cases(case):
+    say(f"grammar case {case}: {RP.GRAMMAR_CASES[case]!r}")
+    err = RP.run_grammar_case(BL, case, 120)
+    assert err is None, err
+
+
+def test_grammar_errors():
+    say("grammar errors")
+    blob, off, eos = RP.grammar_vocab(np.random.default_rng(1), 50)
+    V = len(off) - 1
+    ctx = BL.Context(V, 2, 2)
+    ctx.set_eog(eos, [])
+    ctx.set_vocab(blob, off)
+    ctx.slot_reset(0, BL.Params(), 1)
+    with pytest.raises(BL.BLError) as e:
+        ctx.slot_grammar(0, 'root ::= "a" b\n')
+    assert e.value.code == BL.BL_EGRAMMAR and "grammar: undefined rule 'b'" in str(e.value)
+    with pytest.raises(BL.BLError) as e:
+        ctx.slot_grammar(0, 'root ::= "a"{3,1}\n')
+    assert e.value.code == BL.BL_EGRAMMAR and "repetition maximum is smaller than its minimum" in str(e.value)
+    with pytest.raises(BL.BLError) as e:  # reachable recursion: no finite automaton
+        ctx.slot_grammar(0, 'root ::= v\nv ::= "[" v? "]"\n')
+    assert e.value.code == BL.BL_EUNSUPPORTED
+    with pytest.raises(BL.BLError) as e:  # the reference's 20,000-stack guard
+        ctx.slot_grammar(0, 'root ::= a\na ::= a "x" | "y"\n')
+    assert e.value.code == BL.BL_EGRAMMAR_AMBIG
+    ctx.slot_reset(1, BL.Params(temperature=0.8), 1)
+    with pytest.raises(BL.BLError) as e:
+        ctx.slot_grammar(1, 'root ::= "a"\n')
+    assert e.value.code == BL.BL_EUNSUPPORTED
+    # a finished sentence: forced EOS (src/server.br:319-321); with ignore_eos nothing is allowed (:361)
+    x = np.full(V, -1.0, np.float32)
+    x[ord("{")] = 5.0
+    buf = torch.from_numpy(x).to("cuda:0")
+    for ignore in (0, 1):
+        ctx.slot_reset(0, BL.Params(ignore_eos=ignore), 1)
+        ctx.slot_grammar(0, 'root ::= "{"\n')
+        assert ctx.sample_step([0], buf.data_ptr(), V)[0][0] == ord("{")
+        if ignore:
+            with pytest.raises(BL.BLError) as e:
+                ctx.sample_step([0], buf.data_ptr(), V)
+            assert e.value.code == BL.BL_EGRAMMAR_REJECT
+        else:
+            assert ctx.sample_step([0], buf.data_ptr(), V)[0][0] == eos
+    ctx.close()

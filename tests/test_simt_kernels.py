@@ -52,6 +52,14 @@ def test_full_vocabulary_workloads(simt_lib):
     assert "ok   workload 2" in out and "ok   workload 4" in out and "ok   asynchronous step" in out
 
 
+def test_grammar_masks_and_tokens(simt_lib):
+    """The grammar path (GBNF automaton tables, per-token mask walk, masked greedy, on-device commit of
+    the reply position) against the oracle's whole-reply re-decode: workload 3 and seven adversarial
+    byte-level vocabularies."""
+    out = _run(simt_lib, ["w3:3", "grammar:0-6:40"], {"SIMT_ORDER": "rand"})
+    assert "ok   workload 3" in out and out.count("ok   grammar case") == 7
+
+
 def test_small_cases_address_sanitizer():
     _build("asan")
     pre = []
@@ -60,5 +68,5 @@ def test_small_cases_address_sanitizer():
         assert os.path.isabs(p) and os.path.exists(p), f"{rt} not found"
         pre.append(p)
     env = {"LD_PRELOAD": " ".join(pre), "ASAN_OPTIONS": "detect_leaks=0", "UBSAN_OPTIONS": "print_stacktrace=1"}
-    out = _run(os.path.join(SIMT, "_build", "libbl_simt_asan.so"), ["small:0-10:3"], env)
+    out = _run(os.path.join(SIMT, "_build", "libbl_simt_asan.so"), ["small:0-10:3", "grammar:0-6:20"], env)
     assert "ERROR: AddressSanitizer" not in out and "runtime error" not in out
