@@ -160,7 +160,7 @@ void bl_params_default(bl_params *p) {
 }
 
 int bl_create(int device, int max_slots, int max_rows, int vocab, bl_ctx **out) {
-  if (!out || max_slots <= 0 || max_rows <= 0 || vocab <= 0)
+  if (!out || max_slots <= 0 || max_rows <= 0 || vocab <= 0 || vocab > BL_MAX_CHUNKS * BL_CH)
     return fail(BL_EPARAM, "bl_create: invalid sizes (slots %d, rows %d, vocab %d)", max_slots, max_rows, vocab);
   bl_ctx *c = new bl_ctx;
   c->device = device;
@@ -339,7 +339,7 @@ static int configure(const bl_ctx *c, const bl_params *p, bl_slot_dev &s) {
   if (p->temperature > 0.0f && p->dynatemp_range > 0.0f)
     return fail(BL_EUNSUPPORTED, "dynamic temperature is not supported on the device");
   if (p->post_sampling_probs) return fail(BL_EUNSUPPORTED, "post_sampling_probs is not supported on the device");
-  if (k > BL_KSEL_MAX || c->d.nc * k > BL_LDS_SORT)
+  if (k > BL_KSEL_MAX)
     return fail(BL_EUNSUPPORTED, "top_k/n_probs of %d exceeds the device selection limit", k);
   if (p->repeat_last_n > BL_WCAP) return fail(BL_EUNSUPPORTED, "repeat_last_n above %d", BL_WCAP);
   return BL_OK;

@@ -143,6 +143,26 @@ __device__ __forceinline__ double bl_wave_excl_scan_d(double x, int lane) {
   return inc - x;
 }
 
+/* composed pair of NT consecutive terms at binade e, folded in order by one thread */
+template <int NT>
+__device__ __forceinline__ bl_inc bl_thread_compose(const float *a, int e) {
+  if (e < BL_E_MIN) return bl_inc{BL_SAT, BL_SAT};
+  bl_inc f = bl_inc_ident();
+#pragma unroll
+  for (int k = 0; k < NT; k++) f = bl_compose(f, bl_term_inc(a[k], e));
+  return f;
+}
+
+/* ordered composition across the 4 lanes of a quad (lanes 4q..4q+3 hold consecutive runs); the
+ * result is valid in every lane of the quad */
+__device__ __forceinline__ bl_inc bl_quad_compose(bl_inc f, int lane) {
+  bl_inc o = bl_inc{(uint32_t)__shfl_xor((int)f.d0, 1, 64), (uint32_t)__shfl_xor((int)f.d1, 1, 64)};
+  f = (lane & 1) ? bl_compose(o, f) : bl_compose(f, o);
+  o = bl_inc{(uint32_t)__shfl_xor((int)f.d0, 2, 64), (uint32_t)__shfl_xor((int)f.d1, 2, 64)};
+  f = (lane & 2) ? bl_compose(o, f) : bl_compose(f, o);
+  return f;
+}
+
 /*
  * Phase A for one group, executed by a whole wavefront: `a` is this lane's term (0 beyond the end),
  * `approx_start` the approximate sum before the group. Returns the record (valid in every lane).

@@ -28,6 +28,7 @@
 #define BL_KSEL_MAX 256     /* largest per-chunk candidate count (top_k / n_probs) */
 #define BL_WCAP 8192        /* repeat window ring capacity */
 #define BL_LDS_SORT 4096    /* candidate lists sorted in LDS up to this size */
+#define BL_MAX_CHUNKS 1024  /* vocabulary up to BL_MAX_CHUNKS * BL_CH tokens */
 
 /* per-token flags */
 #define BL_TF_BIAS 1u

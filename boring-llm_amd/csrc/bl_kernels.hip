@@ -75,6 +75,73 @@ __device__ double block_sum_d(double x, double *sd) {
   return r;
 }
 
+/*
+ * Histogram bin search from the top over bins [0, nb) (nb a multiple of NT): res[0] = the bin b where
+ * the count of keys in bins >= b first reaches `need`, res[1] = the count in bins above b, res[2] = the
+ * count in b, res[3] = the total (res[0..2] = 0, total, 0 when the total is below `need`). Thread t
+ * owns the nb/NT consecutive bins ending at nb - t*nb/NT.
+ */
+template <int NT>
+__device__ void block_find_bin(const uint32_t *hist, int nb, uint32_t need, uint32_t *res, uint32_t *wsum) {
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int per = nb / NT;
+  uint32_t local = 0u;
+  for (int q = 0; q < per; q++) local += hist[nb - 1 - (t * per + q)];
+  uint32_t inc = local;
+#pragma unroll
+  for (int k = 1; k < 64; k <<= 1) {
+    uint32_t o = __shfl_up(inc, k, 64);
+    if (lane >= k) inc += o;
+  }
+  if (lane == 63) wsum[w] = inc;
+  __syncthreads();
+  uint32_t above = inc - local, total = 0u;
+  for (int k = 0; k < NT / 64; k++) {
+    if (k < w) above += wsum[k];
+    total += wsum[k];
+  }
+  if (t == 0) {
+    res[3] = total;
+    if (total < need) {
+      res[0] = 0u;
+      res[1] = total;
+      res[2] = 0u;
+    }
+  }
+  if (above < need && above + local >= need) {
+    uint32_t acc = above;
+    for (int q = 0; q < per; q++) {
+      const int b = nb - 1 - (t * per + q);
+      const uint32_t h = hist[b];
+      if (acc + h >= need) {
+        res[0] = (uint32_t)b;
+        res[1] = acc;
+        res[2] = h;
+        break;
+      }
+      acc += h;
+    }
+  }
+  __syncthreads();
+}
+
+/* exclusive scan of a double over the block (NT threads); returns this thread's prefix, *total */
+template <int NT>
+__device__ double block_excl_scan_d(double x, double *sd, double *total) {
+  int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  double ex = bl_wave_excl_scan_d(x, lane);
+  if (lane == 63) sd[w] = ex + x;
+  __syncthreads();
+  double base = 0.0, tot = 0.0;
+  for (int k = 0; k < NT / 64; k++) {
+    if (k < w) base += sd[k];
+    tot += sd[k];
+  }
+  __syncthreads();
+  *total = tot;
+  return base + ex;
+}
+
 /* ------------------------------------------------------------------ K1: row pass */
 __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass(bl_dev d, const float *__restrict__ logits, int64_t ld,
                                                               bl_rows rows) {
@@ -315,63 +382,85 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_exppass(bl_dev d, bl_rows 
   const bl_slot_dev &sp = slot_of(d, slot);
   const int mode = sp.mode;
   if (!(mode & (BL_M_LOGPROBS | BL_M_FULL))) return;
-  __shared__ float xs[BL_CH];
-  __shared__ double gs[64];
   __shared__ float red_m[4];
   __shared__ int red_i[4];
+  __shared__ double red_d[4];
   const int i0 = c * BL_CH;
   const int cnt = min(BL_CH, V - i0);
-  const float *src = d.eff + (int64_t)row * V + i0;
-  for (int i = t; i < BL_CH; i += BL_RP_THREADS) xs[i] = i < cnt ? src[i] : BL_NEG_INF;
-  const float M = row_max(d, row, red_m, red_i); /* includes the barrier that publishes xs */
+  /* this thread's 16 consecutive values (a wavefront reads 4 KB contiguously) */
+  const int j0 = t * 16;
+  float x[16];
+  const float *src = d.eff + (int64_t)row * V + i0 + j0;
+  if (j0 + 16 <= cnt && (((uintptr_t)src) & 15) == 0) {
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      float4 v = reinterpret_cast<const float4 *>(src)[q];
+      x[4 * q] = v.x;
+      x[4 * q + 1] = v.y;
+      x[4 * q + 2] = v.z;
+      x[4 * q + 3] = v.w;
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < 16; k++) x[k] = j0 + k < cnt ? src[k] : BL_NEG_INF;
+  }
+  const float M = row_max(d, row, red_m, red_i);
 
   if (mode & BL_M_LOGPROBS) {
-    /* approximate sum before this chunk, from the row pass statistics */
-    double S0 = 0.0;
-    if (t == 0)
-      for (int k = 0; k < c; k++) {
-        float cm = d.c_max[(int64_t)row * nc + k];
-        if (cm > BL_NEG_INF) S0 += (double)d.c_sum[(int64_t)row * nc + k] * exp((double)cm - (double)M);
-      }
-    /* group sums (approximate) */
-    for (int g = w; g < 64; g += BL_RP_THREADS / 64) {
-      int i = g * 64 + lane;
-      float a = i < cnt ? bl_expf(xs[i] - M) : 0.0f;
-      double sg = bl_wave_sum_d((double)a);
-      if (lane == 0) gs[g] = sg;
+    /* approximate sum of the chunks before this one, from the row pass statistics */
+    double part = 0.0;
+    for (int k = t; k < c; k += BL_RP_THREADS) {
+      float cm = d.c_max[(int64_t)row * nc + k];
+      if (cm > BL_NEG_INF) part += (double)d.c_sum[(int64_t)row * nc + k] * exp((double)cm - (double)M);
     }
-    __shared__ double s0s;
-    if (t == 0) s0s = S0;
-    __syncthreads();
-    if (w == 0) {
-      double v = gs[lane];
-      double ex = bl_wave_excl_scan_d(v, lane);
-      gs[lane] = s0s + ex;
+    const double S0 = block_sum_d<BL_RP_THREADS>(part, red_d);
+    float a[16];
+    double sa = 0.0;
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+      a[k] = j0 + k < cnt ? bl_expf(x[k] - M) : 0.0f;
+      sa += (double)a[k];
     }
-    __syncthreads();
+    double tot;
+    const double before = S0 + block_excl_scan_d<BL_RP_THREADS>(sa, red_d, &tot);
+    /* group of 64 terms = 4 threads; its approximate start is its first thread's prefix */
+    const double gstart = __shfl(before, lane & ~3, 64);
+    bl_grec r;
+    r.E = bl_binade_of(gstart);
+    r.pad = 0;
+#pragma unroll
+    for (int k = 0; k < 3; k++) r.v[k] = bl_quad_compose(bl_thread_compose<16>(a, r.E - 1 + k), lane);
     bl_grec *rec = reinterpret_cast<bl_grec *>(d.grec) + (int64_t)row * 2 * (V / 64 + 64) + (int64_t)c * 64;
-    for (int g = w; g < 64; g += BL_RP_THREADS / 64) {
-      if (i0 + g * 64 >= V) break;
-      int i = g * 64 + lane;
-      float a = i < cnt ? bl_expf(xs[i] - M) : 0.0f;
-      bl_grec r = bl_group_record(a, gs[g], lane);
-      if (lane == 0) rec[g] = r;
-    }
+    if ((lane & 3) == 0 && j0 < cnt) rec[t >> 2] = r;
   }
   if (mode & BL_M_FULL) {
-    float T = sp.temperature;
-    float span = 17.5f * (T > 1.0f ? T : 1.0f);
-    float thr = M - span;
-    for (int i = t; i < cnt; i += BL_RP_THREADS) {
-      float x = xs[i];
-      if (x >= thr) {
-        int pos = atomicAdd(&d.full_n[row], 1);
-        if (pos < V) {
-          d.full_v[(int64_t)row * V + pos] = x;
-          d.full_i[(int64_t)row * V + pos] = i0 + i;
-        }
-      }
+    /* candidates of a full-vocabulary rank: every value within 17.5*max(T,1) of the maximum; one
+     * atomic per wavefront reserves the wavefront's slots */
+    const float T = sp.temperature;
+    const float thr = M - 17.5f * (T > 1.0f ? T : 1.0f);
+    int mine = 0;
+#pragma unroll
+    for (int k = 0; k < 16; k++) mine += (j0 + k < cnt && x[k] >= thr) ? 1 : 0;
+    int incl = mine;
+#pragma unroll
+    for (int k = 1; k < 64; k <<= 1) {
+      int o = __shfl_up(incl, k, 64);
+      if (lane >= k) incl += o;
     }
+    const int wtot = __shfl(incl, 63, 64);
+    int base = 0;
+    if (lane == 0 && wtot > 0) base = atomicAdd(&d.full_n[row], wtot);
+    base = __shfl(base, 0, 64);
+    int pos = base + incl - mine;
+#pragma unroll
+    for (int k = 0; k < 16; k++)
+      if (j0 + k < cnt && x[k] >= thr) {
+        if (pos < V) {
+          d.full_v[(int64_t)row * V + pos] = x[k];
+          d.full_i[(int64_t)row * V + pos] = i0 + j0 + k;
+        }
+        pos++;
+      }
   }
 }
 
@@ -516,6 +605,13 @@ __device__ void block_records(int64_t n, TermF term, bl_grec *recs, double *gsum
 }
 
 struct sel_shared {
+  uint64_t topk[BL_KSEL_MAX];      /* ranked top-K before it moves to keys[0..K) */
+  uint64_t cmin[BL_MAX_CHUNKS];    /* smallest emitted key per chunk */
+  int ccnt[BL_MAX_CHUNKS];         /* emitted keys per chunk */
+  uint64_t tau;
+  uint32_t ucnt;
+  uint32_t fres_u[4];              /* block_find_bin result */
+  uint32_t wsum[SEL_NW];
   uint64_t keys[BL_LDS_SORT];
   bl_grec recs[BL_LDS_SORT / 64];
   double gsum[BL_LDS_SORT / 64];
@@ -661,25 +757,103 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
     __syncthreads();
   }
 
-  /* merged top-K candidates of the row pass: sorted (value desc, index asc) in sh.keys */
+  /* merged top-K candidates of the row pass: sorted (value desc, index asc) in sh.keys[0..K) */
   int n_top = 0;
   const int K = sp.k_sel;
   if (K > 0) {
-    int total = nc * K;
-    int P = 1;
-    while (P < total) P <<= 1;
-    for (int i = t; i < P; i += BL_SEL_THREADS) {
-      uint64_t k = 0ull;
-      if (i < total) {
-        int ch = i / K, q = i % K;
-        int64_t o = ((int64_t)row * nc + ch) * BL_KSEL_MAX + q;
-        int32_t id = d.cand_i[o];
-        if (id >= 0) k = ckey(d.cand_v[o], id);
-      }
-      sh.keys[i] = k;
+    /* each chunk emitted its top K (fewer only when it holds fewer valid values), so the row's K-th key
+     * is at least tau = the largest K-th key of a full chunk: only keys >= tau can rank below K */
+    const int total = nc * K;
+    for (int ch = t; ch < nc; ch += BL_SEL_THREADS) {
+      sh.cmin[ch] = ~0ull;
+      sh.ccnt[ch] = 0;
+    }
+    if (t == 0) {
+      sh.ucnt = 0u;
+      sh.tau = 0ull;
     }
     __syncthreads();
-    bitonic_desc(sh.keys, P);
+    for (int i = t; i < total; i += BL_SEL_THREADS) {
+      const int ch = i / K, q = i - ch * K;
+      const int64_t o = ((int64_t)row * nc + ch) * BL_KSEL_MAX + q;
+      const int32_t id = d.cand_i[o];
+      if (id >= 0) {
+        atomicMin(&sh.cmin[ch], ckey(d.cand_v[o], id));
+        atomicAdd(&sh.ccnt[ch], 1);
+      }
+    }
+    __syncthreads();
+    for (int ch = t; ch < nc; ch += BL_SEL_THREADS)
+      if (sh.ccnt[ch] == K) atomicMax(&sh.tau, sh.cmin[ch]);
+    __syncthreads();
+    const uint64_t tau = sh.tau;
+    auto cand_key = [&](int i, uint64_t &k) -> bool {
+      const int ch = i / K, q = i - ch * K;
+      const int64_t o = ((int64_t)row * nc + ch) * BL_KSEL_MAX + q;
+      const int32_t id = d.cand_i[o];
+      if (id < 0) return false;
+      k = ckey(d.cand_v[o], id);
+      return k >= tau;
+    };
+    for (int i = t; i < total; i += BL_SEL_THREADS) {
+      uint64_t k;
+      if (cand_key(i, k)) atomicAdd(&sh.ucnt, 1u);
+    }
+    __syncthreads();
+    /* lower bound of the kept keys: tau, or, when too many keys reach tau, the K-th largest value
+     * found by a radix selection over the value bits (12 + 10 + 10) of those keys */
+    uint64_t lo = tau;
+    if (sh.ucnt > (uint32_t)BL_LDS_SORT) {
+      uint32_t *hist = reinterpret_cast<uint32_t *>(sh.keys); /* 4096 bins, the list is not built yet */
+      uint32_t prefix = 0u, pmask = 0u;
+      int need = K;
+      for (int pass = 0; pass < 3; pass++) {
+        const int shift = pass == 0 ? 20 : (pass == 1 ? 10 : 0);
+        const int nb = pass == 0 ? 4096 : 1024;
+        __syncthreads();
+        for (int b = t; b < nb; b += BL_SEL_THREADS) hist[b] = 0u;
+        __syncthreads();
+        for (int i = t; i < total; i += BL_SEL_THREADS) {
+          uint64_t k;
+          if (cand_key(i, k)) {
+            const uint32_t f = (uint32_t)(k >> 32);
+            if ((f & pmask) == prefix) atomicAdd(&hist[(f >> shift) & (uint32_t)(nb - 1)], 1u);
+          }
+        }
+        __syncthreads();
+        block_find_bin<BL_SEL_THREADS>(hist, nb, (uint32_t)need, sh.fres_u, sh.wsum);
+        prefix |= sh.fres_u[0] << shift;
+        pmask |= (uint32_t)(nb - 1) << shift;
+        need -= (int)sh.fres_u[1];
+      }
+      lo = (uint64_t)prefix << 32; /* every key of value >= the K-th value (ties carry the index) */
+      __syncthreads();
+    }
+    if (t == 0) sh.ucnt = 0u;
+    __syncthreads();
+    for (int i = t; i < total; i += BL_SEL_THREADS) {
+      uint64_t k;
+      if (cand_key(i, k) && k >= lo) {
+        const uint32_t pos = atomicAdd(&sh.ucnt, 1u);
+        if (pos < BL_LDS_SORT) sh.keys[pos] = k;
+      }
+    }
+    __syncthreads();
+    int ns = (int)sh.ucnt;
+    if (ns > BL_LDS_SORT) {
+      status |= BL_SE_CAND_FULL;
+      ns = BL_LDS_SORT;
+    }
+    /* rank by counting (keys are distinct: they carry the index) */
+    for (int i = t; i < ns; i += BL_SEL_THREADS) {
+      const uint64_t k = sh.keys[i];
+      int r = 0;
+      for (int j = 0; j < ns; j++) r += sh.keys[j] > k ? 1 : 0;
+      if (r < K) sh.topk[r] = k;
+    }
+    __syncthreads();
+    for (int q = t; q < K; q += BL_SEL_THREADS) sh.keys[q] = q < ns ? sh.topk[q] : 0ull;
+    __syncthreads();
     n_top = K;
   }
 

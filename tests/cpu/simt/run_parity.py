@@ -8,7 +8,7 @@ alone) and checks the workloads the GPU parity tests check, at reduced step coun
     python run_parity.py --lib _build/libbl_simt.so small:0-10:25 w2:2 w4:1:8 w5:1 async:2
 
 Items: small:<cases>:<steps>, w2:<steps>, w3:<steps>, w4:<steps>:<rows>, w5:<steps>, async:<steps>,
-grammar:<cases>:<steps>.
+grammar:<cases>:<steps>, bigk:<steps>.
 Prints one line per item ("ok ..." / "FAIL ...") and exits 1 if any failed.
 """
 import argparse
@@ -216,6 +216,38 @@ def run_async(BL, steps):
     return None
 
 
+def run_bigk(BL, steps):
+    """top_k 250 and 256 logprob alternatives at V=151936: 38 chunks x 256 candidates per row."""
+    V, seed = 151936, 11
+    kw = dict(temperature=0.9, top_k=250, top_p=0.95, logprobs=1, n_probs=256, frequency_penalty=0.2)
+    L = O.lib()
+    L.orc_set_eog_tokens(O.ip(O.i32([0])), 0, -1)
+    reply = [int(x) for x in np.random.default_rng(seed).integers(0, V, 64)]
+    op = O.params(**kw)
+    rr = O.i32(reply)
+    h = L.orc_slot_new(O.C.byref(op), BL.seed_rng(seed), O.ip(rr), len(reply), O.ip(rr), len(reply), None, None, 0)
+    ctx = BL.Context(V, 1, 1)
+    ctx.slot_reset(0, BL.Params(**kw), BL.seed_rng(seed), history=reply, reply=reply)
+    buf = MEM.zeros(V, np.float32)
+    try:
+        for t in range(steps):
+            ctx.synth_logits(buf.ptr, V, 2, seed, t, 1, V)
+            x = buf.host()
+            tok, lp, ti, tl = ctx.sample_step([0], buf.ptr, V, top_stride=256)
+            ot, olp = np.zeros(1, np.int32), np.zeros(1, np.float32)
+            oti, otl = np.zeros(256, np.int32), np.zeros(256, np.float32)
+            eg = O.C.c_int()
+            assert L.orc_slot_step(h, O.fp(x), V, 1, 1, O.ip(ot), O.fp(olp), O.ip(oti), O.fp(otl), O.C.byref(eg)) == 0
+            if tok[0] != ot[0] or not lp_close(lp[0], olp[0]):
+                return f"step {t}: token {tok[0]} vs {ot[0]}, logprob {lp[0]} vs {olp[0]}"
+            if ti[0] != list(oti) or not all(lp_close(tl[0][q], otl[q]) for q in range(256)):
+                return f"step {t}: alternatives differ"
+    finally:
+        L.orc_slot_free(h)
+        ctx.close()
+    return None
+
+
 GOLDEN = os.path.join(ROOT, "tests", "golden")
 
 
@@ -397,6 +429,8 @@ def main():
             results.append(("workload 5", run_w5(BL, int(f[1]))))
         elif kind == "async":
             results.append(("asynchronous step", run_async(BL, int(f[1]))))
+        elif kind == "bigk":
+            results.append(("large top-k / n_probs", run_bigk(BL, int(f[1]))))
         elif kind == "w3":
             results.append(("workload 3", run_w3(BL, int(f[1]))))
         elif kind == "grammar":

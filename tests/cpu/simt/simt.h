@@ -123,14 +123,22 @@ inline T atomicAdd(T *p, T v) {
   *p = o + v;
   return o;
 }
-inline int atomicOr(int *p, int v) {
-  int o = *p;
+template <class T>
+inline T atomicOr(T *p, T v) {
+  T o = *p;
   *p = o | v;
   return o;
 }
-inline int atomicMin(int *p, int v) {
-  int o = *p;
+template <class T>
+inline T atomicMin(T *p, T v) {
+  T o = *p;
   *p = std::min(o, v);
+  return o;
+}
+template <class T>
+inline T atomicMax(T *p, T v) {
+  T o = *p;
+  *p = std::max(o, v);
   return o;
 }
 

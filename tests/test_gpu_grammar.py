@@ -22,36 +22,11 @@ import _oracle as O  # noqa: E402
 
 sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "cpu", "simt"))
 import run_parity as RP  # noqa: E402
+from _devmem import TorchMem  # noqa: E402
 
 
 def say(*a):
     print(*a, flush=True)
-
-
-class TorchMem:
-    """Harness buffers in device memory; transfers synchronise the device."""
-
-    _types = {np.float32: torch.float32, np.int32: torch.int32, np.uint32: torch.int32}
-
-    class Buf:
-        def __init__(self, n, dtype):
-            self.dtype = np.dtype(dtype)
-            self.t = torch.zeros(n, dtype=TorchMem._types[self.dtype.type], device="cuda:0")
-            self.ptr = self.t.data_ptr()
-
-        def upload(self, x):
-            a = np.ascontiguousarray(x, dtype=self.dtype)
-            if self.dtype == np.uint32:
-                a = a.view(np.int32)
-            self.t.copy_(torch.from_numpy(a))
-            torch.cuda.synchronize()
-
-        def host(self):
-            torch.cuda.synchronize()
-            return self.t.cpu().numpy().view(self.dtype)
-
-    def zeros(self, n, dtype):
-        return self.Buf(n, dtype)
 
 
 @pytest.fixture(scope="module", autouse=True)

@@ -1,0 +1,37 @@
+"""GPU parity of kernel paths beyond the fixed workloads, through the shared harness with device buffers:
+top_k 250 with 256 logprob alternatives at V=151936 (38 chunks x 256 candidates per row, the merged
+list found by radix selection), and the bound-rows asynchronous step against the synchronous one."""
+import os
+import sys
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+import bl_select as BL  # noqa: E402
+
+sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "cpu", "simt"))
+import run_parity as RP  # noqa: E402
+from _devmem import TorchMem  # noqa: E402
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device_memory():
+    assert torch.cuda.is_available(), "a GPU test ran without a GPU"
+    old = RP.MEM
+    RP.MEM = TorchMem()
+    yield
+    RP.MEM = old
+
+
+def test_large_top_k_and_alternatives():
+    print("top_k 250, n_probs 256, V=151936: 20 steps", flush=True)
+    err = RP.run_bigk(BL, 20)
+    assert err is None, err
+
+
+def test_async_step_equals_sync():
+    print("bound rows, asynchronous step: 4 steps", flush=True)
+    err = RP.run_async(BL, 4)
+    assert err is None, err
