@@ -611,6 +611,8 @@ struct sel_shared {
   uint64_t tau;
   uint32_t ucnt;
   uint32_t fres_u[4];              /* block_find_bin result */
+  float ser_e[BL_SERIAL_MAX];      /* short-list terms exp(v - v0) */
+  float ser_r[BL_SERIAL_MAX];      /* short-list terms exp((v - v0) / T) */
   uint32_t wsum[SEL_NW];
   uint64_t keys[BL_LDS_SORT];
   bl_grec recs[BL_LDS_SORT / 64];
@@ -640,6 +642,85 @@ __device__ int sample_ranked(const bl_slot_dev &sp, ValF val, int64_t n_list, in
     return -1;
   }
   const float v0 = val(0);
+  if (n_list <= BL_SERIAL_MAX) {
+    /* short list: the terms in parallel, then the reference's sequential float32 loops on one lane */
+    const bool filt = sp.top_p < 1.0f || sp.min_p > 0.0f;
+    for (int j = t; j < n_list; j += BL_SEL_THREADS) {
+      const float x = val(j);
+      sh.ser_e[j] = filt ? bl_expf(x - v0) : 0.0f;
+      const float dd = x - v0;
+      const float q = dd / T;
+      sh.ser_r[j] = bl_expf(q);
+    }
+    __syncthreads();
+    if (t == 0) {
+      const int n = (int)n_list;
+      int64_t cut = n_logical;
+      bool unsup = false;
+      if (filt) {
+        float sum_exp = 0.0f;
+        for (int j = 0; j < n; j++) sum_exp += sh.ser_e[j];
+        if (sp.top_p < 1.0f) {
+          float cum = 0.0f;
+          for (int j = 0; j < n; j++) {
+            cum += sh.ser_e[j] / sum_exp;
+            if (j >= keep - 1 && cum >= sp.top_p) {
+              cut = j + 1;
+              break;
+            }
+          }
+        }
+        if (sp.min_p > 0.0f) {
+          const float p0 = sh.ser_e[0] / sum_exp;
+          const float threshold = p0 * sp.min_p;
+          const int64_t lim = cut < n ? cut : n;
+          int64_t first_small = -1;
+          for (int64_t j = keep; j < lim; j++)
+            if (sh.ser_e[j] / sum_exp < threshold) {
+              first_small = j;
+              break;
+            }
+          if (first_small < 0) {
+            if (lim < cut) {
+              /* the next, unmaterialised candidate is below 2^-25 of the top one */
+              if (threshold <= p0 * 5.9604645e-8f) unsup = true;
+              first_small = lim;
+            } else {
+              first_small = cut;
+            }
+          }
+          cut = keep > first_small ? keep : first_small;
+        }
+      }
+      const int n_eff = (int)(cut < n ? cut : n);
+      float S = 0.0f;
+      for (int j = 0; j < n_eff; j++) S += sh.ser_r[j];
+      uint64_t st = rng;
+      for (int k = 0; k < rng_skip; k++) st = bl_xorshift(st);
+      const float target = bl_rng_f32(&st) * S;
+      float run = 0.0f;
+      int64_t f = -1;
+      for (int j = 0; j < n_eff; j++) {
+        run += sh.ser_r[j];
+        if (run >= target) {
+          f = j;
+          break;
+        }
+      }
+      sh.ires[2] = unsup ? -2 : (int)(f >= 0 ? f : cut - 1);
+      *reinterpret_cast<uint64_t *>(&sh.fres[2]) = st;
+    }
+    __syncthreads();
+    const int chosen = sh.ires[2];
+    const uint64_t st = *reinterpret_cast<uint64_t *>(&sh.fres[2]);
+    __syncthreads();
+    if (chosen == -2 || chosen >= n_list) {
+      status |= BL_SE_UNSUPPORTED;
+      return -1;
+    }
+    rng = st;
+    return chosen;
+  }
   int64_t cutoff = n_logical;
   if (sp.top_p < 1.0f || sp.min_p > 0.0f) {
     auto termE = [&](int64_t j) { return bl_expf(val(j) - v0); };
@@ -803,7 +884,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
     /* lower bound of the kept keys: tau, or, when too many keys reach tau, the K-th largest value
      * found by a radix selection over the value bits (12 + 10 + 10) of those keys */
     uint64_t lo = tau;
-    if (sh.ucnt > (uint32_t)BL_LDS_SORT) {
+    if (sh.ucnt > (uint32_t)(2 * K > 512 ? 2 * K : 512)) {
       uint32_t *hist = reinterpret_cast<uint32_t *>(sh.keys); /* 4096 bins, the list is not built yet */
       uint32_t prefix = 0u, pmask = 0u;
       int need = K;
@@ -844,11 +925,15 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
       status |= BL_SE_CAND_FULL;
       ns = BL_LDS_SORT;
     }
-    /* rank by counting (keys are distinct: they carry the index) */
+    /* rank by counting (keys are distinct: they carry the index); four independent reads per step */
     for (int i = t; i < ns; i += BL_SEL_THREADS) {
       const uint64_t k = sh.keys[i];
-      int r = 0;
-      for (int j = 0; j < ns; j++) r += sh.keys[j] > k ? 1 : 0;
+      int r = 0, j = 0;
+      for (; j + 4 <= ns; j += 4) {
+        const uint64_t a0 = sh.keys[j], a1 = sh.keys[j + 1], a2 = sh.keys[j + 2], a3 = sh.keys[j + 3];
+        r += (a0 > k ? 1 : 0) + (a1 > k ? 1 : 0) + (a2 > k ? 1 : 0) + (a3 > k ? 1 : 0);
+      }
+      for (; j < ns; j++) r += sh.keys[j] > k ? 1 : 0;
       if (r < K) sh.topk[r] = k;
     }
     __syncthreads();
