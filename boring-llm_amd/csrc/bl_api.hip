@@ -210,6 +210,7 @@ int bl_create(int device, int max_slots, int max_rows, int vocab, bl_ctx **out) 
   ALLOC(d.full_n, R);
   ALLOC(d.sortk, R * std::max(P2, 2 * V));
   ALLOC(d.gsum, R * G);
+  ALLOC(d.gapx, R * G);
   d.gm_blocks = (vocab + BL_GM_THREADS - 1) / BL_GM_THREADS;
   ALLOC(d.gram, S);
   ALLOC(d.gmask, R * 2 * ((V + 63) / 64));

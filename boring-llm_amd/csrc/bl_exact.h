@@ -116,17 +116,50 @@ __device__ __forceinline__ bl_inc bl_shfl_up(bl_inc v, int k) {
 __device__ __forceinline__ bl_inc bl_shfl(bl_inc v, int l) {
   return bl_inc{(uint32_t)__shfl((int)v.d0, l, 64), (uint32_t)__shfl((int)v.d1, l, 64)};
 }
-/* inclusive ordered scan of composition across the wavefront */
+/* DPP move (gfx9 data-parallel primitives): lanes enabled by row_mask read lane `ctrl` selects,
+ * others keep `old` */
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint32_t bl_dpp(uint32_t old, uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)v, CTRL, ROW_MASK, 0xF, false);
+}
+#define BL_DPP_ROW_SHR(k) (0x110 + (k))
+#define BL_DPP_ROW_BCAST15 0x142
+#define BL_DPP_ROW_BCAST31 0x143
+
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ bl_inc bl_dpp_inc(bl_inc f) {
+  return bl_inc{bl_dpp<CTRL, ROW_MASK>(0u, f.d0), bl_dpp<CTRL, ROW_MASK>(0u, f.d1)};
+}
+
+/* inclusive ordered scan of composition across the wavefront: shifts within 16-lane rows, then the
+ * row broadcasts of lane 15 (to rows 1, 3) and lane 31 (to rows 2, 3); all in VALU, no LDS */
 __device__ __forceinline__ bl_inc bl_wave_scan(bl_inc f, int lane) {
-#pragma unroll
-  for (int k = 1; k < 64; k <<= 1) {
-    bl_inc o = bl_shfl_up(f, k);
-    if (lane >= k) f = bl_compose(o, f);
-  }
+  const int r = lane & 15;
+  bl_inc o;
+  o = bl_dpp_inc<BL_DPP_ROW_SHR(1), 0xF>(f);
+  if (r >= 1) f = bl_compose(o, f);
+  o = bl_dpp_inc<BL_DPP_ROW_SHR(2), 0xF>(f);
+  if (r >= 2) f = bl_compose(o, f);
+  o = bl_dpp_inc<BL_DPP_ROW_SHR(4), 0xF>(f);
+  if (r >= 4) f = bl_compose(o, f);
+  o = bl_dpp_inc<BL_DPP_ROW_SHR(8), 0xF>(f);
+  if (r >= 8) f = bl_compose(o, f);
+  o = bl_dpp_inc<BL_DPP_ROW_BCAST15, 0xA>(f);
+  if (lane & 16) f = bl_compose(o, f);
+  o = bl_dpp_inc<BL_DPP_ROW_BCAST31, 0xC>(f);
+  if (lane >= 32) f = bl_compose(o, f);
   return f;
 }
+/* value of lane l (wave-uniform) in every lane */
+__device__ __forceinline__ uint32_t bl_bcast(uint32_t v, int l) { return (uint32_t)__builtin_amdgcn_readlane((int)v, l); }
+__device__ __forceinline__ float bl_bcastf(float v, int l) { return bl_u2f(bl_bcast(bl_f2u(v), l)); }
+
+/* lane 63's value of a composed scan, in every lane */
+__device__ __forceinline__ bl_inc bl_lane63(bl_inc f) {
+  return bl_inc{(uint32_t)__builtin_amdgcn_readlane((int)f.d0, 63), (uint32_t)__builtin_amdgcn_readlane((int)f.d1, 63)};
+}
 /* ordered reduction; result valid in every lane */
-__device__ __forceinline__ bl_inc bl_wave_reduce(bl_inc f, int lane) { return bl_shfl(bl_wave_scan(f, lane), 63); }
+__device__ __forceinline__ bl_inc bl_wave_reduce(bl_inc f, int lane) { return bl_lane63(bl_wave_scan(f, lane)); }
 
 __device__ __forceinline__ double bl_wave_sum_d(double x) {
 #pragma unroll
@@ -212,7 +245,7 @@ __device__ int bl_seq_walk(int64_t n, TermF term, RecF rec, bool thr_on, float t
     unsigned long long m = __ballot(bad);
     int first = m ? __ffsll((long long)m) - 1 : 64;
     if (first > 0) {
-      N = (uint32_t)__shfl((int)Nend, first - 1, 64);
+      N = bl_bcast(Nend, first - 1);
       g += first;
     }
     if (g >= G) break;
@@ -232,17 +265,17 @@ __device__ int bl_seq_walk(int64_t n, TermF term, RecF rec, bool thr_on, float t
       bool reach = act && !cross && thr_on && j >= min_idx && bl_make(e, Ne) >= thr;
       unsigned long long ms = __ballot(cross || reach);
       if (!ms) {
-        N = (uint32_t)__shfl((int)Ne, 63, 64);
+        N = bl_bcast(Ne, 63);
         break;
       }
       int c = __ffsll((long long)ms) - 1;
-      uint32_t Nbefore = c > start ? (uint32_t)__shfl((int)Ne, c - 1, 64) : N;
-      bool c_reach = __shfl((int)reach, c, 64) != 0;
+      uint32_t Nbefore = c > start ? bl_bcast(Ne, c - 1) : N;
+      bool c_reach = bl_bcast(reach ? 1u : 0u, c) != 0u;
       if (c_reach) {
-        S_out = bl_make(e, (uint32_t)__shfl((int)Ne, c, 64));
+        S_out = bl_make(e, bl_bcast(Ne, c));
         return (int)(j0 + c);
       }
-      float ac = __shfl(a, c, 64);
+      float ac = bl_bcastf(a, c);
       float Sn = bl_make(e, Nbefore) + ac; /* the one real float add at a binade crossing */
       bl_split(Sn, e, N);
       if (thr_on && j0 + c >= min_idx && Sn >= thr) {

@@ -431,7 +431,12 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_exppass(bl_dev d, bl_rows 
 #pragma unroll
     for (int k = 0; k < 3; k++) r.v[k] = bl_quad_compose(bl_thread_compose<16>(a, r.E - 1 + k), lane);
     bl_grec *rec = reinterpret_cast<bl_grec *>(d.grec) + (int64_t)row * 2 * (V / 64 + 64) + (int64_t)c * 64;
-    if ((lane & 3) == 0 && j0 < cnt) rec[t >> 2] = r;
+    float *apx = d.gapx + (int64_t)row * (V / 64 + 64);
+    if ((lane & 3) == 0 && j0 < cnt) {
+      rec[t >> 2] = r;
+      apx[c * 64 + (t >> 2)] = (float)gstart;
+    }
+    if (c == nc - 1 && t == BL_RP_THREADS - 1) apx[(V + 63) / 64] = (float)(S0 + tot); /* the row's total */
   }
   if (mode & BL_M_FULL) {
     /* candidates of a full-vocabulary rank: every value within 17.5*max(T,1) of the maximum; one

@@ -99,12 +99,51 @@ inline unsigned long long simt_ballot(int pred) {
   simt::sync_wave();
   return m;
 }
+/* gfx9 DPP move: row_shr:1..15 (0x111..0x11f), row_bcast:15 (0x142), row_bcast:31 (0x143); lanes whose
+ * row (lane/16) is off in row_mask or bank ((lane%16)/4) off in bank_mask keep `old`; an enabled lane
+ * whose source is out of range reads 0 with bound_ctrl, else keeps `old` */
+inline int simt_update_dpp(int old, int src, int ctrl, int row_mask, int bank_mask, bool bound_ctrl) {
+  uint64_t *slots = simt::wave_slots();
+  const int lane = simt::lane_id();
+  slots[lane] = (uint32_t)src;
+  simt::sync_wave();
+  int out = old;
+  const int row = lane >> 4, bank = (lane & 15) >> 2;
+  if (((row_mask >> row) & 1) && ((bank_mask >> bank) & 1)) {
+    int srcl = -1;
+    if (ctrl >= 0x111 && ctrl <= 0x11f) {
+      const int k = ctrl - 0x110;
+      if ((lane & 15) >= k) srcl = lane - k;
+    } else if (ctrl == 0x142) {
+      if (row >= 1) srcl = row * 16 - 1;
+    } else if (ctrl == 0x143) {
+      if (row >= 2) srcl = 31;
+    } else {
+      abort(); /* a DPP control the emulator does not model */
+    }
+    if (srcl >= 0) out = (int)(uint32_t)slots[srcl];
+    else if (bound_ctrl) out = 0;
+  }
+  simt::sync_wave();
+  return out;
+}
+inline int simt_readlane(int v, int l) {
+  uint64_t *slots = simt::wave_slots();
+  slots[simt::lane_id()] = (uint32_t)v;
+  simt::sync_wave();
+  int r = (int)(uint32_t)slots[l & 63];
+  simt::sync_wave();
+  return r;
+}
+
 /* every wave operation names its call site: lanes of one wave meeting at different sites (a wave
  * operation in divergent code) abort the emulation */
 #define __shfl(...) (simt::wave_site(__FILE__, __LINE__), simt_shfl(__VA_ARGS__))
 #define __shfl_up(...) (simt::wave_site(__FILE__, __LINE__), simt_shfl_up(__VA_ARGS__))
 #define __shfl_xor(...) (simt::wave_site(__FILE__, __LINE__), simt_shfl_xor(__VA_ARGS__))
 #define __ballot(...) (simt::wave_site(__FILE__, __LINE__), simt_ballot(__VA_ARGS__))
+#define __builtin_amdgcn_update_dpp(...) (simt::wave_site(__FILE__, __LINE__), simt_update_dpp(__VA_ARGS__))
+#define __builtin_amdgcn_readlane(...) (simt::wave_site(__FILE__, __LINE__), simt_readlane(__VA_ARGS__))
 
 inline int __ffs(int x) { return ffs(x); }
 inline int __ffs(unsigned x) { return ffs((int)x); }
