@@ -39,6 +39,7 @@
 #define BL_N_TOP (1u << 24)
 #define BL_SAT (1u << 25)
 #define BL_E_MIN (-126)
+#define BL_E_NONE (-100000) /* no binade */
 
 struct bl_inc {
   uint32_t d0, d1;

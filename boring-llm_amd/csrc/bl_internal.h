@@ -30,6 +30,7 @@
 #define BL_LDS_SORT 4096    /* candidate lists sorted in LDS up to this size */
 #define BL_MAX_CHUNKS 1024  /* vocabulary up to BL_MAX_CHUNKS * BL_CH tokens */
 #define BL_SERIAL_MAX 512   /* candidate lists up to this length are summed by one lane */
+#define BL_CRIT_MAX 128     /* critical groups of the fast normaliser (their terms fill 32 KB of LDS) */
 
 /* per-token flags */
 #define BL_TF_BIAS 1u

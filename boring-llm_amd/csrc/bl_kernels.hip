@@ -616,6 +616,13 @@ struct sel_shared {
   uint64_t tau;
   uint32_t ucnt;
   uint32_t fres_u[4];              /* block_find_bin result */
+  int crit[BL_CRIT_MAX];           /* critical groups of the fast normaliser, ascending */
+  bl_inc run_f[BL_CRIT_MAX + 1];   /* composed runs between them */
+  int run_e[BL_CRIT_MAX + 1];      /* binade of each run (BL_E_NONE: not one binade) */
+  int run_n[BL_CRIT_MAX + 1];      /* groups in each run */
+  int cw[SEL_NW];
+  int ncrit;
+  float fast_s;
   float ser_e[BL_SERIAL_MAX];      /* short-list terms exp(v - v0) */
   float ser_r[BL_SERIAL_MAX];      /* short-list terms exp((v - v0) / T) */
   uint32_t wsum[SEL_NW];
@@ -808,6 +815,167 @@ __device__ int sample_ranked(const bl_slot_dev &sp, ValF val, int64_t n_list, in
   return chosen;
 }
 
+/* wavefront-level resolution of one 64-term group from state (e, N), crossing binades as needed
+ * (a real float add at each crossing); `a` is this lane's term, `in` whether it exists */
+__device__ __forceinline__ void elem_resolve(float a, bool in, int &e, uint32_t &N, int lane) {
+  int start = 0;
+  while (true) {
+    const bool act = in && lane >= start;
+    const bl_inc fe = act ? bl_term_inc(a, e) : bl_inc_ident();
+    const uint32_t Ne = bl_apply(bl_wave_scan(fe, lane), N);
+    const unsigned long long ms = __ballot(act && Ne >= BL_N_TOP);
+    if (!ms) {
+      N = bl_bcast(Ne, 63);
+      return;
+    }
+    const int c = __ffsll((long long)ms) - 1;
+    const uint32_t Nbefore = c > start ? bl_bcast(Ne, c - 1) : N;
+    const float Sn = bl_make(e, Nbefore) + bl_bcastf(a, c); /* the one real float add at a crossing */
+    bl_split(Sn, e, N);
+    start = c + 1;
+    if (start >= 64) return;
+  }
+}
+
+/* groups [g_lo, g_hi) from the exact state (e, N), one wavefront: 64 group records per composed scan,
+ * element level where a group crosses a binade or lacks the needed binade */
+template <class TermF, class RecF>
+__device__ void walk_groups(int64_t g_lo, int64_t g_hi, int64_t n, TermF term, RecF rec, int &e, uint32_t &N,
+                            int lane) {
+  int64_t g = g_lo;
+  while (g < g_hi) {
+    const int64_t gl = g + lane;
+    bool valid = gl < g_hi;
+    bl_inc f = bl_inc_ident();
+    if (valid) {
+      const bl_grec r = rec(gl);
+      const int k = e - (r.E - 1);
+      if (k >= 0 && k <= 2 && e >= BL_E_MIN) f = r.v[k];
+      else valid = false;
+    }
+    const uint32_t Nend = bl_apply(bl_wave_scan(f, lane), N);
+    const unsigned long long m = __ballot(!valid || Nend >= BL_N_TOP);
+    const int first = m ? __ffsll((long long)m) - 1 : 64;
+    if (first > 0) {
+      N = bl_bcast(Nend, first - 1);
+      g += first;
+    }
+    if (g >= g_hi) break;
+    if (first == 64) continue;
+    const int64_t j = g * 64 + lane;
+    elem_resolve(j < n ? term(j) : 0.0f, j < n, e, N, lane);
+    g += 1;
+  }
+}
+
+/*
+ * Exact index-order sum of exp(eff[j] - M), j < V (logprob_normalizer, src/sampling.br:254-266), by the
+ * whole block. The exponent pass left, per 64-term group, the composed automaton for the binades around
+ * its approximate start and that approximate start. Groups whose approximate start and end lie in one
+ * binade, away from its edges, form runs that compose in parallel (one wavefront per run); the other
+ * ("critical") groups, where the sum crosses a power of two, are resolved element by element by one
+ * wavefront from terms staged in LDS. Every assumption is checked on the exact state; returns false
+ * (and the caller walks the groups one by one) when a check fails or there are too many critical groups.
+ */
+__device__ float fast_normaliser(const bl_dev &d, int row, float M, sel_shared &sh) {
+  const int V = d.vocab, t = threadIdx.x, w = t >> 6, lane = t & 63;
+  const int G = (V + 63) / 64;
+  const bl_grec *rec = reinterpret_cast<const bl_grec *>(d.grec) + (int64_t)row * 2 * (V / 64 + 64);
+  const float *apx = d.gapx + (int64_t)row * (V / 64 + 64);
+  const float *eff = d.eff + (int64_t)row * V;
+  float *terms = reinterpret_cast<float *>(sh.keys); /* BL_CRIT_MAX * 64 floats; the list is built later */
+  if (t == 0) sh.ncrit = 0;
+  __syncthreads();
+  /* 1. critical groups, in order (ballot compaction) */
+  for (int base = 0; base < G; base += BL_SEL_THREADS) {
+    const int g = base + t;
+    bool crit = false;
+    if (g < G) {
+      const int E = rec[g].E;
+      const float a = apx[g], b = apx[g + 1];
+      const float lo = 0.99999904632568359375f, hi = 1.00000095367431640625f; /* 1 -+ 2^-20 */
+      crit = bl_binade_of((double)a * lo) != E || bl_binade_of((double)a * hi) != E ||
+             bl_binade_of((double)b * lo) != E || bl_binade_of((double)b * hi) != E;
+    }
+    const unsigned long long m = __ballot(crit);
+    if (lane == 0) sh.cw[w] = __popcll(m);
+    __syncthreads();
+    int off = sh.ncrit;
+    for (int k = 0; k < w; k++) off += sh.cw[k];
+    if (crit) {
+      const int idx = off + __popcll(m & ((1ull << lane) - 1ull));
+      if (idx < BL_CRIT_MAX) sh.crit[idx] = g;
+    }
+    __syncthreads();
+    if (t == 0) {
+      int tot = 0;
+      for (int k = 0; k < SEL_NW; k++) tot += sh.cw[k];
+      sh.ncrit += tot;
+    }
+    __syncthreads();
+  }
+  /* past BL_CRIT_MAX critical groups the last run holds the rest (and is walked group by group) */
+  const int ncrit = sh.ncrit < BL_CRIT_MAX ? sh.ncrit : BL_CRIT_MAX;
+  /* 2. runs between critical groups: run r = (crit[r-1], crit[r]) exclusive, one wavefront per run */
+  for (int r = w; r <= ncrit; r += SEL_NW) {
+    const int lo = r == 0 ? 0 : sh.crit[r - 1] + 1;
+    const int hi = r == ncrit ? G : sh.crit[r];
+    const int E = hi > lo ? rec[lo].E : BL_E_NONE;
+    bl_inc acc = bl_inc_ident();
+    bool bad = false;
+    for (int g0 = lo; g0 < hi; g0 += 64) {
+      const int g = g0 + lane;
+      bl_inc f = bl_inc_ident();
+      if (g < hi) {
+        const bl_grec rg = rec[g];
+        bad |= rg.E != E;
+        f = rg.v[1];
+      }
+      acc = bl_compose(acc, bl_wave_reduce(f, lane));
+    }
+    const bool any_bad = __ballot(bad) != 0ull;
+    if (lane == 0) {
+      sh.run_f[r] = acc;
+      sh.run_e[r] = any_bad ? BL_E_NONE : E;
+      sh.run_n[r] = hi - lo;
+    }
+  }
+  /* 3. the critical groups' terms */
+  for (int q = t; q < ncrit * 64; q += BL_SEL_THREADS) {
+    const int64_t j = (int64_t)sh.crit[q >> 6] * 64 + (q & 63);
+    terms[q] = j < V ? bl_expf(eff[j] - M) : 0.0f;
+  }
+  __syncthreads();
+  /* 4. the chain, by one wavefront: a run applies at once when it starts in its binade and stays in it,
+   * otherwise its groups are walked one by one from the exact state */
+  if (w == 0) {
+    int e = BL_E_MIN;
+    uint32_t N = 0u;
+    auto term = [&](int64_t j) { return bl_expf(eff[j] - M); };
+    auto recf = [&](int64_t g) { return rec[g]; };
+    for (int r = 0; r <= ncrit; r++) {
+      if (sh.run_n[r] > 0) {
+        const uint32_t N2 = bl_apply(sh.run_f[r], N);
+        if (sh.run_e[r] == e && N2 < BL_N_TOP) {
+          N = N2;
+        } else {
+          const int lo = r == 0 ? 0 : sh.crit[r - 1] + 1;
+          walk_groups(lo, lo + sh.run_n[r], V, term, recf, e, N, lane);
+        }
+      }
+      if (r < ncrit) {
+        const int64_t j = (int64_t)sh.crit[r] * 64 + lane;
+        elem_resolve(terms[r * 64 + lane], j < V, e, N, lane);
+      }
+    }
+    if (lane == 0) sh.fast_s = bl_make(e, N);
+  }
+  __syncthreads();
+  const float S = sh.fast_s;
+  __syncthreads();
+  return S;
+}
+
 __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows rows) {
   const int V = d.vocab, nc = d.nc;
   const int row = blockIdx.x, t = threadIdx.x, w = t >> 6, lane = t & 63;
@@ -830,18 +998,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
   /* exact index-order normaliser (wave 0 walks the records written by the exponent pass) */
   const float *eff = d.eff + (int64_t)row * V;
   float lse = 0.0f;
-  if (mode & BL_M_LOGPROBS) {
-    if (w == 0) {
-      const bl_grec *rec = reinterpret_cast<const bl_grec *>(d.grec) + (int64_t)row * 2 * (V / 64 + 64);
-      float S;
-      bl_seq_walk((int64_t)V, [&](int64_t j) { return bl_expf(eff[j] - M); }, [&](int64_t g) { return rec[g]; },
-                  false, 0.0f, 0, S, lane);
-      if (lane == 0) sh.fres[4] = (float)log((double)S);
-    }
-    __syncthreads();
-    lse = sh.fres[4];
-    __syncthreads();
-  }
+  if (mode & BL_M_LOGPROBS) lse = (float)log((double)fast_normaliser(d, row, M, sh));
 
   /* merged top-K candidates of the row pass: sorted (value desc, index asc) in sh.keys[0..K) */
   int n_top = 0;
