@@ -31,6 +31,7 @@
 #define BL_MAX_CHUNKS 1024  /* vocabulary up to BL_MAX_CHUNKS * BL_CH tokens */
 #define BL_SERIAL_MAX 512   /* candidate lists up to this length are summed by one lane */
 #define BL_CRIT_MAX 128     /* critical groups of the fast normaliser (their terms fill 32 KB of LDS) */
+#define BL_STAGE_G 4096     /* group records staged in LDS by the fast normaliser (V up to 262144) */
 
 /* per-token flags */
 #define BL_TF_BIAS 1u

@@ -623,6 +623,8 @@ struct sel_shared {
   int cw[SEL_NW];
   int ncrit;
   float fast_s;
+  int16_t sE[BL_STAGE_G];          /* each group's binade, staged for the run compositions */
+  bl_inc sV[BL_STAGE_G];           /* each group's composed automaton at its own binade */
   float ser_e[BL_SERIAL_MAX];      /* short-list terms exp(v - v0) */
   float ser_r[BL_SERIAL_MAX];      /* short-list terms exp((v - v0) / T) */
   uint32_t wsum[SEL_NW];
@@ -892,6 +894,10 @@ __device__ float fast_normaliser(const bl_dev &d, int row, float M, sel_shared &
     bool crit = false;
     if (g < G) {
       const int E = rec[g].E;
+      if (g < BL_STAGE_G) {
+        sh.sE[g] = (int16_t)E;
+        sh.sV[g] = rec[g].v[1];
+      }
       const float a = apx[g], b = apx[g + 1];
       const float lo = 0.99999904632568359375f, hi = 1.00000095367431640625f; /* 1 -+ 2^-20 */
       crit = bl_binade_of((double)a * lo) != E || bl_binade_of((double)a * hi) != E ||
@@ -920,16 +926,23 @@ __device__ float fast_normaliser(const bl_dev &d, int row, float M, sel_shared &
   for (int r = w; r <= ncrit; r += SEL_NW) {
     const int lo = r == 0 ? 0 : sh.crit[r - 1] + 1;
     const int hi = r == ncrit ? G : sh.crit[r];
-    const int E = hi > lo ? rec[lo].E : BL_E_NONE;
+    const int E = hi > lo ? (lo < BL_STAGE_G ? (int)sh.sE[lo] : rec[lo].E) : BL_E_NONE;
     bl_inc acc = bl_inc_ident();
     bool bad = false;
     for (int g0 = lo; g0 < hi; g0 += 64) {
       const int g = g0 + lane;
       bl_inc f = bl_inc_ident();
       if (g < hi) {
-        const bl_grec rg = rec[g];
-        bad |= rg.E != E;
-        f = rg.v[1];
+        int Eg;
+        if (g < BL_STAGE_G) {
+          Eg = sh.sE[g];
+          f = sh.sV[g];
+        } else {
+          const bl_grec rg = rec[g];
+          Eg = rg.E;
+          f = rg.v[1];
+        }
+        bad |= Eg != E;
       }
       acc = bl_compose(acc, bl_wave_reduce(f, lane));
     }
