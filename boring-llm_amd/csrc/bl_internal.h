@@ -30,7 +30,9 @@
 #define BL_LDS_SORT 4096    /* candidate lists sorted in LDS up to this size */
 #define BL_MAX_CHUNKS 1024  /* vocabulary up to BL_MAX_CHUNKS * BL_CH tokens */
 #define BL_SERIAL_MAX 512   /* candidate lists up to this length are summed by one lane */
-#define BL_CRIT_MAX 128     /* critical groups of the fast normaliser (their terms fill 32 KB of LDS) */
+#define BL_CRIT_MAX 32      /* critical groups the fast normaliser precomputes (terms + two scans in LDS) */
+#define BL_PIECE 128        /* groups per piece of a run (at least) */
+#define BL_PIECES_MAX 128   /* pieces of the fast normaliser: 64 + BL_CRIT_MAX + 1 at most */
 #define BL_STAGE_G 4096     /* group records staged in LDS by the fast normaliser (V up to 262144) */
 
 /* per-token flags */

@@ -228,7 +228,7 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass(bl_dev d, const fl
   /* transformed row */
   {
     float *dst = d.eff + (int64_t)row * V + i0;
-    if (cnt == BL_CH) {
+    if (cnt == BL_CH && (((uintptr_t)dst) & 15) == 0) {
 #pragma unroll
       for (int j = 0; j < BL_CH / (4 * BL_RP_THREADS); j++)
         reinterpret_cast<float4 *>(dst)[j * BL_RP_THREADS + t] = reinterpret_cast<float4 *>(xs)[j * BL_RP_THREADS + t];
@@ -609,28 +609,43 @@ __device__ void block_records(int64_t n, TermF term, bl_grec *recs, double *gsum
   __syncthreads();
 }
 
-struct sel_shared {
-  uint64_t topk[BL_KSEL_MAX];      /* ranked top-K before it moves to keys[0..K) */
-  uint64_t cmin[BL_MAX_CHUNKS];    /* smallest emitted key per chunk */
-  int ccnt[BL_MAX_CHUNKS];         /* emitted keys per chunk */
-  uint64_t tau;
-  uint32_t ucnt;
-  uint32_t fres_u[4];              /* block_find_bin result */
-  int crit[BL_CRIT_MAX];           /* critical groups of the fast normaliser, ascending */
-  bl_inc run_f[BL_CRIT_MAX + 1];   /* composed runs between them */
-  int run_e[BL_CRIT_MAX + 1];      /* binade of each run (BL_E_NONE: not one binade) */
-  int run_n[BL_CRIT_MAX + 1];      /* groups in each run */
+/* the fast normaliser's working set (live before the top-K merge) */
+struct sel_norm {
+  int16_t sE[BL_STAGE_G];              /* each group's binade */
+  bl_inc sV[BL_STAGE_G];               /* each group's composed automaton at its own binade */
+  float terms[BL_CRIT_MAX * 64];       /* the critical groups' terms */
+  bl_inc cp[BL_CRIT_MAX * 64];         /* their prefix scans at the predicted start binade */
+  bl_inc cs[BL_CRIT_MAX * 65];         /* their suffix scans at the predicted end binade (+ identity) */
+  int ce0[BL_CRIT_MAX], ce1[BL_CRIT_MAX]; /* those binades */
+  int crit[BL_CRIT_MAX];               /* critical groups, ascending */
+  int p_lo[BL_PIECES_MAX], p_hi[BL_PIECES_MAX], p_e[BL_PIECES_MAX]; /* pieces of runs (<= BL_PIECE groups) */
+  bl_inc p_f[BL_PIECES_MAX];
+  int run_p0[BL_CRIT_MAX + 2];         /* first piece of each run */
   int cw[SEL_NW];
-  int ncrit;
-  float fast_s;
-  int16_t sE[BL_STAGE_G];          /* each group's binade, staged for the run compositions */
-  bl_inc sV[BL_STAGE_G];           /* each group's composed automaton at its own binade */
-  float ser_e[BL_SERIAL_MAX];      /* short-list terms exp(v - v0) */
-  float ser_r[BL_SERIAL_MAX];      /* short-list terms exp((v - v0) / T) */
-  uint32_t wsum[SEL_NW];
-  uint64_t keys[BL_LDS_SORT];
+  int ncrit, npieces;
+  float S;
+};
+/* the top-K merge and the selection (live after the normaliser) */
+struct sel_merge {
+  uint64_t topk[BL_KSEL_MAX];          /* ranked top-K before it moves to keys[0..K) */
+  uint64_t cmin[BL_MAX_CHUNKS];        /* smallest emitted key per chunk */
+  int ccnt[BL_MAX_CHUNKS];             /* emitted keys per chunk */
+  uint64_t keys[BL_LDS_SORT];          /* merged top-K list, or a full-vocabulary list */
   bl_grec recs[BL_LDS_SORT / 64];
   double gsum[BL_LDS_SORT / 64];
+};
+struct sel_shared {
+  union {
+    sel_norm n;
+    sel_merge m;
+  } u;
+  uint64_t tau;
+  uint64_t rng_out;                    /* the RNG state after a draw */
+  uint32_t ucnt;
+  uint32_t fres_u[4];                  /* block_find_bin result */
+  uint32_t wsum[SEL_NW];
+  float ser_e[BL_SERIAL_MAX];          /* short-list terms exp(v - v0) */
+  float ser_r[BL_SERIAL_MAX];          /* short-list terms exp((v - v0) / T) */
   float fres[8];
   int ires[8];
   float red_m[SEL_NW];
@@ -722,11 +737,11 @@ __device__ int sample_ranked(const bl_slot_dev &sp, ValF val, int64_t n_list, in
         }
       }
       sh.ires[2] = unsup ? -2 : (int)(f >= 0 ? f : cut - 1);
-      *reinterpret_cast<uint64_t *>(&sh.fres[2]) = st;
+      sh.rng_out = st;
     }
     __syncthreads();
     const int chosen = sh.ires[2];
-    const uint64_t st = *reinterpret_cast<uint64_t *>(&sh.fres[2]);
+    const uint64_t st = sh.rng_out;
     __syncthreads();
     if (chosen == -2 || chosen >= n_list) {
       status |= BL_SE_UNSUPPORTED;
@@ -803,12 +818,12 @@ __device__ int sample_ranked(const bl_slot_dev &sp, ValF val, int64_t n_list, in
     if (lane == 0) {
       sh.ires[2] = f >= 0 ? f : (int)(cutoff - 1);
       sh.fres[1] = S;
-      *reinterpret_cast<uint64_t *>(&sh.fres[2]) = st;
+      sh.rng_out = st;
     }
   }
   __syncthreads();
   int chosen = sh.ires[2];
-  rng = *reinterpret_cast<uint64_t *>(&sh.fres[2]);
+  rng = sh.rng_out;
   __syncthreads();
   if (chosen >= n_list) {
     status |= BL_SE_UNSUPPORTED;
@@ -817,10 +832,9 @@ __device__ int sample_ranked(const bl_slot_dev &sp, ValF val, int64_t n_list, in
   return chosen;
 }
 
-/* wavefront-level resolution of one 64-term group from state (e, N), crossing binades as needed
- * (a real float add at each crossing); `a` is this lane's term, `in` whether it exists */
-__device__ __forceinline__ void elem_resolve(float a, bool in, int &e, uint32_t &N, int lane) {
-  int start = 0;
+/* wavefront-level resolution of the terms [start, 64) of one 64-term group from state (e, N), crossing
+ * binades as needed (a real float add at each crossing); `a` is this lane's term, `in` whether it exists */
+__device__ __forceinline__ void elem_resolve(float a, bool in, int &e, uint32_t &N, int lane, int start = 0) {
   while (true) {
     const bool act = in && lane >= start;
     const bl_inc fe = act ? bl_term_inc(a, e) : bl_inc_ident();
@@ -873,11 +887,14 @@ __device__ void walk_groups(int64_t g_lo, int64_t g_hi, int64_t n, TermF term, R
 /*
  * Exact index-order sum of exp(eff[j] - M), j < V (logprob_normalizer, src/sampling.br:254-266), by the
  * whole block. The exponent pass left, per 64-term group, the composed automaton for the binades around
- * its approximate start and that approximate start. Groups whose approximate start and end lie in one
- * binade, away from its edges, form runs that compose in parallel (one wavefront per run); the other
- * ("critical") groups, where the sum crosses a power of two, are resolved element by element by one
- * wavefront from terms staged in LDS. Every assumption is checked on the exact state; returns false
- * (and the caller walks the groups one by one) when a check fails or there are too many critical groups.
+ * its approximate start, and that approximate start. Groups whose approximate start and end lie in one
+ * binade, away from its edges, form runs; the runs are cut into pieces of at most `plen` groups that the
+ * wavefronts compose in parallel. The other ("critical") groups, where the sum crosses a power of two,
+ * get their terms and, for the binades predicted at their start and end, a prefix scan and a suffix scan
+ * of their automata. One wavefront then chains pieces and critical groups: a piece applies at once when
+ * the exact state is in its binade and stays there; a critical group needs one ballot for the crossing,
+ * one real float add and the suffix. Every prediction is checked on the exact state, and a piece or group
+ * whose prediction fails is walked element by element instead.
  */
 __device__ float fast_normaliser(const bl_dev &d, int row, float M, sel_shared &sh) {
   const int V = d.vocab, t = threadIdx.x, w = t >> 6, lane = t & 63;
@@ -885,106 +902,166 @@ __device__ float fast_normaliser(const bl_dev &d, int row, float M, sel_shared &
   const bl_grec *rec = reinterpret_cast<const bl_grec *>(d.grec) + (int64_t)row * 2 * (V / 64 + 64);
   const float *apx = d.gapx + (int64_t)row * (V / 64 + 64);
   const float *eff = d.eff + (int64_t)row * V;
-  float *terms = reinterpret_cast<float *>(sh.keys); /* BL_CRIT_MAX * 64 floats; the list is built later */
-  if (t == 0) sh.ncrit = 0;
+  sel_norm &nm = sh.u.n;
+  auto e_of = [&](int g) -> int { return g < BL_STAGE_G ? (int)nm.sE[g] : rec[g].E; };
+  auto v_of = [&](int g) -> bl_inc { return g < BL_STAGE_G ? nm.sV[g] : rec[g].v[1]; };
+  if (t == 0) nm.ncrit = 0;
   __syncthreads();
-  /* 1. critical groups, in order (ballot compaction) */
-  for (int base = 0; base < G; base += BL_SEL_THREADS) {
-    const int g = base + t;
-    bool crit = false;
-    if (g < G) {
-      const int E = rec[g].E;
-      if (g < BL_STAGE_G) {
-        sh.sE[g] = (int16_t)E;
-        sh.sV[g] = rec[g].v[1];
+  /* 1. critical groups in order (ballot compaction); every load of a sweep is issued first */
+  constexpr int RPT = 4;
+  for (int base = 0; base < G; base += RPT * BL_SEL_THREADS) {
+    int Eg[RPT];
+    float ga[RPT], gb[RPT];
+    bl_inc gv[RPT];
+#pragma unroll
+    for (int k = 0; k < RPT; k++) {
+      const int g = base + k * BL_SEL_THREADS + t;
+      if (g < G) {
+        Eg[k] = rec[g].E;
+        gv[k] = rec[g].v[1];
+        ga[k] = apx[g];
+        gb[k] = apx[g + 1];
       }
-      const float a = apx[g], b = apx[g + 1];
-      const float lo = 0.99999904632568359375f, hi = 1.00000095367431640625f; /* 1 -+ 2^-20 */
-      crit = bl_binade_of((double)a * lo) != E || bl_binade_of((double)a * hi) != E ||
-             bl_binade_of((double)b * lo) != E || bl_binade_of((double)b * hi) != E;
     }
-    const unsigned long long m = __ballot(crit);
-    if (lane == 0) sh.cw[w] = __popcll(m);
-    __syncthreads();
-    int off = sh.ncrit;
-    for (int k = 0; k < w; k++) off += sh.cw[k];
-    if (crit) {
-      const int idx = off + __popcll(m & ((1ull << lane) - 1ull));
-      if (idx < BL_CRIT_MAX) sh.crit[idx] = g;
+#pragma unroll
+    for (int k = 0; k < RPT; k++) {
+      const int g = base + k * BL_SEL_THREADS + t;
+      bool crit = false;
+      if (g < G) {
+        if (g < BL_STAGE_G) {
+          nm.sE[g] = (int16_t)Eg[k];
+          nm.sV[g] = gv[k];
+        }
+        const float lo = 0.99999904632568359375f, hi = 1.00000095367431640625f; /* 1 -+ 2^-20 */
+        const int E = Eg[k];
+        crit = bl_binade_of((double)ga[k] * lo) != E || bl_binade_of((double)ga[k] * hi) != E ||
+               bl_binade_of((double)gb[k] * lo) != E || bl_binade_of((double)gb[k] * hi) != E;
+      }
+      const unsigned long long m = __ballot(crit);
+      if (lane == 0) nm.cw[w] = __popcll(m);
+      __syncthreads();
+      int off = nm.ncrit;
+      for (int q = 0; q < w; q++) off += nm.cw[q];
+      if (crit) {
+        const int idx = off + __popcll(m & ((1ull << lane) - 1ull));
+        if (idx < BL_CRIT_MAX) nm.crit[idx] = g;
+      }
+      __syncthreads();
+      if (t == 0) {
+        int tot = 0;
+        for (int q = 0; q < SEL_NW; q++) tot += nm.cw[q];
+        nm.ncrit += tot;
+      }
+      __syncthreads();
     }
-    __syncthreads();
-    if (t == 0) {
-      int tot = 0;
-      for (int k = 0; k < SEL_NW; k++) tot += sh.cw[k];
-      sh.ncrit += tot;
-    }
-    __syncthreads();
   }
-  /* past BL_CRIT_MAX critical groups the last run holds the rest (and is walked group by group) */
-  const int ncrit = sh.ncrit < BL_CRIT_MAX ? sh.ncrit : BL_CRIT_MAX;
-  /* 2. runs between critical groups: run r = (crit[r-1], crit[r]) exclusive, one wavefront per run */
-  for (int r = w; r <= ncrit; r += SEL_NW) {
-    const int lo = r == 0 ? 0 : sh.crit[r - 1] + 1;
-    const int hi = r == ncrit ? G : sh.crit[r];
-    const int E = hi > lo ? (lo < BL_STAGE_G ? (int)sh.sE[lo] : rec[lo].E) : BL_E_NONE;
+  /* past BL_CRIT_MAX critical groups the last run holds the rest (and its pieces fail their checks) */
+  const int ncrit = nm.ncrit < BL_CRIT_MAX ? nm.ncrit : BL_CRIT_MAX;
+  /* 2. runs cut into pieces; plen keeps the count within BL_PIECES_MAX */
+  const int plen = (G + 63) / 64 > BL_PIECE ? (G + 63) / 64 : BL_PIECE;
+  if (t == 0) {
+    int np = 0;
+    for (int r = 0; r <= ncrit; r++) {
+      nm.run_p0[r] = np;
+      const int lo = r == 0 ? 0 : nm.crit[r - 1] + 1;
+      const int hi = r == ncrit ? G : nm.crit[r];
+      for (int q = lo; q < hi && np < BL_PIECES_MAX; q += plen) {
+        nm.p_lo[np] = q;
+        nm.p_hi[np] = q + plen < hi ? q + plen : hi;
+        np++;
+      }
+    }
+    nm.run_p0[ncrit + 1] = np;
+    nm.npieces = np;
+  }
+  __syncthreads();
+  for (int pi = w; pi < nm.npieces; pi += SEL_NW) {
+    const int lo = nm.p_lo[pi], hi = nm.p_hi[pi];
+    const int E = e_of(lo);
     bl_inc acc = bl_inc_ident();
     bool bad = false;
     for (int g0 = lo; g0 < hi; g0 += 64) {
       const int g = g0 + lane;
       bl_inc f = bl_inc_ident();
       if (g < hi) {
-        int Eg;
-        if (g < BL_STAGE_G) {
-          Eg = sh.sE[g];
-          f = sh.sV[g];
-        } else {
-          const bl_grec rg = rec[g];
-          Eg = rg.E;
-          f = rg.v[1];
-        }
-        bad |= Eg != E;
+        bad |= e_of(g) != E;
+        f = v_of(g);
       }
       acc = bl_compose(acc, bl_wave_reduce(f, lane));
     }
     const bool any_bad = __ballot(bad) != 0ull;
     if (lane == 0) {
-      sh.run_f[r] = acc;
-      sh.run_e[r] = any_bad ? BL_E_NONE : E;
-      sh.run_n[r] = hi - lo;
+      nm.p_f[pi] = acc;
+      nm.p_e[pi] = any_bad ? BL_E_NONE : E;
     }
   }
-  /* 3. the critical groups' terms */
-  for (int q = t; q < ncrit * 64; q += BL_SEL_THREADS) {
-    const int64_t j = (int64_t)sh.crit[q >> 6] * 64 + (q & 63);
-    terms[q] = j < V ? bl_expf(eff[j] - M) : 0.0f;
+  /* 3. critical groups: terms, predicted start/end binades, prefix scan and suffix scan */
+  for (int ci = w; ci < ncrit; ci += SEL_NW) {
+    const int g = nm.crit[ci];
+    const int64_t j = (int64_t)g * 64 + lane;
+    const bool in = j < V;
+    const float a = in ? bl_expf(eff[j] - M) : 0.0f;
+    const int e0 = e_of(g), e1 = bl_binade_of((double)apx[g + 1]);
+    nm.terms[ci * 64 + lane] = a;
+    nm.cp[ci * 64 + lane] = bl_wave_scan(in ? bl_term_inc(a, e0) : bl_inc_ident(), lane);
+    bl_inc sf = in ? bl_term_inc(a, e1) : bl_inc_ident(); /* suffix: this term, then the later ones */
+#pragma unroll
+    for (int k = 1; k < 64; k <<= 1) {
+      const bl_inc o = bl_inc{(uint32_t)__shfl_down((int)sf.d0, k, 64), (uint32_t)__shfl_down((int)sf.d1, k, 64)};
+      if (lane + k < 64) sf = bl_compose(sf, o);
+    }
+    nm.cs[ci * 65 + lane] = sf;
+    if (lane == 0) {
+      nm.cs[ci * 65 + 64] = bl_inc_ident();
+      nm.ce0[ci] = e0;
+      nm.ce1[ci] = e1;
+    }
   }
   __syncthreads();
-  /* 4. the chain, by one wavefront: a run applies at once when it starts in its binade and stays in it,
-   * otherwise its groups are walked one by one from the exact state */
+  /* 4. the chain, by one wavefront */
   if (w == 0) {
     int e = BL_E_MIN;
     uint32_t N = 0u;
     auto term = [&](int64_t j) { return bl_expf(eff[j] - M); };
     auto recf = [&](int64_t g) { return rec[g]; };
     for (int r = 0; r <= ncrit; r++) {
-      if (sh.run_n[r] > 0) {
-        const uint32_t N2 = bl_apply(sh.run_f[r], N);
-        if (sh.run_e[r] == e && N2 < BL_N_TOP) {
-          N = N2;
-        } else {
-          const int lo = r == 0 ? 0 : sh.crit[r - 1] + 1;
-          walk_groups(lo, lo + sh.run_n[r], V, term, recf, e, N, lane);
-        }
+      for (int pi = nm.run_p0[r]; pi < nm.run_p0[r + 1]; pi++) {
+        const uint32_t N2 = bl_apply(nm.p_f[pi], N);
+        if (nm.p_e[pi] == e && N2 < BL_N_TOP) N = N2;
+        else walk_groups(nm.p_lo[pi], nm.p_hi[pi], V, term, recf, e, N, lane);
       }
-      if (r < ncrit) {
-        const int64_t j = (int64_t)sh.crit[r] * 64 + lane;
-        elem_resolve(terms[r * 64 + lane], j < V, e, N, lane);
+      if (r == ncrit) {
+        /* groups a capped piece list left out: the tail of the last run */
+        const int done = nm.run_p0[r + 1] > nm.run_p0[r] ? nm.p_hi[nm.run_p0[r + 1] - 1] : (r == 0 ? 0 : nm.crit[r - 1] + 1);
+        if (done < G) walk_groups(done, G, V, term, recf, e, N, lane);
+        break;
       }
+      const int g = nm.crit[r];
+      const bool in = (int64_t)g * 64 + lane < V;
+      const float a = nm.terms[r * 64 + lane];
+      if (e != nm.ce0[r]) {
+        elem_resolve(a, in, e, N, lane, 0);
+        continue;
+      }
+      const uint32_t Ne = bl_apply(nm.cp[r * 64 + lane], N);
+      const unsigned long long ms = __ballot(in && Ne >= BL_N_TOP);
+      if (!ms) {
+        N = bl_bcast(Ne, 63);
+        continue;
+      }
+      const int c = __ffsll((long long)ms) - 1;
+      const uint32_t Nbefore = c > 0 ? bl_bcast(Ne, c - 1) : N;
+      const float Sn = bl_make(e, Nbefore) + bl_bcastf(a, c); /* the one real float add at the crossing */
+      bl_split(Sn, e, N);
+      if (c == 63) continue;
+      const uint32_t N2 = bl_apply(nm.cs[r * 65 + c + 1], N);
+      if (e == nm.ce1[r] && N2 < BL_N_TOP) N = N2;
+      else elem_resolve(a, in, e, N, lane, c + 1);
     }
-    if (lane == 0) sh.fast_s = bl_make(e, N);
+    if (lane == 0) nm.S = bl_make(e, N);
   }
   __syncthreads();
-  const float S = sh.fast_s;
+  const float S = nm.S;
   __syncthreads();
   return S;
 }
@@ -1013,7 +1090,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
   float lse = 0.0f;
   if (mode & BL_M_LOGPROBS) lse = (float)log((double)fast_normaliser(d, row, M, sh));
 
-  /* merged top-K candidates of the row pass: sorted (value desc, index asc) in sh.keys[0..K) */
+  /* merged top-K candidates of the row pass: sorted (value desc, index asc) in sh.u.m.keys[0..K) */
   int n_top = 0;
   const int K = sp.k_sel;
   if (K > 0) {
@@ -1021,8 +1098,8 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
      * is at least tau = the largest K-th key of a full chunk: only keys >= tau can rank below K */
     const int total = nc * K;
     for (int ch = t; ch < nc; ch += BL_SEL_THREADS) {
-      sh.cmin[ch] = ~0ull;
-      sh.ccnt[ch] = 0;
+      sh.u.m.cmin[ch] = ~0ull;
+      sh.u.m.ccnt[ch] = 0;
     }
     if (t == 0) {
       sh.ucnt = 0u;
@@ -1034,13 +1111,13 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
       const int64_t o = ((int64_t)row * nc + ch) * BL_KSEL_MAX + q;
       const int32_t id = d.cand_i[o];
       if (id >= 0) {
-        atomicMin(&sh.cmin[ch], ckey(d.cand_v[o], id));
-        atomicAdd(&sh.ccnt[ch], 1);
+        atomicMin(&sh.u.m.cmin[ch], ckey(d.cand_v[o], id));
+        atomicAdd(&sh.u.m.ccnt[ch], 1);
       }
     }
     __syncthreads();
     for (int ch = t; ch < nc; ch += BL_SEL_THREADS)
-      if (sh.ccnt[ch] == K) atomicMax(&sh.tau, sh.cmin[ch]);
+      if (sh.u.m.ccnt[ch] == K) atomicMax(&sh.tau, sh.u.m.cmin[ch]);
     __syncthreads();
     const uint64_t tau = sh.tau;
     auto cand_key = [&](int i, uint64_t &k) -> bool {
@@ -1060,7 +1137,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
      * found by a radix selection over the value bits (12 + 10 + 10) of those keys */
     uint64_t lo = tau;
     if (sh.ucnt > (uint32_t)(2 * K > 512 ? 2 * K : 512)) {
-      uint32_t *hist = reinterpret_cast<uint32_t *>(sh.keys); /* 4096 bins, the list is not built yet */
+      uint32_t *hist = reinterpret_cast<uint32_t *>(sh.u.m.keys); /* 4096 bins, the list is not built yet */
       uint32_t prefix = 0u, pmask = 0u;
       int need = K;
       for (int pass = 0; pass < 3; pass++) {
@@ -1091,7 +1168,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
       uint64_t k;
       if (cand_key(i, k) && k >= lo) {
         const uint32_t pos = atomicAdd(&sh.ucnt, 1u);
-        if (pos < BL_LDS_SORT) sh.keys[pos] = k;
+        if (pos < BL_LDS_SORT) sh.u.m.keys[pos] = k;
       }
     }
     __syncthreads();
@@ -1102,17 +1179,17 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
     }
     /* rank by counting (keys are distinct: they carry the index); four independent reads per step */
     for (int i = t; i < ns; i += BL_SEL_THREADS) {
-      const uint64_t k = sh.keys[i];
+      const uint64_t k = sh.u.m.keys[i];
       int r = 0, j = 0;
       for (; j + 4 <= ns; j += 4) {
-        const uint64_t a0 = sh.keys[j], a1 = sh.keys[j + 1], a2 = sh.keys[j + 2], a3 = sh.keys[j + 3];
+        const uint64_t a0 = sh.u.m.keys[j], a1 = sh.u.m.keys[j + 1], a2 = sh.u.m.keys[j + 2], a3 = sh.u.m.keys[j + 3];
         r += (a0 > k ? 1 : 0) + (a1 > k ? 1 : 0) + (a2 > k ? 1 : 0) + (a3 > k ? 1 : 0);
       }
-      for (; j < ns; j++) r += sh.keys[j] > k ? 1 : 0;
-      if (r < K) sh.topk[r] = k;
+      for (; j < ns; j++) r += sh.u.m.keys[j] > k ? 1 : 0;
+      if (r < K) sh.u.m.topk[r] = k;
     }
     __syncthreads();
-    for (int q = t; q < K; q += BL_SEL_THREADS) sh.keys[q] = q < ns ? sh.topk[q] : 0ull;
+    for (int q = t; q < K; q += BL_SEL_THREADS) sh.u.m.keys[q] = q < ns ? sh.u.m.topk[q] : 0ull;
     __syncthreads();
     n_top = K;
   }
@@ -1144,7 +1221,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
       if (gi != 0x7fffffff)
         for (int k = t; k < d.gm_blocks; k += BL_SEL_THREADS)
           if (d.gm_arg[go + k] != 0x7fffffff && d.gm_max[go + k] == gm) n_eq += (double)d.gm_eq[go + k];
-      n_eq = block_sum_d<BL_SEL_THREADS>(n_eq, sh.gsum);
+      n_eq = block_sum_d<BL_SEL_THREADS>(n_eq, sh.u.m.gsum);
       if (gi == 0x7fffffff) {
         status |= BL_SE_GREJECT;
       } else {
@@ -1157,9 +1234,9 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
   } else if (mode & BL_M_TOPK) {
     /* top_k_select list: kk = min(top_k, V) entries, unfilled slots are (-1e30, 0) */
     int64_t kk = sp.top_k < V ? sp.top_k : V;
-    auto val = [&](int64_t j) -> float { return sh.keys[j] ? ckey_v(sh.keys[j]) : -1.0e30f; };
-    int pos = sample_ranked(sp, val, kk, kk, rng, skip, sh.recs, sh.gsum, sh, status);
-    if (pos >= 0) tok = sh.keys[pos] ? ckey_i(sh.keys[pos]) : 0;
+    auto val = [&](int64_t j) -> float { return sh.u.m.keys[j] ? ckey_v(sh.u.m.keys[j]) : -1.0e30f; };
+    int pos = sample_ranked(sp, val, kk, kk, rng, skip, sh.u.m.recs, sh.u.m.gsum, sh, status);
+    if (pos >= 0) tok = sh.u.m.keys[pos] ? ckey_i(sh.u.m.keys[pos]) : 0;
   } else {
     /* full-vocabulary rank (src/sampling.br:301-365): candidates from the exponent pass */
     int nf = d.full_n[row];
@@ -1169,15 +1246,15 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
     }
     int P = 1;
     while (P < nf) P <<= 1;
-    uint64_t *keys = P <= BL_LDS_SORT ? sh.keys : d.sortk + (int64_t)row * (2 * (int64_t)V);
+    uint64_t *keys = P <= BL_LDS_SORT ? sh.u.m.keys : d.sortk + (int64_t)row * (2 * (int64_t)V);
     /* when the LDS holds the merged top-K list (logprob alternatives) keep it: sort the full list in global */
-    if (K > 0 && keys == sh.keys) keys = d.sortk + (int64_t)row * (2 * (int64_t)V);
+    if (K > 0 && keys == sh.u.m.keys) keys = d.sortk + (int64_t)row * (2 * (int64_t)V);
     for (int i = t; i < P; i += BL_SEL_THREADS)
       keys[i] = i < nf ? ckey(d.full_v[(int64_t)row * V + i], d.full_i[(int64_t)row * V + i]) : 0ull;
     __syncthreads();
     bitonic_desc(keys, P);
-    bl_grec *recs = sh.recs;
-    double *gsum = sh.gsum;
+    bl_grec *recs = sh.u.m.recs;
+    double *gsum = sh.u.m.gsum;
     if ((nf + 63) / 64 > BL_LDS_SORT / 64) {
       recs = reinterpret_cast<bl_grec *>(d.grec) + (int64_t)row * 2 * (V / 64 + 64) + (V / 64 + 64);
       gsum = d.gsum + (int64_t)row * (V / 64 + 64);
@@ -1203,7 +1280,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
       float a = eff[tok] - M;
       rows.lp[row] = a - lse;
       for (int q = 0; q < sp.n_probs && q < rows.top_stride; q++) {
-        uint64_t k = q < n_top ? sh.keys[q] : 0ull;
+        uint64_t k = q < n_top ? sh.u.m.keys[q] : 0ull;
         int32_t id = k ? ckey_i(k) : 0;
         float v = k ? ckey_v(k) : -1.0e30f;
         rows.top_ids[(int64_t)row * rows.top_stride + q] = id;

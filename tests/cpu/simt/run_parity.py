@@ -8,7 +8,7 @@ alone) and checks the workloads the GPU parity tests check, at reduced step coun
     python run_parity.py --lib _build/libbl_simt.so small:0-10:25 w2:2 w4:1:8 w5:1 async:2
 
 Items: small:<cases>:<steps>, w2:<steps>, w3:<steps>, w4:<steps>:<rows>, w5:<steps>, async:<steps>,
-grammar:<cases>:<steps>, bigk:<steps>.
+grammar:<cases>:<steps>, bigk:<steps>, pair:<case>:<case>:<steps>.
 Prints one line per item ("ok ..." / "FAIL ...") and exits 1 if any failed.
 """
 import argparse
@@ -100,6 +100,52 @@ def run_small(BL, case, steps):
             return "final RNG state differs"
     finally:
         L.orc_slot_free(h)
+        L.orc_set_eog_tokens(O.ip(O.i32([0])), 0, -1)
+        ctx.close()
+    return None
+
+
+def run_pair(BL, ca, cb, steps):
+    """Two small cases stepped together in one call (rows 0 and 1 of an odd-length vocabulary: row 1 starts
+    at a 4-byte but not 16-byte aligned address)."""
+    L = O.lib()
+    L.orc_set_eog_tokens(O.ip(O.i32([EOS] + EOGS)), 1 + len(EOGS), -1)
+    ctx = BL.Context(SMALL_V, 2, 2)
+    ctx.set_eog(EOS, EOGS)
+    hs, rngs, wants = [], [], []
+    for slot, case in enumerate((ca, cb)):
+        kw = CASES[case]
+        rng, hist, reply, bias = small_case_inputs(case)
+        ctx.slot_reset(slot, BL.Params(**kw), BL.seed_rng(100 + case), history=hist, reply=reply, bias=bias)
+        op = O.params(**kw)
+        hh, rr = O.i32(hist), O.i32(reply)
+        bi, bv = O.i32(list(bias.keys())), O.f32(list(bias.values()))
+        hs.append(L.orc_slot_new(O.C.byref(op), BL.seed_rng(100 + case), O.ip(hh), len(hist), O.ip(rr), len(reply),
+                                 O.ip(bi), O.fp(bv), len(bias)))
+        rngs.append(rng)
+        wants.append((1 if kw.get("logprobs") else 0, kw.get("n_probs", 0)))
+    buf = MEM.zeros(2 * SMALL_V, np.float32)
+    stride = max(max(w[1] for w in wants), 1)
+    try:
+        for t in range(steps):
+            xs = [small_case_logits(r) for r in rngs]
+            buf.upload(np.concatenate(xs))
+            tok, lp, ti, tl = ctx.sample_step([0, 1], buf.ptr, SMALL_V, top_stride=stride)
+            for r in range(2):
+                ot, olp = np.zeros(1, np.int32), np.zeros(1, np.float32)
+                oti, otl = np.zeros(stride, np.int32), np.zeros(stride, np.float32)
+                eg = O.C.c_int()
+                assert L.orc_slot_step(hs[r], O.fp(xs[r]), SMALL_V, wants[r][0], 1, O.ip(ot), O.fp(olp), O.ip(oti),
+                                       O.fp(otl), O.C.byref(eg)) == 0
+                if tok[r] != ot[0]:
+                    return f"step {t} row {r}: token {tok[r]} vs {ot[0]}"
+                if wants[r][0] and not eg.value:
+                    n = wants[r][1]
+                    if not lp_close(lp[r], olp[0]) or ti[r][:n] != list(oti[:n]):
+                        return f"step {t} row {r}: logprob {lp[r]} vs {olp[0]} or alternatives differ"
+    finally:
+        for h in hs:
+            L.orc_slot_free(h)
         L.orc_set_eog_tokens(O.ip(O.i32([0])), 0, -1)
         ctx.close()
     return None
@@ -429,6 +475,8 @@ def main():
             results.append(("workload 5", run_w5(BL, int(f[1]))))
         elif kind == "async":
             results.append(("asynchronous step", run_async(BL, int(f[1]))))
+        elif kind == "pair":
+            results.append((f"rows {f[1]} + {f[2]}", run_pair(BL, int(f[1]), int(f[2]), int(f[3]) if len(f) > 3 else 10)))
         elif kind == "bigk":
             results.append(("large top-k / n_probs", run_bigk(BL, int(f[1]))))
         elif kind == "w3":

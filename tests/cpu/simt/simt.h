@@ -85,6 +85,12 @@ inline T simt_shfl_up(T v, unsigned k, int width = 64) {
   return simt_exchange(v, l >= (int)k ? l - (int)k : l);
 }
 template <class T>
+inline T simt_shfl_down(T v, unsigned k, int width = 64) {
+  (void)width;
+  int l = simt::lane_id();
+  return simt_exchange(v, l + (int)k < 64 ? l + (int)k : l);
+}
+template <class T>
 inline T simt_shfl_xor(T v, int k, int width = 64) {
   (void)width;
   return simt_exchange(v, simt::lane_id() ^ k);
@@ -141,6 +147,7 @@ inline int simt_readlane(int v, int l) {
 #define __shfl(...) (simt::wave_site(__FILE__, __LINE__), simt_shfl(__VA_ARGS__))
 #define __shfl_up(...) (simt::wave_site(__FILE__, __LINE__), simt_shfl_up(__VA_ARGS__))
 #define __shfl_xor(...) (simt::wave_site(__FILE__, __LINE__), simt_shfl_xor(__VA_ARGS__))
+#define __shfl_down(...) (simt::wave_site(__FILE__, __LINE__), simt_shfl_down(__VA_ARGS__))
 #define __ballot(...) (simt::wave_site(__FILE__, __LINE__), simt_ballot(__VA_ARGS__))
 #define __builtin_amdgcn_update_dpp(...) (simt::wave_site(__FILE__, __LINE__), simt_update_dpp(__VA_ARGS__))
 #define __builtin_amdgcn_readlane(...) (simt::wave_site(__FILE__, __LINE__), simt_readlane(__VA_ARGS__))

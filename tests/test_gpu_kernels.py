@@ -1,6 +1,7 @@
 """GPU parity of kernel paths beyond the fixed workloads, through the shared harness with device buffers:
 top_k 250 with 256 logprob alternatives at V=151936 (38 chunks x 256 candidates per row, the merged
-list found by radix selection), and the bound-rows asynchronous step against the synchronous one."""
+list found by radix selection), two small configurations stepped as rows 0 and 1 of an odd-length
+vocabulary (row 1 not 16-byte aligned), and the bound-rows asynchronous step against the synchronous one."""
 import os
 import sys
 
@@ -28,6 +29,13 @@ def device_memory():
 def test_large_top_k_and_alternatives():
     print("top_k 250, n_probs 256, V=151936: 20 steps", flush=True)
     err = RP.run_bigk(BL, 20)
+    assert err is None, err
+
+
+@pytest.mark.parametrize("pair", [(3, 8), (9, 5), (6, 10)])
+def test_two_rows_odd_vocabulary(pair):
+    print(f"small cases {pair} stepped together, V=5003: 25 steps", flush=True)
+    err = RP.run_pair(BL, pair[0], pair[1], 25)
     assert err is None, err
 
 

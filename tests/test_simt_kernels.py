@@ -46,10 +46,12 @@ def test_small_cases_random_thread_order(simt_lib):
 
 
 def test_full_vocabulary_workloads(simt_lib):
-    """Workload 2 (the benchmark step), workload 4 (soft-cap, V=262144, top-64 + 20 logprobs) on 2 rows, and
-    the bound-rows asynchronous step against the synchronous one."""
-    out = _run(simt_lib, ["w2:1", "w4:1:2", "async:1"], {"SIMT_ORDER": "rev"})
+    """Workload 2 (the benchmark step), workload 4 (soft-cap, V=262144, top-64 + 20 logprobs) on 2 rows, the
+    bound-rows asynchronous step against the synchronous one, two rows of an odd-length vocabulary in one
+    call, and top_k 250 with 256 alternatives."""
+    out = _run(simt_lib, ["w2:1", "w4:1:2", "async:1", "pair:3:8:6", "bigk:1"], {"SIMT_ORDER": "rev"})
     assert "ok   workload 2" in out and "ok   workload 4" in out and "ok   asynchronous step" in out
+    assert "ok   rows 3 + 8" in out and "ok   large top-k" in out
 
 
 def test_grammar_masks_and_tokens(simt_lib):
