@@ -33,6 +33,7 @@
 #define BL_CRIT_MAX 32      /* critical groups the fast normaliser precomputes (terms + two scans in LDS) */
 #define BL_PIECE 128        /* groups per piece of a run (at least) */
 #define BL_PIECES_MAX 128   /* pieces of the fast normaliser: 64 + BL_CRIT_MAX + 1 at most */
+#define BL_TK_CAP 1024      /* chunk top-K: keys at or above the thread-maximum bound ranked in LDS */
 #define BL_STAGE_G 4096     /* group records staged in LDS by the fast normaliser (V up to 262144) */
 
 /* per-token flags */

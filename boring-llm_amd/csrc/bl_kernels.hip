@@ -30,6 +30,13 @@
 
 __device__ __forceinline__ const bl_slot_dev &slot_of(const bl_dev &d, int s) { return d.slots[s]; }
 
+/* candidate order keys: (fkey(value) << 32) | ~index, larger = earlier in (value desc, index asc) */
+__device__ __forceinline__ uint64_t ckey(float v, int32_t id) {
+  return ((uint64_t)bl_fkey(v) << 32) | (uint64_t)(0xffffffffu - (uint32_t)id);
+}
+__device__ __forceinline__ float ckey_v(uint64_t k) { return bl_fkey_inv((uint32_t)(k >> 32)); }
+__device__ __forceinline__ int32_t ckey_i(uint64_t k) { return (int32_t)(0xffffffffu - (uint32_t)k); }
+
 /* ------------------------------------------------------------------ block reductions (256 threads) */
 __device__ __forceinline__ void argmax_merge(float &m, int &mi, float m2, int mi2) {
   if (m2 > m || (m2 == m && mi2 < mi)) {
@@ -156,6 +163,10 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass(bl_dev d, const fl
   __shared__ double red_d[4];
   __shared__ uint32_t sel[4];
   __shared__ int out_n;
+  __shared__ uint64_t tmax[BL_RP_THREADS];   /* each thread's largest order key */
+  __shared__ uint64_t tkeys[BL_TK_CAP];      /* keys at or above the bound */
+  __shared__ uint64_t tk_tau;
+  __shared__ int tk_n;
 
   const int i0 = c * BL_CH;
   const int cnt = min(BL_CH, V - i0);
@@ -258,9 +269,79 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass(bl_dev d, const fl
     d.c_sum[o] = (float)s;
   }
 
-  /* chunk top-K by (value desc, index asc) over values > -1e30 (src/sampling.br:280-296) */
+  /* chunk top-K by (value desc, index asc) over values > -1e30 (src/sampling.br:280-296). Order keys
+   * (value, then lower index) are distinct integers. Each thread's largest key is a value of the chunk,
+   * so the K-th largest of the 256 thread maxima bounds the chunk's K-th key from below: the keys at or
+   * above it (typically K to 2K of them) are compacted and ranked by counting. When too many reach the
+   * bound, three radix passes find the K-th key instead. */
   const int K = sp.k_sel;
   if (K <= 0) return;
+  const int64_t cbase = ((int64_t)row * nc + c) * BL_KSEL_MAX;
+  {
+    uint64_t best = 0ull;
+#pragma unroll
+    for (int k = 0; k < BL_CH / BL_RP_THREADS; k++) {
+      const int i = t + k * BL_RP_THREADS;
+      if (i < cnt) {
+        const float x = xs[i];
+        if (x > -1.0e30f) {
+          const uint64_t kk = ckey(x, i0 + i);
+          best = kk > best ? kk : best;
+        }
+      }
+    }
+    tmax[t] = best;
+    if (t == 0) {
+      tk_tau = 0ull;
+      tk_n = 0;
+    }
+    __syncthreads();
+    int r = 0;
+    for (int j = 0; j < BL_RP_THREADS; j += 4)
+      r += (tmax[j] > best ? 1 : 0) + (tmax[j + 1] > best ? 1 : 0) + (tmax[j + 2] > best ? 1 : 0) +
+           (tmax[j + 3] > best ? 1 : 0);
+    if (best != 0ull && r == K - 1) tk_tau = best; /* fewer than K valid maxima: no bound (0) */
+    __syncthreads();
+    const uint64_t tau = tk_tau;
+    /* compaction of the keys >= tau, in no particular order */
+#pragma unroll
+    for (int k = 0; k < BL_CH / BL_RP_THREADS; k++) {
+      const int i = t + k * BL_RP_THREADS;
+      if (i < cnt) {
+        const float x = xs[i];
+        if (x > -1.0e30f) {
+          const uint64_t kk = ckey(x, i0 + i);
+          if (kk >= tau) {
+            const int pos = atomicAdd(&tk_n, 1);
+            if (pos < BL_TK_CAP) tkeys[pos] = kk;
+          }
+        }
+      }
+    }
+    __syncthreads();
+    const int nk = tk_n;
+    if (nk <= BL_TK_CAP) {
+      /* rank by counting; the K largest go out in order */
+      for (int q = t; q < nk; q += BL_RP_THREADS) {
+        const uint64_t kk = tkeys[q];
+        int rr = 0, j = 0;
+        for (; j + 4 <= nk; j += 4)
+          rr += (tkeys[j] > kk ? 1 : 0) + (tkeys[j + 1] > kk ? 1 : 0) + (tkeys[j + 2] > kk ? 1 : 0) +
+                (tkeys[j + 3] > kk ? 1 : 0);
+        for (; j < nk; j++) rr += tkeys[j] > kk ? 1 : 0;
+        if (rr < K) {
+          d.cand_v[cbase + rr] = ckey_v(kk);
+          d.cand_i[cbase + rr] = ckey_i(kk);
+        }
+      }
+      for (int q = nk + t; q < K; q += BL_RP_THREADS) {
+        d.cand_v[cbase + q] = BL_NEG_INF;
+        d.cand_i[cbase + q] = -1;
+      }
+      return;
+    }
+    __syncthreads();
+  }
   uint32_t prefix = 0u, pmask = 0u;
   int need = K;
   bool take_all = false;
@@ -321,7 +402,6 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass(bl_dev d, const fl
   /* take_all is uniform: every thread saw the same total */
   if (t == 0) out_n = 0;
   __syncthreads();
-  const int64_t cbase = ((int64_t)row * nc + c) * BL_KSEL_MAX;
   const uint32_t kth = prefix;
   const bool cut_ties = !take_all && (int)sel[2] > need;
   int eq_before = 0; /* ties of kth at smaller indices, for the index-order cut */
@@ -551,12 +631,6 @@ __global__ __launch_bounds__(BL_GM_THREADS) void bl_k_gmask(bl_dev d, bl_rows ro
 /* ------------------------------------------------------------------ K3: per-row selection */
 #define SEL_NW (BL_SEL_THREADS / 64)
 
-/* LDS-resident candidate list as composite keys: (fkey(value) << 32) | ~index, descending order */
-__device__ __forceinline__ uint64_t ckey(float v, int32_t id) {
-  return ((uint64_t)bl_fkey(v) << 32) | (uint64_t)(0xffffffffu - (uint32_t)id);
-}
-__device__ __forceinline__ float ckey_v(uint64_t k) { return bl_fkey_inv((uint32_t)(k >> 32)); }
-__device__ __forceinline__ int32_t ckey_i(uint64_t k) { return (int32_t)(0xffffffffu - (uint32_t)k); }
 
 __device__ void bitonic_desc(uint64_t *s, int P) {
   for (int k = 2; k <= P; k <<= 1)
