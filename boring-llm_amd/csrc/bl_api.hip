@@ -19,7 +19,7 @@
 #include "bl_workload.h"
 
 void bl_launch_step(const bl_dev &d, const float *logits, int64_t ld, const bl_rows &rows, int B, bool need_exp,
-                    bool need_gram, hipStream_t s, hipEvent_t *ev);
+                    bool need_gram, bool need_lp, hipStream_t s, hipEvent_t *ev);
 void bl_launch_gmask(const bl_dev &d, const bl_rows &rows, hipStream_t s);
 void bl_launch_synth(float *out, int64_t ld, int cfg, int64_t seed, int64_t step, int rows, int V, hipStream_t s);
 void bl_launch_math_digest(int fn, uint32_t first_block, int n_blocks, unsigned long long *out, hipStream_t s);
@@ -211,6 +211,7 @@ int bl_create(int device, int max_slots, int max_rows, int vocab, bl_ctx **out) 
   ALLOC(d.sortk, R * std::max(P2, 2 * V));
   ALLOC(d.gsum, R * G);
   ALLOC(d.gapx, R * G);
+  ALLOC(d.lse, R);
   d.gm_blocks = (vocab + BL_GM_THREADS - 1) / BL_GM_THREADS;
   ALLOC(d.gram, S);
   ALLOC(d.gmask, R * 2 * ((V + 63) / 64));
@@ -598,6 +599,12 @@ static bool needs_exp(bl_ctx *c, const int32_t *slots, int B) {
   return false;
 }
 
+static bool needs_lp(bl_ctx *c, const int32_t *slots, int B) {
+  for (int i = 0; i < B; i++)
+    if (c->host_slots[slots[i]].mode & BL_M_LOGPROBS) return true;
+  return false;
+}
+
 static int status_error(int st) {
   if (st & BL_SE_UNSUPPORTED) return fail(BL_EUNSUPPORTED, "a sampler stage outside the device path was reached");
   if (st & BL_SE_TIE) return fail(BL_ETIE, "the full-vocabulary draw landed on equal logits; heap order is not reproduced");
@@ -634,7 +641,8 @@ int bl_sample_step(bl_ctx *c, const int32_t *slots, int B, const float *d_logits
   HIPCHK(hipMemcpyAsync(c->d_slot, c->h_slot, B * sizeof(int32_t), hipMemcpyHostToDevice, c->stream));
   bl_rows rows = make_rows(c, false, 1, top_stride > 0 ? top_stride : 1);
   mark_stepped(c, slots, B);
-  bl_launch_step(c->d, d_logits, ld, rows, B, needs_exp(c, slots, B), needs_gram(c, slots, B), c->stream, nullptr);
+  bl_launch_step(c->d, d_logits, ld, rows, B, needs_exp(c, slots, B), needs_gram(c, slots, B), needs_lp(c, slots, B),
+                 c->stream, nullptr);
   HIPCHK(hipGetLastError());
   HIPCHK(hipMemcpyAsync(c->h_tok, c->d_tok, B * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));
   HIPCHK(hipMemcpyAsync(c->h_status, c->d_status, B * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));
@@ -680,7 +688,8 @@ int bl_sample_step_async(bl_ctx *c, int B, const float *d_logits, int64_t ld, in
       for (int k = 0; k < 4; k++) HIPCHK(hipEventCreate(&c->ev[k]));
     ev = c->ev;
   }
-  bl_launch_step(c->d, d_logits, ld, rows, B, needs_exp(c, c->h_slot, B), needs_gram(c, c->h_slot, B), c->stream, ev);
+  bl_launch_step(c->d, d_logits, ld, rows, B, needs_exp(c, c->h_slot, B), needs_gram(c, c->h_slot, B),
+                 needs_lp(c, c->h_slot, B), c->stream, ev);
   HIPCHK(hipGetLastError());
   if (ev) {
     /* per-kernel durations of this step, accumulated (the caller asked for timing: synchronous) */
@@ -732,10 +741,11 @@ int bl_spec_verify(bl_ctx *c, const int32_t *slots, int B, int k, const float *d
   HIPCHK(hipMemcpyAsync(c->d_slot, c->h_slot, R * sizeof(int32_t), hipMemcpyHostToDevice, c->stream));
   HIPCHK(hipMemcpyAsync(c->d_skip, c->h_skip, R * sizeof(int32_t), hipMemcpyHostToDevice, c->stream));
   bl_rows rows = make_rows(c, true, 0, 1);
+  rows.lp = nullptr; /* no logprobs are returned for speculative rows */
   bool ne = false;
   for (int b = 0; b < B; b++) ne |= (c->host_slots[slots[b]].mode & (BL_M_LOGPROBS | BL_M_FULL)) != 0;
   mark_stepped(c, slots, B);
-  bl_launch_step(c->d, d_rows, ld, rows, R, ne, false, c->stream, nullptr);
+  bl_launch_step(c->d, d_rows, ld, rows, R, ne, false, false, c->stream, nullptr);
   HIPCHK(hipGetLastError());
   HIPCHK(hipMemcpyAsync(c->h_tok, c->d_tok, R * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));
   HIPCHK(hipMemcpyAsync(c->h_status, c->d_status, R * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));

@@ -106,6 +106,7 @@ struct bl_dev {
   uint64_t *sortk;  /* [rows][2^ceil(log2 V)] global sort scratch */
   double *gsum;     /* [rows][V/64 + 64] */
   float *gapx;      /* [rows][V/64 + 64] approximate index-order sum before each 64-term group, then the total */
+  float *lse;       /* [rows] log of the index-order normaliser (logprob rows) */
   /* grammar-constrained sampling */
   bl_gram_view *gram; /* [slots] the slot's compiled grammar (device pointers) */
   const uint8_t *vblob;   /* vocabulary piece bytes */

@@ -12,10 +12,12 @@
  *                 index-order normaliser (src/sampling.br:254-266), and the candidates of a
  *                 full-vocabulary rank (every token within 17.5*max(T,1) of the max; the rest cannot
  *                 change any float32 sum of the chain).
- *   bl_k_select   grid (B) x 1024: greedy / top-k / full-vocabulary candidate sampling with exact
- *                 sequential sums (src/sampling.br:490-607), the draw from the slot's xorshift stream,
- *                 logprobs + alternatives (src/server.br:1027-1035), and the history commit
- *                 (src/server.br:1004, :1037).
+ *   bl_k_select   grid (B, 1 + logprobs) x 1024: greedy / top-k / full-vocabulary candidate sampling
+ *                 with exact sequential sums (src/sampling.br:490-607), the draw from the slot's
+ *                 xorshift stream, alternatives (src/server.br:1027-1035) and the history commit
+ *                 (src/server.br:1004, :1037); a second workgroup per logprob row computes the exact
+ *                 index-order normaliser (src/sampling.br:254-266).
+ *   bl_k_lpfinish grid (B) x 64: subtracts the log-normaliser from the token's and alternatives' x - max.
  * No MFMA: the work is bandwidth- and latency-bound scanning, selection and integer arithmetic.
  */
 #include <hip/hip_runtime.h>
@@ -1140,12 +1142,17 @@ __device__ float fast_normaliser(const bl_dev &d, int row, float M, sel_shared &
   return S;
 }
 
+/* blockIdx.y = 0: candidates, draw, outputs and commit; the logprobs it writes are x - max, and
+ * bl_k_lpfinish subtracts the log-normaliser that blockIdx.y = 1 computes for logprob rows (the two
+ * run side by side; the kernel boundary orders them) */
 __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows rows) {
   const int V = d.vocab, nc = d.nc;
   const int row = blockIdx.x, t = threadIdx.x, w = t >> 6, lane = t & 63;
   const int slot = rows.slot[row];
   bl_slot_dev &sp = d.slots[slot];
   const int mode = sp.mode;
+  const bool norm_role = blockIdx.y == 1;
+  if (norm_role && !((mode & BL_M_LOGPROBS) && rows.lp)) return; /* uniform over the workgroup */
   __shared__ sel_shared sh;
   int status = 0;
 
@@ -1159,10 +1166,13 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
   block_argmax<BL_SEL_THREADS>(M, Mi, sh.red_m, sh.red_i);
   if (Mi == 0x7fffffff) Mi = 0;
 
-  /* exact index-order normaliser (wave 0 walks the records written by the exponent pass) */
+  /* exact index-order normaliser over the records written by the exponent pass */
   const float *eff = d.eff + (int64_t)row * V;
-  float lse = 0.0f;
-  if (mode & BL_M_LOGPROBS) lse = (float)log((double)fast_normaliser(d, row, M, sh));
+  if (norm_role) {
+    const float lse = (float)log((double)fast_normaliser(d, row, M, sh));
+    if (t == 0) d.lse[row] = lse;
+    return;
+  }
 
   /* merged top-K candidates of the row pass: sorted (value desc, index asc) in sh.u.m.keys[0..K) */
   int n_top = 0;
@@ -1351,15 +1361,13 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
     bool is_eog = false;
     for (int k = 0; k < d.n_eog; k++) is_eog |= d.eog[k] == tok;
     if ((mode & BL_M_LOGPROBS) && rows.lp) {
-      float a = eff[tok] - M;
-      rows.lp[row] = a - lse;
+      rows.lp[row] = eff[tok] - M;
       for (int q = 0; q < sp.n_probs && q < rows.top_stride; q++) {
         uint64_t k = q < n_top ? sh.u.m.keys[q] : 0ull;
         int32_t id = k ? ckey_i(k) : 0;
         float v = k ? ckey_v(k) : -1.0e30f;
         rows.top_ids[(int64_t)row * rows.top_stride + q] = id;
-        float b = v - M;
-        rows.top_lp[(int64_t)row * rows.top_stride + q] = b - lse;
+        rows.top_lp[(int64_t)row * rows.top_stride + q] = v - M;
       }
     }
     if (rows.commit && status == 0) {
@@ -1398,6 +1406,20 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
   }
 }
 
+/* logprob = (x - max) - log(normaliser) (src/sampling.br:268-273, src/server.br:1027-1035) */
+__global__ void bl_k_lpfinish(bl_dev d, bl_rows rows) {
+  const int row = blockIdx.x;
+  const bl_slot_dev &sp = d.slots[rows.slot[row]];
+  if (!((sp.mode & BL_M_LOGPROBS) && rows.lp)) return;
+  const float lse = d.lse[row];
+  if (threadIdx.x == 0) rows.lp[row] = rows.lp[row] - lse;
+  const int n = sp.n_probs < rows.top_stride ? sp.n_probs : rows.top_stride;
+  for (int q = threadIdx.x; q < n; q += blockDim.x) {
+    float *o = rows.top_lp + (int64_t)row * rows.top_stride + q;
+    *o = *o - lse;
+  }
+}
+
 /* ------------------------------------------------------------------ synthetic inputs for the benchmark */
 __global__ void bl_k_synth(float *out, int64_t ld, int cfg, int64_t seed, int64_t step0, int rows, int V) {
   int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -1411,7 +1433,8 @@ __global__ void bl_k_synth(float *out, int64_t ld, int cfg, int64_t seed, int64_
 /* ------------------------------------------------------------------ host-side launchers */
 /* ev: optional 4 events recorded before/after the three kernels (kernel timing for the benchmark) */
 void bl_launch_step(const bl_dev &d, const float *logits, int64_t ld, const bl_rows &rows, int B, bool need_exp,
-                    bool need_gram, hipStream_t s, hipEvent_t *ev) {
+                    bool need_gram, bool need_lp, hipStream_t s, hipEvent_t *ev) {
+  need_lp = need_lp && rows.lp;
   dim3 g1(d.nc, B);
   if (ev) (void)hipEventRecord(ev[0], s);
   hipLaunchKernelGGL(bl_k_rowpass, g1, dim3(BL_RP_THREADS), 0, s, d, logits, ld, rows);
@@ -1421,7 +1444,8 @@ void bl_launch_step(const bl_dev &d, const float *logits, int64_t ld, const bl_r
     hipLaunchKernelGGL(bl_k_exppass, g1, dim3(BL_RP_THREADS), 0, s, d, rows);
   }
   if (ev) (void)hipEventRecord(ev[2], s);
-  hipLaunchKernelGGL(bl_k_select, dim3(B), dim3(BL_SEL_THREADS), 0, s, d, rows);
+  hipLaunchKernelGGL(bl_k_select, dim3(B, need_lp ? 2 : 1), dim3(BL_SEL_THREADS), 0, s, d, rows);
+  if (need_lp) hipLaunchKernelGGL(bl_k_lpfinish, dim3(B), dim3(64), 0, s, d, rows);
   if (ev) (void)hipEventRecord(ev[3], s);
 }
 
