@@ -197,7 +197,7 @@ int bl_create(int device, int max_slots, int max_rows, int vocab, bl_ctx **out) 
   ALLOC(d.eff, R * V);
   ALLOC(d.c_max, R * d.nc);
   ALLOC(d.c_arg, R * d.nc);
-  ALLOC(d.c_sum, R * d.nc);
+  ALLOC(d.c_bsum, R * d.nc * BL_SUBS);
   ALLOC(d.cand_v, R * d.nc * BL_KSEL_MAX);
   ALLOC(d.cand_i, R * d.nc * BL_KSEL_MAX);
   {

@@ -52,6 +52,13 @@ struct bl_grec {
   bl_inc v[3];
 };
 
+/* index-order group record: the composed automaton at the binade of the group's approximate start */
+struct bl_grec1 {
+  int32_t E;
+  uint32_t pad;
+  bl_inc v;
+};
+
 BL_SD bl_inc bl_inc_ident() { return bl_inc{0u, 0u}; }
 
 /* f then g */
@@ -187,13 +194,15 @@ __device__ __forceinline__ bl_inc bl_thread_compose(const float *a, int e) {
   return f;
 }
 
-/* ordered composition across the 4 lanes of a quad (lanes 4q..4q+3 hold consecutive runs); the
- * result is valid in every lane of the quad */
-__device__ __forceinline__ bl_inc bl_quad_compose(bl_inc f, int lane) {
-  bl_inc o = bl_inc{(uint32_t)__shfl_xor((int)f.d0, 1, 64), (uint32_t)__shfl_xor((int)f.d1, 1, 64)};
-  f = (lane & 1) ? bl_compose(o, f) : bl_compose(f, o);
-  o = bl_inc{(uint32_t)__shfl_xor((int)f.d0, 2, 64), (uint32_t)__shfl_xor((int)f.d1, 2, 64)};
-  f = (lane & 2) ? bl_compose(o, f) : bl_compose(f, o);
+/* ordered composition across L aligned consecutive lanes (lane L*q + i holds the i-th run); the result
+ * is valid in every lane of the L */
+template <int L>
+__device__ __forceinline__ bl_inc bl_lanes_compose(bl_inc f, int lane) {
+#pragma unroll
+  for (int k = 1; k < L; k <<= 1) {
+    const bl_inc o = bl_inc{(uint32_t)__shfl_xor((int)f.d0, k, 64), (uint32_t)__shfl_xor((int)f.d1, k, 64)};
+    f = (lane & k) ? bl_compose(o, f) : bl_compose(f, o);
+  }
   return f;
 }
 

@@ -24,6 +24,8 @@
 
 #define BL_CH 4096          /* vocabulary chunk per workgroup in the row passes */
 #define BL_RP_THREADS 256   /* row-pass workgroup */
+#define BL_EB 1024          /* exponent pass: terms per workgroup (4 per thread); the row pass sums per BL_EB */
+#define BL_SUBS (BL_CH / BL_EB)
 #define BL_SEL_THREADS 1024 /* per-row selection workgroup */
 #define BL_KSEL_MAX 256     /* largest per-chunk candidate count (top_k / n_probs) */
 #define BL_WCAP 8192        /* repeat window ring capacity */
@@ -96,7 +98,7 @@ struct bl_dev {
   float *eff;       /* [rows][V] transformed row */
   float *c_max;     /* [rows][nc] */
   int32_t *c_arg;   /* [rows][nc] */
-  float *c_sum;     /* [rows][nc] approximate sum of exp(x - c_max) */
+  float *c_bsum;    /* [rows][nc][BL_SUBS] approximate sums of exp(x - c_max) over each BL_EB positions */
   float *cand_v;    /* [rows][nc][KSEL_MAX] */
   int32_t *cand_i;
   void *grec;       /* [rows][2 * (V/64 + 64)] bl_grec: index-order records, then sorted-list records */

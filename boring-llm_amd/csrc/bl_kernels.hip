@@ -7,7 +7,7 @@
  *                 src/server.br:940-944, src/sampling.br:65-107,175-237), writes the transformed
  *                 row, and per chunk: max + first argmax, an approximate exp-sum, and the chunk's
  *                 top-K by (value desc, index asc) via a three-pass LDS radix select.
- *   bl_k_exppass  grid (chunks, B) x 256, rows with logprobs or full-vocabulary sampling: exact
+ *   bl_k_exppass  grid (V/1024, B) x 256, rows with logprobs or full-vocabulary sampling: exact
  *                 exp(x - max) terms (glibc-identical expf), the sequential-sum group records of the
  *                 index-order normaliser (src/sampling.br:254-266), and the candidates of a
  *                 full-vocabulary rank (every token within 17.5*max(T,1) of the max; the rest cannot
@@ -155,19 +155,18 @@ __device__ double block_excl_scan_d(double x, double *sd, double *total) {
 __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass(bl_dev d, const float *__restrict__ logits, int64_t ld,
                                                               bl_rows rows) {
   const int V = d.vocab, nc = d.nc;
-  const int c = blockIdx.x, row = blockIdx.y, t = threadIdx.x;
+  const int c = blockIdx.x, row = blockIdx.y, t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int slot = rows.slot[row];
   const bl_slot_dev &sp = slot_of(d, slot);
   __shared__ float xs[BL_CH];
   __shared__ uint32_t hist[2048];
   __shared__ float red_m[4];
   __shared__ int red_i[4];
-  __shared__ double red_d[4];
+  __shared__ double red_d[4 * BL_SUBS];
   __shared__ uint32_t sel[4];
   __shared__ int out_n;
-  __shared__ uint64_t tmax[BL_RP_THREADS];   /* each thread's largest order key */
   __shared__ uint64_t tkeys[BL_TK_CAP];      /* keys at or above the bound */
-  __shared__ uint64_t tk_tau;
+  __shared__ uint32_t tk_wb[BL_RP_THREADS / 64];
   __shared__ int tk_n;
 
   const int i0 = c * BL_CH;
@@ -189,137 +188,200 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass(bl_dev d, const fl
     }
     return x;
   };
-  if (cnt == BL_CH && (((uintptr_t)src) & 15) == 0) {
+  /* thread t owns the chunk positions j*1024 + 4t + q (j, q < 4): one float4 per 1024; positions past
+   * the row hold -inf */
+  constexpr int NV = BL_CH / (4 * BL_RP_THREADS);
+  auto pos_of = [&](int k) { return (k >> 2) * (4 * BL_RP_THREADS) + 4 * t + (k & 3); };
+  const bool vec = cnt == BL_CH && (((uintptr_t)src) & 15) == 0;
+  float x[4 * NV];
+  if (vec) {
 #pragma unroll
-    for (int j = 0; j < BL_CH / (4 * BL_RP_THREADS); j++) {
-      float4 v = reinterpret_cast<const float4 *>(src)[j * BL_RP_THREADS + t];
-      if (tail) {
-        v.x = finish(v.x);
-        v.y = finish(v.y);
-        v.z = finish(v.z);
-        v.w = finish(v.w);
-      }
-      reinterpret_cast<float4 *>(xs)[j * BL_RP_THREADS + t] = v;
+    for (int j = 0; j < NV; j++) {
+      const float4 v = reinterpret_cast<const float4 *>(src)[j * BL_RP_THREADS + t];
+      x[4 * j] = v.x;
+      x[4 * j + 1] = v.y;
+      x[4 * j + 2] = v.z;
+      x[4 * j + 3] = v.w;
     }
   } else {
-    for (int i = t; i < cnt; i += BL_RP_THREADS) xs[i] = tail ? finish(src[i]) : src[i];
+#pragma unroll
+    for (int k = 0; k < 4 * NV; k++) x[k] = pos_of(k) < cnt ? src[pos_of(k)] : BL_NEG_INF;
   }
-  __syncthreads();
-  /* server stages at the touched tokens of this chunk */
+  if (tail) {
+#pragma unroll
+    for (int k = 0; k < 4 * NV; k++)
+      if (pos_of(k) < cnt) x[k] = finish(x[k]);
+  }
+  /* server stages at the touched tokens among this thread's positions: each 4-position group lies in
+   * one word of the touched bitmap; every touched token's table entries are loaded before any is used */
   {
-    const uint32_t *tw = d.touched + (int64_t)slot * d.words + (i0 >> 5);
-    const int nwords = (cnt + 31) >> 5;
-    const int64_t so = (int64_t)slot * V;
-    const bool fp = sp.fp_on && sp.n_reply > 0;
-    const bool rp = sp.rep_on && sp.n_tokens > 0;
-    for (int w = t; w < nwords; w += BL_RP_THREADS) {
-      uint32_t bits = tw[w];
-      while (bits) {
-        int b = __ffs(bits) - 1;
-        bits &= bits - 1;
-        int li = w * 32 + b;
-        if (li >= cnt) break;
-        int64_t id = so + i0 + li;
-        float x = xs[li];
-        uint32_t f = d.flags[id];
-        if (f & BL_TF_BIAS) x = x + d.bias[id];
-        if (f & BL_TF_SUPPRESS) x = -1000000000.0f;
-        if (fp) {
-          int cc = d.cnt[id];
-          if (cc > 0) {
-            float tcf = (float)cc * sp.frequency_penalty;
-            x = x - tcf;
-            x = x - sp.presence_penalty;
-          }
+    const uint32_t *tw = d.touched + (int64_t)slot * d.words;
+    uint32_t tb[NV];
+    bool any = false;
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+      const int p = j * (4 * BL_RP_THREADS) + 4 * t;
+      tb[j] = p < cnt ? (tw[(i0 + p) >> 5] >> ((i0 + p) & 31)) & 0xFu : 0u;
+      any |= tb[j] != 0u;
+    }
+    if (any) {
+      const int64_t so = (int64_t)slot * V + i0;
+      const bool fp = sp.fp_on && sp.n_reply > 0;
+      const bool rp = sp.rep_on && sp.n_tokens > 0;
+      uint32_t f[4 * NV];
+      float bv[4 * NV];
+      int32_t cc[4 * NV], wc[4 * NV];
+#pragma unroll
+      for (int k = 0; k < 4 * NV; k++) {
+        const bool on = (tb[k >> 2] >> (k & 3)) & 1u;
+        const int64_t id = so + pos_of(k);
+        f[k] = on ? (uint32_t)d.flags[id] : 0u;
+        bv[k] = on ? d.bias[id] : 0.0f;
+        cc[k] = on && fp ? d.cnt[id] : 0;
+        wc[k] = on && rp ? d.wcnt[id] : 0;
+      }
+#pragma unroll
+      for (int k = 0; k < 4 * NV; k++) {
+        if (!((tb[k >> 2] >> (k & 3)) & 1u)) continue;
+        float v = x[k];
+        if (f[k] & BL_TF_BIAS) v = v + bv[k];
+        if (f[k] & BL_TF_SUPPRESS) v = -1000000000.0f;
+        if (cc[k] > 0) {
+          float tcf = (float)cc[k] * sp.frequency_penalty;
+          v = v - tcf;
+          v = v - sp.presence_penalty;
         }
-        if (rp && d.wcnt[id] > 0) x = x > 0.0f ? x / sp.repeat_penalty : x * sp.repeat_penalty;
-        xs[li] = x;
+        if (wc[k] > 0) v = v > 0.0f ? v / sp.repeat_penalty : v * sp.repeat_penalty;
+        x[k] = v;
       }
     }
   }
-  __syncthreads();
   /* transformed row */
   {
     float *dst = d.eff + (int64_t)row * V + i0;
-    if (cnt == BL_CH && (((uintptr_t)dst) & 15) == 0) {
+    if (vec && (((uintptr_t)dst) & 15) == 0) {
 #pragma unroll
-      for (int j = 0; j < BL_CH / (4 * BL_RP_THREADS); j++)
-        reinterpret_cast<float4 *>(dst)[j * BL_RP_THREADS + t] = reinterpret_cast<float4 *>(xs)[j * BL_RP_THREADS + t];
+      for (int j = 0; j < NV; j++)
+        reinterpret_cast<float4 *>(dst)[j * BL_RP_THREADS + t] = make_float4(x[4 * j], x[4 * j + 1], x[4 * j + 2], x[4 * j + 3]);
     } else {
-      for (int i = t; i < cnt; i += BL_RP_THREADS) dst[i] = xs[i];
+#pragma unroll
+      for (int k = 0; k < 4 * NV; k++)
+        if (pos_of(k) < cnt) dst[pos_of(k)] = x[k];
     }
   }
-  /* max, first argmax, approximate exp-sum */
-  float m = BL_NEG_INF;
-  int mi = 0x7fffffff;
-  for (int i = t; i < cnt; i += BL_RP_THREADS) {
-    float x = xs[i];
-    if (x > m) {
-      m = x;
-      mi = i;
+  /* max, first argmax, approximate exp-sums per BL_EB positions: per wavefront relative to the
+   * wavefront's maximum, then combined by thread 0 */
+  static_assert(NV == BL_SUBS, "thread positions j*1024 + ... cover sub-block j");
+  {
+    float m = BL_NEG_INF;
+    int mi = 0x7fffffff;
+#pragma unroll
+    for (int k = 0; k < 4 * NV; k++) /* positions ascend with k: the first maximum is kept */
+      if (x[k] > m) {
+        m = x[k];
+        mi = pos_of(k);
+      }
+#pragma unroll
+    for (int k = 32; k >= 1; k >>= 1) {
+      float m2 = __shfl_xor(m, k, 64);
+      int i2 = __shfl_xor(mi, k, 64);
+      argmax_merge(m, mi, m2, i2);
     }
-  }
-  block_argmax<BL_RP_THREADS>(m, mi, red_m, red_i);
-  double s = 0.0;
-  if (m > BL_NEG_INF)
-    for (int i = t; i < cnt; i += BL_RP_THREADS) s += (double)__expf(xs[i] - m);
-  s = block_sum_d<BL_RP_THREADS>(s, red_d);
-  if (t == 0) {
-    int64_t o = (int64_t)row * nc + c;
-    d.c_max[o] = m;
-    d.c_arg[o] = mi == 0x7fffffff ? i0 : i0 + mi;
-    d.c_sum[o] = (float)s;
+    double sj[NV];
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+      sj[j] = 0.0;
+      if (m > BL_NEG_INF) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) sj[j] += (double)__expf(x[4 * j + q] - m);
+      }
+      sj[j] = bl_wave_sum_d(sj[j]);
+    }
+    if (lane == 0) {
+      red_m[w] = m;
+      red_i[w] = mi;
+#pragma unroll
+      for (int j = 0; j < NV; j++) red_d[w * NV + j] = sj[j];
+    }
+    __syncthreads();
+    if (t == 0) {
+      float cm = red_m[0];
+      int ci = red_i[0];
+      for (int k = 1; k < BL_RP_THREADS / 64; k++) argmax_merge(cm, ci, red_m[k], red_i[k]);
+      double bs[NV];
+      for (int j = 0; j < NV; j++) bs[j] = 0.0;
+      if (cm > BL_NEG_INF)
+        for (int k = 0; k < BL_RP_THREADS / 64; k++)
+          if (red_m[k] > BL_NEG_INF) {
+            const double sc = exp((double)red_m[k] - (double)cm);
+            for (int j = 0; j < NV; j++) bs[j] += red_d[k * NV + j] * sc;
+          }
+      const int64_t o = (int64_t)row * nc + c;
+      d.c_max[o] = cm;
+      d.c_arg[o] = ci == 0x7fffffff ? i0 : i0 + ci;
+      for (int j = 0; j < NV; j++) d.c_bsum[o * BL_SUBS + j] = (float)bs[j];
+    }
   }
 
   /* chunk top-K by (value desc, index asc) over values > -1e30 (src/sampling.br:280-296). Order keys
-   * (value, then lower index) are distinct integers. Each thread's largest key is a value of the chunk,
-   * so the K-th largest of the 256 thread maxima bounds the chunk's K-th key from below: the keys at or
-   * above it (typically K to 2K of them) are compacted and ranked by counting. When too many reach the
-   * bound, three radix passes find the K-th key instead. */
+   * (value, then lower index) are distinct integers. A lower bound on the chunk's K-th value: wavefront w
+   * takes the s_w-th largest of its threads' maxima (each of those threads holds a value at or above
+   * it), with shares s_w proportional to its threads that hold positions of the row and summing to at
+   * least K, and the smallest of the bounds is the chunk's, so at least K values reach it. The keys of
+   * those values (typically K to 2K) are compacted and ranked by counting. A wavefront with fewer valid
+   * maxima than its share sets no bound; when too many values reach the bound, three radix passes find
+   * the K-th key instead. */
   const int K = sp.k_sel;
   if (K <= 0) return;
   const int64_t cbase = ((int64_t)row * nc + c) * BL_KSEL_MAX;
   {
-    uint64_t best = 0ull;
+    uint32_t best = 0u; /* this thread's largest valid value as an order key; 0: none */
 #pragma unroll
-    for (int k = 0; k < BL_CH / BL_RP_THREADS; k++) {
-      const int i = t + k * BL_RP_THREADS;
-      if (i < cnt) {
-        const float x = xs[i];
-        if (x > -1.0e30f) {
-          const uint64_t kk = ckey(x, i0 + i);
-          best = kk > best ? kk : best;
-        }
+    for (int k = 0; k < 4 * NV; k++)
+      if (x[k] > -1.0e30f) {
+        const uint32_t fk = bl_fkey(x[k]);
+        best = fk > best ? fk : best;
       }
-    }
-    tmax[t] = best;
-    if (t == 0) {
-      tk_tau = 0ull;
-      tk_n = 0;
-    }
-    __syncthreads();
-    int r = 0;
-    for (int j = 0; j < BL_RP_THREADS; j += 4)
-      r += (tmax[j] > best ? 1 : 0) + (tmax[j + 1] > best ? 1 : 0) + (tmax[j + 2] > best ? 1 : 0) +
-           (tmax[j + 3] > best ? 1 : 0);
-    if (best != 0ull && r == K - 1) tk_tau = best; /* fewer than K valid maxima: no bound (0) */
-    __syncthreads();
-    const uint64_t tau = tk_tau;
-    /* compaction of the keys >= tau, in no particular order */
+    /* threads holding a position of the row: 4t < cnt */
+    const int n_all = min((cnt + 3) >> 2, BL_RP_THREADS);
+    const int n_w = min(max(n_all - 64 * w, 0), 64);
+    const int share = n_all >= K ? (K * n_w + n_all - 1) / n_all : 64 + 1; /* > 64: no bound */
+    int nge = 0; /* threads of this wavefront whose maximum is at least this thread's */
+#pragma unroll 16
+    for (int i = 0; i < 64; i++) nge += (uint32_t)__builtin_amdgcn_readlane((int)best, i) >= best ? 1 : 0;
+    uint32_t wb = (best != 0u && nge >= share) ? best : 0u;
+    if (share == 0) wb = 0xFFFFFFFFu; /* no threads of the row: no part in the bound */
 #pragma unroll
-    for (int k = 0; k < BL_CH / BL_RP_THREADS; k++) {
-      const int i = t + k * BL_RP_THREADS;
-      if (i < cnt) {
-        const float x = xs[i];
-        if (x > -1.0e30f) {
-          const uint64_t kk = ckey(x, i0 + i);
-          if (kk >= tau) {
-            const int pos = atomicAdd(&tk_n, 1);
-            if (pos < BL_TK_CAP) tkeys[pos] = kk;
-          }
-        }
-      }
+    for (int k = 32; k >= 1; k >>= 1) {
+      const uint32_t o = (uint32_t)__shfl_xor((int)wb, k, 64);
+      wb = o > wb ? o : wb;
     }
+    if (lane == 0) tk_wb[w] = wb;
+    if (t == 0) tk_n = 0;
+    __syncthreads();
+    uint32_t tau = tk_wb[0];
+#pragma unroll
+    for (int k = 1; k < BL_RP_THREADS / 64; k++) tau = tk_wb[k] < tau ? tk_wb[k] : tau;
+    /* compaction of the keys >= tau, in no particular order; one LDS atomic per wavefront */
+    int mine = 0;
+#pragma unroll
+    for (int k = 0; k < 4 * NV; k++) mine += (x[k] > -1.0e30f && bl_fkey(x[k]) >= tau) ? 1 : 0;
+    int incl = mine;
+#pragma unroll
+    for (int k = 1; k < 64; k <<= 1) {
+      const int o = __shfl_up(incl, k, 64);
+      if (lane >= k) incl += o;
+    }
+    const int wtot = __shfl(incl, 63, 64);
+    int wbase = 0;
+    if (lane == 0 && wtot > 0) wbase = atomicAdd(&tk_n, wtot);
+    int pos = __shfl(wbase, 0, 64) + incl - mine;
+#pragma unroll
+    for (int k = 0; k < 4 * NV; k++)
+      if (x[k] > -1.0e30f && bl_fkey(x[k]) >= tau) {
+        if (pos < BL_TK_CAP) tkeys[pos] = ckey(x[k], i0 + pos_of(k));
+        pos++;
+      }
     __syncthreads();
     const int nk = tk_n;
     if (nk <= BL_TK_CAP) {
@@ -344,6 +406,11 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass(bl_dev d, const fl
     }
     __syncthreads();
   }
+  /* fallback: the values go to LDS for the radix passes */
+#pragma unroll
+  for (int j = 0; j < NV; j++)
+    reinterpret_cast<float4 *>(xs)[j * BL_RP_THREADS + t] = make_float4(x[4 * j], x[4 * j + 1], x[4 * j + 2], x[4 * j + 3]);
+  __syncthreads();
   uint32_t prefix = 0u, pmask = 0u;
   int need = K;
   bool take_all = false;
@@ -366,7 +433,6 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass(bl_dev d, const fl
     for (int q = 0; q < per; q++) local += hist[nb - 1 - (t * per + q)];
     /* exclusive scan of `local` over threads 0..255 */
     uint32_t inc = local;
-    int lane = t & 63, w = t >> 6;
 #pragma unroll
     for (int k = 1; k < 64; k <<= 1) {
       uint32_t o = __shfl_up(inc, k, 64);
@@ -421,7 +487,6 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass(bl_dev d, const fl
     }
     if (cut_ties) {
       unsigned long long bm = __ballot(eq);
-      int lane = t & 63, w = t >> 6;
       __shared__ int wcnt_eq[4];
       if (lane == 0) wcnt_eq[w] = __popcll(bm);
       __syncthreads();
@@ -449,76 +514,86 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass(bl_dev d, const fl
 }
 
 /* ------------------------------------------------------------------ K2: exponent pass */
-__device__ float row_max(const bl_dev &d, int row, float *sm, int *si) {
-  float m = BL_NEG_INF;
-  int mi = 0x7fffffff;
-  for (int k = threadIdx.x; k < d.nc; k += blockDim.x) argmax_merge(m, mi, d.c_max[(int64_t)row * d.nc + k], k);
-  block_argmax<BL_RP_THREADS>(m, mi, sm, si);
-  return m;
-}
-
+/* grid (ceil(V / BL_EB), B) x 256 over the rows with logprobs or a full-vocabulary rank; thread t holds
+ * the block's terms 4t..4t+3, a 64-term group is 16 threads */
 __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_exppass(bl_dev d, bl_rows rows) {
   const int V = d.vocab, nc = d.nc;
-  const int c = blockIdx.x, row = blockIdx.y, t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int b = blockIdx.x, row = blockIdx.y, t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int slot = rows.slot[row];
   const bl_slot_dev &sp = slot_of(d, slot);
   const int mode = sp.mode;
   if (!(mode & (BL_M_LOGPROBS | BL_M_FULL))) return;
-  __shared__ float red_m[4];
-  __shared__ int red_i[4];
-  __shared__ double red_d[4];
-  const int i0 = c * BL_CH;
-  const int cnt = min(BL_CH, V - i0);
-  /* this thread's 16 consecutive values (a wavefront reads 4 KB contiguously) */
-  const int j0 = t * 16;
-  float x[16];
+  __shared__ uint64_t s_tab[BL_EXP2_N]; /* expf's 2^(i/32) table */
+  __shared__ double wtot[BL_RP_THREADS / 64];
+  if (t < BL_EXP2_N) s_tab[t] = bl_exp2_tab[t];
+  const int i0 = b * BL_EB;
+  const int cnt = min(BL_EB, V - i0);
+  const int j0 = 4 * t;
+  float x[4];
   const float *src = d.eff + (int64_t)row * V + i0 + j0;
-  if (j0 + 16 <= cnt && (((uintptr_t)src) & 15) == 0) {
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-      float4 v = reinterpret_cast<const float4 *>(src)[q];
-      x[4 * q] = v.x;
-      x[4 * q + 1] = v.y;
-      x[4 * q + 2] = v.z;
-      x[4 * q + 3] = v.w;
-    }
+  if (j0 + 4 <= cnt && (((uintptr_t)src) & 15) == 0) {
+    const float4 v = *reinterpret_cast<const float4 *>(src);
+    x[0] = v.x;
+    x[1] = v.y;
+    x[2] = v.z;
+    x[3] = v.w;
   } else {
 #pragma unroll
-    for (int k = 0; k < 16; k++) x[k] = j0 + k < cnt ? src[k] : BL_NEG_INF;
+    for (int k = 0; k < 4; k++) x[k] = j0 + k < cnt ? src[k] : BL_NEG_INF;
   }
-  const float M = row_max(d, row, red_m, red_i);
+  /* the row maximum, by every wavefront from the chunk maxima */
+  float M = BL_NEG_INF;
+  for (int k = lane; k < nc; k += 64) {
+    const float cm = d.c_max[(int64_t)row * nc + k];
+    M = cm > M ? cm : M;
+  }
+#pragma unroll
+  for (int k = 32; k >= 1; k >>= 1) {
+    const float o = __shfl_xor(M, k, 64);
+    M = o > M ? o : M;
+  }
 
   if (mode & BL_M_LOGPROBS) {
-    /* approximate sum of the chunks before this one, from the row pass statistics */
+    /* approximate sum before this block, from the row pass's sums per BL_EB positions (every
+     * wavefront computes the same value) */
+    const int nsub = i0 / BL_EB;
     double part = 0.0;
-    for (int k = t; k < c; k += BL_RP_THREADS) {
-      float cm = d.c_max[(int64_t)row * nc + k];
-      if (cm > BL_NEG_INF) part += (double)d.c_sum[(int64_t)row * nc + k] * exp((double)cm - (double)M);
+    for (int q = lane; q < nsub; q += 64) {
+      const int k = q / BL_SUBS;
+      const float cm = d.c_max[(int64_t)row * nc + k];
+      if (cm > BL_NEG_INF) part += (double)d.c_bsum[(int64_t)row * nc * BL_SUBS + q] * exp((double)cm - (double)M);
     }
-    const double S0 = block_sum_d<BL_RP_THREADS>(part, red_d);
-    float a[16];
+    const double S0 = bl_wave_sum_d(part);
+    __syncthreads(); /* s_tab */
+    float a[4];
     double sa = 0.0;
 #pragma unroll
-    for (int k = 0; k < 16; k++) {
-      a[k] = j0 + k < cnt ? bl_expf(x[k] - M) : 0.0f;
+    for (int k = 0; k < 4; k++) {
+      a[k] = j0 + k < cnt ? bl_expf_tab(x[k] - M, [&](uint32_t i) { return s_tab[i]; }) : 0.0f;
       sa += (double)a[k];
     }
-    double tot;
-    const double before = S0 + block_excl_scan_d<BL_RP_THREADS>(sa, red_d, &tot);
-    /* group of 64 terms = 4 threads; its approximate start is its first thread's prefix */
-    const double gstart = __shfl(before, lane & ~3, 64);
-    bl_grec r;
+    const double ex = bl_wave_excl_scan_d(sa, lane);
+    if (lane == 63) wtot[w] = ex + sa;
+    __syncthreads();
+    double before = S0 + ex, tot = 0.0;
+    for (int q = 0; q < BL_RP_THREADS / 64; q++) {
+      if (q < w) before += wtot[q];
+      tot += wtot[q];
+    }
+    /* group of 64 terms = 16 threads; its approximate start is its first thread's prefix */
+    const double gstart = __shfl(before, lane & ~15, 64);
+    bl_grec1 r;
     r.E = bl_binade_of(gstart);
     r.pad = 0;
-#pragma unroll
-    for (int k = 0; k < 3; k++) r.v[k] = bl_quad_compose(bl_thread_compose<16>(a, r.E - 1 + k), lane);
-    bl_grec *rec = reinterpret_cast<bl_grec *>(d.grec) + (int64_t)row * 2 * (V / 64 + 64) + (int64_t)c * 64;
+    r.v = bl_lanes_compose<16>(bl_thread_compose<4>(a, r.E), lane);
+    const int g = (i0 + j0) >> 6;
+    bl_grec1 *rec = reinterpret_cast<bl_grec1 *>(reinterpret_cast<bl_grec *>(d.grec) + (int64_t)row * 2 * (V / 64 + 64));
     float *apx = d.gapx + (int64_t)row * (V / 64 + 64);
-    if ((lane & 3) == 0 && j0 < cnt) {
-      rec[t >> 2] = r;
-      apx[c * 64 + (t >> 2)] = (float)gstart;
+    if ((lane & 15) == 0 && j0 < cnt) {
+      rec[g] = r;
+      apx[g] = (float)gstart;
     }
-    if (c == nc - 1 && t == BL_RP_THREADS - 1) apx[(V + 63) / 64] = (float)(S0 + tot); /* the row's total */
+    if (i0 + BL_EB >= V && t == BL_RP_THREADS - 1) apx[(V + 63) / 64] = (float)(S0 + tot); /* the row's total */
   }
   if (mode & BL_M_FULL) {
     /* candidates of a full-vocabulary rank: every value within 17.5*max(T,1) of the maximum; one
@@ -527,20 +602,20 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_exppass(bl_dev d, bl_rows 
     const float thr = M - 17.5f * (T > 1.0f ? T : 1.0f);
     int mine = 0;
 #pragma unroll
-    for (int k = 0; k < 16; k++) mine += (j0 + k < cnt && x[k] >= thr) ? 1 : 0;
+    for (int k = 0; k < 4; k++) mine += (j0 + k < cnt && x[k] >= thr) ? 1 : 0;
     int incl = mine;
 #pragma unroll
     for (int k = 1; k < 64; k <<= 1) {
       int o = __shfl_up(incl, k, 64);
       if (lane >= k) incl += o;
     }
-    const int wtot = __shfl(incl, 63, 64);
+    const int wtot_n = __shfl(incl, 63, 64);
     int base = 0;
-    if (lane == 0 && wtot > 0) base = atomicAdd(&d.full_n[row], wtot);
+    if (lane == 0 && wtot_n > 0) base = atomicAdd(&d.full_n[row], wtot_n);
     base = __shfl(base, 0, 64);
     int pos = base + incl - mine;
 #pragma unroll
-    for (int k = 0; k < 16; k++)
+    for (int k = 0; k < 4; k++)
       if (j0 + k < cnt && x[k] >= thr) {
         if (pos < V) {
           d.full_v[(int64_t)row * V + pos] = x[k];
@@ -975,12 +1050,13 @@ __device__ void walk_groups(int64_t g_lo, int64_t g_hi, int64_t n, TermF term, R
 __device__ float fast_normaliser(const bl_dev &d, int row, float M, sel_shared &sh) {
   const int V = d.vocab, t = threadIdx.x, w = t >> 6, lane = t & 63;
   const int G = (V + 63) / 64;
-  const bl_grec *rec = reinterpret_cast<const bl_grec *>(d.grec) + (int64_t)row * 2 * (V / 64 + 64);
+  const bl_grec1 *rec =
+      reinterpret_cast<const bl_grec1 *>(reinterpret_cast<const bl_grec *>(d.grec) + (int64_t)row * 2 * (V / 64 + 64));
   const float *apx = d.gapx + (int64_t)row * (V / 64 + 64);
   const float *eff = d.eff + (int64_t)row * V;
   sel_norm &nm = sh.u.n;
   auto e_of = [&](int g) -> int { return g < BL_STAGE_G ? (int)nm.sE[g] : rec[g].E; };
-  auto v_of = [&](int g) -> bl_inc { return g < BL_STAGE_G ? nm.sV[g] : rec[g].v[1]; };
+  auto v_of = [&](int g) -> bl_inc { return g < BL_STAGE_G ? nm.sV[g] : rec[g].v; };
   if (t == 0) nm.ncrit = 0;
   __syncthreads();
   /* 1. critical groups in order (ballot compaction); every load of a sweep is issued first */
@@ -994,7 +1070,7 @@ __device__ float fast_normaliser(const bl_dev &d, int row, float M, sel_shared &
       const int g = base + k * BL_SEL_THREADS + t;
       if (g < G) {
         Eg[k] = rec[g].E;
-        gv[k] = rec[g].v[1];
+        gv[k] = rec[g].v;
         ga[k] = apx[g];
         gb[k] = apx[g + 1];
       }
@@ -1099,7 +1175,11 @@ __device__ float fast_normaliser(const bl_dev &d, int row, float M, sel_shared &
     int e = BL_E_MIN;
     uint32_t N = 0u;
     auto term = [&](int64_t j) { return bl_expf(eff[j] - M); };
-    auto recf = [&](int64_t g) { return rec[g]; };
+    /* a record holds its own binade only: a neighbouring binade reads as saturated (element level) */
+    auto recf = [&](int64_t g) {
+      const bl_grec1 r1 = rec[g];
+      return bl_grec{r1.E, 0u, {bl_inc{BL_SAT, BL_SAT}, r1.v, bl_inc{BL_SAT, BL_SAT}}};
+    };
     for (int r = 0; r <= ncrit; r++) {
       for (int pi = nm.run_p0[r]; pi < nm.run_p0[r + 1]; pi++) {
         const uint32_t N2 = bl_apply(nm.p_f[pi], N);
@@ -1441,7 +1521,7 @@ void bl_launch_step(const bl_dev &d, const float *logits, int64_t ld, const bl_r
   if (ev) (void)hipEventRecord(ev[1], s);
   if (need_gram) hipLaunchKernelGGL(bl_k_gmask, dim3(d.gm_blocks, B), dim3(BL_GM_THREADS), 0, s, d, rows, 1);
   if (need_exp) {
-    hipLaunchKernelGGL(bl_k_exppass, g1, dim3(BL_RP_THREADS), 0, s, d, rows);
+    hipLaunchKernelGGL(bl_k_exppass, dim3((d.vocab + BL_EB - 1) / BL_EB, B), dim3(BL_RP_THREADS), 0, s, d, rows);
   }
   if (ev) (void)hipEventRecord(ev[2], s);
   hipLaunchKernelGGL(bl_k_select, dim3(B, need_lp ? 2 : 1), dim3(BL_SEL_THREADS), 0, s, d, rows);

@@ -75,7 +75,9 @@ const uint64_t bl_exp2_tab[BL_EXP2_N] = {
     0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
 
-BL_FN float bl_expf(float x) {
+/* expf with the 2^(i/32) table read through tab(i) (a kernel may stage the table in LDS) */
+template <class Tab>
+BL_FN float bl_expf_tab(float x, Tab tab) {
   /* polynomial for 2^(r/N) - 1 on |r| <= 1/2 (coefficients of the published algorithm, scaled by N) */
   const double N = (double)BL_EXP2_N;
   const double C0 = 0x1.c6af84b912394p-5 / N / N / N, C1 = 0x1.ebfce50fac4f3p-3 / N / N,
@@ -94,7 +96,7 @@ BL_FN float bl_expf(float x) {
   uint64_t ki = bl_d2u(kd);
   kd -= SHIFT;
   double r = BL_FMA(INVLN2N, xd, -kd);
-  uint64_t t = bl_exp2_tab[ki % BL_EXP2_N];
+  uint64_t t = tab((uint32_t)(ki % BL_EXP2_N));
   t += ki << (52 - BL_EXP2_BITS);
   double s = bl_u2d(t);
   double z = BL_FMA(C0, r, C1);
@@ -103,6 +105,10 @@ BL_FN float bl_expf(float x) {
   y = BL_FMA(z, r2, y);
   y = y * s;
   return (float)y;
+}
+
+BL_FN float bl_expf(float x) {
+  return bl_expf_tab(x, [](uint32_t i) { return bl_exp2_tab[i]; });
 }
 
 /* ---------------- expm1f / tanhf (float arithmetic) ---------------- */

@@ -63,7 +63,9 @@ def lp_close(a, b):
     return abs(a - b) <= LP_RTOL * max(abs(a), abs(b)) or abs(a - b) <= 1e-7
 
 
-def run_small(BL, case, steps):
+def run_small(BL, case, steps, coarse=False):
+    """A small case against the oracle; `coarse` floors the logits to a few integers, so that thousands of
+    values tie at the chunk top-K bound (the radix fallback with an index-order cut of the ties)."""
     kw = CASES[case]
     rng, hist, reply, bias = small_case_inputs(case)
     ctx = BL.Context(SMALL_V, 2, 2)
@@ -82,6 +84,8 @@ def run_small(BL, case, steps):
     try:
         for t in range(steps):
             x = small_case_logits(rng)
+            if coarse:
+                x = np.floor(x / np.float32(5.0)).astype(np.float32)
             buf.upload(x)
             tok, lp, ti, tl = ctx.sample_step([1], buf.ptr, SMALL_V, top_stride=max(n_probs, 1))
             ot, olp = np.zeros(1, np.int32), np.zeros(1, np.float32)
@@ -467,6 +471,9 @@ def main():
         if kind == "small":
             for c in parse_range(f[1]):
                 results.append((f"small case {c}", run_small(BL, c, int(f[2]) if len(f) > 2 else 25)))
+        elif kind == "coarse":
+            for c in parse_range(f[1]):
+                results.append((f"coarse case {c}", run_small(BL, c, int(f[2]) if len(f) > 2 else 25, coarse=True)))
         elif kind == "w2":
             results.append(("workload 2", run_w2(BL, int(f[1]))))
         elif kind == "w4":

@@ -38,6 +38,7 @@ struct dim3 {
 struct alignas(16) float4 {
   float x, y, z, w;
 };
+inline float4 make_float4(float x, float y, float z, float w) { return float4{x, y, z, w}; }
 
 namespace simt {
 struct Block;

@@ -1,7 +1,8 @@
 """GPU parity of kernel paths beyond the fixed workloads, through the shared harness with device buffers:
 top_k 250 with 256 logprob alternatives at V=151936 (38 chunks x 256 candidates per row, the merged
 list found by radix selection), two small configurations stepped as rows 0 and 1 of an odd-length
-vocabulary (row 1 not 16-byte aligned), and the bound-rows asynchronous step against the synchronous one."""
+vocabulary (row 1 not 16-byte aligned), small configurations on logits floored to a few integers (thousands
+of ties at each chunk's top-K bound), and the bound-rows asynchronous step against the synchronous one."""
 import os
 import sys
 
@@ -36,6 +37,13 @@ def test_large_top_k_and_alternatives():
 def test_two_rows_odd_vocabulary(pair):
     print(f"small cases {pair} stepped together, V=5003: 25 steps", flush=True)
     err = RP.run_pair(BL, pair[0], pair[1], 25)
+    assert err is None, err
+
+
+@pytest.mark.parametrize("case", [0, 1, 4, 5, 8, 10])
+def test_coarse_logits_tie_at_the_bound(case):
+    print(f"small case {case}, logits floored to a few integers: 20 steps", flush=True)
+    err = RP.run_small(BL, case, 20, coarse=True)
     assert err is None, err
 
 
