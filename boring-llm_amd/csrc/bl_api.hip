@@ -212,6 +212,13 @@ int bl_create(int device, int max_slots, int max_rows, int vocab, bl_ctx **out) 
   ALLOC(d.gsum, R * G);
   ALLOC(d.gapx, R * G);
   ALLOC(d.lse, R);
+  d.nb = (vocab + BL_EB - 1) / BL_EB;
+  {
+    char *b = nullptr;
+    ALLOC(b, R * d.nb * 16);
+    d.brec = b;
+  }
+  ALLOC(d.bcrit, R * d.nb);
   d.gm_blocks = (vocab + BL_GM_THREADS - 1) / BL_GM_THREADS;
   ALLOC(d.gram, S);
   ALLOC(d.gmask, R * 2 * ((V + 63) / 64));

@@ -116,6 +116,14 @@ BL_SD int bl_binade_of(double s) {
   return e;
 }
 
+/* a 64-term group whose approximate start ga and end gb are not both safely (2^-20 relative) inside its
+ * predicted binade E: the exact sum may cross a power of two within it */
+BL_SD bool bl_group_critical(float ga, float gb, int E) {
+  const float lo = 0.99999904632568359375f, hi = 1.00000095367431640625f; /* 1 -+ 2^-20 */
+  return bl_binade_of((double)ga * lo) != E || bl_binade_of((double)ga * hi) != E ||
+         bl_binade_of((double)gb * lo) != E || bl_binade_of((double)gb * hi) != E;
+}
+
 #if defined(__HIPCC__)
 /* ---- wave primitives (wavefront of 64) ---- */
 __device__ __forceinline__ bl_inc bl_shfl_up(bl_inc v, int k) {

@@ -33,10 +33,8 @@
 #define BL_MAX_CHUNKS 1024  /* vocabulary up to BL_MAX_CHUNKS * BL_CH tokens */
 #define BL_SERIAL_MAX 512   /* candidate lists up to this length are summed by one lane */
 #define BL_CRIT_MAX 32      /* critical groups the fast normaliser precomputes (terms + two scans in LDS) */
-#define BL_PIECE 128        /* groups per piece of a run (at least) */
-#define BL_PIECES_MAX 128   /* pieces of the fast normaliser: 64 + BL_CRIT_MAX + 1 at most */
 #define BL_TK_CAP 1024      /* chunk top-K: keys at or above the thread-maximum bound ranked in LDS */
-#define BL_STAGE_G 4096     /* group records staged in LDS by the fast normaliser (V up to 262144) */
+#define BL_STAGE_B 1024     /* block summaries staged in LDS by the fast normaliser (V up to 1M) */
 
 /* per-token flags */
 #define BL_TF_BIAS 1u
@@ -109,6 +107,10 @@ struct bl_dev {
   double *gsum;     /* [rows][V/64 + 64] */
   float *gapx;      /* [rows][V/64 + 64] approximate index-order sum before each 64-term group, then the total */
   float *lse;       /* [rows] log of the index-order normaliser (logprob rows) */
+  void *brec;       /* [rows][nb] bl_grec1 per BL_EB terms: the block's binade and composed automaton, or
+                       BL_E_NONE when it holds a critical group or two binades */
+  uint32_t *bcrit;  /* [rows][nb] the block's critical groups (bit i: group 16 b + i) */
+  int32_t nb;       /* ceil(V / BL_EB) */
   /* grammar-constrained sampling */
   bl_gram_view *gram; /* [slots] the slot's compiled grammar (device pointers) */
   const uint8_t *vblob;   /* vocabulary piece bytes */

@@ -525,6 +525,10 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_exppass(bl_dev d, bl_rows 
   if (!(mode & (BL_M_LOGPROBS | BL_M_FULL))) return;
   __shared__ uint64_t s_tab[BL_EXP2_N]; /* expf's 2^(i/32) table */
   __shared__ double wtot[BL_RP_THREADS / 64];
+  __shared__ uint32_t bs_crit[BL_RP_THREADS / 64];
+  __shared__ int bs_E[BL_RP_THREADS / 64];
+  __shared__ bool bs_same[BL_RP_THREADS / 64];
+  __shared__ bl_inc bs_v[BL_RP_THREADS / 64];
   if (t < BL_EXP2_N) s_tab[t] = bl_exp2_tab[t];
   const int i0 = b * BL_EB;
   const int cnt = min(BL_EB, V - i0);
@@ -594,6 +598,51 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_exppass(bl_dev d, bl_rows 
       apx[g] = (float)gstart;
     }
     if (i0 + BL_EB >= V && t == BL_RP_THREADS - 1) apx[(V + 63) / 64] = (float)(S0 + tot); /* the row's total */
+    /* block summary for the normaliser: the critical groups (approximate start or end not safely inside
+     * the predicted binade), and, when there is none and every group has the same binade, the block's
+     * automaton composed in order (wavefront w holds groups 4w..4w+3) */
+    const int gl = lane & ~15;
+    const double wend = __shfl(before + sa, 63, 64);
+    const double nxt = __shfl(before, gl + 16 < 64 ? gl + 16 : 63, 64);
+    const double gend = gl + 16 < 64 ? nxt : wend;
+    const bool gex = 4 * (t & ~15) < cnt;
+    const bool crit = gex && bl_group_critical((float)gstart, (float)gend, r.E);
+    const bool head = (lane & 15) == 0;
+    const unsigned long long cb = __ballot(crit && head);
+    const unsigned long long eb = __ballot(gex && head);
+    const int E0 = __shfl(r.E, 0, 64);
+    const unsigned long long db = __ballot(gex && head && r.E != E0);
+    bl_inc f = gex ? r.v : bl_inc_ident();
+#pragma unroll
+    for (int k = 16; k < 64; k <<= 1) {
+      const bl_inc o = bl_inc{(uint32_t)__shfl_xor((int)f.d0, k, 64), (uint32_t)__shfl_xor((int)f.d1, k, 64)};
+      f = (lane & k) ? bl_compose(o, f) : bl_compose(f, o);
+    }
+    if (lane == 0) {
+      bs_crit[w] = (uint32_t)((cb & 1ull) | ((cb >> 15) & 2ull) | ((cb >> 30) & 4ull) | ((cb >> 45) & 8ull));
+      bs_E[w] = (eb & 1ull) ? E0 : BL_E_NONE; /* BL_E_NONE: the wavefront holds no group */
+      bs_same[w] = db == 0ull;
+      bs_v[w] = f;
+    }
+    __syncthreads();
+    if (t == 0) {
+      uint32_t mask = 0u;
+      const int Eb = bs_E[0];
+      bool clean = true;
+      bl_inc v = bl_inc_ident();
+      for (int q = 0; q < BL_RP_THREADS / 64; q++) {
+        mask |= bs_crit[q] << (4 * q);
+        if (bs_E[q] == BL_E_NONE) continue;
+        clean = clean && bs_same[q] && bs_E[q] == Eb;
+        v = bl_compose(v, bs_v[q]);
+      }
+      bl_grec1 br;
+      br.E = clean && mask == 0u ? Eb : BL_E_NONE;
+      br.pad = 0;
+      br.v = v;
+      reinterpret_cast<bl_grec1 *>(d.brec)[(int64_t)row * d.nb + b] = br;
+      d.bcrit[(int64_t)row * d.nb + b] = mask;
+    }
   }
   if (mode & BL_M_FULL) {
     /* candidates of a full-vocabulary rank: every value within 17.5*max(T,1) of the maximum; one
@@ -760,20 +809,19 @@ __device__ void block_records(int64_t n, TermF term, bl_grec *recs, double *gsum
   __syncthreads();
 }
 
-/* the fast normaliser's working set (live before the top-K merge) */
+/* the fast normaliser's working set */
 struct sel_norm {
-  int16_t sE[BL_STAGE_G];              /* each group's binade */
-  bl_inc sV[BL_STAGE_G];               /* each group's composed automaton at its own binade */
+  int32_t bE[BL_STAGE_B];              /* each block's binade, BL_E_NONE when not composable as a whole */
+  bl_inc bV[BL_STAGE_B];               /* each block's composed automaton */
   float terms[BL_CRIT_MAX * 64];       /* the critical groups' terms */
   bl_inc cp[BL_CRIT_MAX * 64];         /* their prefix scans at the predicted start binade */
   bl_inc cs[BL_CRIT_MAX * 65];         /* their suffix scans at the predicted end binade (+ identity) */
   int ce0[BL_CRIT_MAX], ce1[BL_CRIT_MAX]; /* those binades */
   int crit[BL_CRIT_MAX];               /* critical groups, ascending */
-  int p_lo[BL_PIECES_MAX], p_hi[BL_PIECES_MAX], p_e[BL_PIECES_MAX]; /* pieces of runs (<= BL_PIECE groups) */
-  bl_inc p_f[BL_PIECES_MAX];
-  int run_p0[BL_CRIT_MAX + 2];         /* first piece of each run */
+  int r_E[BL_CRIT_MAX + 1];            /* runs between them: predicted binade */
+  int r_st[BL_CRIT_MAX + 1];           /* 0 empty, 1 composed in one binade, 2 not composable */
+  bl_inc r_f[BL_CRIT_MAX + 1];         /* composed automaton */
   int cw[SEL_NW];
-  int ncrit, npieces;
   float S;
 };
 /* the top-K merge and the selection (live after the normaliser) */
@@ -1037,140 +1085,131 @@ __device__ void walk_groups(int64_t g_lo, int64_t g_hi, int64_t n, TermF term, R
 
 /*
  * Exact index-order sum of exp(eff[j] - M), j < V (logprob_normalizer, src/sampling.br:254-266), by the
- * whole block. The exponent pass left, per 64-term group, the composed automaton for the binades around
- * its approximate start, and that approximate start. Groups whose approximate start and end lie in one
- * binade, away from its edges, form runs; the runs are cut into pieces of at most `plen` groups that the
- * wavefronts compose in parallel. The other ("critical") groups, where the sum crosses a power of two,
- * get their terms and, for the binades predicted at their start and end, a prefix scan and a suffix scan
- * of their automata. One wavefront then chains pieces and critical groups: a piece applies at once when
- * the exact state is in its binade and stays there; a critical group needs one ballot for the crossing,
- * one real float add and the suffix. Every prediction is checked on the exact state, and a piece or group
- * whose prediction fails is walked element by element instead.
+ * whole block. The exponent pass left, per 64-term group, the composed automaton at the binade of its
+ * approximate start, and per 1024-term block the groups where the sum may cross a power of two
+ * ("critical") and, for a block without them, the block's composed automaton. The groups between two
+ * critical groups form a run in one binade; the wavefronts compose the runs (edge groups, then whole
+ * blocks) and, for each critical group, its terms and, for the binades predicted at its start and end,
+ * a prefix scan and a suffix scan of their automata. One wavefront then chains runs and critical groups:
+ * a run applies at once when the exact state is in its binade and stays there; a critical group needs
+ * one ballot for the crossing, one real float add and the suffix. Every prediction is checked on the
+ * exact state, and a run or group whose prediction fails is walked group by group and element by
+ * element instead.
  */
 __device__ float fast_normaliser(const bl_dev &d, int row, float M, sel_shared &sh) {
   const int V = d.vocab, t = threadIdx.x, w = t >> 6, lane = t & 63;
-  const int G = (V + 63) / 64;
+  const int G = (V + 63) / 64, NB = d.nb;
   const bl_grec1 *rec =
       reinterpret_cast<const bl_grec1 *>(reinterpret_cast<const bl_grec *>(d.grec) + (int64_t)row * 2 * (V / 64 + 64));
+  const bl_grec1 *brec = reinterpret_cast<const bl_grec1 *>(d.brec) + (int64_t)row * NB;
+  const uint32_t *bcrit = d.bcrit + (int64_t)row * NB;
   const float *apx = d.gapx + (int64_t)row * (V / 64 + 64);
   const float *eff = d.eff + (int64_t)row * V;
   sel_norm &nm = sh.u.n;
-  auto e_of = [&](int g) -> int { return g < BL_STAGE_G ? (int)nm.sE[g] : rec[g].E; };
-  auto v_of = [&](int g) -> bl_inc { return g < BL_STAGE_G ? nm.sV[g] : rec[g].v; };
-  if (t == 0) nm.ncrit = 0;
-  __syncthreads();
-  /* 1. critical groups in order (ballot compaction); every load of a sweep is issued first */
-  constexpr int RPT = 4;
-  for (int base = 0; base < G; base += RPT * BL_SEL_THREADS) {
-    int Eg[RPT];
-    float ga[RPT], gb[RPT];
-    bl_inc gv[RPT];
-#pragma unroll
-    for (int k = 0; k < RPT; k++) {
-      const int g = base + k * BL_SEL_THREADS + t;
-      if (g < G) {
-        Eg[k] = rec[g].E;
-        gv[k] = rec[g].v;
-        ga[k] = apx[g];
-        gb[k] = apx[g + 1];
+  /* 1. critical groups in order (a block-wide scan of the per-block counts); block summaries to LDS */
+  int ncrit_all = 0;
+  for (int b0 = 0; b0 < NB; b0 += BL_SEL_THREADS) {
+    const int b = b0 + t;
+    uint32_t m = 0u;
+    if (b < NB) {
+      m = bcrit[b];
+      if (b < BL_STAGE_B) {
+        const bl_grec1 br = brec[b];
+        nm.bE[b] = br.E;
+        nm.bV[b] = br.v;
       }
     }
-#pragma unroll
-    for (int k = 0; k < RPT; k++) {
-      const int g = base + k * BL_SEL_THREADS + t;
-      bool crit = false;
-      if (g < G) {
-        if (g < BL_STAGE_G) {
-          nm.sE[g] = (int16_t)Eg[k];
-          nm.sV[g] = gv[k];
-        }
-        const float lo = 0.99999904632568359375f, hi = 1.00000095367431640625f; /* 1 -+ 2^-20 */
-        const int E = Eg[k];
-        crit = bl_binade_of((double)ga[k] * lo) != E || bl_binade_of((double)ga[k] * hi) != E ||
-               bl_binade_of((double)gb[k] * lo) != E || bl_binade_of((double)gb[k] * hi) != E;
-      }
-      const unsigned long long m = __ballot(crit);
-      if (lane == 0) nm.cw[w] = __popcll(m);
-      __syncthreads();
-      int off = nm.ncrit;
-      for (int q = 0; q < w; q++) off += nm.cw[q];
-      if (crit) {
-        const int idx = off + __popcll(m & ((1ull << lane) - 1ull));
-        if (idx < BL_CRIT_MAX) nm.crit[idx] = g;
-      }
-      __syncthreads();
-      if (t == 0) {
-        int tot = 0;
-        for (int q = 0; q < SEL_NW; q++) tot += nm.cw[q];
-        nm.ncrit += tot;
-      }
-      __syncthreads();
-    }
-  }
-  /* past BL_CRIT_MAX critical groups the last run holds the rest (and its pieces fail their checks) */
-  const int ncrit = nm.ncrit < BL_CRIT_MAX ? nm.ncrit : BL_CRIT_MAX;
-  /* 2. runs cut into pieces; plen keeps the count within BL_PIECES_MAX */
-  const int plen = (G + 63) / 64 > BL_PIECE ? (G + 63) / 64 : BL_PIECE;
-  if (t == 0) {
-    int np = 0;
-    for (int r = 0; r <= ncrit; r++) {
-      nm.run_p0[r] = np;
-      const int lo = r == 0 ? 0 : nm.crit[r - 1] + 1;
-      const int hi = r == ncrit ? G : nm.crit[r];
-      for (int q = lo; q < hi && np < BL_PIECES_MAX; q += plen) {
-        nm.p_lo[np] = q;
-        nm.p_hi[np] = q + plen < hi ? q + plen : hi;
-        np++;
-      }
-    }
-    nm.run_p0[ncrit + 1] = np;
-    nm.npieces = np;
-  }
-  __syncthreads();
-  for (int pi = w; pi < nm.npieces; pi += SEL_NW) {
-    const int lo = nm.p_lo[pi], hi = nm.p_hi[pi];
-    const int E = e_of(lo);
-    bl_inc acc = bl_inc_ident();
-    bool bad = false;
-    for (int g0 = lo; g0 < hi; g0 += 64) {
-      const int g = g0 + lane;
-      bl_inc f = bl_inc_ident();
-      if (g < hi) {
-        bad |= e_of(g) != E;
-        f = v_of(g);
-      }
-      acc = bl_compose(acc, bl_wave_reduce(f, lane));
-    }
-    const bool any_bad = __ballot(bad) != 0ull;
-    if (lane == 0) {
-      nm.p_f[pi] = acc;
-      nm.p_e[pi] = any_bad ? BL_E_NONE : E;
-    }
-  }
-  /* 3. critical groups: terms, predicted start/end binades, prefix scan and suffix scan */
-  for (int ci = w; ci < ncrit; ci += SEL_NW) {
-    const int g = nm.crit[ci];
-    const int64_t j = (int64_t)g * 64 + lane;
-    const bool in = j < V;
-    const float a = in ? bl_expf(eff[j] - M) : 0.0f;
-    const int e0 = e_of(g), e1 = bl_binade_of((double)apx[g + 1]);
-    nm.terms[ci * 64 + lane] = a;
-    nm.cp[ci * 64 + lane] = bl_wave_scan(in ? bl_term_inc(a, e0) : bl_inc_ident(), lane);
-    bl_inc sf = in ? bl_term_inc(a, e1) : bl_inc_ident(); /* suffix: this term, then the later ones */
+    const int pc = __popc(m);
+    int inc = pc;
 #pragma unroll
     for (int k = 1; k < 64; k <<= 1) {
-      const bl_inc o = bl_inc{(uint32_t)__shfl_down((int)sf.d0, k, 64), (uint32_t)__shfl_down((int)sf.d1, k, 64)};
-      if (lane + k < 64) sf = bl_compose(sf, o);
+      const int o = __shfl_up(inc, k, 64);
+      if (lane >= k) inc += o;
     }
-    nm.cs[ci * 65 + lane] = sf;
-    if (lane == 0) {
-      nm.cs[ci * 65 + 64] = bl_inc_ident();
-      nm.ce0[ci] = e0;
-      nm.ce1[ci] = e1;
+    if (lane == 63) nm.cw[w] = inc;
+    __syncthreads();
+    int off = ncrit_all + inc - pc, tot = 0;
+    for (int q = 0; q < SEL_NW; q++) {
+      if (q < w) off += nm.cw[q];
+      tot += nm.cw[q];
+    }
+    while (m) {
+      const int j = __ffs(m) - 1;
+      m &= m - 1u;
+      if (off < BL_CRIT_MAX) nm.crit[off] = b * (BL_EB / 64) + j;
+      off++;
+    }
+    ncrit_all += tot;
+    __syncthreads();
+  }
+  /* past BL_CRIT_MAX critical groups the last run holds the rest (its blocks are not composable) */
+  const int ncrit = ncrit_all < BL_CRIT_MAX ? ncrit_all : BL_CRIT_MAX;
+  auto run_lo = [&](int r) { return r == 0 ? 0 : nm.crit[r - 1] + 1; };
+  auto run_hi = [&](int r) { return r == ncrit ? G : nm.crit[r]; };
+  auto blk_E = [&](int b) -> int { return b < BL_STAGE_B ? nm.bE[b] : brec[b].E; };
+  auto blk_v = [&](int b) -> bl_inc { return b < BL_STAGE_B ? nm.bV[b] : brec[b].v; };
+  /* 2. runs (edge groups and whole blocks) and critical groups, one per wavefront at a time */
+  const int nrun = ncrit + 1;
+  for (int it = w; it < nrun + ncrit; it += SEL_NW) {
+    if (it < nrun) {
+      const int lo = run_lo(it), hi = run_hi(it);
+      int st = 0, Er = BL_E_NONE;
+      bl_inc acc = bl_inc_ident();
+      if (lo < hi) {
+        Er = rec[lo].E;
+        const int gb0 = min((lo + 15) & ~15, hi), gb1 = max(hi & ~15, gb0);
+        const int npre = gb0 - lo, nblk = (gb1 - gb0) >> 4, nit = npre + nblk + (hi - gb1);
+        bool bad = false;
+        for (int i0 = 0; i0 < nit; i0 += 64) {
+          const int i = i0 + lane;
+          bl_inc f = bl_inc_ident();
+          if (i < nit) {
+            int Ei;
+            if (i < npre || i >= npre + nblk) {
+              const bl_grec1 gr = rec[i < npre ? lo + i : gb1 + (i - npre - nblk)];
+              Ei = gr.E;
+              f = gr.v;
+            } else {
+              const int bb = (gb0 >> 4) + (i - npre);
+              Ei = blk_E(bb);
+              f = blk_v(bb);
+            }
+            bad |= Ei != Er;
+          }
+          acc = bl_compose(acc, bl_wave_reduce(f, lane));
+        }
+        st = __ballot(bad) ? 2 : 1;
+      }
+      if (lane == 0) {
+        nm.r_E[it] = Er;
+        nm.r_st[it] = st;
+        nm.r_f[it] = acc;
+      }
+    } else {
+      const int ci = it - nrun;
+      const int g = nm.crit[ci];
+      const int64_t j = (int64_t)g * 64 + lane;
+      const bool in = j < V;
+      const float a = in ? bl_expf(eff[j] - M) : 0.0f;
+      const int e0 = rec[g].E, e1 = bl_binade_of((double)apx[g + 1]);
+      nm.terms[ci * 64 + lane] = a;
+      nm.cp[ci * 64 + lane] = bl_wave_scan(in ? bl_term_inc(a, e0) : bl_inc_ident(), lane);
+      bl_inc sf = in ? bl_term_inc(a, e1) : bl_inc_ident(); /* suffix: this term, then the later ones */
+#pragma unroll
+      for (int k = 1; k < 64; k <<= 1) {
+        const bl_inc o = bl_inc{(uint32_t)__shfl_down((int)sf.d0, k, 64), (uint32_t)__shfl_down((int)sf.d1, k, 64)};
+        if (lane + k < 64) sf = bl_compose(sf, o);
+      }
+      nm.cs[ci * 65 + lane] = sf;
+      if (lane == 0) {
+        nm.cs[ci * 65 + 64] = bl_inc_ident();
+        nm.ce0[ci] = e0;
+        nm.ce1[ci] = e1;
+      }
     }
   }
   __syncthreads();
-  /* 4. the chain, by one wavefront */
+  /* 3. the chain, by one wavefront; lane r holds run r */
   if (w == 0) {
     int e = BL_E_MIN;
     uint32_t N = 0u;
@@ -1180,18 +1219,18 @@ __device__ float fast_normaliser(const bl_dev &d, int row, float M, sel_shared &
       const bl_grec1 r1 = rec[g];
       return bl_grec{r1.E, 0u, {bl_inc{BL_SAT, BL_SAT}, r1.v, bl_inc{BL_SAT, BL_SAT}}};
     };
+    const int rl = lane < nrun ? lane : 0;
+    const int rE = nm.r_E[rl], rst = nm.r_st[rl];
+    const bl_inc rf = nm.r_f[rl];
     for (int r = 0; r <= ncrit; r++) {
-      for (int pi = nm.run_p0[r]; pi < nm.run_p0[r + 1]; pi++) {
-        const uint32_t N2 = bl_apply(nm.p_f[pi], N);
-        if (nm.p_e[pi] == e && N2 < BL_N_TOP) N = N2;
-        else walk_groups(nm.p_lo[pi], nm.p_hi[pi], V, term, recf, e, N, lane);
+      const int st = (int)bl_bcast((uint32_t)rst, r);
+      if (st != 0) {
+        const bl_inc f = bl_inc{bl_bcast(rf.d0, r), bl_bcast(rf.d1, r)};
+        const uint32_t N2 = bl_apply(f, N);
+        if (st == 1 && (int)bl_bcast((uint32_t)rE, r) == e && N2 < BL_N_TOP) N = N2;
+        else walk_groups(run_lo(r), run_hi(r), V, term, recf, e, N, lane);
       }
-      if (r == ncrit) {
-        /* groups a capped piece list left out: the tail of the last run */
-        const int done = nm.run_p0[r + 1] > nm.run_p0[r] ? nm.p_hi[nm.run_p0[r + 1] - 1] : (r == 0 ? 0 : nm.crit[r - 1] + 1);
-        if (done < G) walk_groups(done, G, V, term, recf, e, N, lane);
-        break;
-      }
+      if (r == ncrit) break;
       const int g = nm.crit[r];
       const bool in = (int64_t)g * 64 + lane < V;
       const float a = nm.terms[r * 64 + lane];

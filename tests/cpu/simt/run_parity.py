@@ -63,9 +63,11 @@ def lp_close(a, b):
     return abs(a - b) <= LP_RTOL * max(abs(a), abs(b)) or abs(a - b) <= 1e-7
 
 
-def run_small(BL, case, steps, coarse=False):
+def run_small(BL, case, steps, coarse=False, ramp=False):
     """A small case against the oracle; `coarse` floors the logits to a few integers, so that thousands of
-    values tie at the chunk top-K bound (the radix fallback with an index-order cut of the ties)."""
+    values tie at the chunk top-K bound (the radix fallback with an index-order cut of the ties); `ramp`
+    adds a slope of ln 2 per 63 tokens, so that the index-order sum crosses a power of two in nearly every
+    64-term group (more critical groups than the normaliser precomputes)."""
     kw = CASES[case]
     rng, hist, reply, bias = small_case_inputs(case)
     ctx = BL.Context(SMALL_V, 2, 2)
@@ -86,6 +88,8 @@ def run_small(BL, case, steps, coarse=False):
             x = small_case_logits(rng)
             if coarse:
                 x = np.floor(x / np.float32(5.0)).astype(np.float32)
+            if ramp:
+                x = (x * np.float32(0.05) + np.arange(SMALL_V, dtype=np.float32) * np.float32(0.011)).astype(np.float32)
             buf.upload(x)
             tok, lp, ti, tl = ctx.sample_step([1], buf.ptr, SMALL_V, top_stride=max(n_probs, 1))
             ot, olp = np.zeros(1, np.int32), np.zeros(1, np.float32)
@@ -474,6 +478,9 @@ def main():
         elif kind == "coarse":
             for c in parse_range(f[1]):
                 results.append((f"coarse case {c}", run_small(BL, c, int(f[2]) if len(f) > 2 else 25, coarse=True)))
+        elif kind == "ramp":
+            for c in parse_range(f[1]):
+                results.append((f"ramp case {c}", run_small(BL, c, int(f[2]) if len(f) > 2 else 25, ramp=True)))
         elif kind == "w2":
             results.append(("workload 2", run_w2(BL, int(f[1]))))
         elif kind == "w4":

@@ -2,7 +2,8 @@
 top_k 250 with 256 logprob alternatives at V=151936 (38 chunks x 256 candidates per row, the merged
 list found by radix selection), two small configurations stepped as rows 0 and 1 of an odd-length
 vocabulary (row 1 not 16-byte aligned), small configurations on logits floored to a few integers (thousands
-of ties at each chunk's top-K bound), and the bound-rows asynchronous step against the synchronous one."""
+of ties at each chunk's top-K bound) and on a ramp (the index-order sum crosses a power of two in nearly
+every group), and the bound-rows asynchronous step against the synchronous one."""
 import os
 import sys
 
@@ -44,6 +45,13 @@ def test_two_rows_odd_vocabulary(pair):
 def test_coarse_logits_tie_at_the_bound(case):
     print(f"small case {case}, logits floored to a few integers: 20 steps", flush=True)
     err = RP.run_small(BL, case, 20, coarse=True)
+    assert err is None, err
+
+
+@pytest.mark.parametrize("case", [7, 8, 10])
+def test_ramp_logits_many_crossings(case):
+    print(f"small case {case}, logits on a ramp (a power of two crossed in nearly every group): 20 steps", flush=True)
+    err = RP.run_small(BL, case, 20, ramp=True)
     assert err is None, err
 
 

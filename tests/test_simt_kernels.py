@@ -45,11 +45,13 @@ def test_small_cases_random_thread_order(simt_lib):
     assert out.count("ok   small case") == 11
 
 
-def test_coarse_logits_tie_at_the_bound(simt_lib):
+def test_coarse_and_ramp_logits(simt_lib):
     """Logits floored to a few integers: greedy and top-k rows whose chunk top-K bound is reached by
-    thousands of tied values (top_k 200 takes the radix fallback and cuts the ties in index order)."""
-    out = _run(simt_lib, ["coarse:0,1,4,5,8,10:4"], {"SIMT_ORDER": "rand"})
-    assert out.count("ok   coarse case") == 6
+    thousands of tied values (top_k 200 takes the radix fallback and cuts the ties in index order).
+    Logits on a ramp: the index-order sum crosses a power of two in nearly every group, past the
+    normaliser's precomputed critical groups (the rest is walked group by group)."""
+    out = _run(simt_lib, ["coarse:0,1,4,5,8,10:4", "ramp:7,8,10:3"], {"SIMT_ORDER": "rand"})
+    assert out.count("ok   coarse case") == 6 and out.count("ok   ramp case") == 3
 
 
 def test_full_vocabulary_workloads(simt_lib):
@@ -77,5 +79,5 @@ def test_small_cases_address_sanitizer():
         assert os.path.isabs(p) and os.path.exists(p), f"{rt} not found"
         pre.append(p)
     env = {"LD_PRELOAD": " ".join(pre), "ASAN_OPTIONS": "detect_leaks=0", "UBSAN_OPTIONS": "print_stacktrace=1"}
-    out = _run(os.path.join(SIMT, "_build", "libbl_simt_asan.so"), ["small:0-10:3", "coarse:1,5:3", "grammar:0-6:20"], env)
+    out = _run(os.path.join(SIMT, "_build", "libbl_simt_asan.so"), ["small:0-10:3", "coarse:1,5:3", "ramp:8:2", "grammar:0-6:20"], env)
     assert "ERROR: AddressSanitizer" not in out and "runtime error" not in out
