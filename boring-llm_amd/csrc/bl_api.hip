@@ -18,8 +18,8 @@
 #include "bl_math.h"
 #include "bl_workload.h"
 
-void bl_launch_step(const bl_dev &d, const float *logits, int64_t ld, const bl_rows &rows, int B, bool need_exp,
-                    bool need_gram, bool need_lp, hipStream_t s, hipEvent_t *ev);
+void bl_launch_step(const bl_dev &d, const float *logits, int64_t ld, const bl_rows &rows, int B, bool need_pass2,
+                    bool need_gram, hipStream_t s, hipEvent_t *ev);
 void bl_launch_gmask(const bl_dev &d, const bl_rows &rows, hipStream_t s);
 void bl_launch_synth(float *out, int64_t ld, int cfg, int64_t seed, int64_t step, int rows, int V, hipStream_t s);
 void bl_launch_math_digest(int fn, uint32_t first_block, int n_blocks, unsigned long long *out, hipStream_t s);
@@ -211,7 +211,7 @@ int bl_create(int device, int max_slots, int max_rows, int vocab, bl_ctx **out) 
   ALLOC(d.sortk, R * std::max(P2, 2 * V));
   ALLOC(d.gsum, R * G);
   ALLOC(d.gapx, R * G);
-  ALLOC(d.lse, R);
+  ALLOC(d.mkey, (size_t)R * BL_KSEL_MAX);
   d.nb = (vocab + BL_EB - 1) / BL_EB;
   {
     char *b = nullptr;
@@ -600,15 +600,12 @@ static void mark_stepped(bl_ctx *c, const int32_t *slots, int B) {
   for (int i = 0; i < B; i++) c->stepped[slots[i]] = 1;
 }
 
-static bool needs_exp(bl_ctx *c, const int32_t *slots, int B) {
-  for (int i = 0; i < B; i++)
-    if (c->host_slots[slots[i]].mode & (BL_M_LOGPROBS | BL_M_FULL)) return true;
-  return false;
-}
-
-static bool needs_lp(bl_ctx *c, const int32_t *slots, int B) {
-  for (int i = 0; i < B; i++)
-    if (c->host_slots[slots[i]].mode & BL_M_LOGPROBS) return true;
+/* the exponent pass runs when a row has logprobs, a full-vocabulary rank or top-K candidates to merge */
+static bool needs_pass2(bl_ctx *c, const int32_t *slots, int B) {
+  for (int i = 0; i < B; i++) {
+    const bl_slot_dev &s = c->host_slots[slots[i]];
+    if ((s.mode & (BL_M_LOGPROBS | BL_M_FULL)) || s.k_sel > 0) return true;
+  }
   return false;
 }
 
@@ -648,8 +645,7 @@ int bl_sample_step(bl_ctx *c, const int32_t *slots, int B, const float *d_logits
   HIPCHK(hipMemcpyAsync(c->d_slot, c->h_slot, B * sizeof(int32_t), hipMemcpyHostToDevice, c->stream));
   bl_rows rows = make_rows(c, false, 1, top_stride > 0 ? top_stride : 1);
   mark_stepped(c, slots, B);
-  bl_launch_step(c->d, d_logits, ld, rows, B, needs_exp(c, slots, B), needs_gram(c, slots, B), needs_lp(c, slots, B),
-                 c->stream, nullptr);
+  bl_launch_step(c->d, d_logits, ld, rows, B, needs_pass2(c, slots, B), needs_gram(c, slots, B), c->stream, nullptr);
   HIPCHK(hipGetLastError());
   HIPCHK(hipMemcpyAsync(c->h_tok, c->d_tok, B * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));
   HIPCHK(hipMemcpyAsync(c->h_status, c->d_status, B * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));
@@ -695,8 +691,8 @@ int bl_sample_step_async(bl_ctx *c, int B, const float *d_logits, int64_t ld, in
       for (int k = 0; k < 4; k++) HIPCHK(hipEventCreate(&c->ev[k]));
     ev = c->ev;
   }
-  bl_launch_step(c->d, d_logits, ld, rows, B, needs_exp(c, c->h_slot, B), needs_gram(c, c->h_slot, B),
-                 needs_lp(c, c->h_slot, B), c->stream, ev);
+  bl_launch_step(c->d, d_logits, ld, rows, B, needs_pass2(c, c->h_slot, B), needs_gram(c, c->h_slot, B), c->stream,
+                 ev);
   HIPCHK(hipGetLastError());
   if (ev) {
     /* per-kernel durations of this step, accumulated (the caller asked for timing: synchronous) */
@@ -749,10 +745,8 @@ int bl_spec_verify(bl_ctx *c, const int32_t *slots, int B, int k, const float *d
   HIPCHK(hipMemcpyAsync(c->d_skip, c->h_skip, R * sizeof(int32_t), hipMemcpyHostToDevice, c->stream));
   bl_rows rows = make_rows(c, true, 0, 1);
   rows.lp = nullptr; /* no logprobs are returned for speculative rows */
-  bool ne = false;
-  for (int b = 0; b < B; b++) ne |= (c->host_slots[slots[b]].mode & (BL_M_LOGPROBS | BL_M_FULL)) != 0;
   mark_stepped(c, slots, B);
-  bl_launch_step(c->d, d_rows, ld, rows, R, ne, false, false, c->stream, nullptr);
+  bl_launch_step(c->d, d_rows, ld, rows, R, needs_pass2(c, slots, B), false, c->stream, nullptr);
   HIPCHK(hipGetLastError());
   HIPCHK(hipMemcpyAsync(c->h_tok, c->d_tok, R * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));
   HIPCHK(hipMemcpyAsync(c->h_status, c->d_status, R * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));

@@ -35,6 +35,8 @@
 #define BL_CRIT_MAX 32      /* critical groups the fast normaliser precomputes (terms + two scans in LDS) */
 #define BL_TK_CAP 1024      /* chunk top-K: keys at or above the thread-maximum bound ranked in LDS */
 #define BL_STAGE_B 1024     /* block summaries staged in LDS by the fast normaliser (V up to 1M) */
+#define BL_RANK_MAX 1024    /* full-vocabulary candidate lists up to this size are sorted by counting */
+#define BL_EOG_LDS 64       /* end-of-generation ids the selection keeps in LDS */
 
 /* per-token flags */
 #define BL_TF_BIAS 1u
@@ -106,7 +108,7 @@ struct bl_dev {
   uint64_t *sortk;  /* [rows][2^ceil(log2 V)] global sort scratch */
   double *gsum;     /* [rows][V/64 + 64] */
   float *gapx;      /* [rows][V/64 + 64] approximate index-order sum before each 64-term group, then the total */
-  float *lse;       /* [rows] log of the index-order normaliser (logprob rows) */
+  uint64_t *mkey;   /* [rows][KSEL_MAX] the row's top K order keys, sorted (0: unfilled) */
   void *brec;       /* [rows][nb] bl_grec1 per BL_EB terms: the block's binade and composed automaton, or
                        BL_E_NONE when it holds a critical group or two binades */
   uint32_t *bcrit;  /* [rows][nb] the block's critical groups (bit i: group 16 b + i) */

@@ -7,17 +7,16 @@
  *                 src/server.br:940-944, src/sampling.br:65-107,175-237), writes the transformed
  *                 row, and per chunk: max + first argmax, an approximate exp-sum, and the chunk's
  *                 top-K by (value desc, index asc) via a three-pass LDS radix select.
- *   bl_k_exppass  grid (V/1024, B) x 256, rows with logprobs or full-vocabulary sampling: exact
- *                 exp(x - max) terms (glibc-identical expf), the sequential-sum group records of the
- *                 index-order normaliser (src/sampling.br:254-266), and the candidates of a
- *                 full-vocabulary rank (every token within 17.5*max(T,1) of the max; the rest cannot
- *                 change any float32 sum of the chain).
- *   bl_k_select   grid (B, 1 + logprobs) x 1024: greedy / top-k / full-vocabulary candidate sampling
- *                 with exact sequential sums (src/sampling.br:490-607), the draw from the slot's
- *                 xorshift stream, alternatives (src/server.br:1027-1035) and the history commit
- *                 (src/server.br:1004, :1037); a second workgroup per logprob row computes the exact
- *                 index-order normaliser (src/sampling.br:254-266).
- *   bl_k_lpfinish grid (B) x 64: subtracts the log-normaliser from the token's and alternatives' x - max.
+ *   bl_k_exppass  grid (1 + V/1024, B) x 256: workgroup 0 merges a row's chunk top-K lists into its
+ *                 sorted top K (top-k sampling and logprob alternatives); the others, for rows with
+ *                 logprobs or full-vocabulary sampling, compute the exact exp(x - max) terms
+ *                 (glibc-identical expf), the sequential-sum group records of the index-order normaliser
+ *                 (src/sampling.br:254-266), and the candidates of a full-vocabulary rank (every token
+ *                 within 17.5*max(T,1) of the max; the rest cannot change any float32 sum of the chain).
+ *   bl_k_select   grid (B) x 1024: greedy / top-k / full-vocabulary candidate sampling with exact
+ *                 sequential sums (src/sampling.br:490-607), the draw from the slot's xorshift stream,
+ *                 the exact index-order normaliser of logprob rows (src/sampling.br:254-273),
+ *                 alternatives (src/server.br:1027-1035) and the history commit (src/server.br:1004, :1037).
  * No MFMA: the work is bandwidth- and latency-bound scanning, selection and integer arithmetic.
  */
 #include <hip/hip_runtime.h>
@@ -513,15 +512,156 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass(bl_dev d, const fl
   }
 }
 
-/* ------------------------------------------------------------------ K2: exponent pass */
-/* grid (ceil(V / BL_EB), B) x 256 over the rows with logprobs or a full-vocabulary rank; thread t holds
- * the block's terms 4t..4t+3, a 64-term group is 16 threads */
+/* ------------------------------------------------------------------ K2: exponent pass + top-K merge */
+/*
+ * The row's top K keys (value desc, index asc; top_k_select, src/sampling.br:280-296) from the chunks'
+ * lists of the row pass (each sorted, K long), into d.mkey[row][0..K) (0 = unfilled: the row holds fewer
+ * than K values above -1e30). merge_lists takes the first L keys of every list: a radix selection over the
+ * 64-bit order keys, 8 bits per pass from the top, narrows them until the keys at or above the current
+ * bound number at most `cap` (at the last pass the bound is the K-th key itself, so exactly K remain);
+ * those are ranked by counting. The keys are distinct (they carry the index), so ranks are a permutation.
+ * Keys stay in registers when the lists hold at most BL_MERGE_REG per thread, and are re-read from memory
+ * per pass otherwise. Returns the K-th key of the merged prefixes (0 when they hold fewer than K).
+ */
+#define BL_MERGE_REG 16
+#define BL_MERGE_CAP 512
+#define BL_MERGE_L 16      /* keys per list of the first, prefix-only merge */
+#define BL_MERGE_PREFIX 1024 /* the prefix merge's key budget (nc * L) */
+static_assert(BL_MERGE_CAP >= BL_KSEL_MAX, "the last radix pass leaves exactly K keys");
+__device__ uint64_t merge_lists(const bl_dev &d, int row, int K, int L, int cap) {
+  constexpr int NT = BL_RP_THREADS;
+  const int nc = d.nc, t = threadIdx.x;
+  const int total = nc * L;
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t res[4];
+  __shared__ uint32_t wsum[NT / 64];
+  __shared__ uint64_t surv[BL_MERGE_CAP];
+  __shared__ int s_cnt;
+  __shared__ uint64_t s_kth;
+  auto load_key = [&](int i) -> uint64_t {
+    const int ch = i / L, q = i - ch * L;
+    const int64_t o = ((int64_t)row * nc + ch) * BL_KSEL_MAX + q;
+    const int32_t id = d.cand_i[o];
+    return id >= 0 ? ckey(d.cand_v[o], id) : 0ull;
+  };
+  const bool inreg = total <= NT * BL_MERGE_REG;
+  uint64_t kr[BL_MERGE_REG];
+#pragma unroll
+  for (int j = 0; j < BL_MERGE_REG; j++) {
+    const int i = t + j * NT;
+    kr[j] = inreg && i < total ? load_key(i) : 0ull;
+  }
+  auto each = [&](auto f) {
+    if (inreg) {
+#pragma unroll
+      for (int j = 0; j < BL_MERGE_REG; j++) f(kr[j]);
+    } else {
+      for (int i = t; i < total; i += NT) f(load_key(i));
+    }
+  };
+  /* valid keys */
+  int mine = 0;
+  each([&](uint64_t k) { mine += k != 0ull ? 1 : 0; });
+  if (t == 0) {
+    s_cnt = 0;
+    s_kth = 0ull;
+  }
+  __syncthreads();
+  if (mine) atomicAdd(&s_cnt, mine);
+  __syncthreads();
+  const int n_valid = s_cnt;
+  uint64_t lo = 1ull; /* survivors: keys >= lo (every valid key when the lists hold at most K) */
+  if (n_valid > K) {
+    uint64_t prefix = 0ull, pmask = 0ull;
+    int need = K;
+    for (int shift = 56; shift >= 0; shift -= 8) {
+      static_assert(NT == 256, "one histogram bin per thread");
+      hist[t] = 0u;
+      __syncthreads();
+      each([&](uint64_t k) {
+        if (k != 0ull && (k & pmask) == prefix) atomicAdd(&hist[(uint32_t)(k >> shift) & 255u], 1u);
+      });
+      __syncthreads();
+      block_find_bin<NT>(hist, 256, (uint32_t)need, res, wsum);
+      const uint32_t bin = res[0], above = res[1], inbin = res[2];
+      prefix |= (uint64_t)bin << shift;
+      pmask |= 0xFFull << shift;
+      lo = prefix;
+      if ((K - need) + (int)(above + inbin) <= cap) break;
+      need -= (int)above;
+    }
+  }
+  __syncthreads();
+  if (t == 0) s_cnt = 0;
+  __syncthreads();
+  each([&](uint64_t k) {
+    if (k != 0ull && k >= lo) {
+      const int p = atomicAdd(&s_cnt, 1);
+      if (p < cap) surv[p] = k;
+    }
+  });
+  __syncthreads();
+  const int ns = min(s_cnt, cap);
+  uint64_t *out = d.mkey + (int64_t)row * BL_KSEL_MAX;
+  for (int i = t; i < ns; i += NT) {
+    const uint64_t k = surv[i];
+    int r = 0, j = 0;
+    for (; j + 4 <= ns; j += 4)
+      r += (surv[j] > k ? 1 : 0) + (surv[j + 1] > k ? 1 : 0) + (surv[j + 2] > k ? 1 : 0) + (surv[j + 3] > k ? 1 : 0);
+    for (; j < ns; j++) r += surv[j] > k ? 1 : 0;
+    if (r < K) out[r] = k;
+    if (r == K - 1) s_kth = k;
+  }
+  for (int q = ns + t; q < K; q += NT) out[q] = 0ull;
+  __syncthreads();
+  const uint64_t kth = s_kth;
+  __syncthreads();
+  return kth;
+}
+
+/* The merge from the first L keys of every list is the row's exact top K unless some list was cut while its
+ * last key read is above the K-th key found (then its unread keys could rank in the top K): that case, and
+ * K <= L, merge the whole lists. */
+__device__ void merge_topk(const bl_dev &d, int row, int K) {
+  const int nc = d.nc, t = threadIdx.x;
+  const int L = min(BL_MERGE_L, BL_MERGE_PREFIX / nc);
+  if (L >= 1 && L < K) {
+    __shared__ int s_cut;
+    const uint64_t kth = merge_lists(d, row, K, L, K <= 96 ? 128 : BL_MERGE_CAP);
+    if (t == 0) s_cut = 0;
+    __syncthreads();
+    for (int ch = t; ch < nc; ch += BL_RP_THREADS) {
+      const int64_t o = ((int64_t)row * nc + ch) * BL_KSEL_MAX + (L - 1);
+      const int32_t id = d.cand_i[o];
+      if (id >= 0 && ckey(d.cand_v[o], id) > kth) s_cut = 1;
+    }
+    __syncthreads();
+    const int cut = s_cut;
+    __syncthreads();
+    if (!cut) return;
+  }
+  merge_lists(d, row, K, K, BL_MERGE_CAP);
+}
+
+/* grid (1 + ceil(V / BL_EB), B) x 256. The first B workgroups in dispatch order merge the top-K candidates
+ * of rows that have them (sampling or logprob alternatives); the others serve the rows with logprobs or a
+ * full-vocabulary rank: thread t holds the block's terms 4t..4t+3, a 64-term group is 16 threads */
 __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_exppass(bl_dev d, bl_rows rows) {
   const int V = d.vocab, nc = d.nc;
-  const int b = blockIdx.x, row = blockIdx.y, t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  /* linear workgroup ids 0..B-1 (dispatched first) merge; the rest are row-major exponent blocks */
+  const int nrows = (int)gridDim.y, nbx = (int)gridDim.x - 1;
+  const int lin = (int)blockIdx.y * (int)gridDim.x + (int)blockIdx.x;
+  const bool merger = lin < nrows;
+  const int row = merger ? lin : (lin - nrows) / nbx;
+  const int b = merger ? 0 : (lin - nrows) - row * nbx;
   const int slot = rows.slot[row];
   const bl_slot_dev &sp = slot_of(d, slot);
   const int mode = sp.mode;
+  if (merger) {
+    if (sp.k_sel > 0) merge_topk(d, row, sp.k_sel);
+    return;
+  }
   if (!(mode & (BL_M_LOGPROBS | BL_M_FULL))) return;
   __shared__ uint64_t s_tab[BL_EXP2_N]; /* expf's 2^(i/32) table */
   __shared__ double wtot[BL_RP_THREADS / 64];
@@ -822,133 +962,130 @@ struct sel_norm {
   int r_st[BL_CRIT_MAX + 1];           /* 0 empty, 1 composed in one binade, 2 not composable */
   bl_inc r_f[BL_CRIT_MAX + 1];         /* composed automaton */
   int cw[SEL_NW];
-  float S;
+  int ncrit;                           /* critical groups kept (at most BL_CRIT_MAX) */
+  float S;                             /* the normaliser */
 };
-/* the top-K merge and the selection (live after the normaliser) */
-struct sel_merge {
-  uint64_t topk[BL_KSEL_MAX];          /* ranked top-K before it moves to keys[0..K) */
-  uint64_t cmin[BL_MAX_CHUNKS];        /* smallest emitted key per chunk */
-  int ccnt[BL_MAX_CHUNKS];             /* emitted keys per chunk */
-  uint64_t keys[BL_LDS_SORT];          /* merged top-K list, or a full-vocabulary list */
+/* a sampled row's ranked candidate list */
+struct sel_cand {
+  uint64_t keys[BL_LDS_SORT];          /* the merged top-K keys, or the sorted full-vocabulary candidates */
+  uint64_t tmp[BL_RANK_MAX];           /* full-vocabulary candidates before ranking by counting */
   bl_grec recs[BL_LDS_SORT / 64];
   double gsum[BL_LDS_SORT / 64];
 };
 struct sel_shared {
-  union {
-    sel_norm n;
-    sel_merge m;
-  } u;
-  uint64_t tau;
+  sel_norm n; /* both live at once: the normaliser's chain runs beside the draw */
+  sel_cand c;
   uint64_t rng_out;                    /* the RNG state after a draw */
-  uint32_t ucnt;
-  uint32_t fres_u[4];                  /* block_find_bin result */
-  uint32_t wsum[SEL_NW];
   float ser_e[BL_SERIAL_MAX];          /* short-list terms exp(v - v0) */
   float ser_r[BL_SERIAL_MAX];          /* short-list terms exp((v - v0) / T) */
   float fres[8];
   int ires[8];
   float red_m[SEL_NW];
   int red_i[SEL_NW];
+  int32_t eog[BL_EOG_LDS];             /* the first end-of-generation ids */
 };
 
-/*
- * sample_candidates_with_probs (src/sampling.br:490-607) for T > 0 on the ranked list `vals/ids`
- * (n_list entries materialised; n_logical >= n_list is the reference's candidate count, the
- * entries past n_list being too small to change any float32 sum). Returns the chosen position,
- * or -1 with `status` set.
- */
-template <class ValF>
-__device__ int sample_ranked(const bl_slot_dev &sp, ValF val, int64_t n_list, int64_t n_logical, uint64_t &rng,
-                             int rng_skip, bl_grec *recs, double *gsum, sel_shared &sh, int &status) {
-  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
-  const float T = sp.temperature;
-  int64_t keep = sp.min_keep > 1 ? sp.min_keep : 1;
+/* sample_candidates_with_probs (src/sampling.br:490-607) for T > 0: the stages without a device path, and
+ * a min_keep that reaches past the materialised list, leave the row unsupported */
+__device__ __forceinline__ bool ranked_supported(const bl_slot_dev &sp, int64_t n_list, int64_t n_logical,
+                                                 int64_t &keep) {
+  keep = sp.min_keep > 1 ? sp.min_keep : 1;
   if (keep > n_logical) keep = n_logical;
-  if (sp.typical_p < 1.0f || (sp.xtc_probability > 0.0f && sp.xtc_threshold <= 0.5f) || sp.dynatemp_range > 0.0f ||
-      keep > n_list) {
-    status |= BL_SE_UNSUPPORTED;
-    return -1;
-  }
+  return !(sp.typical_p < 1.0f || (sp.xtc_probability > 0.0f && sp.xtc_threshold <= 0.5f) ||
+           sp.dynatemp_range > 0.0f || keep > n_list);
+}
+
+/* a short ranked list (n_list <= BL_SERIAL_MAX), by every thread: the terms exp(v - v0) of the untempered
+ * softmax (with top-p or min-p) and exp((v - v0) / T) of the draw */
+template <class ValF>
+__device__ void ranked_terms(const bl_slot_dev &sp, ValF val, int64_t n_list, float *ser_e, float *ser_r) {
+  const float T = sp.temperature;
+  const bool filt = sp.top_p < 1.0f || sp.min_p > 0.0f;
   const float v0 = val(0);
-  if (n_list <= BL_SERIAL_MAX) {
-    /* short list: the terms in parallel, then the reference's sequential float32 loops on one lane */
-    const bool filt = sp.top_p < 1.0f || sp.min_p > 0.0f;
-    for (int j = t; j < n_list; j += BL_SEL_THREADS) {
-      const float x = val(j);
-      sh.ser_e[j] = filt ? bl_expf(x - v0) : 0.0f;
-      const float dd = x - v0;
-      const float q = dd / T;
-      sh.ser_r[j] = bl_expf(q);
-    }
-    __syncthreads();
-    if (t == 0) {
-      const int n = (int)n_list;
-      int64_t cut = n_logical;
-      bool unsup = false;
-      if (filt) {
-        float sum_exp = 0.0f;
-        for (int j = 0; j < n; j++) sum_exp += sh.ser_e[j];
-        if (sp.top_p < 1.0f) {
-          float cum = 0.0f;
-          for (int j = 0; j < n; j++) {
-            cum += sh.ser_e[j] / sum_exp;
-            if (j >= keep - 1 && cum >= sp.top_p) {
-              cut = j + 1;
-              break;
-            }
-          }
-        }
-        if (sp.min_p > 0.0f) {
-          const float p0 = sh.ser_e[0] / sum_exp;
-          const float threshold = p0 * sp.min_p;
-          const int64_t lim = cut < n ? cut : n;
-          int64_t first_small = -1;
-          for (int64_t j = keep; j < lim; j++)
-            if (sh.ser_e[j] / sum_exp < threshold) {
-              first_small = j;
-              break;
-            }
-          if (first_small < 0) {
-            if (lim < cut) {
-              /* the next, unmaterialised candidate is below 2^-25 of the top one */
-              if (threshold <= p0 * 5.9604645e-8f) unsup = true;
-              first_small = lim;
-            } else {
-              first_small = cut;
-            }
-          }
-          cut = keep > first_small ? keep : first_small;
-        }
-      }
-      const int n_eff = (int)(cut < n ? cut : n);
-      float S = 0.0f;
-      for (int j = 0; j < n_eff; j++) S += sh.ser_r[j];
-      uint64_t st = rng;
-      for (int k = 0; k < rng_skip; k++) st = bl_xorshift(st);
-      const float target = bl_rng_f32(&st) * S;
-      float run = 0.0f;
-      int64_t f = -1;
-      for (int j = 0; j < n_eff; j++) {
-        run += sh.ser_r[j];
-        if (run >= target) {
-          f = j;
+  for (int j = threadIdx.x; j < n_list; j += BL_SEL_THREADS) {
+    const float x = val(j);
+    ser_e[j] = filt ? bl_expf(x - v0) : 0.0f;
+    const float dd = x - v0;
+    const float q = dd / T;
+    ser_r[j] = bl_expf(q);
+  }
+}
+
+/* ... then the reference's sequential float32 loops over those terms, by one thread: softmax sum, top-p
+ * prefix, min-p cut, tempered sum and the draw. Returns the chosen position, or -2 when the cut would need
+ * a candidate past the materialised list; *rng_out = the state after the draw */
+__device__ int ranked_serial(const bl_slot_dev &sp, int n, int64_t n_logical, int64_t keep, uint64_t rng,
+                             int rng_skip, const float *ser_e, const float *ser_r, uint64_t *rng_out) {
+  const bool filt = sp.top_p < 1.0f || sp.min_p > 0.0f;
+  int64_t cut = n_logical;
+  bool unsup = false;
+  if (filt) {
+    float sum_exp = 0.0f;
+    for (int j = 0; j < n; j++) sum_exp += ser_e[j];
+    if (sp.top_p < 1.0f) {
+      float cum = 0.0f;
+      for (int j = 0; j < n; j++) {
+        cum += ser_e[j] / sum_exp;
+        if (j >= keep - 1 && cum >= sp.top_p) {
+          cut = j + 1;
           break;
         }
       }
-      sh.ires[2] = unsup ? -2 : (int)(f >= 0 ? f : cut - 1);
-      sh.rng_out = st;
     }
-    __syncthreads();
-    const int chosen = sh.ires[2];
-    const uint64_t st = sh.rng_out;
-    __syncthreads();
-    if (chosen == -2 || chosen >= n_list) {
-      status |= BL_SE_UNSUPPORTED;
-      return -1;
+    if (sp.min_p > 0.0f) {
+      const float p0 = ser_e[0] / sum_exp;
+      const float threshold = p0 * sp.min_p;
+      const int64_t lim = cut < n ? cut : n;
+      int64_t first_small = -1;
+      for (int64_t j = keep; j < lim; j++)
+        if (ser_e[j] / sum_exp < threshold) {
+          first_small = j;
+          break;
+        }
+      if (first_small < 0) {
+        if (lim < cut) {
+          /* the next, unmaterialised candidate is below 2^-25 of the top one */
+          if (threshold <= p0 * 5.9604645e-8f) unsup = true;
+          first_small = lim;
+        } else {
+          first_small = cut;
+        }
+      }
+      cut = keep > first_small ? keep : first_small;
     }
-    rng = st;
-    return chosen;
   }
+  const int n_eff = (int)(cut < n ? cut : n);
+  float S = 0.0f;
+  for (int j = 0; j < n_eff; j++) S += ser_r[j];
+  uint64_t st = rng;
+  for (int k = 0; k < rng_skip; k++) st = bl_xorshift(st);
+  const float target = bl_rng_f32(&st) * S;
+  float run = 0.0f;
+  int64_t f = -1;
+  for (int j = 0; j < n_eff; j++) {
+    run += ser_r[j];
+    if (run >= target) {
+      f = j;
+      break;
+    }
+  }
+  *rng_out = st;
+  return unsup ? -2 : (int)(f >= 0 ? f : cut - 1);
+}
+
+/*
+ * A long ranked list (more than BL_SERIAL_MAX entries) by the whole block: the sequential sums of
+ * sample_candidates_with_probs (src/sampling.br:490-607) through the exact-sum records. n_list entries are
+ * materialised; n_logical >= n_list is the reference's candidate count, the entries past n_list being too
+ * small to change any float32 sum. Returns the chosen position, or -1 with `status` set.
+ */
+template <class ValF>
+__device__ int sample_ranked_long(const bl_slot_dev &sp, ValF val, int64_t n_list, int64_t n_logical, int64_t keep,
+                                  uint64_t &rng, int rng_skip, bl_grec *recs, double *gsum, sel_shared &sh,
+                                  int &status) {
+  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+  const float T = sp.temperature;
+  const float v0 = val(0);
   int64_t cutoff = n_logical;
   if (sp.top_p < 1.0f || sp.min_p > 0.0f) {
     auto termE = [&](int64_t j) { return bl_expf(val(j) - v0); };
@@ -1085,7 +1222,7 @@ __device__ void walk_groups(int64_t g_lo, int64_t g_hi, int64_t n, TermF term, R
 
 /*
  * Exact index-order sum of exp(eff[j] - M), j < V (logprob_normalizer, src/sampling.br:254-266), by the
- * whole block. The exponent pass left, per 64-term group, the composed automaton at the binade of its
+ * whole block (norm_prep) and one wavefront (norm_chain). The exponent pass left, per 64-term group, the composed automaton at the binade of its
  * approximate start, and per 1024-term block the groups where the sum may cross a power of two
  * ("critical") and, for a block without them, the block's composed automaton. The groups between two
  * critical groups form a run in one binade; the wavefronts compose the runs (edge groups, then whole
@@ -1096,7 +1233,7 @@ __device__ void walk_groups(int64_t g_lo, int64_t g_hi, int64_t n, TermF term, R
  * exact state, and a run or group whose prediction fails is walked group by group and element by
  * element instead.
  */
-__device__ float fast_normaliser(const bl_dev &d, int row, float M, sel_shared &sh) {
+__device__ void norm_prep(const bl_dev &d, int row, float M, sel_shared &sh, uint32_t m_pre, bl_grec1 br_pre) {
   const int V = d.vocab, t = threadIdx.x, w = t >> 6, lane = t & 63;
   const int G = (V + 63) / 64, NB = d.nb;
   const bl_grec1 *rec =
@@ -1105,16 +1242,16 @@ __device__ float fast_normaliser(const bl_dev &d, int row, float M, sel_shared &
   const uint32_t *bcrit = d.bcrit + (int64_t)row * NB;
   const float *apx = d.gapx + (int64_t)row * (V / 64 + 64);
   const float *eff = d.eff + (int64_t)row * V;
-  sel_norm &nm = sh.u.n;
+  sel_norm &nm = sh.n;
   /* 1. critical groups in order (a block-wide scan of the per-block counts); block summaries to LDS */
   int ncrit_all = 0;
   for (int b0 = 0; b0 < NB; b0 += BL_SEL_THREADS) {
     const int b = b0 + t;
     uint32_t m = 0u;
     if (b < NB) {
-      m = bcrit[b];
+      m = b0 == 0 ? m_pre : bcrit[b]; /* the first BL_SEL_THREADS blocks were loaded by the caller */
       if (b < BL_STAGE_B) {
-        const bl_grec1 br = brec[b];
+        const bl_grec1 br = b0 == 0 ? br_pre : brec[b];
         nm.bE[b] = br.E;
         nm.bV[b] = br.v;
       }
@@ -1208,200 +1345,191 @@ __device__ float fast_normaliser(const bl_dev &d, int row, float M, sel_shared &
       }
     }
   }
+  if (t == 0) nm.ncrit = ncrit;
   __syncthreads();
-  /* 3. the chain, by one wavefront; lane r holds run r */
-  if (w == 0) {
-    int e = BL_E_MIN;
-    uint32_t N = 0u;
-    auto term = [&](int64_t j) { return bl_expf(eff[j] - M); };
-    /* a record holds its own binade only: a neighbouring binade reads as saturated (element level) */
-    auto recf = [&](int64_t g) {
-      const bl_grec1 r1 = rec[g];
-      return bl_grec{r1.E, 0u, {bl_inc{BL_SAT, BL_SAT}, r1.v, bl_inc{BL_SAT, BL_SAT}}};
-    };
-    const int rl = lane < nrun ? lane : 0;
-    const int rE = nm.r_E[rl], rst = nm.r_st[rl];
-    const bl_inc rf = nm.r_f[rl];
-    for (int r = 0; r <= ncrit; r++) {
-      const int st = (int)bl_bcast((uint32_t)rst, r);
-      if (st != 0) {
-        const bl_inc f = bl_inc{bl_bcast(rf.d0, r), bl_bcast(rf.d1, r)};
-        const uint32_t N2 = bl_apply(f, N);
-        if (st == 1 && (int)bl_bcast((uint32_t)rE, r) == e && N2 < BL_N_TOP) N = N2;
-        else walk_groups(run_lo(r), run_hi(r), V, term, recf, e, N, lane);
-      }
-      if (r == ncrit) break;
-      const int g = nm.crit[r];
-      const bool in = (int64_t)g * 64 + lane < V;
-      const float a = nm.terms[r * 64 + lane];
-      if (e != nm.ce0[r]) {
-        elem_resolve(a, in, e, N, lane, 0);
-        continue;
-      }
-      const uint32_t Ne = bl_apply(nm.cp[r * 64 + lane], N);
+}
+
+/*
+ * The chain of the index-order normaliser, by one whole wavefront after norm_prep; nm.S = the sum. Lane r
+ * holds run r's composed automaton and critical group r's index and predicted binades, so the walk reads
+ * them with readlane; a critical group's per-lane term, prefix scan and suffix scan (lane c holds the
+ * suffix after c) are loaded one group ahead.
+ */
+__device__ void norm_chain(const bl_dev &d, int row, float M, sel_shared &sh) {
+  const int V = d.vocab, lane = threadIdx.x & 63;
+  const int G = (V + 63) / 64;
+  const bl_grec1 *rec =
+      reinterpret_cast<const bl_grec1 *>(reinterpret_cast<const bl_grec *>(d.grec) + (int64_t)row * 2 * (V / 64 + 64));
+  const float *eff = d.eff + (int64_t)row * V;
+  const sel_norm &nm = sh.n;
+  const int ncrit = nm.ncrit, nrun = ncrit + 1;
+  static_assert(BL_CRIT_MAX + 1 <= 64, "one lane per run and per critical group");
+  const int rl = lane < nrun ? lane : 0;
+  const int rE = nm.r_E[rl], rst = nm.r_st[rl];
+  const bl_inc rf = nm.r_f[rl];
+  const int cl = lane < ncrit ? lane : 0;
+  const int cg = nm.crit[cl], ce0 = nm.ce0[cl], ce1 = nm.ce1[cl];
+  auto crit_of = [&](int r) { return (int)bl_bcast((uint32_t)cg, r); };
+  auto run_lo = [&](int r) { return r == 0 ? 0 : crit_of(r - 1) + 1; };
+  auto run_hi = [&](int r) { return r == ncrit ? G : crit_of(r); };
+  int e = BL_E_MIN;
+  uint32_t N = 0u;
+  auto term = [&](int64_t j) { return bl_expf(eff[j] - M); };
+  /* a record holds its own binade only: a neighbouring binade reads as saturated (element level) */
+  auto recf = [&](int64_t g) {
+    const bl_grec1 r1 = rec[g];
+    return bl_grec{r1.E, 0u, {bl_inc{BL_SAT, BL_SAT}, r1.v, bl_inc{BL_SAT, BL_SAT}}};
+  };
+  float a = 0.0f;
+  bl_inc cp = bl_inc_ident(), cs = bl_inc_ident();
+  if (ncrit > 0) {
+    a = nm.terms[lane];
+    cp = nm.cp[lane];
+    cs = nm.cs[lane + 1];
+  }
+  for (int r = 0; r <= ncrit; r++) {
+    float a_nx = 0.0f;
+    bl_inc cp_nx = bl_inc_ident(), cs_nx = bl_inc_ident();
+    if (r + 1 < ncrit) {
+      a_nx = nm.terms[(r + 1) * 64 + lane];
+      cp_nx = nm.cp[(r + 1) * 64 + lane];
+      cs_nx = nm.cs[(r + 1) * 65 + lane + 1];
+    }
+    const int st = (int)bl_bcast((uint32_t)rst, r);
+    if (st != 0) {
+      const bl_inc f = bl_inc{bl_bcast(rf.d0, r), bl_bcast(rf.d1, r)};
+      const uint32_t N2 = bl_apply(f, N);
+      if (st == 1 && (int)bl_bcast((uint32_t)rE, r) == e && N2 < BL_N_TOP) N = N2;
+      else walk_groups(run_lo(r), run_hi(r), V, term, recf, e, N, lane);
+    }
+    if (r == ncrit) break;
+    const bool in = (int64_t)crit_of(r) * 64 + lane < V;
+    if (e != (int)bl_bcast((uint32_t)ce0, r)) {
+      elem_resolve(a, in, e, N, lane, 0);
+    } else {
+      const uint32_t Ne = bl_apply(cp, N);
       const unsigned long long ms = __ballot(in && Ne >= BL_N_TOP);
       if (!ms) {
         N = bl_bcast(Ne, 63);
-        continue;
+      } else {
+        const int c = __ffsll((long long)ms) - 1;
+        const uint32_t Nbefore = c > 0 ? bl_bcast(Ne, c - 1) : N;
+        const float Sn = bl_make(e, Nbefore) + bl_bcastf(a, c); /* the one real float add at the crossing */
+        bl_split(Sn, e, N);
+        if (c < 63) {
+          const uint32_t N2 = bl_apply(bl_inc{bl_bcast(cs.d0, c), bl_bcast(cs.d1, c)}, N);
+          if (e == (int)bl_bcast((uint32_t)ce1, r) && N2 < BL_N_TOP) N = N2;
+          else elem_resolve(a, in, e, N, lane, c + 1);
+        }
       }
-      const int c = __ffsll((long long)ms) - 1;
-      const uint32_t Nbefore = c > 0 ? bl_bcast(Ne, c - 1) : N;
-      const float Sn = bl_make(e, Nbefore) + bl_bcastf(a, c); /* the one real float add at the crossing */
-      bl_split(Sn, e, N);
-      if (c == 63) continue;
-      const uint32_t N2 = bl_apply(nm.cs[r * 65 + c + 1], N);
-      if (e == nm.ce1[r] && N2 < BL_N_TOP) N = N2;
-      else elem_resolve(a, in, e, N, lane, c + 1);
     }
-    if (lane == 0) nm.S = bl_make(e, N);
+    a = a_nx;
+    cp = cp_nx;
+    cs = cs_nx;
   }
-  __syncthreads();
-  const float S = nm.S;
-  __syncthreads();
-  return S;
+  if (lane == 0) sh.n.S = bl_make(e, N);
 }
 
-/* blockIdx.y = 0: candidates, draw, outputs and commit; the logprobs it writes are x - max, and
- * bl_k_lpfinish subtracts the log-normaliser that blockIdx.y = 1 computes for logprob rows (the two
- * run side by side; the kernel boundary orders them) */
+/*
+ * K3: grid (B) x 1024, one workgroup per row. The row maximum and first argmax come from the chunk
+ * statistics. A sampled row's ranked list is the merged top-K (exponent pass, workgroup 0) or the
+ * full-vocabulary candidates, sorted here. A logprob row's exact index-order normaliser is prepared by
+ * every wavefront and chained by wavefront 0 while wavefront 1 runs a short list's sequential float32
+ * loops. Then the outputs (the token, its logprob (x - max) - ln(normaliser) and the alternatives,
+ * src/server.br:1027-1035) and the history commit (src/server.br:1004, :1037): counts and bitmap bits by
+ * atomics that nothing waits for, the slot's scalar state read at the start.
+ */
 __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows rows) {
   const int V = d.vocab, nc = d.nc;
   const int row = blockIdx.x, t = threadIdx.x, w = t >> 6, lane = t & 63;
-  const int slot = rows.slot[row];
-  bl_slot_dev &sp = d.slots[slot];
-  const int mode = sp.mode;
-  const bool norm_role = blockIdx.y == 1;
-  if (norm_role && !((mode & BL_M_LOGPROBS) && rows.lp)) return; /* uniform over the workgroup */
   __shared__ sel_shared sh;
-  int status = 0;
-
-  /* row max and first argmax from the chunk statistics */
+  /* loads that need only the row index go out first */
   float M = BL_NEG_INF;
   int Mi = 0x7fffffff;
-  for (int k = t; k < nc; k += BL_SEL_THREADS) {
-    float cm = d.c_max[(int64_t)row * nc + k];
-    argmax_merge(M, Mi, cm, d.c_arg[(int64_t)row * nc + k]);
+  for (int k = t; k < nc; k += BL_SEL_THREADS)
+    argmax_merge(M, Mi, d.c_max[(int64_t)row * nc + k], d.c_arg[(int64_t)row * nc + k]);
+  const uint64_t mk = t < BL_KSEL_MAX ? d.mkey[(int64_t)row * BL_KSEL_MAX + t] : 0ull; /* used when K > t */
+  uint32_t m_pre = 0u; /* the normaliser's first block flags and summaries (used by logprob rows) */
+  bl_grec1 br_pre{};
+  if (t < d.nb) {
+    m_pre = d.bcrit[(int64_t)row * d.nb + t];
+    br_pre = reinterpret_cast<const bl_grec1 *>(d.brec)[(int64_t)row * d.nb + t];
   }
+  const int slot = rows.slot[row];
+  bl_slot_dev &sp = d.slots[slot];
+  const int mode = sp.mode, K = sp.k_sel;
+  const float T = sp.temperature;
+  const bool lp_row = (mode & BL_M_LOGPROBS) && rows.lp;
+  /* slot state the commit updates */
+  const int rl = sp.repeat_last_n, win_len = sp.win_len, win_head = sp.win_head;
+  const int n_tokens0 = sp.n_tokens, n_reply0 = sp.n_reply;
+  const bool rep_on = sp.rep_on != 0, fp_on = sp.fp_on != 0, g_on = sp.g_on != 0;
+  const bool ring_full = rep_on && rl > 0 && win_len == rl;
+  const int32_t ring_old = (t == 0 && rows.commit && ring_full) ? d.ring[(int64_t)slot * BL_WCAP + win_head] : 0;
+  const int n_eog = d.n_eog;
+  if (t < n_eog && t < BL_EOG_LDS) sh.eog[t] = d.eog[t];
   block_argmax<BL_SEL_THREADS>(M, Mi, sh.red_m, sh.red_i);
   if (Mi == 0x7fffffff) Mi = 0;
 
-  /* exact index-order normaliser over the records written by the exponent pass */
   const float *eff = d.eff + (int64_t)row * V;
-  if (norm_role) {
-    const float lse = (float)log((double)fast_normaliser(d, row, M, sh));
-    if (t == 0) d.lse[row] = lse;
-    return;
-  }
-
-  /* merged top-K candidates of the row pass: sorted (value desc, index asc) in sh.u.m.keys[0..K) */
-  int n_top = 0;
-  const int K = sp.k_sel;
-  if (K > 0) {
-    /* each chunk emitted its top K (fewer only when it holds fewer valid values), so the row's K-th key
-     * is at least tau = the largest K-th key of a full chunk: only keys >= tau can rank below K */
-    const int total = nc * K;
-    for (int ch = t; ch < nc; ch += BL_SEL_THREADS) {
-      sh.u.m.cmin[ch] = ~0ull;
-      sh.u.m.ccnt[ch] = 0;
-    }
-    if (t == 0) {
-      sh.ucnt = 0u;
-      sh.tau = 0ull;
-    }
-    __syncthreads();
-    for (int i = t; i < total; i += BL_SEL_THREADS) {
-      const int ch = i / K, q = i - ch * K;
-      const int64_t o = ((int64_t)row * nc + ch) * BL_KSEL_MAX + q;
-      const int32_t id = d.cand_i[o];
-      if (id >= 0) {
-        atomicMin(&sh.u.m.cmin[ch], ckey(d.cand_v[o], id));
-        atomicAdd(&sh.u.m.ccnt[ch], 1);
-      }
-    }
-    __syncthreads();
-    for (int ch = t; ch < nc; ch += BL_SEL_THREADS)
-      if (sh.u.m.ccnt[ch] == K) atomicMax(&sh.tau, sh.u.m.cmin[ch]);
-    __syncthreads();
-    const uint64_t tau = sh.tau;
-    auto cand_key = [&](int i, uint64_t &k) -> bool {
-      const int ch = i / K, q = i - ch * K;
-      const int64_t o = ((int64_t)row * nc + ch) * BL_KSEL_MAX + q;
-      const int32_t id = d.cand_i[o];
-      if (id < 0) return false;
-      k = ckey(d.cand_v[o], id);
-      return k >= tau;
-    };
-    for (int i = t; i < total; i += BL_SEL_THREADS) {
-      uint64_t k;
-      if (cand_key(i, k)) atomicAdd(&sh.ucnt, 1u);
-    }
-    __syncthreads();
-    /* lower bound of the kept keys: tau, or, when too many keys reach tau, the K-th largest value
-     * found by a radix selection over the value bits (12 + 10 + 10) of those keys */
-    uint64_t lo = tau;
-    if (sh.ucnt > (uint32_t)(2 * K > 512 ? 2 * K : 512)) {
-      uint32_t *hist = reinterpret_cast<uint32_t *>(sh.u.m.keys); /* 4096 bins, the list is not built yet */
-      uint32_t prefix = 0u, pmask = 0u;
-      int need = K;
-      for (int pass = 0; pass < 3; pass++) {
-        const int shift = pass == 0 ? 20 : (pass == 1 ? 10 : 0);
-        const int nb = pass == 0 ? 4096 : 1024;
-        __syncthreads();
-        for (int b = t; b < nb; b += BL_SEL_THREADS) hist[b] = 0u;
-        __syncthreads();
-        for (int i = t; i < total; i += BL_SEL_THREADS) {
-          uint64_t k;
-          if (cand_key(i, k)) {
-            const uint32_t f = (uint32_t)(k >> 32);
-            if ((f & pmask) == prefix) atomicAdd(&hist[(f >> shift) & (uint32_t)(nb - 1)], 1u);
-          }
-        }
-        __syncthreads();
-        block_find_bin<BL_SEL_THREADS>(hist, nb, (uint32_t)need, sh.fres_u, sh.wsum);
-        prefix |= sh.fres_u[0] << shift;
-        pmask |= (uint32_t)(nb - 1) << shift;
-        need -= (int)sh.fres_u[1];
-      }
-      lo = (uint64_t)prefix << 32; /* every key of value >= the K-th value (ties carry the index) */
-      __syncthreads();
-    }
-    if (t == 0) sh.ucnt = 0u;
-    __syncthreads();
-    for (int i = t; i < total; i += BL_SEL_THREADS) {
-      uint64_t k;
-      if (cand_key(i, k) && k >= lo) {
-        const uint32_t pos = atomicAdd(&sh.ucnt, 1u);
-        if (pos < BL_LDS_SORT) sh.u.m.keys[pos] = k;
-      }
-    }
-    __syncthreads();
-    int ns = (int)sh.ucnt;
-    if (ns > BL_LDS_SORT) {
-      status |= BL_SE_CAND_FULL;
-      ns = BL_LDS_SORT;
-    }
-    /* rank by counting (keys are distinct: they carry the index); four independent reads per step */
-    for (int i = t; i < ns; i += BL_SEL_THREADS) {
-      const uint64_t k = sh.u.m.keys[i];
-      int r = 0, j = 0;
-      for (; j + 4 <= ns; j += 4) {
-        const uint64_t a0 = sh.u.m.keys[j], a1 = sh.u.m.keys[j + 1], a2 = sh.u.m.keys[j + 2], a3 = sh.u.m.keys[j + 3];
-        r += (a0 > k ? 1 : 0) + (a1 > k ? 1 : 0) + (a2 > k ? 1 : 0) + (a3 > k ? 1 : 0);
-      }
-      for (; j < ns; j++) r += sh.u.m.keys[j] > k ? 1 : 0;
-      if (r < K) sh.u.m.topk[r] = k;
-    }
-    __syncthreads();
-    for (int q = t; q < K; q += BL_SEL_THREADS) sh.u.m.keys[q] = q < ns ? sh.u.m.topk[q] : 0ull;
-    __syncthreads();
-    n_top = K;
-  }
-
+  int status = 0;
   uint64_t rng = sp.rng;
   const int skip = rows.rng_skip ? rows.rng_skip[row] : 0;
   int32_t tok = Mi;
-  const float T = sp.temperature;
-  if (mode & BL_M_GRAMMAR) {
+  float tokv = M;
+  const bool gram = (mode & BL_M_GRAMMAR) != 0;
+  const bool sampled = !gram && T > 0.0f;
+  /* the ranked candidate list of a sampled row */
+  uint64_t *keys = sh.c.keys;
+  int64_t n_list = 0, n_logical = 0;
+  if (sampled && (mode & BL_M_TOPK)) {
+    /* top_k_select list: kk = min(top_k, V) <= K entries, unfilled slots are (-1e30, 0) */
+    const int kk = sp.top_k < V ? sp.top_k : V;
+    if (t < kk) keys[t] = mk;
+    n_list = n_logical = kk;
+  } else if (sampled) {
+    /* full-vocabulary rank (src/sampling.br:301-365): the exponent pass's candidates, sorted */
+    int nf = d.full_n[row];
+    if (nf > V) {
+      nf = V;
+      status |= BL_SE_CAND_FULL;
+    }
+    const float *fv = d.full_v + (int64_t)row * V;
+    const int32_t *fi = d.full_i + (int64_t)row * V;
+    if (nf <= BL_RANK_MAX) {
+      for (int i = t; i < nf; i += BL_SEL_THREADS) sh.c.tmp[i] = ckey(fv[i], fi[i]);
+      __syncthreads();
+      /* rank by counting (keys are distinct: they carry the index) */
+      for (int i = t; i < nf; i += BL_SEL_THREADS) {
+        const uint64_t k = sh.c.tmp[i];
+        int r = 0, j = 0;
+        for (; j + 4 <= nf; j += 4)
+          r += (sh.c.tmp[j] > k ? 1 : 0) + (sh.c.tmp[j + 1] > k ? 1 : 0) + (sh.c.tmp[j + 2] > k ? 1 : 0) +
+               (sh.c.tmp[j + 3] > k ? 1 : 0);
+        for (; j < nf; j++) r += sh.c.tmp[j] > k ? 1 : 0;
+        keys[r] = k;
+      }
+    } else {
+      int P = 1;
+      while (P < nf) P <<= 1;
+      if (P > BL_LDS_SORT) keys = d.sortk + (int64_t)row * (2 * (int64_t)V);
+      for (int i = t; i < P; i += BL_SEL_THREADS) keys[i] = i < nf ? ckey(fv[i], fi[i]) : 0ull;
+      __syncthreads();
+      bitonic_desc(keys, P);
+    }
+    n_list = nf;
+    n_logical = V;
+  }
+  __syncthreads();
+  auto val = [&](int64_t j) -> float { return keys[j] ? ckey_v(keys[j]) : -1.0e30f; };
+  int64_t keep = 1;
+  const bool short_list = n_list <= BL_SERIAL_MAX;
+  if (sampled) {
+    if (!ranked_supported(sp, n_list, n_logical, keep)) status |= BL_SE_UNSUPPORTED;
+    if (!status && short_list) ranked_terms(sp, val, n_list, sh.ser_e, sh.ser_r);
+  }
+
+  if (gram) {
     /* sample_grammar_token, greedy (src/server.br:308-361): the frontier's status, then the first
      * allowed candidate in rank order = the allowed maximum; the lowest index among equal allowed
      * maxima is top_k_select's order but not the heap rank's, so a tie is reported */
@@ -1412,6 +1540,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
       status |= BL_SE_GDEAD;
     } else if (gst & BL_GR_FORCED) {
       tok = d.eos_id;
+      tokv = eff[tok];
     } else if (d.gamb[row]) {
       status |= BL_SE_GAMBIG;
     } else {
@@ -1424,118 +1553,106 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
       if (gi != 0x7fffffff)
         for (int k = t; k < d.gm_blocks; k += BL_SEL_THREADS)
           if (d.gm_arg[go + k] != 0x7fffffff && d.gm_max[go + k] == gm) n_eq += (double)d.gm_eq[go + k];
-      n_eq = block_sum_d<BL_SEL_THREADS>(n_eq, sh.u.m.gsum);
+      n_eq = block_sum_d<BL_SEL_THREADS>(n_eq, sh.c.gsum);
       if (gi == 0x7fffffff) {
         status |= BL_SE_GREJECT;
       } else {
         tok = gi;
+        tokv = gm;
         if (n_eq > 1.0) status |= BL_SE_TIE;
       }
     }
-  } else if (T <= 0.0f) {
-    tok = Mi; /* sample_greedy over the full penalised row (src/sampling.br:752-754) */
-  } else if (mode & BL_M_TOPK) {
-    /* top_k_select list: kk = min(top_k, V) entries, unfilled slots are (-1e30, 0) */
-    int64_t kk = sp.top_k < V ? sp.top_k : V;
-    auto val = [&](int64_t j) -> float { return sh.u.m.keys[j] ? ckey_v(sh.u.m.keys[j]) : -1.0e30f; };
-    int pos = sample_ranked(sp, val, kk, kk, rng, skip, sh.u.m.recs, sh.u.m.gsum, sh, status);
-    if (pos >= 0) tok = sh.u.m.keys[pos] ? ckey_i(sh.u.m.keys[pos]) : 0;
-  } else {
-    /* full-vocabulary rank (src/sampling.br:301-365): candidates from the exponent pass */
-    int nf = d.full_n[row];
-    if (nf > V) {
-      nf = V;
-      status |= BL_SE_CAND_FULL;
+  }
+
+  /* the normaliser, prepared by every wavefront; then wavefront 0 chains it while wavefront 1 runs the
+   * short list's sequential loops */
+  if (lp_row) norm_prep(d, row, M, sh, m_pre, br_pre);
+  __syncthreads();
+  if (lp_row && w == 0) norm_chain(d, row, M, sh);
+  if (sampled && !status && short_list && w == 1 && lane == 0)
+    sh.ires[2] = ranked_serial(sp, (int)n_list, n_logical, keep, rng, skip, sh.ser_e, sh.ser_r, &sh.rng_out);
+  __syncthreads();
+  if (sampled && !status) {
+    int pos;
+    if (short_list) {
+      pos = sh.ires[2];
+      if (pos == -2 || pos >= n_list) {
+        status |= BL_SE_UNSUPPORTED;
+        pos = -1;
+      } else {
+        rng = sh.rng_out;
+      }
+    } else {
+      bl_grec *recs = sh.c.recs;
+      double *gsum = sh.c.gsum;
+      if ((n_list + 63) / 64 > BL_LDS_SORT / 64) {
+        recs = reinterpret_cast<bl_grec *>(d.grec) + (int64_t)row * 2 * (V / 64 + 64) + (V / 64 + 64);
+        gsum = d.gsum + (int64_t)row * (V / 64 + 64);
+      }
+      pos = sample_ranked_long(sp, val, n_list, n_logical, keep, rng, skip, recs, gsum, sh, status);
     }
-    int P = 1;
-    while (P < nf) P <<= 1;
-    uint64_t *keys = P <= BL_LDS_SORT ? sh.u.m.keys : d.sortk + (int64_t)row * (2 * (int64_t)V);
-    /* when the LDS holds the merged top-K list (logprob alternatives) keep it: sort the full list in global */
-    if (K > 0 && keys == sh.u.m.keys) keys = d.sortk + (int64_t)row * (2 * (int64_t)V);
-    for (int i = t; i < P; i += BL_SEL_THREADS)
-      keys[i] = i < nf ? ckey(d.full_v[(int64_t)row * V + i], d.full_i[(int64_t)row * V + i]) : 0ull;
-    __syncthreads();
-    bitonic_desc(keys, P);
-    bl_grec *recs = sh.u.m.recs;
-    double *gsum = sh.u.m.gsum;
-    if ((nf + 63) / 64 > BL_LDS_SORT / 64) {
-      recs = reinterpret_cast<bl_grec *>(d.grec) + (int64_t)row * 2 * (V / 64 + 64) + (V / 64 + 64);
-      gsum = d.gsum + (int64_t)row * (V / 64 + 64);
-    }
-    auto val = [&](int64_t j) -> float { return ckey_v(keys[j]); };
-    int pos = sample_ranked(sp, val, nf, (int64_t)V, rng, skip, recs, gsum, sh, status);
     if (pos >= 0) {
-      tok = ckey_i(keys[pos]);
+      const uint64_t kp = keys[pos];
+      tok = kp ? ckey_i(kp) : 0;
+      tokv = kp ? ckey_v(kp) : eff[tok];
       /* the heap rank orders equal values its own way (src/sampling.br:310-364): a tie at the chosen
        * position is reported instead of guessing */
-      float vp = val(pos);
-      if ((pos > 0 && val(pos - 1) == vp) || (pos + 1 < nf && val(pos + 1) == vp)) status |= BL_SE_TIE;
+      if (mode & BL_M_FULL) {
+        const float vp = val(pos);
+        if ((pos > 0 && val(pos - 1) == vp) || (pos + 1 < n_list && val(pos + 1) == vp)) status |= BL_SE_TIE;
+      }
     }
   }
 
-  /* outputs, logprobs (src/server.br:1027-1035) */
+  /* outputs, logprobs (src/server.br:1027-1035): alternatives = the first n_probs of the merged list */
+  const float lse = lp_row ? (float)log((double)sh.n.S) : 0.0f;
+  if (lp_row) {
+    const int n = sp.n_probs < rows.top_stride ? sp.n_probs : rows.top_stride;
+    if (t < n) {
+      const uint64_t k = t < K ? mk : 0ull;
+      const float v = k ? ckey_v(k) : -1.0e30f;
+      rows.top_ids[(int64_t)row * rows.top_stride + t] = k ? ckey_i(k) : 0;
+      rows.top_lp[(int64_t)row * rows.top_stride + t] = (v - M) - lse;
+    }
+  }
   if (t == 0) {
     rows.tok[row] = tok;
     if (rows.status) rows.status[row] = status;
+    if (lp_row) rows.lp[row] = (tokv - M) - lse;
     bool is_eog = false;
-    for (int k = 0; k < d.n_eog; k++) is_eog |= d.eog[k] == tok;
-    if ((mode & BL_M_LOGPROBS) && rows.lp) {
-      rows.lp[row] = eff[tok] - M;
-      for (int q = 0; q < sp.n_probs && q < rows.top_stride; q++) {
-        uint64_t k = q < n_top ? sh.u.m.keys[q] : 0ull;
-        int32_t id = k ? ckey_i(k) : 0;
-        float v = k ? ckey_v(k) : -1.0e30f;
-        rows.top_ids[(int64_t)row * rows.top_stride + q] = id;
-        rows.top_lp[(int64_t)row * rows.top_stride + q] = v - M;
-      }
-    }
+    for (int k = 0; k < n_eog; k++) is_eog |= (k < BL_EOG_LDS ? sh.eog[k] : d.eog[k]) == tok;
     if (rows.commit && status == 0) {
       /* tokens.push (src/server.br:1004): repeat window; reply_tokens.push unless EOG (:1037) */
       const int64_t so = (int64_t)slot * V;
-      uint32_t *tw = d.touched + (int64_t)slot * d.words;
-      sp.n_tokens += 1;
-      if (sp.rep_on) {
-        int rl = sp.repeat_last_n;
+      uint32_t *tw = d.touched + (int64_t)slot * d.words + (tok >> 5);
+      const uint32_t bit = 1u << (tok & 31);
+      sp.n_tokens = n_tokens0 + 1;
+      if (rep_on) {
         if (rl > 0) {
           int32_t *ring = d.ring + (int64_t)slot * BL_WCAP;
-          if (sp.win_len == rl) {
-            int32_t old = ring[sp.win_head];
-            d.wcnt[so + old] -= 1;
-            ring[sp.win_head] = tok;
-            sp.win_head = (sp.win_head + 1) % rl;
+          if (ring_full) {
+            atomicAdd(&d.wcnt[so + ring_old], -1);
+            ring[win_head] = tok;
+            sp.win_head = (win_head + 1) % rl;
           } else {
-            ring[(sp.win_head + sp.win_len) % rl] = tok;
-            sp.win_len += 1;
+            ring[(win_head + win_len) % rl] = tok;
+            sp.win_len = win_len + 1;
           }
         }
-        d.wcnt[so + tok] += 1;
-        tw[tok >> 5] |= 1u << (tok & 31);
+        atomicAdd(&d.wcnt[so + tok], 1);
+        atomicOr(tw, bit);
       }
       if (!is_eog) {
-        sp.n_reply += 1;
-        if (sp.fp_on) {
-          d.cnt[so + tok] += 1;
-          tw[tok >> 5] |= 1u << (tok & 31);
+        sp.n_reply = n_reply0 + 1;
+        if (fp_on) {
+          atomicAdd(&d.cnt[so + tok], 1);
+          atomicOr(tw, bit);
         }
-        if (sp.g_on) grammar_commit(d, sp, d.gram[slot], tok);
+        if (g_on) grammar_commit(d, sp, d.gram[slot], tok);
       }
       sp.rng = rng;
     }
     if (status) sp.err |= status;
-  }
-}
-
-/* logprob = (x - max) - log(normaliser) (src/sampling.br:268-273, src/server.br:1027-1035) */
-__global__ void bl_k_lpfinish(bl_dev d, bl_rows rows) {
-  const int row = blockIdx.x;
-  const bl_slot_dev &sp = d.slots[rows.slot[row]];
-  if (!((sp.mode & BL_M_LOGPROBS) && rows.lp)) return;
-  const float lse = d.lse[row];
-  if (threadIdx.x == 0) rows.lp[row] = rows.lp[row] - lse;
-  const int n = sp.n_probs < rows.top_stride ? sp.n_probs : rows.top_stride;
-  for (int q = threadIdx.x; q < n; q += blockDim.x) {
-    float *o = rows.top_lp + (int64_t)row * rows.top_stride + q;
-    *o = *o - lse;
   }
 }
 
@@ -1551,20 +1668,17 @@ __global__ void bl_k_synth(float *out, int64_t ld, int cfg, int64_t seed, int64_
 
 /* ------------------------------------------------------------------ host-side launchers */
 /* ev: optional 4 events recorded before/after the three kernels (kernel timing for the benchmark) */
-void bl_launch_step(const bl_dev &d, const float *logits, int64_t ld, const bl_rows &rows, int B, bool need_exp,
-                    bool need_gram, bool need_lp, hipStream_t s, hipEvent_t *ev) {
-  need_lp = need_lp && rows.lp;
+void bl_launch_step(const bl_dev &d, const float *logits, int64_t ld, const bl_rows &rows, int B, bool need_pass2,
+                    bool need_gram, hipStream_t s, hipEvent_t *ev) {
   dim3 g1(d.nc, B);
   if (ev) (void)hipEventRecord(ev[0], s);
   hipLaunchKernelGGL(bl_k_rowpass, g1, dim3(BL_RP_THREADS), 0, s, d, logits, ld, rows);
   if (ev) (void)hipEventRecord(ev[1], s);
   if (need_gram) hipLaunchKernelGGL(bl_k_gmask, dim3(d.gm_blocks, B), dim3(BL_GM_THREADS), 0, s, d, rows, 1);
-  if (need_exp) {
-    hipLaunchKernelGGL(bl_k_exppass, dim3((d.vocab + BL_EB - 1) / BL_EB, B), dim3(BL_RP_THREADS), 0, s, d, rows);
-  }
+  if (need_pass2)
+    hipLaunchKernelGGL(bl_k_exppass, dim3(1 + (d.vocab + BL_EB - 1) / BL_EB, B), dim3(BL_RP_THREADS), 0, s, d, rows);
   if (ev) (void)hipEventRecord(ev[2], s);
-  hipLaunchKernelGGL(bl_k_select, dim3(B, need_lp ? 2 : 1), dim3(BL_SEL_THREADS), 0, s, d, rows);
-  if (need_lp) hipLaunchKernelGGL(bl_k_lpfinish, dim3(B), dim3(64), 0, s, d, rows);
+  hipLaunchKernelGGL(bl_k_select, dim3(B), dim3(BL_SEL_THREADS), 0, s, d, rows);
   if (ev) (void)hipEventRecord(ev[3], s);
 }
 

@@ -58,7 +58,7 @@ struct Fiber {
 };
 
 struct Block {
-  dim3 bid, bdim;
+  dim3 bid, bdim, gdim;
   int n = 0;
   std::vector<Fiber> f;
   void *sched_sp = nullptr;
@@ -85,6 +85,7 @@ dim3 tidx() {
 }
 dim3 bidx() { return g_blk->bid; }
 dim3 bdim() { return g_blk->bdim; }
+dim3 gdim() { return g_blk->gdim; }
 int lane_id() { return g_tid & 63; }
 uint64_t *wave_slots() { return g_blk->slots[g_tid >> 6].data(); }
 
@@ -220,6 +221,7 @@ void launch(dim3 grid, dim3 block, const std::function<void()> &body) {
         Block b;
         b.bid = dim3(bx, by, bz);
         b.bdim = block;
+        b.gdim = grid;
         b.n = n;
         b.f.resize(n);
         b.wave_gen.assign(nw, 0);

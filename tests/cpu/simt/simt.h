@@ -45,6 +45,7 @@ struct Block;
 dim3 tidx();
 dim3 bidx();
 dim3 bdim();
+dim3 gdim();
 void sync_block_at(const char *file, int line);
 void sync_wave();
 void wave_site(const char *file, int line);
@@ -56,6 +57,7 @@ void launch(dim3 grid, dim3 block, const std::function<void()> &body);
 #define threadIdx (simt::tidx())
 #define blockIdx (simt::bidx())
 #define blockDim (simt::bdim())
+#define gridDim (simt::gdim())
 
 #define __syncthreads() simt::sync_block_at(__FILE__, __LINE__)
 inline void __threadfence() {}
