@@ -20,7 +20,9 @@
  *            approximate (double) prefix predicts.
  *   Phase B (one wavefront): walks the groups 64 at a time with a composed scan, and drops to
  *            element level only in a group that crosses a binade, lacks the needed binade, or contains
- *            the element a threshold search is looking for.
+ *            the element a threshold search is looking for. At element level the group's terms are
+ *            added one at a time in float32 from the exact running sum (at most 64 adds, each term
+ *            broadcast from its lane), which is the reference's own computation.
  */
 #ifndef BL_EXACT_H
 #define BL_EXACT_H
@@ -268,41 +270,27 @@ __device__ int bl_seq_walk(int64_t n, TermF term, RecF rec, bool thr_on, float t
     }
     if (g >= G) break;
     if (first == 64) continue;
-    /* ---- element level in group g ---- */
-    int64_t j0 = g * 64;
-    int64_t j = j0 + lane;
-    float a = j < n ? term(j) : 0.0f;
-    bool in = j < n;
-    int start = 0;
-    while (true) {
-      bl_inc fe = (in && lane >= start) ? bl_term_inc(a, e) : bl_inc_ident();
-      bl_inc se = bl_wave_scan(fe, lane);
-      uint32_t Ne = bl_apply(se, N);
-      bool act = in && lane >= start;
-      bool cross = act && Ne >= BL_N_TOP;
-      bool reach = act && !cross && thr_on && j >= min_idx && bl_make(e, Ne) >= thr;
-      unsigned long long ms = __ballot(cross || reach);
-      if (!ms) {
-        N = bl_bcast(Ne, 63);
-        break;
+    /* ---- element level in group g: the group crosses a binade, lacks the needed binade or reaches the
+     * threshold, so its terms are added one at a time in float32 from the exact running sum ---- */
+    const int64_t j0 = g * 64;
+    const int64_t j = j0 + lane;
+    const float a = j < n ? term(j) : 0.0f;
+    const int n_in = (int)(n - j0 < 64 ? n - j0 : 64);
+    float S = bl_make(e, N);
+    int hit = -1; /* first index reaching the threshold */
+#pragma unroll
+    for (int c = 0; c < 64; c++) {
+      const float x = bl_bcastf(a, c);
+      if (c < n_in && hit < 0) {
+        S = S + x;
+        if (thr_on && j0 + c >= min_idx && S >= thr) hit = c;
       }
-      int c = __ffsll((long long)ms) - 1;
-      uint32_t Nbefore = c > start ? bl_bcast(Ne, c - 1) : N;
-      bool c_reach = bl_bcast(reach ? 1u : 0u, c) != 0u;
-      if (c_reach) {
-        S_out = bl_make(e, bl_bcast(Ne, c));
-        return (int)(j0 + c);
-      }
-      float ac = bl_bcastf(a, c);
-      float Sn = bl_make(e, Nbefore) + ac; /* the one real float add at a binade crossing */
-      bl_split(Sn, e, N);
-      if (thr_on && j0 + c >= min_idx && Sn >= thr) {
-        S_out = Sn;
-        return (int)(j0 + c);
-      }
-      start = c + 1;
-      if (start >= 64) break;
     }
+    if (hit >= 0) {
+      S_out = S;
+      return (int)(j0 + hit);
+    }
+    bl_split(S, e, N);
     g += 1;
   }
   S_out = bl_make(e, N);

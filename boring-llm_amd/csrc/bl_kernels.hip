@@ -1168,25 +1168,21 @@ __device__ int sample_ranked_long(const bl_slot_dev &sp, ValF val, int64_t n_lis
   return chosen;
 }
 
-/* wavefront-level resolution of the terms [start, 64) of one 64-term group from state (e, N), crossing
- * binades as needed (a real float add at each crossing); `a` is this lane's term, `in` whether it exists */
+/* wavefront-level resolution of the terms [start, 64) of one 64-term group from state (e, N): the group
+ * crosses a binade (or its prediction failed), so its terms are added one at a time in float32 from the
+ * exact running sum, as the reference's loop does (src/sampling.br:262-264). `a` is this lane's term and
+ * `in` whether it exists (the existing terms are a prefix of the lanes). */
 __device__ __forceinline__ void elem_resolve(float a, bool in, int &e, uint32_t &N, int lane, int start = 0) {
-  while (true) {
-    const bool act = in && lane >= start;
-    const bl_inc fe = act ? bl_term_inc(a, e) : bl_inc_ident();
-    const uint32_t Ne = bl_apply(bl_wave_scan(fe, lane), N);
-    const unsigned long long ms = __ballot(act && Ne >= BL_N_TOP);
-    if (!ms) {
-      N = bl_bcast(Ne, 63);
-      return;
-    }
-    const int c = __ffsll((long long)ms) - 1;
-    const uint32_t Nbefore = c > start ? bl_bcast(Ne, c - 1) : N;
-    const float Sn = bl_make(e, Nbefore) + bl_bcastf(a, c); /* the one real float add at a crossing */
-    bl_split(Sn, e, N);
-    start = c + 1;
-    if (start >= 64) return;
+  (void)lane;
+  const int n_in = __popcll(__ballot(in));
+  float S = bl_make(e, N);
+  /* unrolled: the broadcasts do not depend on the running sum and issue ahead of the adds */
+#pragma unroll
+  for (int j = 0; j < 64; j++) {
+    const float x = bl_bcastf(a, j);
+    if (j >= start && j < n_in) S = S + x;
   }
+  bl_split(S, e, N);
 }
 
 /* groups [g_lo, g_hi) from the exact state (e, N), one wavefront: 64 group records per composed scan,
