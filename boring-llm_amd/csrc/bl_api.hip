@@ -104,7 +104,7 @@ __global__ void bl_k_commit(bl_dev d, int slot, const int32_t *toks, int n, int 
         int32_t *ring = d.ring + (int64_t)slot * BL_WCAP;
         if (sp.win_len == rl) {
           int32_t old = ring[sp.win_head];
-          d.wcnt[so + old] -= 1;
+          d.tokst[so + old].wcnt -= 1;
           ring[sp.win_head] = tok;
           sp.win_head = (sp.win_head + 1) % rl;
         } else {
@@ -112,13 +112,13 @@ __global__ void bl_k_commit(bl_dev d, int slot, const int32_t *toks, int n, int 
           sp.win_len += 1;
         }
       }
-      d.wcnt[so + tok] += 1;
+      d.tokst[so + tok].wcnt += 1;
       tw[tok >> 5] |= 1u << (tok & 31);
     }
     if (!is_eog) {
       sp.n_reply += 1;
       if (sp.fp_on) {
-        d.cnt[so + tok] += 1;
+        d.tokst[so + tok].cnt += 1;
         tw[tok >> 5] |= 1u << (tok & 31);
       }
       if (sp.g_on) grammar_commit(d, sp, d.gram[slot], tok);
@@ -188,10 +188,7 @@ int bl_create(int device, int max_slots, int max_rows, int vocab, bl_ctx **out) 
   } while (0)
   ALLOC(d.slots, S);
   ALLOC(d.touched, S * d.words);
-  ALLOC(d.flags, S * V);
-  ALLOC(d.bias, S * V);
-  ALLOC(d.cnt, S * V);
-  ALLOC(d.wcnt, S * V);
+  ALLOC(d.tokst, S * V);
   ALLOC(d.ring, S * BL_WCAP);
   ALLOC(d.eog, 1024);
   ALLOC(d.eff, R * V);
@@ -370,13 +367,12 @@ int bl_slot_reset(bl_ctx *c, int slot, const bl_params *p, uint64_t rng_state, c
     if (bias_ids[i] < 0 || bias_ids[i] >= V)
       return fail(BL_EPARAM, "logit_bias token id %d is outside the vocabulary", bias_ids[i]);
   std::vector<uint32_t> touched(c->d.words, 0u);
-  std::vector<uint8_t> flags(V, 0);
-  std::vector<float> bias(V, 0.0f);
-  std::vector<int32_t> cnt(V, 0), wcnt(V, 0), ring(BL_WCAP, 0);
+  std::vector<bl_tok> tk(V, bl_tok{0.0f, 0, 0, 0u});
+  std::vector<int32_t> ring(BL_WCAP, 0);
   auto touch = [&](int32_t id) { touched[id >> 5] |= 1u << (id & 31); };
   for (int i = 0; i < n_bias; i++) {
-    flags[bias_ids[i]] |= BL_TF_BIAS;
-    bias[bias_ids[i]] = bias_vals[i]; /* a repeated id keeps the last value, as a JSON object would */
+    tk[bias_ids[i]].flags |= BL_TF_BIAS;
+    tk[bias_ids[i]].bias = bias_vals[i]; /* a repeated id keeps the last value, as a JSON object would */
     touch(bias_ids[i]);
   }
   if (p->ignore_eos) {
@@ -384,20 +380,20 @@ int bl_slot_reset(bl_ctx *c, int slot, const bl_params *p, uint64_t rng_state, c
     if (c->d.n_eog) HIPCHK(hipMemcpy(eog.data(), c->d.eog, eog.size() * sizeof(int32_t), hipMemcpyDeviceToHost));
     for (int32_t id : eog)
       if (id >= 0 && id < V) {
-        flags[id] |= BL_TF_SUPPRESS;
+        tk[id].flags |= BL_TF_SUPPRESS;
         touch(id);
       }
   }
   if (s.fp_on)
     for (int i = 0; i < n_reply; i++) {
-      cnt[reply[i]] += 1;
+      tk[reply[i]].cnt += 1;
       touch(reply[i]);
     }
   if (s.rep_on) {
     int rl = p->repeat_last_n;
     int win = (rl > 0 && n_hist > rl) ? rl : n_hist;
     for (int i = n_hist - win; i < n_hist; i++) {
-      wcnt[history[i]] += 1;
+      tk[history[i]].wcnt += 1;
       touch(history[i]);
     }
     if (rl > 0) {
@@ -416,10 +412,7 @@ int bl_slot_reset(bl_ctx *c, int slot, const bl_params *p, uint64_t rng_state, c
   const size_t so = (size_t)slot * V;
   HIPCHK(hipStreamSynchronize(c->stream));
   HIPCHK(hipMemcpy(c->d.touched + (size_t)slot * c->d.words, touched.data(), touched.size() * 4, hipMemcpyHostToDevice));
-  HIPCHK(hipMemcpy(c->d.flags + so, flags.data(), V, hipMemcpyHostToDevice));
-  HIPCHK(hipMemcpy(c->d.bias + so, bias.data(), (size_t)V * 4, hipMemcpyHostToDevice));
-  HIPCHK(hipMemcpy(c->d.cnt + so, cnt.data(), (size_t)V * 4, hipMemcpyHostToDevice));
-  HIPCHK(hipMemcpy(c->d.wcnt + so, wcnt.data(), (size_t)V * 4, hipMemcpyHostToDevice));
+  HIPCHK(hipMemcpy(c->d.tokst + so, tk.data(), (size_t)V * sizeof(bl_tok), hipMemcpyHostToDevice));
   HIPCHK(hipMemcpy(c->d.ring + (size_t)slot * BL_WCAP, ring.data(), BL_WCAP * 4, hipMemcpyHostToDevice));
   HIPCHK(hipMemcpy(c->d.slots + slot, &s, sizeof s, hipMemcpyHostToDevice));
   c->host_slots[slot] = s;

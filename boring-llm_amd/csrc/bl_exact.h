@@ -119,11 +119,15 @@ BL_SD int bl_binade_of(double s) {
 }
 
 /* a 64-term group whose approximate start ga and end gb are not both safely (2^-20 relative) inside its
- * predicted binade E: the exact sum may cross a power of two within it */
-BL_SD bool bl_group_critical(float ga, float gb, int E) {
+ * predicted binade E: the exact sum may cross a power of two within it. `floor` is an exact lower bound
+ * of the running sum over the group (a float sum of non-negative terms is never below a term already
+ * added), so the lower side of the margin stops there: a sum that a term of exactly 1.0 (the row
+ * maximum's exp(0)) has just raised to 1 + tiny stays in binade 0. */
+BL_SD bool bl_group_critical(float ga, float gb, int E, double floor) {
   const float lo = 0.99999904632568359375f, hi = 1.00000095367431640625f; /* 1 -+ 2^-20 */
-  return bl_binade_of((double)ga * lo) != E || bl_binade_of((double)ga * hi) != E ||
-         bl_binade_of((double)gb * lo) != E || bl_binade_of((double)gb * hi) != E;
+  const double la = (double)ga * lo, lb = (double)gb * lo;
+  return bl_binade_of(la > floor ? la : floor) != E || bl_binade_of((double)ga * hi) != E ||
+         bl_binade_of(lb > floor ? lb : floor) != E || bl_binade_of((double)gb * hi) != E;
 }
 
 #if defined(__HIPCC__)

@@ -5,12 +5,11 @@
  *   bl_slot_dev            sampling parameters + scalar state (RNG, history lengths, window ring head)
  *   touched[V/32]          bit t set when token t's logit is modified by the step (logit_bias,
  *                          ignore_eos suppression, a reply count, a repeat-window count)
- *   flags[V] u8, bias[V]   logit_bias presence/value and suppression, per token
- *   cnt[V]                 occurrences of the token in the reply (frequency / presence penalties)
- *   wcnt[V]                occurrences of the token in the repeat window
+ *   tokst[V]               bl_tok, 16 bytes per token: logit_bias value, reply count (frequency /
+ *                          presence penalties), repeat-window count, flags (bias present, suppressed)
  *   ring[WCAP]             the last repeat_last_n tokens, for window eviction
- * The row pass reads `touched` densely (V/8 bytes per row, ~3% of the logits traffic) and the other
- * tables only at set bits. Committing a token is O(1) writes.
+ * The row pass reads `touched` densely (V/8 bytes per row, ~3% of the logits traffic) and the token
+ * records only at set bits, one cache line each. Committing a token is O(1) writes.
  *
  * Per step workspace, rows = B: transformed rows, per-chunk statistics and top-K candidates,
  * sequential-sum group records, full-vocabulary candidate lists and sort scratch.
@@ -66,6 +65,14 @@
 #define BL_SE_GREJECT 32
 #define BL_SE_GAMBIG 64
 
+/* one token's server-stage inputs in one slot (src/server.br:940-944, src/sampling.br:65-107, :175-237) */
+struct alignas(16) bl_tok {
+  float bias;     /* logit_bias value (flags & BL_TF_BIAS) */
+  int32_t cnt;    /* occurrences in the reply */
+  int32_t wcnt;   /* occurrences in the repeat window */
+  uint32_t flags; /* BL_TF_* */
+};
+
 struct bl_slot_dev {
   /* parameters (SamplingParams, src/model.br:1565-1584, and server extras) */
   float temperature, dynatemp_range, dynatemp_exponent, top_n_sigma;
@@ -87,10 +94,7 @@ struct bl_dev {
   int64_t words; /* V/32 rounded up */
   bl_slot_dev *slots;
   uint32_t *touched; /* [slots][words] */
-  uint8_t *flags;    /* [slots][V] */
-  float *bias;       /* [slots][V] */
-  int32_t *cnt;      /* [slots][V] */
-  int32_t *wcnt;     /* [slots][V] */
+  bl_tok *tokst;     /* [slots][V] */
   int32_t *ring;     /* [slots][WCAP] */
   int32_t *eog;      /* [n_eog] end-of-generation ids */
   int32_t n_eog;

@@ -161,7 +161,6 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass(bl_dev d, const fl
   __shared__ uint32_t hist[2048];
   __shared__ float red_m[4];
   __shared__ int red_i[4];
-  __shared__ double red_d[4 * BL_SUBS];
   __shared__ uint32_t sel[4];
   __shared__ int out_n;
   __shared__ uint64_t tkeys[BL_TK_CAP];      /* keys at or above the bound */
@@ -233,11 +232,11 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass(bl_dev d, const fl
 #pragma unroll
       for (int k = 0; k < 4 * NV; k++) {
         const bool on = (tb[k >> 2] >> (k & 3)) & 1u;
-        const int64_t id = so + pos_of(k);
-        f[k] = on ? (uint32_t)d.flags[id] : 0u;
-        bv[k] = on ? d.bias[id] : 0.0f;
-        cc[k] = on && fp ? d.cnt[id] : 0;
-        wc[k] = on && rp ? d.wcnt[id] : 0;
+        const bl_tok r = on ? d.tokst[so + pos_of(k)] : bl_tok{0.0f, 0, 0, 0u};
+        f[k] = r.flags;
+        bv[k] = r.bias;
+        cc[k] = fp ? r.cnt : 0;
+        wc[k] = rp ? r.wcnt : 0;
       }
 #pragma unroll
       for (int k = 0; k < 4 * NV; k++) {
@@ -268,9 +267,10 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass(bl_dev d, const fl
         if (pos_of(k) < cnt) dst[pos_of(k)] = x[k];
     }
   }
-  /* max, first argmax, approximate exp-sums per BL_EB positions: per wavefront relative to the
-   * wavefront's maximum, then combined by thread 0 */
-  static_assert(NV == BL_SUBS, "thread positions j*1024 + ... cover sub-block j");
+  /* max and first argmax; then, for logprob rows, approximate sums of exp(x - chunk max) over each BL_EB
+   * positions, from which the exponent pass predicts the binades of the normaliser's running sum
+   * (wavefront j reduces sub-block j) */
+  static_assert(NV == BL_SUBS && BL_RP_THREADS / 64 == BL_SUBS, "thread positions j*1024 + ... cover sub-block j");
   {
     float m = BL_NEG_INF;
     int mi = 0x7fffffff;
@@ -286,39 +286,38 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass(bl_dev d, const fl
       int i2 = __shfl_xor(mi, k, 64);
       argmax_merge(m, mi, m2, i2);
     }
-    double sj[NV];
-#pragma unroll
-    for (int j = 0; j < NV; j++) {
-      sj[j] = 0.0;
-      if (m > BL_NEG_INF) {
-#pragma unroll
-        for (int q = 0; q < 4; q++) sj[j] += (double)__expf(x[4 * j + q] - m);
-      }
-      sj[j] = bl_wave_sum_d(sj[j]);
-    }
     if (lane == 0) {
       red_m[w] = m;
       red_i[w] = mi;
-#pragma unroll
-      for (int j = 0; j < NV; j++) red_d[w * NV + j] = sj[j];
     }
     __syncthreads();
+    float cm = red_m[0];
+    int ci = red_i[0];
+#pragma unroll
+    for (int k = 1; k < BL_RP_THREADS / 64; k++) argmax_merge(cm, ci, red_m[k], red_i[k]);
+    const int64_t o = (int64_t)row * nc + c;
+    if (sp.mode & BL_M_LOGPROBS) {
+      float *red_s = xs; /* [BL_SUBS][BL_RP_THREADS]; xs is free until the radix fallback */
+#pragma unroll
+      for (int j = 0; j < NV; j++) {
+        float sj = 0.0f;
+        if (cm > BL_NEG_INF) {
+#pragma unroll
+          for (int q = 0; q < 4; q++) sj += __expf(x[4 * j + q] - cm);
+        }
+        red_s[j * BL_RP_THREADS + t] = sj;
+      }
+      __syncthreads();
+      double v = 0.0;
+#pragma unroll
+      for (int i = 0; i < BL_RP_THREADS / 64; i++) v += (double)red_s[w * BL_RP_THREADS + lane + 64 * i];
+      v = bl_wave_sum_d(v);
+      if (lane == 0) d.c_bsum[o * BL_SUBS + w] = (float)v;
+      __syncthreads(); /* red_s (xs) is read before the fallback reuses it */
+    }
     if (t == 0) {
-      float cm = red_m[0];
-      int ci = red_i[0];
-      for (int k = 1; k < BL_RP_THREADS / 64; k++) argmax_merge(cm, ci, red_m[k], red_i[k]);
-      double bs[NV];
-      for (int j = 0; j < NV; j++) bs[j] = 0.0;
-      if (cm > BL_NEG_INF)
-        for (int k = 0; k < BL_RP_THREADS / 64; k++)
-          if (red_m[k] > BL_NEG_INF) {
-            const double sc = exp((double)red_m[k] - (double)cm);
-            for (int j = 0; j < NV; j++) bs[j] += red_d[k * NV + j] * sc;
-          }
-      const int64_t o = (int64_t)row * nc + c;
       d.c_max[o] = cm;
       d.c_arg[o] = ci == 0x7fffffff ? i0 : i0 + ci;
-      for (int j = 0; j < NV; j++) d.c_bsum[o * BL_SUBS + j] = (float)bs[j];
     }
   }
 
@@ -685,16 +684,15 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_exppass(bl_dev d, bl_rows 
 #pragma unroll
     for (int k = 0; k < 4; k++) x[k] = j0 + k < cnt ? src[k] : BL_NEG_INF;
   }
-  /* the row maximum, by every wavefront from the chunk maxima */
+  /* the row maximum and its first index, by every wavefront from the chunk statistics */
   float M = BL_NEG_INF;
-  for (int k = lane; k < nc; k += 64) {
-    const float cm = d.c_max[(int64_t)row * nc + k];
-    M = cm > M ? cm : M;
-  }
+  int Mi = 0x7fffffff;
+  for (int k = lane; k < nc; k += 64) argmax_merge(M, Mi, d.c_max[(int64_t)row * nc + k], d.c_arg[(int64_t)row * nc + k]);
 #pragma unroll
   for (int k = 32; k >= 1; k >>= 1) {
     const float o = __shfl_xor(M, k, 64);
-    M = o > M ? o : M;
+    const int oi = __shfl_xor(Mi, k, 64);
+    argmax_merge(M, Mi, o, oi);
   }
 
   if (mode & BL_M_LOGPROBS) {
@@ -724,8 +722,12 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_exppass(bl_dev d, bl_rows 
       if (q < w) before += wtot[q];
       tot += wtot[q];
     }
-    /* group of 64 terms = 16 threads; its approximate start is its first thread's prefix */
-    const double gstart = __shfl(before, lane & ~15, 64);
+    /* group of 64 terms = 16 threads; its approximate start is its first thread's prefix, raised to the
+     * exact floor 1.0 once the row maximum's term exp(0) = 1 is behind it */
+    const int gs = i0 + 4 * (t & ~15);
+    const double floor1 = gs > Mi ? 1.0 : 0.0;
+    const double gs0 = __shfl(before, lane & ~15, 64);
+    const double gstart = gs0 > floor1 ? gs0 : floor1;
     bl_grec1 r;
     r.E = bl_binade_of(gstart);
     r.pad = 0;
@@ -746,7 +748,7 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_exppass(bl_dev d, bl_rows 
     const double nxt = __shfl(before, gl + 16 < 64 ? gl + 16 : 63, 64);
     const double gend = gl + 16 < 64 ? nxt : wend;
     const bool gex = 4 * (t & ~15) < cnt;
-    const bool crit = gex && bl_group_critical((float)gstart, (float)gend, r.E);
+    const bool crit = gex && bl_group_critical((float)gstart, (float)(gend > floor1 ? gend : floor1), r.E, floor1);
     const bool head = (lane & 15) == 0;
     const unsigned long long cb = __ballot(crit && head);
     const unsigned long long eb = __ballot(gex && head);
@@ -1627,7 +1629,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
         if (rl > 0) {
           int32_t *ring = d.ring + (int64_t)slot * BL_WCAP;
           if (ring_full) {
-            atomicAdd(&d.wcnt[so + ring_old], -1);
+            atomicAdd(&d.tokst[so + ring_old].wcnt, -1);
             ring[win_head] = tok;
             sp.win_head = (win_head + 1) % rl;
           } else {
@@ -1635,13 +1637,13 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
             sp.win_len = win_len + 1;
           }
         }
-        atomicAdd(&d.wcnt[so + tok], 1);
+        atomicAdd(&d.tokst[so + tok].wcnt, 1);
         atomicOr(tw, bit);
       }
       if (!is_eog) {
         sp.n_reply = n_reply0 + 1;
         if (fp_on) {
-          atomicAdd(&d.cnt[so + tok], 1);
+          atomicAdd(&d.tokst[so + tok].cnt, 1);
           atomicOr(tw, bit);
         }
         if (g_on) grammar_commit(d, sp, d.gram[slot], tok);
