@@ -64,6 +64,19 @@ def cpu_baseline(target_s):
             "ms_per_step": 1e3 * sec / steps}
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_step_b8_v151936.json")
+
+
+def measured_traffic():
+    """HBM bytes per launch of each step kernel (FETCH_SIZE + WRITE_SIZE, scaled by the copy calibration),
+    from the committed hardware-counter summary; None when it is absent."""
+    if not os.path.exists(TRAFFIC_FILE):
+        return None
+    with open(TRAFFIC_FILE) as f:
+        t = json.load(f)
+    return {k: v["bytes_per_launch"] for k, v in t["kernels"].items()}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -71,6 +84,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-graph", action="store_true", help="direct launches (hardware-counter runs)")
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="run only a plain 256 MiB device-to-device copy (calibrates FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU; the path shards by slot with no exchange "
@@ -78,6 +94,17 @@ def main():
         sys.exit(2)
 
     import torch
+
+    if args.copy_calib:
+        n = 64 << 20  # 256 MiB of float32 each way
+        a = torch.ones(n, dtype=torch.float32, device="cuda:0")
+        b = torch.empty_like(a)
+        for _ in range(5):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calib_bytes_read": 4 * n, "copy_calib_bytes_written": 4 * n, "launches": 5}))
+        return
+
     import bl_select as BL
 
     dev = torch.device("cuda:0")
@@ -102,6 +129,8 @@ def main():
     # one HIP graph per pool entry (no allocation, no host sync inside a step)
     graphs = []
     try:
+        if args.no_graph:
+            raise RuntimeError("--no-graph")
         for p in range(POOL):
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, stream=stream):
@@ -109,7 +138,8 @@ def main():
             graphs.append(g)
         use_graph = True
     except Exception as e:  # noqa: BLE001
-        print(f"bench.py: graph capture failed ({e}); timing direct launches", file=sys.stderr)
+        if not args.no_graph:
+            print(f"bench.py: graph capture failed ({e}); timing direct launches", file=sys.stderr)
         graphs, use_graph = [], False
     torch.cuda.synchronize()
 
@@ -156,6 +186,7 @@ def main():
     dom = int(np.argmax(kms))
     alg_bytes = 4.0 * B * V  # logits each step must read (the path's algorithmic traffic)
     achieved = alg_bytes / (kms[dom] * 1e-3) / 1e9
+    traffic = measured_traffic()
     out = {
         "metric": METRIC,
         "value": args.steps / elapsed,
@@ -175,8 +206,13 @@ def main():
                    "batch": B, "vocab": V, "hip_graph": use_graph, "logits_pool_MB": POOL * B * V * 4 / 1e6},
         "kernels_us": {names[k]: 1e3 * kms[k] for k in range(3)},
         "roofline": {"bound": "hbm", "kernel": names[dom], "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": traffic.get(names[dom]) if traffic else None,
                      "algorithmic_bytes_per_launch": alg_bytes},
+        "traffic_bytes_per_launch": traffic,
+        # each kernel's measured HBM bytes (counters) over its event-timed duration
+        "kernel_hbm_GBs": ({names[k]: traffic[names[k]] / (kms[k] * 1e-3) / 1e9 for k in range(3)}
+                           if traffic else None),
         "hbm_GBs_step": alg_bytes / (1e-3 * sum(kms)) / 1e9,
     }
     if not args.no_cpu:
