@@ -160,7 +160,7 @@ void bl_params_default(bl_params *p) {
 }
 
 int bl_create(int device, int max_slots, int max_rows, int vocab, bl_ctx **out) {
-  if (!out || max_slots <= 0 || max_rows <= 0 || vocab <= 0 || vocab > BL_MAX_CHUNKS * BL_CH)
+  if (!out || max_slots <= 0 || max_slots > 32767 || max_rows <= 0 || vocab <= 0 || vocab > BL_MAX_CHUNKS * BL_CH)
     return fail(BL_EPARAM, "bl_create: invalid sizes (slots %d, rows %d, vocab %d)", max_slots, max_rows, vocab);
   bl_ctx *c = new bl_ctx;
   c->device = device;
@@ -557,6 +557,7 @@ int bl_grammar_mask(bl_ctx *c, int slot, uint32_t *d_mask_out, int32_t *forced_e
   HIPCHK(hipMemcpy(c->d_mslot, &slot, sizeof(int32_t), hipMemcpyHostToDevice));
   bl_rows rows{};
   rows.slot = c->d_mslot; /* its own row table: the bound rows of the asynchronous step stay intact */
+  rows.slot_inline[0] = (int16_t)slot;
   bl_launch_gmask(c->d, rows, c->stream);
   HIPCHK(hipGetLastError());
   const size_t words = ((size_t)c->d.vocab + 31) / 32;
@@ -616,6 +617,7 @@ static int status_error(int st) {
 static bl_rows make_rows(bl_ctx *c, bool with_skip, int commit, int top_stride) {
   bl_rows r{};
   r.slot = c->d_slot;
+  for (int i = 0; i < BL_ROWS_INLINE && i < c->d.max_rows; i++) r.slot_inline[i] = (int16_t)c->h_slot[i];
   r.rng_skip = with_skip ? c->d_skip : nullptr;
   r.commit = commit;
   r.tok = c->d_tok;

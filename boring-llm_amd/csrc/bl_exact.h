@@ -183,20 +183,79 @@ __device__ __forceinline__ bl_inc bl_lane63(bl_inc f) {
 /* ordered reduction; result valid in every lane */
 __device__ __forceinline__ bl_inc bl_wave_reduce(bl_inc f, int lane) { return bl_lane63(bl_wave_scan(f, lane)); }
 
+/* inclusive ordered scan with `op` across the wavefront on 32-bit lanes: row shifts, then the row
+ * broadcasts of lanes 15 and 31 (DPP, in VALU; no LDS round trip) */
+template <class Op>
+__device__ __forceinline__ uint32_t bl_wscan_u32(uint32_t v, int lane, Op op) {
+  const int r = lane & 15;
+  uint32_t o;
+  o = bl_dpp<BL_DPP_ROW_SHR(1), 0xF>(0u, v);
+  if (r >= 1) v = op(o, v);
+  o = bl_dpp<BL_DPP_ROW_SHR(2), 0xF>(0u, v);
+  if (r >= 2) v = op(o, v);
+  o = bl_dpp<BL_DPP_ROW_SHR(4), 0xF>(0u, v);
+  if (r >= 4) v = op(o, v);
+  o = bl_dpp<BL_DPP_ROW_SHR(8), 0xF>(0u, v);
+  if (r >= 8) v = op(o, v);
+  o = bl_dpp<BL_DPP_ROW_BCAST15, 0xA>(0u, v);
+  if (lane & 16) v = op(o, v);
+  o = bl_dpp<BL_DPP_ROW_BCAST31, 0xC>(0u, v);
+  if (lane >= 32) v = op(o, v);
+  return v;
+}
+__device__ __forceinline__ uint32_t bl_wmax_u32(uint32_t v, int lane) {
+  return bl_bcast(bl_wscan_u32(v, lane, [](uint32_t a, uint32_t b) { return a > b ? a : b; }), 63);
+}
+__device__ __forceinline__ uint32_t bl_wmin_u32(uint32_t v, int lane) {
+  return bl_bcast(bl_wscan_u32(v, lane, [](uint32_t a, uint32_t b) { return a < b ? a : b; }), 63);
+}
+/* inclusive prefix sum of an int */
+__device__ __forceinline__ int bl_wscan_add(int v, int lane) {
+  return (int)bl_wscan_u32((uint32_t)v, lane, [](uint32_t a, uint32_t b) { return a + b; });
+}
+/* the wavefront's first maximum: the largest value (NaN never wins, -0 equals +0 and comes back as +0)
+ * and the lowest index holding it; result in every lane */
+__device__ __forceinline__ void bl_wargmax(float &m, int &mi, int lane) {
+  const uint32_t k = m != m ? 0u : bl_fkey(m + 0.0f);
+  const uint32_t km = bl_wmax_u32(k, lane);
+  mi = (int)bl_wmin_u32(k == km ? (uint32_t)mi : 0xFFFFFFFFu, lane);
+  m = bl_fkey_inv(km);
+}
+/* doubles: both halves moved by DPP */
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ double bl_dpp_d(double v) {
+  const uint64_t b = bl_d2u(v);
+  const uint64_t lo = bl_dpp<CTRL, ROW_MASK>(0u, (uint32_t)b), hi = bl_dpp<CTRL, ROW_MASK>(0u, (uint32_t)(b >> 32));
+  return bl_u2d(lo | (hi << 32));
+}
+__device__ __forceinline__ double bl_wscan_add_d(double v, int lane) {
+  const int r = lane & 15;
+  double o;
+  o = bl_dpp_d<BL_DPP_ROW_SHR(1), 0xF>(v);
+  if (r >= 1) v = o + v;
+  o = bl_dpp_d<BL_DPP_ROW_SHR(2), 0xF>(v);
+  if (r >= 2) v = o + v;
+  o = bl_dpp_d<BL_DPP_ROW_SHR(4), 0xF>(v);
+  if (r >= 4) v = o + v;
+  o = bl_dpp_d<BL_DPP_ROW_SHR(8), 0xF>(v);
+  if (r >= 8) v = o + v;
+  o = bl_dpp_d<BL_DPP_ROW_BCAST15, 0xA>(v);
+  if (lane & 16) v = o + v;
+  o = bl_dpp_d<BL_DPP_ROW_BCAST31, 0xC>(v);
+  if (lane >= 32) v = o + v;
+  return v;
+}
+__device__ __forceinline__ double bl_bcast_d(double v, int l) {
+  const uint64_t b = bl_d2u(v);
+  const uint64_t lo = bl_bcast((uint32_t)b, l), hi = bl_bcast((uint32_t)(b >> 32), l);
+  return bl_u2d(lo | (hi << 32));
+}
+/* approximate wave sum (the association is the scan's; used for predictions only), in every lane */
 __device__ __forceinline__ double bl_wave_sum_d(double x) {
-#pragma unroll
-  for (int k = 32; k >= 1; k >>= 1) x += __shfl_xor(x, k, 64);
-  return x;
+  const int lane = (int)(threadIdx.x & 63);
+  return bl_bcast_d(bl_wscan_add_d(x, lane), 63);
 }
-__device__ __forceinline__ double bl_wave_excl_scan_d(double x, int lane) {
-  double inc = x;
-#pragma unroll
-  for (int k = 1; k < 64; k <<= 1) {
-    double o = __shfl_up(inc, k, 64);
-    if (lane >= k) inc += o;
-  }
-  return inc - x;
-}
+__device__ __forceinline__ double bl_wave_excl_scan_d(double x, int lane) { return bl_wscan_add_d(x, lane) - x; }
 
 /* composed pair of NT consecutive terms at binade e, folded in order by one thread */
 template <int NT>

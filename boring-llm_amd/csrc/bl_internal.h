@@ -131,9 +131,13 @@ struct bl_dev {
   int32_t *gm_eq;         /* allowed tokens equal to it */
 };
 
-/* one step's row table (device pointers) */
+#define BL_ROWS_INLINE 64 /* rows whose slot index travels in the kernel arguments */
+
+/* one step's row table (device pointers; the first BL_ROWS_INLINE slot indices also by value, so a
+ * kernel reads its row's slot without a dependent load) */
 struct bl_rows {
   const int32_t *slot;     /* [B] */
+  int16_t slot_inline[BL_ROWS_INLINE];
   const int32_t *rng_skip; /* [B] draws consumed before this row's draw (speculative rows), or null */
   int32_t commit;          /* append the chosen token to the slot history */
   int32_t *tok;            /* [B] */
@@ -145,6 +149,10 @@ struct bl_rows {
 };
 
 #if defined(__HIPCC__)
+__device__ __forceinline__ int bl_row_slot(const bl_rows &r, int row) {
+  return row < BL_ROWS_INLINE ? (int)r.slot_inline[row] : r.slot[row];
+}
+
 /* appends token `tok`'s bytes to the slot's grammar position (reply_tokens.push of a non-EOG token,
  * src/server.br:1037); one thread */
 __device__ inline void grammar_commit(const bl_dev &d, bl_slot_dev &sp, const bl_gram_view &g, int32_t tok) {

@@ -155,7 +155,7 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass(bl_dev d, const fl
                                                               bl_rows rows) {
   const int V = d.vocab, nc = d.nc;
   const int c = blockIdx.x, row = blockIdx.y, t = threadIdx.x, lane = t & 63, w = t >> 6;
-  const int slot = rows.slot[row];
+  const int slot = bl_row_slot(rows, row);
   const bl_slot_dev &sp = slot_of(d, slot);
   __shared__ float xs[BL_CH];
   __shared__ uint32_t hist[2048];
@@ -280,12 +280,7 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass(bl_dev d, const fl
         m = x[k];
         mi = pos_of(k);
       }
-#pragma unroll
-    for (int k = 32; k >= 1; k >>= 1) {
-      float m2 = __shfl_xor(m, k, 64);
-      int i2 = __shfl_xor(mi, k, 64);
-      argmax_merge(m, mi, m2, i2);
-    }
+    bl_wargmax(m, mi, lane);
     if (lane == 0) {
       red_m[w] = m;
       red_i[w] = mi;
@@ -344,16 +339,15 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass(bl_dev d, const fl
     const int n_all = min((cnt + 3) >> 2, BL_RP_THREADS);
     const int n_w = min(max(n_all - 64 * w, 0), 64);
     const int share = n_all >= K ? (K * n_w + n_all - 1) / n_all : 64 + 1; /* > 64: no bound */
-    int nge = 0; /* threads of this wavefront whose maximum is at least this thread's */
-#pragma unroll 16
-    for (int i = 0; i < 64; i++) nge += (uint32_t)__builtin_amdgcn_readlane((int)best, i) >= best ? 1 : 0;
-    uint32_t wb = (best != 0u && nge >= share) ? best : 0u;
-    if (share == 0) wb = 0xFFFFFFFFu; /* no threads of the row: no part in the bound */
+    /* the share-th largest of the wavefront's maxima: the largest key v with at least `share` maxima >= v,
+     * bit by bit from the top (0 when fewer than `share` threads hold a valid value) */
+    uint32_t wb = 0u;
 #pragma unroll
-    for (int k = 32; k >= 1; k >>= 1) {
-      const uint32_t o = (uint32_t)__shfl_xor((int)wb, k, 64);
-      wb = o > wb ? o : wb;
+    for (int bit = 31; bit >= 0; bit--) {
+      const uint32_t cand = wb | (1u << bit);
+      if (__popcll(__ballot(best >= cand)) >= share) wb = cand;
     }
+    if (share == 0) wb = 0xFFFFFFFFu; /* no threads of the row: no part in the bound */
     if (lane == 0) tk_wb[w] = wb;
     if (t == 0) tk_n = 0;
     __syncthreads();
@@ -364,16 +358,11 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass(bl_dev d, const fl
     int mine = 0;
 #pragma unroll
     for (int k = 0; k < 4 * NV; k++) mine += (x[k] > -1.0e30f && bl_fkey(x[k]) >= tau) ? 1 : 0;
-    int incl = mine;
-#pragma unroll
-    for (int k = 1; k < 64; k <<= 1) {
-      const int o = __shfl_up(incl, k, 64);
-      if (lane >= k) incl += o;
-    }
-    const int wtot = __shfl(incl, 63, 64);
+    const int incl = bl_wscan_add(mine, lane);
+    const int wtot = (int)bl_bcast((uint32_t)incl, 63);
     int wbase = 0;
     if (lane == 0 && wtot > 0) wbase = atomicAdd(&tk_n, wtot);
-    int pos = __shfl(wbase, 0, 64) + incl - mine;
+    int pos = (int)bl_bcast((uint32_t)wbase, 0) + incl - mine;
 #pragma unroll
     for (int k = 0; k < 4 * NV; k++)
       if (x[k] > -1.0e30f && bl_fkey(x[k]) >= tau) {
@@ -654,7 +643,7 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_exppass(bl_dev d, bl_rows 
   const bool merger = lin < nrows;
   const int row = merger ? lin : (lin - nrows) / nbx;
   const int b = merger ? 0 : (lin - nrows) - row * nbx;
-  const int slot = rows.slot[row];
+  const int slot = bl_row_slot(rows, row);
   const bl_slot_dev &sp = slot_of(d, slot);
   const int mode = sp.mode;
   if (merger) {
@@ -688,12 +677,7 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_exppass(bl_dev d, bl_rows 
   float M = BL_NEG_INF;
   int Mi = 0x7fffffff;
   for (int k = lane; k < nc; k += 64) argmax_merge(M, Mi, d.c_max[(int64_t)row * nc + k], d.c_arg[(int64_t)row * nc + k]);
-#pragma unroll
-  for (int k = 32; k >= 1; k >>= 1) {
-    const float o = __shfl_xor(M, k, 64);
-    const int oi = __shfl_xor(Mi, k, 64);
-    argmax_merge(M, Mi, o, oi);
-  }
+  bl_wargmax(M, Mi, lane);
 
   if (mode & BL_M_LOGPROBS) {
     /* approximate sum before this block, from the row pass's sums per BL_EB positions (every
@@ -794,16 +778,11 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_exppass(bl_dev d, bl_rows 
     int mine = 0;
 #pragma unroll
     for (int k = 0; k < 4; k++) mine += (j0 + k < cnt && x[k] >= thr) ? 1 : 0;
-    int incl = mine;
-#pragma unroll
-    for (int k = 1; k < 64; k <<= 1) {
-      int o = __shfl_up(incl, k, 64);
-      if (lane >= k) incl += o;
-    }
-    const int wtot_n = __shfl(incl, 63, 64);
+    const int incl = bl_wscan_add(mine, lane);
+    const int wtot_n = (int)bl_bcast((uint32_t)incl, 63);
     int base = 0;
     if (lane == 0 && wtot_n > 0) base = atomicAdd(&d.full_n[row], wtot_n);
-    base = __shfl(base, 0, 64);
+    base = (int)bl_bcast((uint32_t)base, 0);
     int pos = base + incl - mine;
 #pragma unroll
     for (int k = 0; k < 4; k++)
@@ -829,7 +808,7 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_exppass(bl_dev d, bl_rows 
  */
 __global__ __launch_bounds__(BL_GM_THREADS) void bl_k_gmask(bl_dev d, bl_rows rows, int with_values) {
   const int V = d.vocab, row = blockIdx.y, t = threadIdx.x, lane = t & 63, w = t >> 6;
-  const int slot = rows.slot[row];
+  const int slot = bl_row_slot(rows, row);
   const bl_slot_dev &sp = d.slots[slot];
   if (!sp.g_on) return;
   __shared__ float red_m[BL_GM_THREADS / 64];
@@ -1453,7 +1432,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
     m_pre = d.bcrit[(int64_t)row * d.nb + t];
     br_pre = reinterpret_cast<const bl_grec1 *>(d.brec)[(int64_t)row * d.nb + t];
   }
-  const int slot = rows.slot[row];
+  const int slot = bl_row_slot(rows, row);
   bl_slot_dev &sp = d.slots[slot];
   const int mode = sp.mode, K = sp.k_sel;
   const float T = sp.temperature;

@@ -67,8 +67,9 @@ typedef struct {
 
 void bl_params_default(bl_params *p);
 
-/* Context on `device` for up to `max_slots` concurrent requests and `max_rows` rows per call, over a
- * vocabulary of `vocab` tokens. Replaces nothing in the reference (it holds no device state). */
+/* Context on `device` for up to `max_slots` (<= 32767) concurrent requests and `max_rows` rows per call,
+ * over a vocabulary of `vocab` tokens (<= 4,194,304). Replaces nothing in the reference (it holds no
+ * device state). */
 int bl_create(int device, int max_slots, int max_rows, int vocab, bl_ctx **out);
 void bl_destroy(bl_ctx *ctx);
 const char *bl_last_error(void);
