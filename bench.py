@@ -108,11 +108,9 @@ def main():
     import bl_select as BL
 
     dev = torch.device("cuda:0")
-    stream = torch.cuda.Stream()
     ctx = BL.Context(V, B, B)
     setup_slots(BL, ctx)
     ctx.bind_rows(list(range(B)))
-    ctx.set_stream(stream.cuda_stream)
     pool = torch.empty((POOL, B, V), dtype=torch.float32, device=dev)
     for p in range(POOL):
         ctx.synth_logits(pool[p].data_ptr(), V, 2, SEED, p, B, V)
@@ -126,61 +124,51 @@ def main():
         ctx.sample_step_async(B, pool[p].data_ptr(), V, d_tok.data_ptr(), d_lp.data_ptr(), d_ti.data_ptr(),
                               d_tl.data_ptr(), TOPN)
 
-    # one HIP graph per pool entry (no allocation, no host sync inside a step)
+    # one HIP graph per pool entry, captured by the library on its own stream (bl_step_graph_create): no
+    # allocation and no host synchronisation inside a step
     graphs = []
-    try:
-        if args.no_graph:
-            raise RuntimeError("--no-graph")
-        for p in range(POOL):
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g, stream=stream):
-                launch(p)
-            graphs.append(g)
-        use_graph = True
-    except Exception as e:  # noqa: BLE001
-        if not args.no_graph:
-            print(f"bench.py: graph capture failed ({e}); timing direct launches", file=sys.stderr)
-        graphs, use_graph = [], False
-    torch.cuda.synchronize()
+    if not args.no_graph:
+        graphs = [ctx.step_graph(B, pool[p].data_ptr(), V, d_tok.data_ptr(), d_lp.data_ptr(), d_ti.data_ptr(),
+                                 d_tl.data_ptr(), TOPN) for p in range(POOL)]
+    use_graph = bool(graphs)
 
     def step(i):
-        with torch.cuda.stream(stream):
-            if use_graph:
-                graphs[i % POOL].replay()
-            else:
-                launch(i % POOL)
+        if use_graph:
+            ctx.graph_launch(graphs[i % POOL])
+        else:
+            launch(i % POOL)
 
     for i in range(args.warmup):
         step(i)
-    torch.cuda.synchronize()
+    ctx.sync()
 
     # throughput: K back-to-back steps
     t0 = time.perf_counter()
     for i in range(args.steps):
         step(args.warmup + i)
-    torch.cuda.synchronize()
+    ctx.sync()
     elapsed = time.perf_counter() - t0
 
-    # latency: one step + sync
+    # latency: one step + stream synchronisation
     lat = []
     base = args.warmup + args.steps
     for i in range(min(args.steps, 1000)):
         a = time.perf_counter()
         step(base + i)
-        stream.synchronize()
+        ctx.sync()
         lat.append(time.perf_counter() - a)
     p50_us = 1e6 * float(np.median(lat))
-    torch.cuda.synchronize()
 
     # per-kernel durations (events around each kernel on the launch stream)
     ctx.set_timing(True)
     n_t = min(args.steps, 400)
     for i in range(n_t):
-        with torch.cuda.stream(stream):
-            launch((base + i) % POOL)
+        launch((base + i) % POOL)
     kms, nsteps = ctx.get_timing()
     ctx.set_timing(False)
-    torch.cuda.synchronize()
+    ctx.sync()
+    for g in graphs:
+        BL.Context.graph_destroy(g)
 
     names = ["bl_k_rowpass", "bl_k_exppass", "bl_k_select"]
     dom = int(np.argmax(kms))

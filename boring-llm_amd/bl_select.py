@@ -48,7 +48,8 @@ EXPORTS = [
     "bl_slot_reset", "bl_slot_rng", "bl_slot_commit", "bl_sample_step", "bl_bind_rows", "bl_sample_step_async",
     "bl_spec_verify", "bl_synth_logits", "bl_math_digest", "bl_workload_ids", "bl_workload_bias",
     "bl_workload_drafts", "bl_set_timing", "bl_get_timing", "bl_set_vocab", "bl_slot_grammar", "bl_grammar_mask",
-    "bl_workload_c3_vocab",
+    "bl_workload_c3_vocab", "bl_step_graph_create", "bl_step_graph_launch", "bl_step_graph_destroy",
+    "bl_stream_sync",
 ]
 
 _lib = None
@@ -79,6 +80,11 @@ def lib():
         L.bl_sample_step_async.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p,
                                            C.c_void_p, C.c_void_p, C.c_int]
         L.bl_spec_verify.argtypes = [C.c_void_p, i32p, C.c_int, C.c_int, C.c_void_p, C.c_int64, i32p, i32p, i32p]
+        L.bl_step_graph_create.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p,
+                                           C.c_void_p, C.c_void_p, C.c_int, C.POINTER(C.c_void_p)]
+        L.bl_step_graph_launch.argtypes = [C.c_void_p, C.c_void_p]
+        L.bl_step_graph_destroy.argtypes = [C.c_void_p]
+        L.bl_stream_sync.argtypes = [C.c_void_p]
         L.bl_synth_logits.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_int, C.c_int64, C.c_int64, C.c_int,
                                       C.c_int]
         L.bl_math_digest.argtypes = [C.c_void_p, C.c_int, C.c_uint32, C.c_int, u64p]
@@ -181,6 +187,23 @@ class Context:
     def sample_step_async(self, B, d_logits_ptr, ld, d_tok, d_lp=0, d_top_ids=0, d_top_lp=0, top_stride=0):
         _check(lib().bl_sample_step_async(self.h, B, C.c_void_p(d_logits_ptr), ld, C.c_void_p(d_tok),
                                           C.c_void_p(d_lp), C.c_void_p(d_top_ids), C.c_void_p(d_top_lp), top_stride))
+
+    def step_graph(self, B, d_logits_ptr, ld, d_tok, d_lp=0, d_top_ids=0, d_top_lp=0, top_stride=0):
+        """One bound-rows step captured into a HIP graph; returns its handle (bl_step_graph_create)."""
+        g = C.c_void_p()
+        _check(lib().bl_step_graph_create(self.h, B, C.c_void_p(d_logits_ptr), ld, C.c_void_p(d_tok), C.c_void_p(d_lp),
+                                          C.c_void_p(d_top_ids), C.c_void_p(d_top_lp), top_stride, C.byref(g)))
+        return g
+
+    def graph_launch(self, g):
+        _check(lib().bl_step_graph_launch(self.h, g))
+
+    @staticmethod
+    def graph_destroy(g):
+        _check(lib().bl_step_graph_destroy(g))
+
+    def sync(self):
+        _check(lib().bl_stream_sync(self.h))
 
     def spec_verify(self, slots, k, d_rows_ptr, ld, drafts):
         B = len(slots)

@@ -702,6 +702,47 @@ int bl_sample_step_async(bl_ctx *c, int B, const float *d_logits, int64_t ld, in
   return BL_OK;
 }
 
+int bl_step_graph_create(bl_ctx *c, int B, const float *d_logits, int64_t ld, int32_t *d_tokens, float *d_logprobs,
+                         int32_t *d_top_ids, float *d_top_logprobs, int top_stride, void **graph_out) {
+  if (!c || !graph_out) return fail(BL_EPARAM, "bl_step_graph_create: invalid arguments");
+  if (c->timing) return fail(BL_EPARAM, "bl_step_graph_create: kernel timing is enabled");
+  hipSetDevice(c->device);
+  hipGraph_t g = nullptr;
+  hipGraphExec_t ge = nullptr;
+  HIPCHK(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+  const int rc = bl_sample_step_async(c, B, d_logits, ld, d_tokens, d_logprobs, d_top_ids, d_top_logprobs, top_stride);
+  const std::string msg = g_err;
+  hipError_t e = hipStreamEndCapture(c->stream, &g);
+  if (rc != BL_OK) {
+    if (e == hipSuccess && g) hipGraphDestroy(g);
+    g_err = msg;
+    return rc;
+  }
+  if (e != hipSuccess) return fail(BL_EDEVICE, "hipStreamEndCapture: %s", hipGetErrorString(e));
+  e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+  hipGraphDestroy(g);
+  if (e != hipSuccess) return fail(BL_EDEVICE, "hipGraphInstantiate: %s", hipGetErrorString(e));
+  *graph_out = (void *)ge;
+  return BL_OK;
+}
+
+int bl_step_graph_launch(bl_ctx *c, void *graph) {
+  if (!c || !graph) return fail(BL_EPARAM, "bl_step_graph_launch: invalid arguments");
+  HIPCHK(hipGraphLaunch((hipGraphExec_t)graph, c->stream));
+  return BL_OK;
+}
+
+int bl_step_graph_destroy(void *graph) {
+  if (graph) HIPCHK(hipGraphExecDestroy((hipGraphExec_t)graph));
+  return BL_OK;
+}
+
+int bl_stream_sync(bl_ctx *c) {
+  if (!c) return fail(BL_EPARAM, "null context");
+  HIPCHK(hipStreamSynchronize(c->stream));
+  return BL_OK;
+}
+
 int bl_set_timing(bl_ctx *c, int enable) {
   if (!c) return fail(BL_EPARAM, "null context");
   c->timing = enable != 0;

@@ -125,6 +125,20 @@ int bl_bind_rows(bl_ctx *ctx, const int32_t *slots, int B);
 int bl_sample_step_async(bl_ctx *ctx, int B, const float *d_logits, int64_t ld, int32_t *d_tokens, float *d_logprobs,
                          int32_t *d_top_ids, float *d_top_logprobs, int top_stride);
 
+/* A serving loop's step without host work (no reference counterpart; the reference samples on the host):
+ * bl_step_graph_create captures one bl_sample_step_async of the bound rows, with these buffers, into an
+ * instantiated HIP graph (*graph_out, a hipGraphExec_t); bl_step_graph_launch replays it on the context
+ * stream; bl_stream_sync waits for the stream. A replay reads the slots' current state and parameters,
+ * so it follows later bl_slot_commit calls and resets that keep each row's kind; rebinding rows,
+ * changing buffers, or a reset that changes which passes a row needs (logprobs, top-k / n_probs, a
+ * grammar, full-vocabulary sampling) needs a new graph. BL_EPARAM while kernel timing is enabled (it
+ * synchronises). */
+int bl_step_graph_create(bl_ctx *ctx, int B, const float *d_logits, int64_t ld, int32_t *d_tokens, float *d_logprobs,
+                         int32_t *d_top_ids, float *d_top_logprobs, int top_stride, void **graph_out);
+int bl_step_graph_launch(bl_ctx *ctx, void *graph);
+int bl_step_graph_destroy(void *graph);
+int bl_stream_sync(bl_ctx *ctx);
+
 /* Kernel timing for measurement (no reference counterpart): while enabled, bl_sample_step_async records
  * HIP events around its three kernels (row pass, exponent pass, selection) on the context stream,
  * waits for them, and accumulates the durations; bl_get_timing returns the totals in ms and the

@@ -197,10 +197,20 @@ typedef int hipError_t;
 enum { hipSuccess = 0, hipErrorInvalidValue = 1 };
 typedef struct simt_stream *hipStream_t;
 typedef struct simt_event *hipEvent_t;
+/* graph capture has no CPU emulation: the entry points report it unsupported */
+typedef struct simt_graph *hipGraph_t;
+typedef struct simt_graph_exec *hipGraphExec_t;
+enum { hipStreamCaptureModeThreadLocal = 1, hipErrorNotSupported = 801 };
 enum hipMemcpyKind { hipMemcpyHostToDevice, hipMemcpyDeviceToHost, hipMemcpyDeviceToDevice, hipMemcpyHostToHost };
 #define hipStreamNonBlocking 1
 inline const char *hipGetErrorString(hipError_t) { return "simt"; }
 inline hipError_t hipSetDevice(int) { return hipSuccess; }
+inline hipError_t hipStreamBeginCapture(hipStream_t, int) { return hipErrorNotSupported; }
+inline hipError_t hipStreamEndCapture(hipStream_t, hipGraph_t *) { return hipErrorNotSupported; }
+inline hipError_t hipGraphInstantiate(hipGraphExec_t *, hipGraph_t, void *, void *, size_t) { return hipErrorNotSupported; }
+inline hipError_t hipGraphDestroy(hipGraph_t) { return hipErrorNotSupported; }
+inline hipError_t hipGraphLaunch(hipGraphExec_t, hipStream_t) { return hipErrorNotSupported; }
+inline hipError_t hipGraphExecDestroy(hipGraphExec_t) { return hipErrorNotSupported; }
 inline hipError_t hipGetLastError() { return hipSuccess; }
 inline hipError_t hipMalloc(void **p, size_t n) {
   *p = malloc(n);
