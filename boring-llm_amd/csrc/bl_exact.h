@@ -154,8 +154,30 @@ __device__ __forceinline__ bl_inc bl_dpp_inc(bl_inc f) {
 }
 
 /* inclusive ordered scan of composition across the wavefront: shifts within 16-lane rows, then the
- * row broadcasts of lane 15 (to rows 1, 3) and lane 31 (to rows 2, 3); all in VALU, no LDS */
+ * row broadcasts of lane 15 (to rows 1, 3) and lane 31 (to rows 2, 3); all in VALU, no LDS. With
+ * REV the composition runs the other way (lane l holds f_l then ... then f_0): scanning terms placed in
+ * reversed lane order gives their suffix compositions. */
+template <bool REV = false>
 __device__ __forceinline__ bl_inc bl_wave_scan(bl_inc f, int lane) {
+  const int r = lane & 15;
+  auto cmp = [](bl_inc earlier, bl_inc later) { return REV ? bl_compose(later, earlier) : bl_compose(earlier, later); };
+  bl_inc o;
+  o = bl_dpp_inc<BL_DPP_ROW_SHR(1), 0xF>(f);
+  if (r >= 1) f = cmp(o, f);
+  o = bl_dpp_inc<BL_DPP_ROW_SHR(2), 0xF>(f);
+  if (r >= 2) f = cmp(o, f);
+  o = bl_dpp_inc<BL_DPP_ROW_SHR(4), 0xF>(f);
+  if (r >= 4) f = cmp(o, f);
+  o = bl_dpp_inc<BL_DPP_ROW_SHR(8), 0xF>(f);
+  if (r >= 8) f = cmp(o, f);
+  o = bl_dpp_inc<BL_DPP_ROW_BCAST15, 0xA>(f);
+  if (lane & 16) f = cmp(o, f);
+  o = bl_dpp_inc<BL_DPP_ROW_BCAST31, 0xC>(f);
+  if (lane >= 32) f = cmp(o, f);
+  return f;
+}
+/* inclusive ordered scan of composition within each 16-lane row (lane 16q + 15 holds its row's total) */
+__device__ __forceinline__ bl_inc bl_row_scan(bl_inc f, int lane) {
   const int r = lane & 15;
   bl_inc o;
   o = bl_dpp_inc<BL_DPP_ROW_SHR(1), 0xF>(f);
@@ -166,12 +188,9 @@ __device__ __forceinline__ bl_inc bl_wave_scan(bl_inc f, int lane) {
   if (r >= 4) f = bl_compose(o, f);
   o = bl_dpp_inc<BL_DPP_ROW_SHR(8), 0xF>(f);
   if (r >= 8) f = bl_compose(o, f);
-  o = bl_dpp_inc<BL_DPP_ROW_BCAST15, 0xA>(f);
-  if (lane & 16) f = bl_compose(o, f);
-  o = bl_dpp_inc<BL_DPP_ROW_BCAST31, 0xC>(f);
-  if (lane >= 32) f = bl_compose(o, f);
   return f;
 }
+
 /* value of lane l (wave-uniform) in every lane */
 __device__ __forceinline__ uint32_t bl_bcast(uint32_t v, int l) { return (uint32_t)__builtin_amdgcn_readlane((int)v, l); }
 __device__ __forceinline__ float bl_bcastf(float v, int l) { return bl_u2f(bl_bcast(bl_f2u(v), l)); }

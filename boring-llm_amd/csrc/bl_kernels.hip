@@ -684,10 +684,15 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_exppass(bl_dev d, bl_rows 
      * wavefront computes the same value) */
     const int nsub = i0 / BL_EB;
     double part = 0.0;
-    for (int q = lane; q < nsub; q += 64) {
-      const int k = q / BL_SUBS;
+    for (int k = lane; k * BL_SUBS < nsub; k += 64) { /* lane k: chunk k's sub-blocks before this block */
       const float cm = d.c_max[(int64_t)row * nc + k];
-      if (cm > BL_NEG_INF) part += (double)d.c_bsum[(int64_t)row * nc * BL_SUBS + q] * exp((double)cm - (double)M);
+      if (cm > BL_NEG_INF) {
+        double cs = 0.0;
+#pragma unroll
+        for (int j = 0; j < BL_SUBS; j++)
+          if (k * BL_SUBS + j < nsub) cs += (double)d.c_bsum[((int64_t)row * nc + k) * BL_SUBS + j];
+        part += cs * exp((double)cm - (double)M);
+      }
     }
     const double S0 = bl_wave_sum_d(part);
     __syncthreads(); /* s_tab */
@@ -706,20 +711,26 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_exppass(bl_dev d, bl_rows 
       if (q < w) before += wtot[q];
       tot += wtot[q];
     }
-    /* group of 64 terms = 16 threads; its approximate start is its first thread's prefix, raised to the
-     * exact floor 1.0 once the row maximum's term exp(0) = 1 is behind it */
+    /* group of 64 terms = 16 threads (one row of the wavefront); its approximate start is its first
+     * thread's prefix, raised to the exact floor 1.0 once the row maximum's term exp(0) = 1 is behind it.
+     * The row's last lane holds the group's composed automaton (row scan) and its approximate end (its own
+     * inclusive prefix), and writes the record. */
     const int gs = i0 + 4 * (t & ~15);
     const double floor1 = gs > Mi ? 1.0 : 0.0;
     const double gs0 = __shfl(before, lane & ~15, 64);
     const double gstart = gs0 > floor1 ? gs0 : floor1;
-    bl_grec1 r;
-    r.E = bl_binade_of(gstart);
-    r.pad = 0;
-    r.v = bl_lanes_compose<16>(bl_thread_compose<4>(a, r.E), lane);
-    const int g = (i0 + j0) >> 6;
+    const int E = bl_binade_of(gstart);
+    const bl_inc gv = bl_row_scan(bl_thread_compose<4>(a, E), lane);
+    const bool tail = (lane & 15) == 15;
+    const bool gex = 4 * (t & ~15) < cnt;
+    const int g = (i0 + 4 * (t & ~15)) >> 6;
     bl_grec1 *rec = reinterpret_cast<bl_grec1 *>(reinterpret_cast<bl_grec *>(d.grec) + (int64_t)row * 2 * (V / 64 + 64));
     float *apx = d.gapx + (int64_t)row * (V / 64 + 64);
-    if ((lane & 15) == 0 && j0 < cnt) {
+    if (tail && gex) {
+      bl_grec1 r;
+      r.E = E;
+      r.pad = 0;
+      r.v = gv;
       rec[g] = r;
       apx[g] = (float)gstart;
     }
@@ -727,26 +738,19 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_exppass(bl_dev d, bl_rows 
     /* block summary for the normaliser: the critical groups (approximate start or end not safely inside
      * the predicted binade), and, when there is none and every group has the same binade, the block's
      * automaton composed in order (wavefront w holds groups 4w..4w+3) */
-    const int gl = lane & ~15;
-    const double wend = __shfl(before + sa, 63, 64);
-    const double nxt = __shfl(before, gl + 16 < 64 ? gl + 16 : 63, 64);
-    const double gend = gl + 16 < 64 ? nxt : wend;
-    const bool gex = 4 * (t & ~15) < cnt;
-    const bool crit = gex && bl_group_critical((float)gstart, (float)(gend > floor1 ? gend : floor1), r.E, floor1);
-    const bool head = (lane & 15) == 0;
-    const unsigned long long cb = __ballot(crit && head);
-    const unsigned long long eb = __ballot(gex && head);
-    const int E0 = __shfl(r.E, 0, 64);
-    const unsigned long long db = __ballot(gex && head && r.E != E0);
-    bl_inc f = gex ? r.v : bl_inc_ident();
+    const double gend = before + sa;
+    const bool crit = gex && bl_group_critical((float)gstart, (float)(gend > floor1 ? gend : floor1), E, floor1);
+    const unsigned long long cb = __ballot(crit && tail);
+    const unsigned long long eb = __ballot(gex && tail);
+    const int E0 = (int)bl_bcast((uint32_t)E, 15);
+    const unsigned long long db = __ballot(gex && tail && E != E0);
+    bl_inc f = bl_inc_ident();
 #pragma unroll
-    for (int k = 16; k < 64; k <<= 1) {
-      const bl_inc o = bl_inc{(uint32_t)__shfl_xor((int)f.d0, k, 64), (uint32_t)__shfl_xor((int)f.d1, k, 64)};
-      f = (lane & k) ? bl_compose(o, f) : bl_compose(f, o);
-    }
+    for (int q = 0; q < 4; q++)
+      if ((eb >> (16 * q + 15)) & 1ull) f = bl_compose(f, bl_inc{bl_bcast(gv.d0, 16 * q + 15), bl_bcast(gv.d1, 16 * q + 15)});
     if (lane == 0) {
-      bs_crit[w] = (uint32_t)((cb & 1ull) | ((cb >> 15) & 2ull) | ((cb >> 30) & 4ull) | ((cb >> 45) & 8ull));
-      bs_E[w] = (eb & 1ull) ? E0 : BL_E_NONE; /* BL_E_NONE: the wavefront holds no group */
+      bs_crit[w] = (uint32_t)(((cb >> 15) & 1ull) | ((cb >> 30) & 2ull) | ((cb >> 45) & 4ull) | ((cb >> 60) & 8ull));
+      bs_E[w] = ((eb >> 15) & 1ull) ? E0 : BL_E_NONE; /* BL_E_NONE: the wavefront holds no group */
       bs_same[w] = db == 0ull;
       bs_v[w] = f;
     }
@@ -1234,12 +1238,7 @@ __device__ void norm_prep(const bl_dev &d, int row, float M, sel_shared &sh, uin
       }
     }
     const int pc = __popc(m);
-    int inc = pc;
-#pragma unroll
-    for (int k = 1; k < 64; k <<= 1) {
-      const int o = __shfl_up(inc, k, 64);
-      if (lane >= k) inc += o;
-    }
+    const int inc = bl_wscan_add(pc, lane);
     if (lane == 63) nm.cw[w] = inc;
     __syncthreads();
     int off = ncrit_all + inc - pc, tot = 0;
@@ -1308,13 +1307,11 @@ __device__ void norm_prep(const bl_dev &d, int row, float M, sel_shared &sh, uin
       const int e0 = rec[g].E, e1 = bl_binade_of((double)apx[g + 1]);
       nm.terms[ci * 64 + lane] = a;
       nm.cp[ci * 64 + lane] = bl_wave_scan(in ? bl_term_inc(a, e0) : bl_inc_ident(), lane);
-      bl_inc sf = in ? bl_term_inc(a, e1) : bl_inc_ident(); /* suffix: this term, then the later ones */
-#pragma unroll
-      for (int k = 1; k < 64; k <<= 1) {
-        const bl_inc o = bl_inc{(uint32_t)__shfl_down((int)sf.d0, k, 64), (uint32_t)__shfl_down((int)sf.d1, k, 64)};
-        if (lane + k < 64) sf = bl_compose(sf, o);
-      }
-      nm.cs[ci * 65 + lane] = sf;
+      /* suffixes: lane l takes term 63 - l, and the reversed scan leaves in it the composition of terms
+       * 63 - l .. 63 in order */
+      const float ar = __shfl(a, 63 - lane, 64);
+      const bool inr = (int64_t)g * 64 + (63 - lane) < V;
+      nm.cs[ci * 65 + (63 - lane)] = bl_wave_scan<true>(inr ? bl_term_inc(ar, e1) : bl_inc_ident(), lane);
       if (lane == 0) {
         nm.cs[ci * 65 + 64] = bl_inc_ident();
         nm.ce0[ci] = e0;
@@ -1420,11 +1417,18 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
   const int V = d.vocab, nc = d.nc;
   const int row = blockIdx.x, t = threadIdx.x, w = t >> 6, lane = t & 63;
   __shared__ sel_shared sh;
-  /* loads that need only the row index go out first */
+  /* loads that need only the row index go out first; wavefront 0 reduces the row maximum and its first
+   * index from the chunk statistics */
   float M = BL_NEG_INF;
   int Mi = 0x7fffffff;
-  for (int k = t; k < nc; k += BL_SEL_THREADS)
-    argmax_merge(M, Mi, d.c_max[(int64_t)row * nc + k], d.c_arg[(int64_t)row * nc + k]);
+  if (w == 0) {
+    for (int k = lane; k < nc; k += 64) argmax_merge(M, Mi, d.c_max[(int64_t)row * nc + k], d.c_arg[(int64_t)row * nc + k]);
+    bl_wargmax(M, Mi, lane);
+    if (lane == 0) {
+      sh.red_m[0] = M;
+      sh.red_i[0] = Mi;
+    }
+  }
   const uint64_t mk = t < BL_KSEL_MAX ? d.mkey[(int64_t)row * BL_KSEL_MAX + t] : 0ull; /* used when K > t */
   uint32_t m_pre = 0u; /* the normaliser's first block flags and summaries (used by logprob rows) */
   bl_grec1 br_pre{};
@@ -1445,7 +1449,9 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
   const int32_t ring_old = (t == 0 && rows.commit && ring_full) ? d.ring[(int64_t)slot * BL_WCAP + win_head] : 0;
   const int n_eog = d.n_eog;
   if (t < n_eog && t < BL_EOG_LDS) sh.eog[t] = d.eog[t];
-  block_argmax<BL_SEL_THREADS>(M, Mi, sh.red_m, sh.red_i);
+  __syncthreads();
+  M = sh.red_m[0];
+  Mi = sh.red_i[0];
   if (Mi == 0x7fffffff) Mi = 0;
 
   const float *eff = d.eff + (int64_t)row * V;
