@@ -605,7 +605,8 @@ static bool needs_pass2(bl_ctx *c, const int32_t *slots, int B) {
 
 static int status_error(int st) {
   if (st & BL_SE_UNSUPPORTED) return fail(BL_EUNSUPPORTED, "a sampler stage outside the device path was reached");
-  if (st & BL_SE_TIE) return fail(BL_ETIE, "the full-vocabulary draw landed on equal logits; heap order is not reproduced");
+  if (st & BL_SE_TIE)
+    return fail(BL_ETIE, "the draw landed on equal logits past the device's heap-order simulation");
   if (st & BL_SE_CAND_FULL) return fail(BL_EDEVICE, "candidate buffer overflow");
   if (st & BL_SE_EMPTY) return fail(BL_EEMPTY, "sample_candidates: empty or mismatched candidates");
   if (st & BL_SE_GDEAD) return fail(BL_EGRAMMAR_DEAD, "the reply no longer matches the grammar");

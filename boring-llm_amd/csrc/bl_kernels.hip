@@ -1405,6 +1405,117 @@ __device__ void norm_chain(const bl_dev &d, int row, float M, sel_shared &sh) {
 }
 
 /*
+ * The heap rank's order among equal values (all_candidates_sorted, src/sampling.br:301-365), for a
+ * full-vocabulary draw that landed on position `pos` of the sorted list whose value has equal neighbours.
+ * The drawn position depends only on the values (equal terms sum alike in any order); which token sits
+ * there is the heap's choice. Elements below the tied value never move an element at or above it: a sift
+ * compares them only with each other or loses to it, and below the current level the sub-heaps hold only
+ * smaller values under a smaller root. So the heap is simulated on the nb elements >= the tied value (the
+ * sorted prefix), every other position reading as smaller than all of them:
+ *   - occupancy (position -> element of the prefix, or -1) in `occ_g`, V entries of global scratch; the
+ *     bottom-up build runs level by level, the parents of one level owning disjoint subtrees;
+ *   - after the build the prefix forms a rooted subtree; when it lies within the first BL_TIE_OCC
+ *     positions, one lane replays the extractions up to `pos` on an LDS copy of that occupancy.
+ * Returns the token id, or -1 when the prefix exceeds BL_TIE_MAX elements or its subtree the LDS copy (the
+ * caller then reports the tie).
+ */
+#define BL_TIE_MAX 8192                                     /* elements >= the tied value */
+#define BL_TIE_OCC ((int)(sizeof(sel_norm) / sizeof(int16_t))) /* positions copied to LDS */
+template <class KeyF>
+__device__ int heap_tie_id(KeyF key, bool keys_in_lds, int64_t n_list, int64_t pos, int V, int32_t *occ_g,
+                           sel_shared &sh) {
+  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+  const float vp = ckey_v(key(pos));
+  /* nb = first index past pos whose value is below vp (the list is sorted: binary search, every thread) */
+  int64_t lo = pos + 1, hi = n_list;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (ckey_v(key(mid)) == vp) lo = mid + 1;
+    else hi = mid;
+  }
+  const int nb = (int)lo;
+  if (nb > BL_TIE_MAX) return -1;
+  /* the prefix's values, in LDS (the list itself when it is there, else a float copy in its place) */
+  float *bval = reinterpret_cast<float *>(sh.c.keys);
+  if (!keys_in_lds)
+    for (int k = t; k < nb; k += BL_SEL_THREADS) bval[k] = ckey_v(key(k));
+  auto vbig = [&](int k) -> float { return keys_in_lds ? ckey_v(key(k)) : bval[k]; };
+  /* k above j (-1: a position below the whole prefix) */
+  auto above = [&](int k, int j) -> bool {
+    if (k < 0) return false;
+    if (j < 0) return true;
+    return vbig(k) > vbig(j);
+  };
+  for (int p = t; p < V; p += BL_SEL_THREADS) occ_g[p] = -1;
+  __syncthreads();
+  for (int k = t; k < nb; k += BL_SEL_THREADS) occ_g[ckey_i(key(k))] = k;
+  __syncthreads();
+  /* sift-down with a strict `>` on the larger child and on the root, as the reference */
+  auto sift = [&](int root, int size, auto get, auto set) {
+    while (true) {
+      const int l = 2 * root + 1;
+      if (l >= size) return;
+      const int r = l + 1;
+      const int ol = get(l), orr = r < size ? get(r) : -1;
+      int c = l, oc = ol;
+      if (r < size && above(orr, ol)) {
+        c = r;
+        oc = orr;
+      }
+      const int oroot = get(root);
+      if (!above(oc, oroot)) return;
+      set(root, oc);
+      set(c, oroot);
+      root = c;
+    }
+  };
+  auto gget = [&](int p) -> int { return occ_g[p]; };
+  auto gset = [&](int p, int v) { occ_g[p] = v; };
+  const int depth_max = 31 - __clz(V);
+  for (int L = depth_max; L >= 0; L--) {
+    const int p0 = (1 << L) - 1, p1 = min((2 << L) - 1, V / 2); /* the parents of level L: 2p + 1 < V */
+    for (int p = p0 + t; p < p1; p += BL_SEL_THREADS) sift(p, V, gget, gset);
+    __syncthreads();
+  }
+  /* the prefix's subtree must fit the LDS copy */
+  int far = -1;
+  for (int p = t; p < V; p += BL_SEL_THREADS)
+    if (occ_g[p] >= 0) far = p;
+  far = (int)bl_wmax_u32((uint32_t)(far + 1), lane) - 1;
+  if (lane == 0) sh.red_i[w] = far;
+  __syncthreads();
+  far = -1;
+  for (int q = 0; q < SEL_NW; q++) far = max(far, sh.red_i[q]);
+  if (far >= BL_TIE_OCC) return -1; /* uniform */
+  const int n_occ = min(V, BL_TIE_OCC);
+  int16_t *occ_l = reinterpret_cast<int16_t *>(&sh.n);
+  for (int p = t; p < n_occ; p += BL_SEL_THREADS) occ_l[p] = (int16_t)occ_g[p];
+  __syncthreads();
+  if (t == 0) {
+    auto lget = [&](int p) -> int { return p < n_occ ? (int)occ_l[p] : -1; };
+    auto lset = [&](int p, int v) { occ_l[p] = (int16_t)v; }; /* only positions holding prefix elements */
+    int size = V, res = -1;
+    for (int64_t i = 0; i <= pos; i++) {
+      const int o = lget(0);
+      if (i == pos) {
+        res = o;
+        break;
+      }
+      size -= 1;
+      if (size > 0) {
+        lset(0, lget(size));
+        sift(0, size, lget, lset);
+      }
+    }
+    sh.ires[4] = res;
+  }
+  __syncthreads();
+  const int res = sh.ires[4];
+  __syncthreads();
+  return res >= 0 ? ckey_i(key(res)) : -1;
+}
+
+/*
  * K3: grid (B) x 1024, one workgroup per row. The row maximum and first argmax come from the chunk
  * statistics. A sampled row's ranked list is the merged top-K (exponent pass, workgroup 0) or the
  * full-vocabulary candidates, sorted here. A logprob row's exact index-order normaliser is prepared by
@@ -1555,6 +1666,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
   if (sampled && !status && short_list && w == 1 && lane == 0)
     sh.ires[2] = ranked_serial(sp, (int)n_list, n_logical, keep, rng, skip, sh.ser_e, sh.ser_r, &sh.rng_out);
   __syncthreads();
+  const float S_norm = sh.n.S; /* the normaliser's LDS is scratch from here on (heap ties) */
   if (sampled && !status) {
     int pos;
     if (short_list) {
@@ -1578,17 +1690,22 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
       const uint64_t kp = keys[pos];
       tok = kp ? ckey_i(kp) : 0;
       tokv = kp ? ckey_v(kp) : eff[tok];
-      /* the heap rank orders equal values its own way (src/sampling.br:310-364): a tie at the chosen
-       * position is reported instead of guessing */
+      /* the heap rank orders equal values its own way (src/sampling.br:310-364): a draw on a tie takes
+       * the heap's token (or reports the tie when the simulation does not fit) */
       if (mode & BL_M_FULL) {
         const float vp = val(pos);
-        if ((pos > 0 && val(pos - 1) == vp) || (pos + 1 < n_list && val(pos + 1) == vp)) status |= BL_SE_TIE;
+        if ((pos > 0 && val(pos - 1) == vp) || (pos + 1 < n_list && val(pos + 1) == vp)) {
+          const int hid = heap_tie_id([&](int64_t j) { return keys[j]; }, keys == sh.c.keys, n_list, pos, V,
+                                      d.full_i + (int64_t)row * V, sh);
+          if (hid >= 0) tok = hid;
+          else status |= BL_SE_TIE;
+        }
       }
     }
   }
 
   /* outputs, logprobs (src/server.br:1027-1035): alternatives = the first n_probs of the merged list */
-  const float lse = lp_row ? (float)log((double)sh.n.S) : 0.0f;
+  const float lse = lp_row ? (float)log((double)S_norm) : 0.0f;
   if (lp_row) {
     const int n = sp.n_probs < rows.top_stride ? sp.n_probs : rows.top_stride;
     if (t < n) {

@@ -32,7 +32,8 @@ enum {
   BL_EGRAMMAR_REJECT = -6, /* "the grammar rejected every vocabulary token" (src/server.br:361) */
   BL_EGRAMMAR_AMBIG = -7,  /* "grammar is left-recursive or too ambiguous to match" (src/grammar.br:354) */
   BL_EUNSUPPORTED = -8,    /* a sampler stage this library does not run on the device yet */
-  BL_ETIE = -9             /* full-vocabulary draw landed on equal logits (heap order needed) */
+  BL_ETIE = -9             /* a draw on equal logits whose heap order is past the device simulation (more than
+                              8192 values at or above the tied one), or equal allowed maxima of a grammar row */
 };
 
 /* SamplingParams (src/model.br:1565-1584) + the per-request server fields (src/server.br:665-760).

@@ -63,7 +63,17 @@ def lp_close(a, b):
     return abs(a - b) <= LP_RTOL * max(abs(a), abs(b)) or abs(a - b) <= 1e-7
 
 
-def run_small(BL, case, steps, coarse=False, ramp=False):
+def quantize(x, mode):
+    """Logits with ties: `bf16` rounds to bfloat16 (nearest even), as the output of a bf16 LM head
+    converted to float32; `q4` rounds to multiples of 0.25."""
+    if mode == "bf16":
+        u = x.astype(np.float32).view(np.uint32).astype(np.uint64)
+        u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+        return u.astype(np.uint32).view(np.float32)
+    return (np.round(x * np.float32(4.0)) / np.float32(4.0)).astype(np.float32)
+
+
+def run_small(BL, case, steps, coarse=False, ramp=False, quant=None):
     """A small case against the oracle; `coarse` floors the logits to a few integers, so that thousands of
     values tie at the chunk top-K bound (the radix fallback with an index-order cut of the ties); `ramp`
     adds a slope of ln 2 per 63 tokens, so that the index-order sum crosses a power of two in nearly every
@@ -90,6 +100,8 @@ def run_small(BL, case, steps, coarse=False, ramp=False):
                 x = np.floor(x / np.float32(5.0)).astype(np.float32)
             if ramp:
                 x = (x * np.float32(0.05) + np.arange(SMALL_V, dtype=np.float32) * np.float32(0.011)).astype(np.float32)
+            if quant:
+                x = quantize(x, quant)
             buf.upload(x)
             tok, lp, ti, tl = ctx.sample_step([1], buf.ptr, SMALL_V, top_stride=max(n_probs, 1))
             ot, olp = np.zeros(1, np.int32), np.zeros(1, np.float32)
@@ -109,6 +121,43 @@ def run_small(BL, case, steps, coarse=False, ramp=False):
     finally:
         L.orc_slot_free(h)
         L.orc_set_eog_tokens(O.ip(O.i32([0])), 0, -1)
+        ctx.close()
+    return None
+
+
+def run_bigties(BL, steps):
+    """Two full-vocabulary rows (T 1.0 with min-p 0.05; T 0.7 with top-p 0.95 and min-p 0.02) at V=151936 on
+    N(0, 3^2) logits rounded to bfloat16 (several tokens share each bfloat16 value within 4 of the maximum,
+    where min-p keeps the draws), so that draws land on runs of equal values: the heap simulation against
+    the oracle's heap sort."""
+    V = 151936
+    rng = np.random.default_rng(11)
+    kws = [dict(temperature=1.0, min_p=0.05), dict(temperature=0.7, top_p=0.95, min_p=0.02)]
+    ctx = BL.Context(V, 2, 2)
+    L = O.lib()
+    hs = []
+    for r, kw in enumerate(kws):
+        ctx.slot_reset(r, BL.Params(**kw), BL.seed_rng(700 + r))
+        op = O.params(**kw)
+        hs.append(L.orc_slot_new(O.C.byref(op), BL.seed_rng(700 + r), None, 0, None, 0, None, None, 0))
+    buf = MEM.zeros(2 * V, np.float32)
+    try:
+        for t in range(steps):
+            x = quantize((rng.standard_normal(2 * V) * 3.0).astype(np.float32), "bf16")
+            buf.upload(x)
+            tok = ctx.sample_step([0, 1], buf.ptr, V)[0]
+            for r in range(2):
+                ot, olp = np.zeros(1, np.int32), np.zeros(1, np.float32)
+                oti, otl = np.zeros(1, np.int32), np.zeros(1, np.float32)
+                eog = O.C.c_int()
+                row = np.ascontiguousarray(x[r * V:(r + 1) * V])
+                assert L.orc_slot_step(hs[r], O.fp(row), V, 0, 1, O.ip(ot), O.fp(olp), O.ip(oti), O.fp(otl),
+                                       O.C.byref(eog)) == 0
+                if tok[r] != ot[0]:
+                    return f"step {t} row {r}: token {tok[r]} vs {ot[0]}"
+    finally:
+        for h in hs:
+            L.orc_slot_free(h)
         ctx.close()
     return None
 
@@ -478,6 +527,9 @@ def main():
         elif kind == "coarse":
             for c in parse_range(f[1]):
                 results.append((f"coarse case {c}", run_small(BL, c, int(f[2]) if len(f) > 2 else 25, coarse=True)))
+        elif kind in ("bf16", "q4"):
+            for c in parse_range(f[1]):
+                results.append((f"{kind} case {c}", run_small(BL, c, int(f[2]) if len(f) > 2 else 25, quant=kind)))
         elif kind == "ramp":
             for c in parse_range(f[1]):
                 results.append((f"ramp case {c}", run_small(BL, c, int(f[2]) if len(f) > 2 else 25, ramp=True)))
@@ -491,6 +543,8 @@ def main():
             results.append(("asynchronous step", run_async(BL, int(f[1]))))
         elif kind == "pair":
             results.append((f"rows {f[1]} + {f[2]}", run_pair(BL, int(f[1]), int(f[2]), int(f[3]) if len(f) > 3 else 10)))
+        elif kind == "bigties":
+            results.append(("bf16 ties at V=151936", run_bigties(BL, int(f[1]))))
         elif kind == "bigk":
             results.append(("large top-k / n_probs", run_bigk(BL, int(f[1]))))
         elif kind == "w3":

@@ -161,6 +161,7 @@ inline int __ffsll(long long x) { return ffsll(x); }
 inline int __ffsll(unsigned long long x) { return ffsll((long long)x); }
 inline int __popcll(unsigned long long x) { return __builtin_popcountll(x); }
 inline int __popc(unsigned x) { return __builtin_popcount(x); }
+inline int __clz(int x) { return x ? __builtin_clz((unsigned)x) : 32; }
 inline int __clzll(long long x) { return x ? __builtin_clzll((unsigned long long)x) : 64; }
 inline uint64_t __umul64hi(uint64_t a, uint64_t b) { return (uint64_t)(((unsigned __int128)a * b) >> 64); }
 inline float __expf(float x) { return expf(x); }
@@ -189,6 +190,12 @@ template <class T>
 inline T atomicMax(T *p, T v) {
   T o = *p;
   *p = std::max(o, v);
+  return o;
+}
+template <class T>
+inline T atomicCAS(T *p, T cmp, T v) {
+  T o = *p;
+  if (o == cmp) *p = v;
   return o;
 }
 

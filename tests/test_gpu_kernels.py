@@ -1,4 +1,5 @@
 """GPU parity of kernel paths beyond the fixed workloads, through the shared harness with device buffers:
+full-vocabulary draws on equal values (bfloat16-rounded, quantised and floored logits: the heap's order),
 top_k 250 with 256 logprob alternatives at V=151936 (38 chunks x 256 candidates per row, the merged
 list found by radix selection), two small configurations stepped as rows 0 and 1 of an odd-length
 vocabulary (row 1 not 16-byte aligned), small configurations on logits floored to a few integers (thousands
@@ -52,6 +53,20 @@ def test_coarse_logits_tie_at_the_bound(case):
 def test_ramp_logits_many_crossings(case):
     print(f"small case {case}, logits on a ramp (a power of two crossed in nearly every group): 20 steps", flush=True)
     err = RP.run_small(BL, case, 20, ramp=True)
+    assert err is None, err
+
+
+@pytest.mark.parametrize("quant", ["bf16", "q4", "coarse"])
+@pytest.mark.parametrize("case", [2, 3, 6, 9])
+def test_full_vocabulary_ties_heap_order(case, quant):
+    print(f"small case {case}, {quant} logits (draws on equal values, the heap's order): 20 steps", flush=True)
+    err = RP.run_small(BL, case, 20, coarse=quant == "coarse", quant=None if quant == "coarse" else quant)
+    assert err is None, err
+
+
+def test_bf16_ties_full_vocabulary():
+    print("two full-vocabulary rows on bfloat16 logits, V=151936: 10 steps", flush=True)
+    err = RP.run_bigties(BL, 10)
     assert err is None, err
 
 

@@ -54,6 +54,15 @@ def test_coarse_and_ramp_logits(simt_lib):
     assert out.count("ok   coarse case") == 6 and out.count("ok   ramp case") == 3
 
 
+def test_heap_tie_order(simt_lib):
+    """Full-vocabulary rows whose draws land on equal values: logits rounded to bfloat16 or to multiples
+    of 0.25, floored to a few integers, and bfloat16 N(0, 3^2) rows at V=151936. The token comes from the
+    device's simulation of the reference's heap; the oracle runs the heap sort itself."""
+    out = _run(simt_lib, ["bf16:2,3,6,9:8", "q4:2,3,6,9:8", "coarse:2,3,6,9:6", "bigties:2"], {"SIMT_ORDER": "rand"})
+    assert out.count("ok   bf16 case") == 4 and out.count("ok   q4 case") == 4 and out.count("ok   coarse case") == 4
+    assert "ok   bf16 ties at V=151936" in out
+
+
 def test_full_vocabulary_workloads(simt_lib):
     """Workload 2 (the benchmark step), workload 4 (soft-cap, V=262144, top-64 + 20 logprobs) on 2 rows, the
     bound-rows asynchronous step against the synchronous one, two rows of an odd-length vocabulary in one
@@ -79,5 +88,5 @@ def test_small_cases_address_sanitizer():
         assert os.path.isabs(p) and os.path.exists(p), f"{rt} not found"
         pre.append(p)
     env = {"LD_PRELOAD": " ".join(pre), "ASAN_OPTIONS": "detect_leaks=0", "UBSAN_OPTIONS": "print_stacktrace=1"}
-    out = _run(os.path.join(SIMT, "_build", "libbl_simt_asan.so"), ["small:0-10:3", "coarse:1,5:3", "ramp:8:2", "grammar:0-6:20"], env)
+    out = _run(os.path.join(SIMT, "_build", "libbl_simt_asan.so"), ["small:0-10:3", "coarse:1,5:3", "ramp:8:2", "grammar:0-6:20", "q4:2,9:4"], env)
     assert "ERROR: AddressSanitizer" not in out and "runtime error" not in out
