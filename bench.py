@@ -77,6 +77,173 @@ def measured_traffic():
     return {k: v["bytes_per_launch"] for k, v in t["kernels"].items()}
 
 
+def cpu_sample(run, target_s, unit_steps=1):
+    """Doubles the oracle's step count until its own timer passes target_s; returns (steps, seconds)."""
+    import ctypes
+    steps = 2
+    while True:
+        us = ctypes.c_double()
+        run(steps, ctypes.byref(us))
+        sec = us.value / 1e6
+        if sec >= target_s or steps >= 4096:
+            return steps, sec
+        steps = min(4096, max(steps * 2, int(steps * target_s / max(sec, 1e-3)) + 1))
+
+
+def bench_workload(args, wl):
+    """Configs 1, 3, 4 and 5 of BASELINE.json (parity-tested elsewhere; timed here on request)."""
+    import torch
+    import bl_select as BL
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import _oracle as O
+    L = O.lib()
+    dev = torch.device("cuda:0")
+    out = {"metric": f"workload {wl} steps/s + p50 us/step", "unit": "steps/s", "n_gpus": 1, "higher_is_better": True,
+           "dtype": "f32", "data": f"synthetic (seeded integer-hash inputs, BASELINE configs[{wl - 1}])", "vs_baseline": None}
+    lat, elapsed, steps = [], 0.0, args.steps
+    if wl in (1, 4):
+        if wl == 1:
+            V, B, seed, pool_n, cfg = 151936, 1, 1234, 512, 1
+            params = [BL.Params(temperature=0.8, top_k=40, top_p=0.95, min_p=0.05, repeat_penalty=1.1, repeat_last_n=64)]
+            desc = "B=1, V=151936, T 0.8, top_k 40, top_p 0.95, min_p 0.05, repeat 1.1 over the last 64 of 512 ids"
+        else:
+            V, B, seed, pool_n, cfg = 262144, 32, 7, 16, 4
+            params = [BL.Params(temperature=1.0, top_k=64, top_p=0.95, logprobs=1, n_probs=20, final_softcap=30.0)] * B
+            desc = "B=32, V=262144, soft-cap 30, T 1.0, top_k 64, top_p 0.95, 20 logprobs"
+        ctx = BL.Context(V, B, B)
+        for r in range(B):
+            hist = BL.workload_ids(0, 1, seed, 0, 512, V) if wl == 1 else []
+            ctx.slot_reset(r, params[r], BL.seed_rng(seed + r), history=hist)
+        ctx.bind_rows(list(range(B)))
+        pool = torch.empty((pool_n, B, V), dtype=torch.float32, device=dev)
+        for p in range(pool_n):
+            ctx.synth_logits(pool[p].data_ptr(), V, cfg, seed, p, B, V)
+        topn = 20 if wl == 4 else 0
+        d_tok = torch.zeros(B, dtype=torch.int32, device=dev)
+        d_lp = torch.zeros(B, dtype=torch.float32, device=dev)
+        d_ti = torch.zeros(max(B * topn, 1), dtype=torch.int32, device=dev)
+        d_tl = torch.zeros(max(B * topn, 1), dtype=torch.float32, device=dev)
+        torch.cuda.synchronize()
+        graphs = [ctx.step_graph(B, pool[p].data_ptr(), V, d_tok.data_ptr(), d_lp.data_ptr(), d_ti.data_ptr(),
+                                 d_tl.data_ptr(), topn) for p in range(pool_n)]
+        for i in range(args.warmup):
+            ctx.graph_launch(graphs[i % pool_n])
+        ctx.sync()
+        t0 = time.perf_counter()
+        for i in range(steps):
+            ctx.graph_launch(graphs[i % pool_n])
+        ctx.sync()
+        elapsed = time.perf_counter() - t0
+        for i in range(min(steps, 500)):
+            a = time.perf_counter()
+            ctx.graph_launch(graphs[i % pool_n])
+            ctx.sync()
+            lat.append(time.perf_counter() - a)
+        for g in graphs:
+            BL.Context.graph_destroy(g)
+        ctx.close()
+        out["config"] = {"workload": desc, "batch": B, "vocab": V, "hip_graph": True,
+                         "logits_pool_MB": pool_n * B * V * 4 / 1e6}
+        if not args.no_cpu:
+            if wl == 1:
+                n, sec = cpu_sample(lambda k, us: L.orc_run_c1(seed, k, O.ip(np.zeros(k, np.int32)), us), args.cpu_seconds)
+            else:
+                def run4(k, us):
+                    z = lambda m, t: np.zeros(m, t)
+                    L.orc_run_c4(seed, k, B, O.ip(z(k * B, np.int32)), O.fp(z(k * B, np.float32)),
+                                 O.ip(z(k * B * 20, np.int32)), O.fp(z(k * B * 20, np.float32)), us)
+                n, sec = cpu_sample(run4, args.cpu_seconds)
+    elif wl == 3:
+        V, seed = 151936, 3
+        blob, off, eos = BL.workload_c3_vocab(seed, V)
+        with open(os.path.join(ROOT, "tests", "golden", "c3_schema.gbnf")) as f:
+            gbnf = f.read()
+        ctx = BL.Context(V, 1, 1)
+        ctx.set_eog(eos, [])
+        ctx.set_vocab(blob, off)
+
+        def restart():
+            ctx.slot_reset(0, BL.Params(), BL.seed_rng(seed))
+            ctx.slot_grammar(0, gbnf)
+
+        restart()
+        pool_n = 256
+        pool = torch.empty((pool_n, V), dtype=torch.float32, device=dev)
+        for p in range(pool_n):
+            ctx.synth_logits(pool[p].data_ptr(), V, 3, seed, p, 1, V)
+        torch.cuda.synchronize()
+        steps = min(steps, 256)
+        for i in range(steps + args.warmup):
+            a = time.perf_counter()
+            tok = ctx.sample_step([0], pool[i % pool_n].data_ptr(), V)[0][0]
+            dt = time.perf_counter() - a
+            if i >= args.warmup:
+                lat.append(dt)
+                elapsed += dt
+            if tok == eos:
+                restart()  # the forced EOS ends the reply; the next request starts over (not timed)
+        ctx.close()
+        out["config"] = {"workload": "B=1 grammar-constrained greedy, V=151936 synthetic vocabulary, the config-3 "
+                                     "JSON-Schema GBNF; synchronous bl_sample_step (host outputs)", "batch": 1,
+                         "vocab": V, "hip_graph": False}
+        if not args.no_cpu:
+            L.orc_set_eog_tokens(O.ip(O.i32([0])), 0, -1)
+            n, sec = cpu_sample(lambda k, us: L.orc_run_c3(seed, k, 0, O.ip(np.zeros(k, np.int32)),
+                                                            np.zeros(k, np.uint32).ctypes.data_as(
+                                                                O.C.POINTER(O.C.c_uint32)),
+                                                            O.ip(np.zeros(k, np.int32)), us), args.cpu_seconds)
+    elif wl == 5:
+        S, K, V, seed = 16, 8, 151936, 5
+        R = S * (K + 1)
+        pool_n = 4
+        g, sm = BL.Context(V, S, R), BL.Context(V, S, R)
+        for b in range(S):
+            g.slot_reset(b, BL.Params(), BL.seed_rng(seed + b))
+            sm.slot_reset(b, BL.Params(temperature=0.7), BL.seed_rng(seed + b))
+        pool = torch.empty((pool_n, R, V), dtype=torch.float32, device=dev)
+        drafts = []
+        for p in range(pool_n):
+            g.synth_logits(pool[p].data_ptr(), V, 5, seed, p, R, V)
+            am = pool[p].argmax(dim=1).cpu().numpy()
+            dp = []
+            for b in range(S):
+                dp += BL.workload_drafts(seed, p, b, [int(x) for x in am[b * (K + 1):b * (K + 1) + K]], V)
+            drafts.append(dp)
+        torch.cuda.synchronize()
+        steps = min(steps, 200)
+        per = {}
+        for name, ctx in (("greedy", g), ("sampled_T0.7", sm)):
+            for i in range(args.warmup):
+                ctx.spec_verify(list(range(S)), K, pool[i % pool_n].data_ptr(), V, drafts[i % pool_n])
+            ts = []
+            for i in range(steps):
+                a = time.perf_counter()
+                ctx.spec_verify(list(range(S)), K, pool[i % pool_n].data_ptr(), V, drafts[i % pool_n])
+                ts.append(time.perf_counter() - a)
+            per[name] = {"steps_per_s": len(ts) / sum(ts), "p50_us": 1e6 * float(np.median(ts))}
+            lat += ts
+            elapsed += sum(ts)
+        g.close()
+        sm.close()
+        steps = len(lat)
+        out["config"] = {"workload": "speculative verification, 16 sequences x 9 rows, V=151936, greedy and "
+                                     "sampled (T 0.7, top_k 0) contexts; synchronous bl_spec_verify", "batch": R,
+                         "vocab": V, "hip_graph": False, "per_mode": per}
+        if not args.no_cpu:
+            def run5(k, us):
+                z = lambda m: np.zeros(m, np.int32)
+                L.orc_run_c5(seed, k, S, O.ip(z(k * R)), O.ip(z(k * S)), O.ip(z(k * R)), O.ip(z(k * S)), us)
+            n, sec = cpu_sample(run5, args.cpu_seconds)
+    else:
+        raise SystemExit(f"bench.py: unknown workload {wl}")
+    out.update({"value": steps / elapsed, "steps": steps, "warmup": args.warmup, "ms_per_step": 1e3 * elapsed / steps,
+                "p50_us_per_step": 1e6 * float(np.median(lat)), "scaling": "weak"})
+    if not args.no_cpu:
+        out["cpu_baseline"] = {"value": n / sec, "unit": "steps/s", "cores": 1, "kind": "port",
+                               "sample": f"first {n} steps of workload {wl}, oracle on one host core; {sec:.1f} s"}
+    print(json.dumps(out))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -87,6 +254,8 @@ def main():
     ap.add_argument("--no-graph", action="store_true", help="direct launches (hardware-counter runs)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="run only a plain 256 MiB device-to-device copy (calibrates FETCH_SIZE/WRITE_SIZE)")
+    ap.add_argument("--workload", type=int, default=2,
+                    help="BASELINE.json config (1-5); 2, the headline workload, is the default")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU; the path shards by slot with no exchange "
@@ -103,6 +272,10 @@ def main():
             b.copy_(a)
         torch.cuda.synchronize()
         print(json.dumps({"copy_calib_bytes_read": 4 * n, "copy_calib_bytes_written": 4 * n, "launches": 5}))
+        return
+
+    if args.workload != 2:
+        bench_workload(args, args.workload)
         return
 
     import bl_select as BL
