@@ -55,6 +55,7 @@ struct bl_ctx {
   float *h_lp = nullptr, *h_top_lp = nullptr;
   int32_t *d_commit_toks = nullptr;
   int32_t *d_mslot = nullptr; /* row table of bl_grammar_mask */
+  int32_t *d_bslot = nullptr, *d_acc = nullptr, *h_acc = nullptr; /* speculative verification: slots, accepted */
   int bound_B = 0;
   std::vector<void *> allocs;
   bool timing = false;
@@ -84,47 +85,85 @@ static hipError_t dalloc(bl_ctx *c, T **p, size_t n) {
   return e;
 }
 
-/* ------------------------------------------------------------------ commit kernel */
-/* tokens.push / reply_tokens.push for externally chosen tokens (one thread: a handful of writes) */
+/* ------------------------------------------------------------------ commit kernels */
+/* tokens.push / reply_tokens.push of one token (src/server.br:1004, :1037): repeat window, reply counts,
+ * touched bits, grammar position; one thread */
+__device__ void commit_one(const bl_dev &d, bl_slot_dev &sp, int slot, int32_t tok) {
+  const int V = d.vocab;
+  if (tok < 0 || tok >= V) return;
+  const int64_t so = (int64_t)slot * V;
+  uint32_t *tw = d.touched + (int64_t)slot * d.words;
+  bool is_eog = false;
+  for (int k = 0; k < d.n_eog; k++) is_eog |= d.eog[k] == tok;
+  sp.n_tokens += 1;
+  if (sp.rep_on) {
+    int rl = sp.repeat_last_n;
+    if (rl > 0) {
+      int32_t *ring = d.ring + (int64_t)slot * BL_WCAP;
+      if (sp.win_len == rl) {
+        int32_t old = ring[sp.win_head];
+        d.tokst[so + old].wcnt -= 1;
+        ring[sp.win_head] = tok;
+        sp.win_head = (sp.win_head + 1) % rl;
+      } else {
+        ring[(sp.win_head + sp.win_len) % rl] = tok;
+        sp.win_len += 1;
+      }
+    }
+    d.tokst[so + tok].wcnt += 1;
+    tw[tok >> 5] |= 1u << (tok & 31);
+  }
+  if (!is_eog) {
+    sp.n_reply += 1;
+    if (sp.fp_on) {
+      d.tokst[so + tok].cnt += 1;
+      tw[tok >> 5] |= 1u << (tok & 31);
+    }
+    if (sp.g_on) grammar_commit(d, sp, d.gram[slot], tok);
+  }
+}
+
+/* tokens chosen outside the library (one thread: a handful of writes) */
 __global__ void bl_k_commit(bl_dev d, int slot, const int32_t *toks, int n, int rng_draws) {
   if (threadIdx.x != 0 || blockIdx.x != 0) return;
   bl_slot_dev &sp = d.slots[slot];
-  const int V = d.vocab;
-  const int64_t so = (int64_t)slot * V;
-  uint32_t *tw = d.touched + (int64_t)slot * d.words;
-  for (int i = 0; i < n; i++) {
-    int32_t tok = toks[i];
-    if (tok < 0 || tok >= V) continue;
-    bool is_eog = false;
-    for (int k = 0; k < d.n_eog; k++) is_eog |= d.eog[k] == tok;
-    sp.n_tokens += 1;
-    if (sp.rep_on) {
-      int rl = sp.repeat_last_n;
-      if (rl > 0) {
-        int32_t *ring = d.ring + (int64_t)slot * BL_WCAP;
-        if (sp.win_len == rl) {
-          int32_t old = ring[sp.win_head];
-          d.tokst[so + old].wcnt -= 1;
-          ring[sp.win_head] = tok;
-          sp.win_head = (sp.win_head + 1) % rl;
-        } else {
-          ring[(sp.win_head + sp.win_len) % rl] = tok;
-          sp.win_len += 1;
-        }
-      }
-      d.tokst[so + tok].wcnt += 1;
-      tw[tok >> 5] |= 1u << (tok & 31);
-    }
-    if (!is_eog) {
-      sp.n_reply += 1;
-      if (sp.fp_on) {
-        d.tokst[so + tok].cnt += 1;
-        tw[tok >> 5] |= 1u << (tok & 31);
-      }
-      if (sp.g_on) grammar_commit(d, sp, d.gram[slot], tok);
-    }
-  }
+  for (int i = 0; i < n; i++) commit_one(d, sp, slot, toks[i]);
   for (int k = 0; k < rng_draws; k++) sp.rng = bl_xorshift(sp.rng);
+}
+
+/*
+ * Speculative verification after the selection, one workgroup per sequence (src/server.br:1173-1216):
+ * the accepted prefix (leading rows whose token equals the draft and is not end-of-generation), then the
+ * accepted drafts and the next row's token are pushed and the RNG advances by the draws a sequential
+ * decode makes (accepted + 1 for a sampled slot). Nothing is committed when any row of the call reported
+ * a status (the call then fails as a whole).
+ */
+__global__ void bl_k_spec_commit(bl_dev d, const int32_t *slots, const int32_t *drafts, int k, const int32_t *tok,
+                                 const int32_t *status, int R, int32_t *accepted) {
+  const int b = blockIdx.x;
+  __shared__ int bad;
+  if (threadIdx.x == 0) bad = 0;
+  __syncthreads();
+  for (int i = threadIdx.x; i < R; i += blockDim.x)
+    if (status[i]) bad = 1;
+  __syncthreads();
+  if (threadIdx.x != 0) return;
+  const int32_t *tb = tok + (int64_t)b * (k + 1), *db = drafts + (int64_t)b * k;
+  int a = 0;
+  while (a < k && tb[a] == db[a]) {
+    bool eog = false;
+    for (int q = 0; q < d.n_eog; q++) eog |= d.eog[q] == tb[a];
+    if (eog) break;
+    a++;
+  }
+  accepted[b] = a;
+  if (bad) return;
+  const int slot = slots[b];
+  bl_slot_dev &sp = d.slots[slot];
+  for (int i = 0; i < a; i++) commit_one(d, sp, slot, db[i]);
+  commit_one(d, sp, slot, tb[a]);
+  if (sp.temperature > 0.0f)
+    for (int q = 0; q <= a; q++) sp.rng = bl_xorshift(sp.rng);
 }
 
 __global__ void bl_k_bump(float *out, const int32_t *ids, int n, float add) {
@@ -234,6 +273,8 @@ int bl_create(int device, int max_slots, int max_rows, int vocab, bl_ctx **out) 
   ALLOC(c->d_top_lp, R * 256);
   ALLOC(c->d_commit_toks, 4096);
   ALLOC(c->d_mslot, 1);
+  ALLOC(c->d_bslot, R);
+  ALLOC(c->d_acc, R);
 #undef ALLOC
   d.n_eog = 0;
   if (hipHostMalloc((void **)&c->h_slot, R * sizeof(int32_t)) != hipSuccess ||
@@ -242,7 +283,8 @@ int bl_create(int device, int max_slots, int max_rows, int vocab, bl_ctx **out) 
       hipHostMalloc((void **)&c->h_status, R * sizeof(int32_t)) != hipSuccess ||
       hipHostMalloc((void **)&c->h_lp, R * sizeof(float)) != hipSuccess ||
       hipHostMalloc((void **)&c->h_top_ids, R * 256 * sizeof(int32_t)) != hipSuccess ||
-      hipHostMalloc((void **)&c->h_top_lp, R * 256 * sizeof(float)) != hipSuccess) {
+      hipHostMalloc((void **)&c->h_top_lp, R * 256 * sizeof(float)) != hipSuccess ||
+      hipHostMalloc((void **)&c->h_acc, R * sizeof(int32_t)) != hipSuccess) {
     bl_destroy(c);
     return fail(BL_EDEVICE, "hipHostMalloc failed");
   }
@@ -270,7 +312,7 @@ void bl_destroy(bl_ctx *c) {
   }
   if (c->d_vblob) hipFree(c->d_vblob);
   if (c->d_voff) hipFree(c->d_voff);
-  void *hp[] = {c->h_slot, c->h_skip, c->h_tok, c->h_status, c->h_lp, c->h_top_ids, c->h_top_lp};
+  void *hp[] = {c->h_slot, c->h_skip, c->h_tok, c->h_status, c->h_lp, c->h_top_ids, c->h_top_lp, c->h_acc};
   for (void *p : hp)
     if (p) hipHostFree(p);
   for (hipEvent_t e : c->ev)
@@ -764,7 +806,8 @@ int bl_spec_verify(bl_ctx *c, const int32_t *slots, int B, int k, const float *d
   int rc = check_rows(c, slots, B);
   if (rc) return rc;
   const int R = B * (k + 1);
-  if (k < 0 || R > c->d.max_rows || !d_rows || !tokens || !accepted || ld < c->d.vocab)
+  if (k < 0 || R > c->d.max_rows || !d_rows || !tokens || !accepted || ld < c->d.vocab || (k > 0 && !drafts) ||
+      (int64_t)B * k > 4096)
     return fail(BL_EPARAM, "bl_spec_verify: invalid arguments (B %d, k %d)", B, k);
   for (int b = 0; b < B; b++) {
     const bl_slot_dev &s = c->host_slots[slots[b]];
@@ -780,35 +823,24 @@ int bl_spec_verify(bl_ctx *c, const int32_t *slots, int B, int k, const float *d
     }
   HIPCHK(hipMemcpyAsync(c->d_slot, c->h_slot, R * sizeof(int32_t), hipMemcpyHostToDevice, c->stream));
   HIPCHK(hipMemcpyAsync(c->d_skip, c->h_skip, R * sizeof(int32_t), hipMemcpyHostToDevice, c->stream));
+  if (k > 0) HIPCHK(hipMemcpyAsync(c->d_commit_toks, drafts, (size_t)B * k * 4, hipMemcpyHostToDevice, c->stream));
+  HIPCHK(hipMemcpyAsync(c->d_bslot, slots, B * sizeof(int32_t), hipMemcpyHostToDevice, c->stream));
   bl_rows rows = make_rows(c, true, 0, 1);
   rows.lp = nullptr; /* no logprobs are returned for speculative rows */
   mark_stepped(c, slots, B);
   bl_launch_step(c->d, d_rows, ld, rows, R, needs_pass2(c, slots, B), false, c->stream, nullptr);
+  hipLaunchKernelGGL(bl_k_spec_commit, dim3(B), dim3(64), 0, c->stream, c->d, c->d_bslot, c->d_commit_toks, k,
+                     c->d_tok, c->d_status, R, c->d_acc);
   HIPCHK(hipGetLastError());
   HIPCHK(hipMemcpyAsync(c->h_tok, c->d_tok, R * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));
   HIPCHK(hipMemcpyAsync(c->h_status, c->d_status, R * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(hipMemcpyAsync(c->h_acc, c->d_acc, B * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));
   HIPCHK(hipStreamSynchronize(c->stream));
   int st = 0;
   for (int i = 0; i < R; i++) st |= c->h_status[i];
   memcpy(tokens, c->h_tok, R * sizeof(int32_t));
   if ((rc = status_error(st))) return rc;
-  std::vector<int32_t> eog(c->d.n_eog);
-  if (c->d.n_eog) HIPCHK(hipMemcpy(eog.data(), c->d.eog, eog.size() * 4, hipMemcpyDeviceToHost));
-  for (int b = 0; b < B; b++) {
-    int a = 0;
-    while (a < k && tokens[b * (k + 1) + a] == drafts[b * k + a] &&
-           std::find(eog.begin(), eog.end(), tokens[b * (k + 1) + a]) == eog.end())
-      a++;
-    accepted[b] = a;
-    std::vector<int32_t> commit(drafts + b * k, drafts + b * k + a);
-    commit.push_back(tokens[b * (k + 1) + a]);
-    HIPCHK(hipMemcpyAsync(c->d_commit_toks, commit.data(), commit.size() * 4, hipMemcpyHostToDevice, c->stream));
-    int draws = c->host_slots[slots[b]].temperature > 0.0f ? a + 1 : 0;
-    hipLaunchKernelGGL(bl_k_commit, dim3(1), dim3(64), 0, c->stream, c->d, slots[b], c->d_commit_toks,
-                       (int)commit.size(), draws);
-    HIPCHK(hipGetLastError());
-    HIPCHK(hipStreamSynchronize(c->stream));
-  }
+  memcpy(accepted, c->h_acc, B * sizeof(int32_t));
   return BL_OK;
 }
 
