@@ -35,6 +35,7 @@
 #define BL_TK_CAP 1024      /* chunk top-K: keys at or above the thread-maximum bound ranked in LDS */
 #define BL_STAGE_B 1024     /* block summaries staged in LDS by the fast normaliser (V up to 1M) */
 #define BL_RANK_MAX 1024    /* full-vocabulary candidate lists up to this size are sorted by counting */
+#define BL_NBUCKET 8192     /* value buckets of the sort of longer lists (more than BL_LDS_SORT) */
 #define BL_EOG_LDS 64       /* end-of-generation ids the selection keeps in LDS */
 
 /* per-token flags */

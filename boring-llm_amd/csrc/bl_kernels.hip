@@ -775,10 +775,12 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_exppass(bl_dev d, bl_rows 
     }
   }
   if (mode & BL_M_FULL) {
-    /* candidates of a full-vocabulary rank: every value within 17.5*max(T,1) of the maximum; one
-     * atomic per wavefront reserves the wavefront's slots */
+    /* candidates of a full-vocabulary rank: every value within 17.5*span of the maximum, where span is
+     * max(T, 1) when top-p or min-p read the untempered softmax and T otherwise (only the tempered sum is
+     * formed then); one atomic per wavefront reserves the wavefront's slots */
     const float T = sp.temperature;
-    const float thr = M - 17.5f * (T > 1.0f ? T : 1.0f);
+    const bool filt = sp.top_p < 1.0f || sp.min_p > 0.0f;
+    const float thr = M - 17.5f * (filt && T < 1.0f ? 1.0f : T);
     int mine = 0;
 #pragma unroll
     for (int k = 0; k < 4; k++) mine += (j0 + k < cnt && x[k] >= thr) ? 1 : 0;
@@ -1419,6 +1421,8 @@ __device__ void norm_chain(const bl_dev &d, int row, float M, sel_shared &sh) {
  * Returns the token id, or -1 when the prefix exceeds BL_TIE_MAX elements or its subtree the LDS copy (the
  * caller then reports the tie).
  */
+static_assert(BL_NBUCKET * sizeof(uint32_t) <= sizeof(sel_cand::keys), "bucket counters live in the list's LDS");
+static_assert(BL_NBUCKET % BL_SEL_THREADS == 0, "whole buckets per thread");
 #define BL_TIE_MAX 8192                                     /* elements >= the tied value */
 #define BL_TIE_OCC ((int)(sizeof(sel_norm) / sizeof(int16_t))) /* positions copied to LDS */
 template <class KeyF>
@@ -1603,13 +1607,62 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
         for (; j < nf; j++) r += sh.c.tmp[j] > k ? 1 : 0;
         keys[r] = k;
       }
-    } else {
+    } else if (nf <= BL_LDS_SORT) {
       int P = 1;
       while (P < nf) P <<= 1;
-      if (P > BL_LDS_SORT) keys = d.sortk + (int64_t)row * (2 * (int64_t)V);
       for (int i = t; i < P; i += BL_SEL_THREADS) keys[i] = i < nf ? ckey(fv[i], fi[i]) : 0ull;
       __syncthreads();
       bitonic_desc(keys, P);
+    } else {
+      /* a large list: buckets by value over the candidates' span (larger values in lower buckets, equal
+       * values in one bucket), a scatter by bucket, then a rank by counting within each bucket */
+      uint64_t *A = d.sortk + (int64_t)row * (2 * (int64_t)V), *Bk = A + V;
+      uint32_t *cnt = reinterpret_cast<uint32_t *>(sh.c.keys); /* BL_NBUCKET counters; the list is in memory */
+      const bool filt = sp.top_p < 1.0f || sp.min_p > 0.0f;
+      const float span = 17.5f * (filt && T < 1.0f ? 1.0f : T); /* the exponent pass's candidate span */
+      const float scale = (float)BL_NBUCKET / span;
+      auto bucket = [&](float v) -> int {
+        const float q = (M - v) * scale;
+        return q >= 0.0f ? (q < (float)(BL_NBUCKET - 1) ? (int)q : BL_NBUCKET - 1) : 0;
+      };
+      for (int b = t; b < BL_NBUCKET; b += BL_SEL_THREADS) cnt[b] = 0u;
+      __syncthreads();
+      for (int i = t; i < nf; i += BL_SEL_THREADS) atomicAdd(&cnt[bucket(fv[i])], 1u);
+      __syncthreads();
+      /* exclusive offsets: thread t owns buckets [t*PB, (t+1)*PB) */
+      constexpr int PB = BL_NBUCKET / BL_SEL_THREADS;
+      uint32_t loc[PB], own = 0u;
+#pragma unroll
+      for (int q = 0; q < PB; q++) {
+        loc[q] = cnt[t * PB + q];
+        own += loc[q];
+      }
+      const uint32_t incl = (uint32_t)bl_wscan_add((int)own, lane);
+      if (lane == 63) sh.red_i[w] = (int)incl;
+      __syncthreads();
+      uint32_t run = incl - own;
+      for (int q = 0; q < w; q++) run += (uint32_t)sh.red_i[q];
+#pragma unroll
+      for (int q = 0; q < PB; q++) {
+        cnt[t * PB + q] = run;
+        run += loc[q];
+      }
+      __syncthreads();
+      for (int i = t; i < nf; i += BL_SEL_THREADS) {
+        const float v = fv[i];
+        A[atomicAdd(&cnt[bucket(v)], 1u)] = ckey(v, fi[i]);
+      }
+      __syncthreads(); /* cnt[b] is now the end of bucket b */
+      for (int p = t; p < nf; p += BL_SEL_THREADS) {
+        const uint64_t k = A[p];
+        const int b = bucket(ckey_v(k));
+        const int s0 = b > 0 ? (int)cnt[b - 1] : 0, e0 = (int)cnt[b];
+        int r = 0;
+        for (int j = s0; j < e0; j++) r += A[j] > k ? 1 : 0;
+        Bk[s0 + r] = k;
+      }
+      __syncthreads();
+      keys = Bk;
     }
     n_list = nf;
     n_logical = V;
