@@ -241,14 +241,15 @@ int bl_create(int device, int max_slots, int max_rows, int vocab, bl_ctx **out) 
     ALLOC(g, R * 2 * G * 32);
     d.grec = g;
   }
-  ALLOC(d.full_v, R * V);
-  ALLOC(d.full_i, R * V);
-  ALLOC(d.full_n, R);
+  d.nb = (vocab + BL_EB - 1) / BL_EB;
+  ALLOC(d.full_v, R * d.nb * BL_EB);
+  ALLOC(d.full_i, R * d.nb * BL_EB);
+  ALLOC(d.full_cnt, R * d.nb);
+  ALLOC(d.full_s, R * d.nb);
   ALLOC(d.sortk, R * std::max(P2, 2 * V));
   ALLOC(d.gsum, R * G);
   ALLOC(d.gapx, R * G);
   ALLOC(d.mkey, (size_t)R * BL_KSEL_MAX);
-  d.nb = (vocab + BL_EB - 1) / BL_EB;
   {
     char *b = nullptr;
     ALLOC(b, R * d.nb * 16);

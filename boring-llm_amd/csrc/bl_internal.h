@@ -107,9 +107,10 @@ struct bl_dev {
   float *cand_v;    /* [rows][nc][KSEL_MAX] */
   int32_t *cand_i;
   void *grec;       /* [rows][2 * (V/64 + 64)] bl_grec: index-order records, then sorted-list records */
-  float *full_v;    /* [rows][V] full-vocabulary candidates */
+  float *full_v;    /* [rows][nb][BL_EB] full-vocabulary candidates, exponent block b's in region b */
   int32_t *full_i;
-  int32_t *full_n;  /* [rows] */
+  int32_t *full_cnt; /* [rows][nb] candidates in each region */
+  double *full_s;    /* [rows][nb] approximate tempered sum over each region (rows without top-p/min-p) */
   uint64_t *sortk;  /* [rows][2^ceil(log2 V)] global sort scratch */
   double *gsum;     /* [rows][V/64 + 64] */
   float *gapx;      /* [rows][V/64 + 64] approximate index-order sum before each 64-term group, then the total */

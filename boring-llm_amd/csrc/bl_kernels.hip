@@ -172,7 +172,6 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass(bl_dev d, const fl
   const float *src = logits + (int64_t)row * ld + i0;
   if (c == 0 && t == 0) {
     /* consumed by the kernels that run after this one */
-    d.full_n[row] = 0;
     d.gamb[row] = 0;
   }
   /* model tail (src/model.br:973-984), applied in registers by the thread that loads the value */
@@ -777,7 +776,9 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_exppass(bl_dev d, bl_rows 
   if (mode & BL_M_FULL) {
     /* candidates of a full-vocabulary rank: every value within 17.5*span of the maximum, where span is
      * max(T, 1) when top-p or min-p read the untempered softmax and T otherwise (only the tempered sum is
-     * formed then); one atomic per wavefront reserves the wavefront's slots */
+     * formed then). The block writes them in index order to its own BL_EB-entry region, and their count:
+     * no counter is shared between workgroups (one would serialise device-scope atomics across XCDs) */
+    __shared__ int f_w[BL_RP_THREADS / 64];
     const float T = sp.temperature;
     const bool filt = sp.top_p < 1.0f || sp.min_p > 0.0f;
     const float thr = M - 17.5f * (filt && T < 1.0f ? 1.0f : T);
@@ -785,20 +786,42 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_exppass(bl_dev d, bl_rows 
 #pragma unroll
     for (int k = 0; k < 4; k++) mine += (j0 + k < cnt && x[k] >= thr) ? 1 : 0;
     const int incl = bl_wscan_add(mine, lane);
-    const int wtot_n = (int)bl_bcast((uint32_t)incl, 63);
-    int base = 0;
-    if (lane == 0 && wtot_n > 0) base = atomicAdd(&d.full_n[row], wtot_n);
-    base = (int)bl_bcast((uint32_t)base, 0);
-    int pos = base + incl - mine;
+    if (lane == 63) f_w[w] = incl;
+    __syncthreads();
+    int pos = incl - mine, tot = 0;
+#pragma unroll
+    for (int q = 0; q < BL_RP_THREADS / 64; q++) {
+      if (q < w) pos += f_w[q];
+      tot += f_w[q];
+    }
+    const int64_t ro = ((int64_t)row * d.nb + b) * BL_EB;
 #pragma unroll
     for (int k = 0; k < 4; k++)
       if (j0 + k < cnt && x[k] >= thr) {
-        if (pos < V) {
-          d.full_v[(int64_t)row * V + pos] = x[k];
-          d.full_i[(int64_t)row * V + pos] = i0 + j0 + k;
-        }
+        d.full_v[ro + pos] = x[k];
+        d.full_i[ro + pos] = i0 + j0 + k;
         pos++;
       }
+    if (t == 0) d.full_cnt[(int64_t)row * d.nb + b] = tot;
+    if (!filt && T > 0.0f) {
+      /* the block's share of the tempered sum, approximately (hardware exponential, double partials):
+       * the selection derives a lower bound on the draw's running sum from it */
+      const float rT = 1.0f / T;
+      float ps = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 4; k++)
+        if (j0 + k < cnt && x[k] >= thr) ps += __expf((x[k] - M) * rT);
+      const double ws = bl_wave_sum_d((double)ps);
+      __shared__ double f_s[BL_RP_THREADS / 64];
+      if (lane == 0) f_s[w] = ws;
+      __syncthreads();
+      if (t == 0) {
+        double bs = 0.0;
+#pragma unroll
+        for (int q = 0; q < BL_RP_THREADS / 64; q++) bs += f_s[q];
+        d.full_s[(int64_t)row * d.nb + b] = bs;
+      }
+    }
   }
 }
 
@@ -959,6 +982,13 @@ struct sel_cand {
   bl_grec recs[BL_LDS_SORT / 64];
   double gsum[BL_LDS_SORT / 64];
 };
+/* the bucket sort of a long full-vocabulary list keeps the region offsets, then a tile of the bucketed
+ * list, in the normaliser's LDS (free until norm_prep) */
+#define BL_BOFF_BYTES (((BL_MAX_CHUNKS * BL_SUBS + 1) * 4 + 15) / 16 * 16)
+#define BL_RTILE 4096 /* keys per rank tile */
+#define BL_CAND_U 8   /* candidate loads in flight per lane */
+static_assert(BL_BOFF_BYTES + BL_RTILE * 8 <= sizeof(sel_norm), "rank tile");
+static_assert(BL_RTILE % BL_SEL_THREADS == 0, "rank tile");
 struct sel_shared {
   sel_norm n; /* both live at once: the normaliser's chain runs beside the draw */
   sel_cand c;
@@ -1416,15 +1446,20 @@ __device__ void norm_chain(const bl_dev &d, int row, float M, sel_shared &sh) {
  * sorted prefix), every other position reading as smaller than all of them:
  *   - occupancy (position -> element of the prefix, or -1) in `occ_g`, V entries of global scratch; the
  *     bottom-up build runs level by level, the parents of one level owning disjoint subtrees;
- *   - after the build the prefix forms a rooted subtree; when it lies within the first BL_TIE_OCC
- *     positions, one lane replays the extractions up to `pos` on an LDS copy of that occupancy.
- * Returns the token id, or -1 when the prefix exceeds BL_TIE_MAX elements or its subtree the LDS copy (the
- * caller then reports the tie).
+ *   - after the build the prefix forms a rooted subtree; one lane replays the extractions up to `pos` on
+ *     an LDS copy of that occupancy: the first BL_TIE_OCC positions densely, the subtree's positions past
+ *     them in an open-addressing table (BL_TIE_HASH slots, filled to at most 3/4). An extraction moves
+ *     elements of the prefix only into positions that held one, so the table needs no insertion later.
+ * Returns the token id, or -1 when the prefix exceeds BL_TIE_MAX elements or its deep positions the table
+ * (the caller then reports the tie).
  */
 static_assert(BL_NBUCKET * sizeof(uint32_t) <= sizeof(sel_cand::keys), "bucket counters live in the list's LDS");
 static_assert(BL_NBUCKET % BL_SEL_THREADS == 0, "whole buckets per thread");
 #define BL_TIE_MAX 8192                                     /* elements >= the tied value */
 #define BL_TIE_OCC ((int)(sizeof(sel_norm) / sizeof(int16_t))) /* positions copied to LDS */
+#define BL_TIE_HASH BL_RANK_MAX /* slots of the deep-position table (the counting sort's LDS, free by now) */
+static_assert((BL_TIE_HASH & (BL_TIE_HASH - 1)) == 0, "table size is a power of two");
+__device__ __forceinline__ uint32_t tie_slot(int p) { return ((uint32_t)p * 2654435761u) >> 22 & (BL_TIE_HASH - 1); }
 template <class KeyF>
 __device__ int heap_tie_id(KeyF key, bool keys_in_lds, int64_t n_list, int64_t pos, int V, int32_t *occ_g,
                            sel_shared &sh) {
@@ -1481,23 +1516,53 @@ __device__ int heap_tie_id(KeyF key, bool keys_in_lds, int64_t n_list, int64_t p
     for (int p = p0 + t; p < p1; p += BL_SEL_THREADS) sift(p, V, gget, gset);
     __syncthreads();
   }
-  /* the prefix's subtree must fit the LDS copy */
-  int far = -1;
-  for (int p = t; p < V; p += BL_SEL_THREADS)
-    if (occ_g[p] >= 0) far = p;
-  far = (int)bl_wmax_u32((uint32_t)(far + 1), lane) - 1;
-  if (lane == 0) sh.red_i[w] = far;
-  __syncthreads();
-  far = -1;
-  for (int q = 0; q < SEL_NW; q++) far = max(far, sh.red_i[q]);
-  if (far >= BL_TIE_OCC) return -1; /* uniform */
+  /* the prefix's positions past the dense copy go to the table: (position + 1) << 32 | element, 0 empty */
   const int n_occ = min(V, BL_TIE_OCC);
+  uint64_t *htab = sh.c.tmp;
+  for (int i = t; i < BL_TIE_HASH; i += BL_SEL_THREADS) htab[i] = 0ull;
+  __syncthreads();
+  int deep = 0;
+  for (int p = n_occ + t; p < V; p += BL_SEL_THREADS)
+    if (occ_g[p] >= 0) deep++;
+  deep = bl_wscan_add(deep, lane);
+  if (lane == 63) sh.red_i[w] = deep;
+  __syncthreads();
+  deep = 0;
+  for (int q = 0; q < SEL_NW; q++) deep += sh.red_i[q];
+  if (deep > BL_TIE_HASH * 3 / 4) return -1; /* uniform */
+  if (deep > 0)
+    for (int p = n_occ + t; p < V; p += BL_SEL_THREADS) {
+      const int o = occ_g[p];
+      if (o < 0) continue;
+      const uint64_t e = (uint64_t)(uint32_t)(p + 1) << 32 | (uint32_t)o;
+      for (uint32_t h = tie_slot(p);; h = (h + 1) & (BL_TIE_HASH - 1))
+        if (atomicCAS(reinterpret_cast<unsigned long long *>(&htab[h]), 0ull, (unsigned long long)e) == 0ull) break;
+    }
   int16_t *occ_l = reinterpret_cast<int16_t *>(&sh.n);
   for (int p = t; p < n_occ; p += BL_SEL_THREADS) occ_l[p] = (int16_t)occ_g[p];
   __syncthreads();
   if (t == 0) {
-    auto lget = [&](int p) -> int { return p < n_occ ? (int)occ_l[p] : -1; };
-    auto lset = [&](int p, int v) { occ_l[p] = (int16_t)v; }; /* only positions holding prefix elements */
+    /* the table slot of position p (past the dense copy), or -1 when p holds no prefix element */
+    auto hfind = [&](int p) -> int {
+      for (uint32_t h = tie_slot(p);; h = (h + 1) & (BL_TIE_HASH - 1)) {
+        const uint64_t e = htab[h];
+        if (e == 0ull) return -1;
+        if ((uint32_t)(e >> 32) == (uint32_t)(p + 1)) return (int)h;
+      }
+    };
+    auto lget = [&](int p) -> int {
+      if (p < n_occ) return (int)occ_l[p];
+      const int h = hfind(p);
+      return h < 0 ? -1 : (int)(int32_t)(uint32_t)htab[h];
+    };
+    auto lset = [&](int p, int v) { /* only positions that held prefix elements after the build */
+      if (p < n_occ) {
+        occ_l[p] = (int16_t)v;
+      } else {
+        const int h = hfind(p);
+        if (h >= 0) htab[h] = (htab[h] & 0xffffffff00000000ull) | (uint32_t)v;
+      }
+    };
     int size = V, res = -1;
     for (int64_t i = 0; i <= pos; i++) {
       const int o = lget(0);
@@ -1586,16 +1651,55 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
     if (t < kk) keys[t] = mk;
     n_list = n_logical = kk;
   } else if (sampled) {
-    /* full-vocabulary rank (src/sampling.br:301-365): the exponent pass's candidates, sorted */
-    int nf = d.full_n[row];
-    if (nf > V) {
-      nf = V;
-      status |= BL_SE_CAND_FULL;
+    /* full-vocabulary rank (src/sampling.br:301-365): the exponent blocks' candidates (block b's at
+     * [b*BL_EB, b*BL_EB + count)), concatenated by the prefix sum of the counts, then sorted */
+    const int NB = d.nb;
+    const float *fv = d.full_v + (int64_t)row * NB * BL_EB;
+    const int32_t *fi = d.full_i + (int64_t)row * NB * BL_EB;
+    int *boff = reinterpret_cast<int *>(&sh.n); /* [NB + 1]; the normaliser's LDS is free until norm_prep */
+    const bool filt = sp.top_p < 1.0f || sp.min_p > 0.0f;
+    int nf = 0;
+    double s_ap = 0.0; /* the exponent blocks' approximate tempered sum (unfiltered rows) */
+    for (int b0 = 0; b0 < NB; b0 += BL_SEL_THREADS) {
+      const int bb = b0 + t;
+      const int c = bb < NB ? d.full_cnt[(int64_t)row * NB + bb] : 0;
+      const double bsum = (!filt && bb < NB) ? d.full_s[(int64_t)row * NB + bb] : 0.0;
+      const int incl = bl_wscan_add(c, lane);
+      const double ws = bl_wave_sum_d(bsum);
+      if (lane == 63) {
+        sh.red_i[w] = incl;
+        sh.c.gsum[w] = ws;
+      }
+      __syncthreads();
+      int base = nf + incl - c, tot = 0;
+      for (int q = 0; q < SEL_NW; q++) {
+        if (q < w) base += sh.red_i[q];
+        tot += sh.red_i[q];
+        s_ap += sh.c.gsum[q];
+      }
+      if (bb < NB) boff[bb] = base;
+      nf += tot;
+      __syncthreads();
     }
-    const float *fv = d.full_v + (int64_t)row * V;
-    const int32_t *fi = d.full_i + (int64_t)row * V;
+    if (t == 0) boff[NB] = nf;
+    __syncthreads();
+    /* f(flat index, value, id) over every candidate; candidate i lies in the region lo with
+     * boff[lo] <= i < boff[lo + 1] (binary search in LDS, so every thread's loads are independent) */
+    auto each_cand = [&](auto f) {
+      for (int i = t; i < nf; i += BL_SEL_THREADS) {
+        int lo = 0, hi = NB;
+        while (hi - lo > 1) {
+          const int mid = (lo + hi) >> 1;
+          if (boff[mid] <= i) lo = mid;
+          else hi = mid;
+        }
+        const int64_t src = (int64_t)lo * BL_EB + (i - boff[lo]);
+        f(i, fv[src], fi[src]);
+      }
+    };
+    int nl = nf;
     if (nf <= BL_RANK_MAX) {
-      for (int i = t; i < nf; i += BL_SEL_THREADS) sh.c.tmp[i] = ckey(fv[i], fi[i]);
+      each_cand([&](int i, float v, int32_t id) { sh.c.tmp[i] = ckey(v, id); });
       __syncthreads();
       /* rank by counting (keys are distinct: they carry the index) */
       for (int i = t; i < nf; i += BL_SEL_THREADS) {
@@ -1610,24 +1714,66 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
     } else if (nf <= BL_LDS_SORT) {
       int P = 1;
       while (P < nf) P <<= 1;
-      for (int i = t; i < P; i += BL_SEL_THREADS) keys[i] = i < nf ? ckey(fv[i], fi[i]) : 0ull;
+      for (int i = nf + t; i < P; i += BL_SEL_THREADS) keys[i] = 0ull;
+      each_cand([&](int i, float v, int32_t id) { keys[i] = ckey(v, id); });
       __syncthreads();
       bitonic_desc(keys, P);
     } else {
-      /* a large list: buckets by value over the candidates' span (larger values in lower buckets, equal
-       * values in one bucket), a scatter by bucket, then a rank by counting within each bucket */
+      /* a large list: the candidates the draw can still see (below), bucketed by value (larger values in
+       * lower buckets, equal values in one bucket), scattered by bucket, then ranked by counting within
+       * each bucket, one LDS tile of the bucketed list at a time */
+      const float T = sp.temperature;
+      float thr = M - 17.5f * (filt && T < 1.0f ? 1.0f : T); /* the exponent pass's candidate span */
+      if (!filt) {
+        /* the draw adds exp((v - M) / T) in descending order. With u = 2^-24 and m <= V terms, the float
+         * running sum past every term >= 2^(k-24) is at least (1 - g) (S - V 2^(k-24)), g = m u / (1 - m u)
+         * (recursive summation bound), S the exact sum; that is >= 2^k when S >= 2^k (1 / (1 - g) + V u).
+         * A term below half an ulp of the running sum leaves it unchanged, and so does every later
+         * (smaller) term: the terms below 2^(k-24) are never seen by the draw. S is bounded from below by
+         * the exponent blocks' approximate sum with a 10^-3 margin, the cut in logit space with a 10^-3
+         * margin on the exponent (both far above the hardware exponential's error) */
+        const double mu = (double)V * 0x1p-24;
+        const double g = mu / (1.0 - mu);
+        const double need = 1.0 / (1.0 - g) + mu;
+        const double s_lo = s_ap * 0.999 / need;
+        if (mu < 0.5 && s_lo > 0.0) {
+          const int k = (int)((bl_d2u(s_lo) >> 52) & 0x7ff) - 1023; /* floor(log2 s_lo), s_lo normal */
+          const float cut = M + T * ((float)((double)(k - 24) * 0.6931471805599453) - 1.0e-3f);
+          thr = fmaxf(thr, cut);
+        }
+      }
       uint64_t *A = d.sortk + (int64_t)row * (2 * (int64_t)V), *Bk = A + V;
       uint32_t *cnt = reinterpret_cast<uint32_t *>(sh.c.keys); /* BL_NBUCKET counters; the list is in memory */
-      const bool filt = sp.top_p < 1.0f || sp.min_p > 0.0f;
-      const float span = 17.5f * (filt && T < 1.0f ? 1.0f : T); /* the exponent pass's candidate span */
-      const float scale = (float)BL_NBUCKET / span;
+      const float span = M - thr;
+      const float scale = span > 0.0f ? (float)BL_NBUCKET / span : 0.0f;
       auto bucket = [&](float v) -> int {
         const float q = (M - v) * scale;
         return q >= 0.0f ? (q < (float)(BL_NBUCKET - 1) ? (int)q : BL_NBUCKET - 1) : 0;
       };
       for (int b = t; b < BL_NBUCKET; b += BL_SEL_THREADS) cnt[b] = 0u;
       __syncthreads();
-      for (int i = t; i < nf; i += BL_SEL_THREADS) atomicAdd(&cnt[bucket(fv[i])], 1u);
+      /* wavefront w reads regions w, w + SEL_NW, ...; each lane keeps BL_CAND_U loads in flight */
+      auto each_region = [&](auto f) {
+        for (int bb = w; bb < NB; bb += SEL_NW) {
+          const int c = boff[bb + 1] - boff[bb];
+          const float *pv = fv + (int64_t)bb * BL_EB;
+          const int32_t *pi = fi + (int64_t)bb * BL_EB;
+          for (int j0 = 0; j0 < c; j0 += 64 * BL_CAND_U) {
+            float v[BL_CAND_U];
+#pragma unroll
+            for (int u = 0; u < BL_CAND_U; u++) {
+              const int j = j0 + lane + 64 * u;
+              v[u] = j < c ? pv[j] : BL_NEG_INF;
+            }
+            f(v, pi + j0 + lane);
+          }
+        }
+      };
+      each_region([&](const float *v, const int32_t *) {
+#pragma unroll
+        for (int u = 0; u < BL_CAND_U; u++)
+          if (v[u] >= thr) atomicAdd(&cnt[bucket(v[u])], 1u);
+      });
       __syncthreads();
       /* exclusive offsets: thread t owns buckets [t*PB, (t+1)*PB) */
       constexpr int PB = BL_NBUCKET / BL_SEL_THREADS;
@@ -1641,30 +1787,57 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
       if (lane == 63) sh.red_i[w] = (int)incl;
       __syncthreads();
       uint32_t run = incl - own;
-      for (int q = 0; q < w; q++) run += (uint32_t)sh.red_i[q];
+      int nk = 0;
+      for (int q = 0; q < SEL_NW; q++) {
+        if (q < w) run += (uint32_t)sh.red_i[q];
+        nk += sh.red_i[q];
+      }
 #pragma unroll
       for (int q = 0; q < PB; q++) {
         cnt[t * PB + q] = run;
         run += loc[q];
       }
       __syncthreads();
-      for (int i = t; i < nf; i += BL_SEL_THREADS) {
-        const float v = fv[i];
-        A[atomicAdd(&cnt[bucket(v)], 1u)] = ckey(v, fi[i]);
-      }
+      each_region([&](const float *v, const int32_t *pi) {
+        int32_t id[BL_CAND_U];
+#pragma unroll
+        for (int u = 0; u < BL_CAND_U; u++) id[u] = v[u] >= thr ? pi[64 * u] : 0;
+#pragma unroll
+        for (int u = 0; u < BL_CAND_U; u++)
+          if (v[u] >= thr) A[atomicAdd(&cnt[bucket(v[u])], 1u)] = ckey(v[u], id[u]);
+      });
       __syncthreads(); /* cnt[b] is now the end of bucket b */
-      for (int p = t; p < nf; p += BL_SEL_THREADS) {
-        const uint64_t k = A[p];
-        const int b = bucket(ckey_v(k));
-        const int s0 = b > 0 ? (int)cnt[b - 1] : 0, e0 = (int)cnt[b];
-        int r = 0;
-        for (int j = s0; j < e0; j++) r += A[j] > k ? 1 : 0;
-        Bk[s0 + r] = k;
+      uint64_t *tile = reinterpret_cast<uint64_t *>(reinterpret_cast<char *>(&sh.n) + BL_BOFF_BYTES);
+      for (int base = 0; base < nk; base += BL_RTILE) {
+        const int n_t = min(BL_RTILE, nk - base);
+#pragma unroll
+        for (int u = 0; u < BL_RTILE / BL_SEL_THREADS; u++) {
+          const int i = t + u * BL_SEL_THREADS;
+          if (i < n_t) tile[i] = A[base + i];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < BL_RTILE / BL_SEL_THREADS; u++) {
+          const int i = t + u * BL_SEL_THREADS;
+          if (i < n_t) {
+            const uint64_t k = tile[i];
+            const int bk = bucket(ckey_v(k));
+            const int s0 = bk > 0 ? (int)cnt[bk - 1] : 0, e0 = (int)cnt[bk];
+            int r = 0;
+            if (s0 >= base && e0 <= base + n_t) {
+              for (int j = s0 - base; j < e0 - base; j++) r += tile[j] > k ? 1 : 0;
+            } else { /* a bucket across the tile's edge */
+              for (int j = s0; j < e0; j++) r += A[j] > k ? 1 : 0;
+            }
+            Bk[s0 + r] = k;
+          }
+        }
+        __syncthreads();
       }
-      __syncthreads();
       keys = Bk;
+      nl = nk;
     }
-    n_list = nf;
+    n_list = nl;
     n_logical = V;
   }
   __syncthreads();
@@ -1749,7 +1922,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
         const float vp = val(pos);
         if ((pos > 0 && val(pos - 1) == vp) || (pos + 1 < n_list && val(pos + 1) == vp)) {
           const int hid = heap_tie_id([&](int64_t j) { return keys[j]; }, keys == sh.c.keys, n_list, pos, V,
-                                      d.full_i + (int64_t)row * V, sh);
+                                      d.full_i + (int64_t)row * d.nb * BL_EB, sh);
           if (hid >= 0) tok = hid;
           else status |= BL_SE_TIE;
         }

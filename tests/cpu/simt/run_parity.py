@@ -162,6 +162,66 @@ def run_bigties(BL, steps):
     return None
 
 
+UNFILT_ROWS = [(0.7, 3.0, None), (0.3, 3.0, None), (1.5, 2.0, None), (0.7, 3.0, "bf16"), (1.0, 0.5, None),
+               (0.05, 3.0, None)]
+
+
+def distinct(x):
+    """x with equal values moved apart by ulps (float32 rows whose draws reach far down the ranking, past
+    the device's heap simulation of equal values)"""
+    x = x.copy()
+    for _ in range(16):
+        u, inv, cnt = np.unique(x, return_inverse=True, return_counts=True)
+        if len(u) == len(x):
+            return x
+        for v in np.nonzero(cnt > 1)[0]:
+            idx = np.nonzero(inv == v)[0]
+            for j, i in enumerate(idx[1:]):
+                for _ in range(j + 1):
+                    x[i] = np.nextafter(x[i], np.float32(np.inf))
+    raise AssertionError("could not make the values distinct")
+
+
+def run_unfiltered(BL, steps, rows=None):
+    """Full-vocabulary rows without top-p or min-p at V=151936 (temperature, N(0, sigma^2) logits, rounding):
+    the draw sees only the tempered sum, and the selection drops the candidates whose terms fall below half
+    an ulp of every running sum that can precede them (bounded from the exponent blocks' sums). Large and
+    small sums, a bfloat16 row (draws on equal values near the top) and a near-greedy temperature; the
+    float32 rows hold distinct values."""
+    V = 151936
+    spec = [UNFILT_ROWS[i] for i in (rows if rows is not None else range(len(UNFILT_ROWS)))]
+    R = len(spec)
+    rng = np.random.default_rng(23)
+    ctx = BL.Context(V, R, R)
+    L = O.lib()
+    hs = []
+    for r, (T, _, _) in enumerate(spec):
+        ctx.slot_reset(r, BL.Params(temperature=T), BL.seed_rng(900 + r))
+        op = O.params(temperature=T)
+        hs.append(L.orc_slot_new(O.C.byref(op), BL.seed_rng(900 + r), None, 0, None, 0, None, None, 0))
+    buf = MEM.zeros(R * V, np.float32)
+    try:
+        for t in range(steps):
+            x = np.concatenate([quantize((rng.standard_normal(V) * sg).astype(np.float32), q) if q else
+                                distinct((rng.standard_normal(V) * sg).astype(np.float32)) for (_, sg, q) in spec])
+            buf.upload(x)
+            tok = ctx.sample_step(list(range(R)), buf.ptr, V)[0]
+            for r in range(R):
+                ot, olp = np.zeros(1, np.int32), np.zeros(1, np.float32)
+                oti, otl = np.zeros(1, np.int32), np.zeros(1, np.float32)
+                eog = O.C.c_int()
+                row = np.ascontiguousarray(x[r * V:(r + 1) * V])
+                assert L.orc_slot_step(hs[r], O.fp(row), V, 0, 1, O.ip(ot), O.fp(olp), O.ip(oti), O.fp(otl),
+                                       O.C.byref(eog)) == 0
+                if tok[r] != ot[0]:
+                    return f"step {t} row {r} {spec[r]}: token {tok[r]} vs {ot[0]}"
+    finally:
+        for h in hs:
+            L.orc_slot_free(h)
+        ctx.close()
+    return None
+
+
 def run_pair(BL, ca, cb, steps):
     """Two small cases stepped together in one call (rows 0 and 1 of an odd-length vocabulary: row 1 starts
     at a 4-byte but not 16-byte aligned address)."""
@@ -545,6 +605,9 @@ def main():
             results.append((f"rows {f[1]} + {f[2]}", run_pair(BL, int(f[1]), int(f[2]), int(f[3]) if len(f) > 3 else 10)))
         elif kind == "bigties":
             results.append(("bf16 ties at V=151936", run_bigties(BL, int(f[1]))))
+        elif kind == "unfilt":
+            rows = [int(v) for v in f[2].split(",")] if len(f) > 2 else None
+            results.append(("unfiltered rows at V=151936", run_unfiltered(BL, int(f[1]), rows)))
         elif kind == "bigk":
             results.append(("large top-k / n_probs", run_bigk(BL, int(f[1]))))
         elif kind == "w3":

@@ -4,7 +4,8 @@ top_k 250 with 256 logprob alternatives at V=151936 (38 chunks x 256 candidates 
 list found by radix selection), two small configurations stepped as rows 0 and 1 of an odd-length
 vocabulary (row 1 not 16-byte aligned), small configurations on logits floored to a few integers (thousands
 of ties at each chunk's top-K bound) and on a ramp (the index-order sum crosses a power of two in nearly
-every group), and the bound-rows asynchronous step against the synchronous one."""
+every group), full-vocabulary rows without top-p or min-p (the draw's own candidate cut), and the
+bound-rows asynchronous step against the synchronous one."""
 import os
 import sys
 
@@ -67,6 +68,12 @@ def test_full_vocabulary_ties_heap_order(case, quant):
 def test_bf16_ties_full_vocabulary():
     print("two full-vocabulary rows on bfloat16 logits, V=151936: 10 steps", flush=True)
     err = RP.run_bigties(BL, 10)
+    assert err is None, err
+
+
+def test_unfiltered_full_vocabulary_rows():
+    print("six full-vocabulary rows without top-p / min-p, V=151936: 12 steps", flush=True)
+    err = RP.run_unfiltered(BL, 12)
     assert err is None, err
 
 

@@ -63,6 +63,14 @@ def test_heap_tie_order(simt_lib):
     assert "ok   bf16 ties at V=151936" in out
 
 
+def test_unfiltered_candidate_cut(simt_lib):
+    """Full-vocabulary rows without top-p or min-p at V=151936: the candidates cut at half an ulp of the
+    draw's running sum (six rows, 12 steps; the bfloat16 row's draws on equal values include one whose heap
+    subtree reaches past the dense LDS copy, resolved through the deep-position table)."""
+    out = _run(simt_lib, ["unfilt:12"], {"SIMT_ORDER": "rev"})
+    assert "ok   unfiltered rows at V=151936" in out
+
+
 def test_full_vocabulary_workloads(simt_lib):
     """Workload 2 (the benchmark step), workload 4 (soft-cap, V=262144, top-64 + 20 logprobs) on 2 rows, the
     bound-rows asynchronous step against the synchronous one, two rows of an odd-length vocabulary in one
