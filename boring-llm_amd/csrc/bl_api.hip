@@ -215,8 +215,6 @@ int bl_create(int device, int max_slots, int max_rows, int vocab, bl_ctx **out) 
   d.max_rows = max_rows;
   d.words = (vocab + 31) / 32;
   const size_t V = (size_t)vocab, S = (size_t)max_slots, R = (size_t)max_rows;
-  size_t P2 = 1;
-  while (P2 < V) P2 <<= 1;
   const size_t G = V / 64 + 64;
 #define ALLOC(p, n)                                   \
   do {                                                \
@@ -246,7 +244,7 @@ int bl_create(int device, int max_slots, int max_rows, int vocab, bl_ctx **out) 
   ALLOC(d.full_i, R * d.nb * BL_EB);
   ALLOC(d.full_cnt, R * d.nb);
   ALLOC(d.full_s, R * d.nb);
-  ALLOC(d.sortk, R * std::max(P2, 2 * V));
+  ALLOC(d.sortk, R * 2 * V);
   ALLOC(d.gsum, R * G);
   ALLOC(d.gapx, R * G);
   ALLOC(d.mkey, (size_t)R * BL_KSEL_MAX);

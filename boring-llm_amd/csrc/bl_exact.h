@@ -316,6 +316,25 @@ __device__ __forceinline__ bl_grec bl_group_record(float a, double approx_start,
 }
 
 /*
+ * bl_group_record when the running sum before the group is known to within a relative `margin` of
+ * `approx_start`: if both ends of that interval lie in one binade, the sum starts there and only that
+ * variant is composed (the others read as saturated, which sends a mistaken prediction to the element
+ * level). Otherwise all three.
+ */
+__device__ __forceinline__ bl_grec bl_group_record_pred(float a, double approx_start, double margin, int lane) {
+  const int E = bl_binade_of(approx_start);
+  if (bl_binade_of(approx_start * (1.0 - margin)) == E && bl_binade_of(approx_start * (1.0 + margin)) == E) {
+    bl_grec r;
+    r.E = E;
+    r.pad = 0;
+    r.v[0] = r.v[2] = bl_inc{BL_SAT, BL_SAT};
+    r.v[1] = bl_wave_reduce(bl_term_inc(a, E), lane);
+    return r;
+  }
+  return bl_group_record(a, approx_start, lane);
+}
+
+/*
  * Phase B: sequential-sum walk over n terms in groups of 64, by one wavefront.
  *   term(j)   -> float term j (only called for j < n)
  *   rec(g)    -> bl_grec of group g

@@ -111,7 +111,7 @@ struct bl_dev {
   int32_t *full_i;
   int32_t *full_cnt; /* [rows][nb] candidates in each region */
   double *full_s;    /* [rows][nb] approximate tempered sum over each region (rows without top-p/min-p) */
-  uint64_t *sortk;  /* [rows][2^ceil(log2 V)] global sort scratch */
+  uint64_t *sortk;  /* [rows][2V]: bucketed keys, then the sorted list; the draw's terms in the first half */
   double *gsum;     /* [rows][V/64 + 64] */
   float *gapx;      /* [rows][V/64 + 64] approximate index-order sum before each 64-term group, then the total */
   uint64_t *mkey;   /* [rows][KSEL_MAX] the row's top K order keys, sorted (0: unfilled) */

@@ -22,6 +22,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "bl_exact.h"
 #include "bl_internal.h"
 #include "bl_math.h"
@@ -926,15 +928,28 @@ __device__ void bitonic_desc(uint64_t *s, int P) {
     }
 }
 
-/* Phase A over a list of n terms, records into `recs`, approximate sums through `gsum` */
-template <class TermF>
-__device__ void block_records(int64_t n, TermF term, bl_grec *recs, double *gsum) {
+/* Phase A over a list of n terms term(val(j)), records into `recs`, approximate sums through `gsum`; the
+ * terms are kept in `tbuf` for the walks. A record composes only the predicted binade's variant when the
+ * float running sum before its group, g*64 terms, is within g*64*2^-24 (recursive summation bound, with
+ * a 1% margin) of the approximate prefix and that interval lies in one binade. */
+template <class ValF, class TermF>
+__device__ void block_records(int64_t n, ValF val, TermF term, bl_grec *recs, double *gsum, float *tbuf) {
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int64_t G = (n + 63) / 64;
+  /* each loop loads the next group's inputs before this group's stores: global stores share the
+   * in-order load counter, so a load issued after a store would wait for the store as well */
+  auto vload = [&](int64_t g) -> float {
+    const int64_t j = g * 64 + lane;
+    return g < G && j < n ? val(j) : 0.0f;
+  };
+  float vn = vload(w);
   for (int64_t g = w; g < G; g += SEL_NW) {
-    int64_t j = g * 64 + lane;
-    float a = j < n ? term(j) : 0.0f;
-    double sg = bl_wave_sum_d((double)a);
+    const float vc = vn;
+    vn = vload(g + SEL_NW);
+    const bool in = g * 64 + lane < n;
+    const float a = in ? term(vc) : 0.0f;
+    if (in) tbuf[g * 64 + lane] = a;
+    const double sg = bl_wave_sum_d((double)a);
     if (lane == 0) gsum[g] = sg;
   }
   __syncthreads();
@@ -950,10 +965,20 @@ __device__ void block_records(int64_t n, TermF term, bl_grec *recs, double *gsum
     }
   }
   __syncthreads();
+  /* a group's terms were stored by this same lane */
+  auto aload = [&](int64_t g) -> float {
+    const int64_t j = g * 64 + lane;
+    return g < G && j < n ? tbuf[j] : 0.0f;
+  };
+  float an = aload(w);
+  double sn = w < G ? gsum[w] : 0.0;
   for (int64_t g = w; g < G; g += SEL_NW) {
-    int64_t j = g * 64 + lane;
-    float a = j < n ? term(j) : 0.0f;
-    bl_grec r = bl_group_record(a, gsum[g], lane);
+    const float a = an;
+    const double sc = sn;
+    an = aload(g + SEL_NW);
+    sn = g + SEL_NW < G ? gsum[g + SEL_NW] : 0.0;
+    const double margin = (double)(g * 64) * 0x1.02p-24 + 0x1p-40;
+    bl_grec r = bl_group_record_pred(a, sc, margin, lane);
     if (lane == 0) recs[g] = r;
   }
   __syncthreads();
@@ -1000,7 +1025,10 @@ struct sel_shared {
   float red_m[SEL_NW];
   int red_i[SEL_NW];
   int32_t eog[BL_EOG_LDS];             /* the first end-of-generation ids */
+  uint64_t etab[BL_EXP2_N];            /* expf's 2^(i/32) table (a global table read is a dependent load) */
 };
+/* expf through the selection's LDS copy of the table */
+#define SEL_EXPF(x) bl_expf_tab((x), [&](uint32_t i_) { return sh.etab[i_]; })
 
 /* sample_candidates_with_probs (src/sampling.br:490-607) for T > 0: the stages without a device path, and
  * a min_keep that reaches past the materialised list, leave the row unsupported */
@@ -1015,16 +1043,17 @@ __device__ __forceinline__ bool ranked_supported(const bl_slot_dev &sp, int64_t 
 /* a short ranked list (n_list <= BL_SERIAL_MAX), by every thread: the terms exp(v - v0) of the untempered
  * softmax (with top-p or min-p) and exp((v - v0) / T) of the draw */
 template <class ValF>
-__device__ void ranked_terms(const bl_slot_dev &sp, ValF val, int64_t n_list, float *ser_e, float *ser_r) {
+__device__ void ranked_terms(const bl_slot_dev &sp, ValF val, int64_t n_list, float *ser_e, float *ser_r,
+                             const sel_shared &sh) {
   const float T = sp.temperature;
   const bool filt = sp.top_p < 1.0f || sp.min_p > 0.0f;
   const float v0 = val(0);
   for (int j = threadIdx.x; j < n_list; j += BL_SEL_THREADS) {
     const float x = val(j);
-    ser_e[j] = filt ? bl_expf(x - v0) : 0.0f;
+    ser_e[j] = filt ? SEL_EXPF(x - v0) : 0.0f;
     const float dd = x - v0;
     const float q = dd / T;
-    ser_r[j] = bl_expf(q);
+    ser_r[j] = SEL_EXPF(q);
   }
 }
 
@@ -1098,29 +1127,28 @@ __device__ int ranked_serial(const bl_slot_dev &sp, int n, int64_t n_logical, in
  */
 template <class ValF>
 __device__ int sample_ranked_long(const bl_slot_dev &sp, ValF val, int64_t n_list, int64_t n_logical, int64_t keep,
-                                  uint64_t &rng, int rng_skip, bl_grec *recs, double *gsum, sel_shared &sh,
-                                  int &status) {
+                                  uint64_t &rng, int rng_skip, bl_grec *recs, double *gsum, float *tbuf,
+                                  sel_shared &sh, int &status) {
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   const float T = sp.temperature;
   const float v0 = val(0);
   int64_t cutoff = n_logical;
   if (sp.top_p < 1.0f || sp.min_p > 0.0f) {
-    auto termE = [&](int64_t j) { return bl_expf(val(j) - v0); };
-    block_records(n_list, termE, recs, gsum);
+    block_records(n_list, val, [&](float v) { return SEL_EXPF(v - v0); }, recs, gsum, tbuf);
     if (w == 0) {
       float S;
-      bl_seq_walk(n_list, termE, [&](int64_t g) { return recs[g]; }, false, 0.0f, 0, S, lane);
+      bl_seq_walk(n_list, [&](int64_t j) { return tbuf[j]; }, [&](int64_t g) { return recs[g]; }, false, 0.0f, 0, S, lane);
       if (lane == 0) sh.fres[0] = S;
     }
     __syncthreads();
     const float sum_exp = sh.fres[0];
     __syncthreads();
-    auto termP = [&](int64_t j) { return bl_expf(val(j) - v0) / sum_exp; };
+    auto termP = [&](int64_t j) { return SEL_EXPF(val(j) - v0) / sum_exp; };
     if (sp.top_p < 1.0f) {
-      block_records(n_list, termP, recs, gsum);
+      block_records(n_list, val, [&](float v) { return SEL_EXPF(v - v0) / sum_exp; }, recs, gsum, tbuf);
       if (w == 0) {
         float S;
-        int f = bl_seq_walk(n_list, termP, [&](int64_t g) { return recs[g]; }, true, sp.top_p, keep - 1, S, lane);
+        int f = bl_seq_walk(n_list, [&](int64_t j) { return tbuf[j]; }, [&](int64_t g) { return recs[g]; }, true, sp.top_p, keep - 1, S, lane);
         if (lane == 0) sh.ires[0] = f;
       }
       __syncthreads();
@@ -1153,21 +1181,22 @@ __device__ int sample_ranked_long(const bl_slot_dev &sp, ValF val, int64_t n_lis
   }
   if (status) return -1;
   const int64_t n_eff = cutoff < n_list ? cutoff : n_list;
-  auto termR = [&](int64_t j) {
-    float dd = val(j) - v0;
+  auto termRv = [&](float v) {
+    float dd = v - v0;
     float q = dd / T;
-    return bl_expf(q);
+    return SEL_EXPF(q);
   };
-  block_records(n_eff, termR, recs, gsum);
+  block_records(n_eff, val, termRv, recs, gsum, tbuf);
+  auto termT = [&](int64_t j) { return tbuf[j]; };
   if (w == 0) {
     float S;
-    bl_seq_walk(n_eff, termR, [&](int64_t g) { return recs[g]; }, false, 0.0f, 0, S, lane);
+    bl_seq_walk(n_eff, termT, [&](int64_t g) { return recs[g]; }, false, 0.0f, 0, S, lane);
     uint64_t st = rng;
     for (int k = 0; k < rng_skip; k++) st = bl_xorshift(st);
     float r01 = bl_rng_f32(&st);
     float target = r01 * S;
     float S2;
-    int f = bl_seq_walk(n_eff, termR, [&](int64_t g) { return recs[g]; }, true, target, 0, S2, lane);
+    int f = bl_seq_walk(n_eff, termT, [&](int64_t g) { return recs[g]; }, true, target, 0, S2, lane);
     if (lane == 0) {
       sh.ires[2] = f >= 0 ? f : (int)(cutoff - 1);
       sh.fres[1] = S;
@@ -1335,7 +1364,7 @@ __device__ void norm_prep(const bl_dev &d, int row, float M, sel_shared &sh, uin
       const int g = nm.crit[ci];
       const int64_t j = (int64_t)g * 64 + lane;
       const bool in = j < V;
-      const float a = in ? bl_expf(eff[j] - M) : 0.0f;
+      const float a = in ? SEL_EXPF(eff[j] - M) : 0.0f;
       const int e0 = rec[g].E, e1 = bl_binade_of((double)apx[g + 1]);
       nm.terms[ci * 64 + lane] = a;
       nm.cp[ci * 64 + lane] = bl_wave_scan(in ? bl_term_inc(a, e0) : bl_inc_ident(), lane);
@@ -1380,7 +1409,7 @@ __device__ void norm_chain(const bl_dev &d, int row, float M, sel_shared &sh) {
   auto run_hi = [&](int r) { return r == ncrit ? G : crit_of(r); };
   int e = BL_E_MIN;
   uint32_t N = 0u;
-  auto term = [&](int64_t j) { return bl_expf(eff[j] - M); };
+  auto term = [&](int64_t j) { return SEL_EXPF(eff[j] - M); };
   /* a record holds its own binade only: a neighbouring binade reads as saturated (element level) */
   auto recf = [&](int64_t g) {
     const bl_grec1 r1 = rec[g];
@@ -1629,6 +1658,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
   const int32_t ring_old = (t == 0 && rows.commit && ring_full) ? d.ring[(int64_t)slot * BL_WCAP + win_head] : 0;
   const int n_eog = d.n_eog;
   if (t < n_eog && t < BL_EOG_LDS) sh.eog[t] = d.eog[t];
+  if (t < BL_EXP2_N) sh.etab[t] = bl_exp2_tab[t];
   __syncthreads();
   M = sh.red_m[0];
   Mi = sh.red_i[0];
@@ -1752,24 +1782,46 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
       };
       for (int b = t; b < BL_NBUCKET; b += BL_SEL_THREADS) cnt[b] = 0u;
       __syncthreads();
-      /* wavefront w reads regions w, w + SEL_NW, ...; each lane keeps BL_CAND_U loads in flight */
-      auto each_region = [&](auto f) {
-        for (int bb = w; bb < NB; bb += SEL_NW) {
-          const int c = boff[bb + 1] - boff[bb];
-          const float *pv = fv + (int64_t)bb * BL_EB;
-          const int32_t *pi = fi + (int64_t)bb * BL_EB;
-          for (int j0 = 0; j0 < c; j0 += 64 * BL_CAND_U) {
-            float v[BL_CAND_U];
-#pragma unroll
-            for (int u = 0; u < BL_CAND_U; u++) {
-              const int j = j0 + lane + 64 * u;
-              v[u] = j < c ? pv[j] : BL_NEG_INF;
-            }
-            f(v, pi + j0 + lane);
-          }
+      /* wavefront w reads regions w, w + SEL_NW, ... in batches of 64 * BL_CAND_U candidates; each lane
+       * keeps BL_CAND_U loads (values, and ids when asked) in flight, the next batch's issued before this
+       * batch's stores (stores share the in-order load counter) */
+      auto next_batch = [&](int &bb, int &j0) {
+        j0 += 64 * BL_CAND_U;
+        while (bb < NB && j0 >= boff[bb + 1] - boff[bb]) {
+          bb += SEL_NW;
+          j0 = 0;
         }
       };
-      each_region([&](const float *v, const int32_t *) {
+      auto each_region = [&](auto with_id, auto f) {
+        constexpr bool WID = decltype(with_id)::value;
+        float v[BL_CAND_U], vn[BL_CAND_U];
+        int32_t id[BL_CAND_U], idn[BL_CAND_U];
+        auto load = [&](int bb, int j0, float *vv, int32_t *ii) {
+          const int c = bb < NB ? boff[bb + 1] - boff[bb] : 0;
+          const float *pv = fv + (int64_t)bb * BL_EB;
+          const int32_t *pi = fi + (int64_t)bb * BL_EB;
+#pragma unroll
+          for (int u = 0; u < BL_CAND_U; u++) {
+            const int j = j0 + lane + 64 * u;
+            vv[u] = j < c ? pv[j] : BL_NEG_INF;
+            if (WID) ii[u] = j < c ? pi[j] : 0;
+          }
+        };
+        int bb = w, j0 = -64 * BL_CAND_U;
+        next_batch(bb, j0);
+        load(bb, j0, vn, idn);
+        while (bb < NB) {
+#pragma unroll
+          for (int u = 0; u < BL_CAND_U; u++) {
+            v[u] = vn[u];
+            id[u] = idn[u];
+          }
+          next_batch(bb, j0);
+          load(bb, j0, vn, idn);
+          f(v, id);
+        }
+      };
+      each_region(std::false_type{}, [&](const float *v, const int32_t *) {
 #pragma unroll
         for (int u = 0; u < BL_CAND_U; u++)
           if (v[u] >= thr) atomicAdd(&cnt[bucket(v[u])], 1u);
@@ -1798,26 +1850,29 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
         run += loc[q];
       }
       __syncthreads();
-      each_region([&](const float *v, const int32_t *pi) {
-        int32_t id[BL_CAND_U];
-#pragma unroll
-        for (int u = 0; u < BL_CAND_U; u++) id[u] = v[u] >= thr ? pi[64 * u] : 0;
+      each_region(std::true_type{}, [&](const float *v, const int32_t *id) {
 #pragma unroll
         for (int u = 0; u < BL_CAND_U; u++)
           if (v[u] >= thr) A[atomicAdd(&cnt[bucket(v[u])], 1u)] = ckey(v[u], id[u]);
       });
       __syncthreads(); /* cnt[b] is now the end of bucket b */
       uint64_t *tile = reinterpret_cast<uint64_t *>(reinterpret_cast<char *>(&sh.n) + BL_BOFF_BYTES);
+      constexpr int TU = BL_RTILE / BL_SEL_THREADS;
+      uint64_t pre[TU]; /* the next tile, loaded before this tile's stores */
+#pragma unroll
+      for (int u = 0; u < TU; u++) pre[u] = t + u * BL_SEL_THREADS < nk ? A[t + u * BL_SEL_THREADS] : 0ull;
       for (int base = 0; base < nk; base += BL_RTILE) {
         const int n_t = min(BL_RTILE, nk - base);
 #pragma unroll
-        for (int u = 0; u < BL_RTILE / BL_SEL_THREADS; u++) {
-          const int i = t + u * BL_SEL_THREADS;
-          if (i < n_t) tile[i] = A[base + i];
-        }
+        for (int u = 0; u < TU; u++) tile[t + u * BL_SEL_THREADS] = pre[u];
         __syncthreads();
 #pragma unroll
-        for (int u = 0; u < BL_RTILE / BL_SEL_THREADS; u++) {
+        for (int u = 0; u < TU; u++) {
+          const int i = base + BL_RTILE + t + u * BL_SEL_THREADS;
+          pre[u] = i < nk ? A[i] : 0ull;
+        }
+#pragma unroll
+        for (int u = 0; u < TU; u++) {
           const int i = t + u * BL_SEL_THREADS;
           if (i < n_t) {
             const uint64_t k = tile[i];
@@ -1846,7 +1901,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
   const bool short_list = n_list <= BL_SERIAL_MAX;
   if (sampled) {
     if (!ranked_supported(sp, n_list, n_logical, keep)) status |= BL_SE_UNSUPPORTED;
-    if (!status && short_list) ranked_terms(sp, val, n_list, sh.ser_e, sh.ser_r);
+    if (!status && short_list) ranked_terms(sp, val, n_list, sh.ser_e, sh.ser_r, sh);
   }
 
   if (gram) {
@@ -1910,7 +1965,8 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
         recs = reinterpret_cast<bl_grec *>(d.grec) + (int64_t)row * 2 * (V / 64 + 64) + (V / 64 + 64);
         gsum = d.gsum + (int64_t)row * (V / 64 + 64);
       }
-      pos = sample_ranked_long(sp, val, n_list, n_logical, keep, rng, skip, recs, gsum, sh, status);
+      float *tbuf = reinterpret_cast<float *>(d.sortk + (int64_t)row * 2 * V); /* free once the list is sorted */
+      pos = sample_ranked_long(sp, val, n_list, n_logical, keep, rng, skip, recs, gsum, tbuf, sh, status);
     }
     if (pos >= 0) {
       const uint64_t kp = keys[pos];
