@@ -370,7 +370,8 @@ static int configure(const bl_ctx *c, const bl_params *p, bl_slot_dev &s) {
   if (p->temperature <= 0.0f) mode |= BL_M_GREEDY;
   else if (p->top_k > 0 && p->top_k < V) mode |= BL_M_TOPK;
   else mode |= BL_M_FULL;
-  if (p->logprobs) mode |= BL_M_LOGPROBS;
+  /* logprobs: the effective logits' normaliser and top n_probs, or the draw's own probabilities */
+  if (p->logprobs) mode |= p->post_sampling_probs ? BL_M_PSP : BL_M_LOGPROBS;
   s.mode = mode;
   int k = 0;
   if (mode & BL_M_TOPK) k = p->top_k;
@@ -381,11 +382,8 @@ static int configure(const bl_ctx *c, const bl_params *p, bl_slot_dev &s) {
   if (p->dry_multiplier != 0.0f && p->dry_base >= 1.0f && p->dry_penalty_last_n != 0)
     return fail(BL_EUNSUPPORTED, "DRY is not supported on the device");
   if (p->temperature > 0.0f && p->typical_p < 1.0f) return fail(BL_EUNSUPPORTED, "typical_p is not supported on the device");
-  if (p->temperature > 0.0f && p->xtc_probability > 0.0f && p->xtc_threshold <= 0.5f)
-    return fail(BL_EUNSUPPORTED, "XTC is not supported on the device");
   if (p->temperature > 0.0f && p->dynatemp_range > 0.0f)
     return fail(BL_EUNSUPPORTED, "dynamic temperature is not supported on the device");
-  if (p->post_sampling_probs) return fail(BL_EUNSUPPORTED, "post_sampling_probs is not supported on the device");
   if (k > BL_KSEL_MAX)
     return fail(BL_EUNSUPPORTED, "top_k/n_probs of %d exceeds the device selection limit", k);
   if (p->repeat_last_n > BL_WCAP) return fail(BL_EUNSUPPORTED, "repeat_last_n above %d", BL_WCAP);
@@ -813,6 +811,9 @@ int bl_spec_verify(bl_ctx *c, const int32_t *slots, int B, int k, const float *d
     if (k > 0 && (s.fp_on || s.rep_on))
       return fail(BL_EUNSUPPORTED, "speculative rows with history-dependent penalties are not supported on the device");
     if (s.g_on) return fail(BL_EUNSUPPORTED, "speculative rows of a grammar-constrained slot are not supported on the device");
+    /* each row's draw starts at its position in the RNG chain; an XTC chance draw would shift the rest */
+    if (k > 0 && s.temperature > 0.0f && s.xtc_probability > 0.0f && s.xtc_threshold <= 0.5f)
+      return fail(BL_EUNSUPPORTED, "speculative rows with XTC are not supported on the device");
   }
   hipSetDevice(c->device);
   for (int b = 0; b < B; b++)

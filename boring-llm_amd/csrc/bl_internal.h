@@ -48,6 +48,7 @@
 #define BL_M_FULL 4
 #define BL_M_LOGPROBS 8
 #define BL_M_GRAMMAR 16
+#define BL_M_PSP 32 /* logprobs as post-sampling probabilities (src/server.br:1015-1025) */
 
 /* grammar mask kernel: tokens per workgroup */
 #define BL_GM_THREADS 256
@@ -153,6 +154,27 @@ struct bl_rows {
 #if defined(__HIPCC__)
 __device__ __forceinline__ int bl_row_slot(const bl_rows &r, int row) {
   return row < BL_ROWS_INLINE ? (int)r.slot_inline[row] : r.slot[row];
+}
+
+/* XTC runs (src/sampling.br:552-572): it draws its chance whenever the candidates reach two */
+__device__ __forceinline__ bool bl_xtc_on(const bl_slot_dev &sp) {
+  return sp.xtc_probability > 0.0f && sp.xtc_threshold <= 0.5f;
+}
+/* the untempered softmax is formed (top-p, min-p or XTC read it) */
+__device__ __forceinline__ bool bl_probs_on(const bl_slot_dev &sp) {
+  return sp.top_p < 1.0f || sp.min_p > 0.0f || bl_xtc_on(sp);
+}
+/* A full-vocabulary rank's candidates: every value within this span of the row maximum. Past it a term
+ * exp(v - v0) (untempered, when formed) or exp((v - v0) / T) of the draw is below 2^-25 of the first
+ * term, too small to change a float32 sum that holds the first term (17.5 > 25 ln 2). The span is
+ * 17.5 max(T, 1) when the untempered softmax is formed and 17.5 T otherwise. XTC may start the draw at a
+ * later candidate v_first, whose probability, at least the threshold, puts it within -ln(threshold)
+ * (+0.05 for the rounding of the probabilities and their sum) of the maximum: the span grows by that. */
+__device__ __forceinline__ float bl_cand_span(const bl_slot_dev &sp) {
+  const float T = sp.temperature;
+  float span = 17.5f * (bl_probs_on(sp) && T < 1.0f ? 1.0f : T);
+  if (bl_xtc_on(sp)) span = sp.xtc_threshold > 1.0e-30f ? span + (-__logf(sp.xtc_threshold) + 0.05f) : 3.0e38f;
+  return span;
 }
 
 /* appends token `tok`'s bytes to the slot's grammar position (reply_tokens.push of a non-EOG token,

@@ -776,14 +776,13 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_exppass(bl_dev d, bl_rows 
     }
   }
   if (mode & BL_M_FULL) {
-    /* candidates of a full-vocabulary rank: every value within 17.5*span of the maximum, where span is
-     * max(T, 1) when top-p or min-p read the untempered softmax and T otherwise (only the tempered sum is
-     * formed then). The block writes them in index order to its own BL_EB-entry region, and their count:
-     * no counter is shared between workgroups (one would serialise device-scope atomics across XCDs) */
+    /* candidates of a full-vocabulary rank (within bl_cand_span of the maximum). The block writes them
+     * in index order to its own BL_EB-entry region, and their count: no counter is shared between
+     * workgroups (one would serialise device-scope atomics across XCDs) */
     __shared__ int f_w[BL_RP_THREADS / 64];
     const float T = sp.temperature;
-    const bool filt = sp.top_p < 1.0f || sp.min_p > 0.0f;
-    const float thr = M - 17.5f * (filt && T < 1.0f ? 1.0f : T);
+    const bool filt = bl_probs_on(sp);
+    const float thr = M - bl_cand_span(sp);
     int mine = 0;
 #pragma unroll
     for (int k = 0; k < 4; k++) mine += (j0 + k < cnt && x[k] >= thr) ? 1 : 0;
@@ -1014,12 +1013,22 @@ struct sel_cand {
 #define BL_CAND_U 8   /* candidate loads in flight per lane */
 static_assert(BL_BOFF_BYTES + BL_RTILE * 8 <= sizeof(sel_norm), "rank tile");
 static_assert(BL_RTILE % BL_SEL_THREADS == 0, "rank tile");
+/* the draw of a ranked list: the chosen position (-2: a cut would need a candidate past the materialised
+ * list), the drawn range [first, cut) and its renormalised sum, whose terms the list's term array holds
+ * from `first` (src/sampling.br:576-607) */
+struct sel_draw {
+  int pos, first, cut;
+  float S;
+};
+
 struct sel_shared {
   sel_norm n; /* both live at once: the normaliser's chain runs beside the draw */
   sel_cand c;
   uint64_t rng_out;                    /* the RNG state after a draw */
   float ser_e[BL_SERIAL_MAX];          /* short-list terms exp(v - v0) */
-  float ser_r[BL_SERIAL_MAX];          /* short-list terms exp((v - v0) / T) */
+  float ser_r[BL_SERIAL_MAX];          /* short-list terms exp((v - v0) / T), from the draw's first candidate */
+  float ser_v[BL_SERIAL_MAX];          /* short-list values */
+  sel_draw draw;                        /* the draw's range and sum */
   float fres[8];
   int ires[8];
   float red_m[SEL_NW];
@@ -1036,37 +1045,39 @@ __device__ __forceinline__ bool ranked_supported(const bl_slot_dev &sp, int64_t 
                                                  int64_t &keep) {
   keep = sp.min_keep > 1 ? sp.min_keep : 1;
   if (keep > n_logical) keep = n_logical;
-  return !(sp.typical_p < 1.0f || (sp.xtc_probability > 0.0f && sp.xtc_threshold <= 0.5f) ||
-           sp.dynatemp_range > 0.0f || keep > n_list);
+  return !(sp.typical_p < 1.0f || sp.dynatemp_range > 0.0f || keep > n_list);
 }
 
-/* a short ranked list (n_list <= BL_SERIAL_MAX), by every thread: the terms exp(v - v0) of the untempered
- * softmax (with top-p or min-p) and exp((v - v0) / T) of the draw */
+/* a short ranked list (n_list <= BL_SERIAL_MAX), by every thread: the values, the terms exp(v - v0) of
+ * the untempered softmax (when formed) and exp((v - v0) / T) of the draw */
 template <class ValF>
-__device__ void ranked_terms(const bl_slot_dev &sp, ValF val, int64_t n_list, float *ser_e, float *ser_r,
-                             const sel_shared &sh) {
+__device__ void ranked_terms(const bl_slot_dev &sp, ValF val, int64_t n_list, sel_shared &sh) {
   const float T = sp.temperature;
-  const bool filt = sp.top_p < 1.0f || sp.min_p > 0.0f;
+  const bool filt = bl_probs_on(sp);
   const float v0 = val(0);
   for (int j = threadIdx.x; j < n_list; j += BL_SEL_THREADS) {
     const float x = val(j);
-    ser_e[j] = filt ? SEL_EXPF(x - v0) : 0.0f;
+    sh.ser_v[j] = x;
+    sh.ser_e[j] = filt ? SEL_EXPF(x - v0) : 0.0f;
     const float dd = x - v0;
     const float q = dd / T;
-    ser_r[j] = SEL_EXPF(q);
+    sh.ser_r[j] = SEL_EXPF(q);
   }
 }
 
 /* ... then the reference's sequential float32 loops over those terms, by one thread: softmax sum, top-p
- * prefix, min-p cut, tempered sum and the draw. Returns the chosen position, or -2 when the cut would need
- * a candidate past the materialised list; *rng_out = the state after the draw */
-__device__ int ranked_serial(const bl_slot_dev &sp, int n, int64_t n_logical, int64_t keep, uint64_t rng,
-                             int rng_skip, const float *ser_e, const float *ser_r, uint64_t *rng_out) {
-  const bool filt = sp.top_p < 1.0f || sp.min_p > 0.0f;
+ * prefix, min-p cut, XTC, tempered sum and the draw (src/sampling.br:505-607); *rng_out = the state after
+ * the draw */
+__device__ sel_draw ranked_serial(const bl_slot_dev &sp, int n, int64_t n_logical, int64_t keep, uint64_t rng,
+                                 int rng_skip, sel_shared &sh, uint64_t *rng_out) {
+  const float *ser_e = sh.ser_e, *ser_v = sh.ser_v;
+  float *ser_r = sh.ser_r;
+  const bool xtc = bl_xtc_on(sp);
+  const bool filt = bl_probs_on(sp);
   int64_t cut = n_logical;
   bool unsup = false;
+  float sum_exp = 0.0f;
   if (filt) {
-    float sum_exp = 0.0f;
     for (int j = 0; j < n; j++) sum_exp += ser_e[j];
     if (sp.top_p < 1.0f) {
       float cum = 0.0f;
@@ -1100,15 +1111,38 @@ __device__ int ranked_serial(const bl_slot_dev &sp, int n, int64_t n_logical, in
       cut = keep > first_small ? keep : first_small;
     }
   }
-  const int n_eff = (int)(cut < n ? cut : n);
-  float S = 0.0f;
-  for (int j = 0; j < n_eff; j++) S += ser_r[j];
   uint64_t st = rng;
   for (int k = 0; k < rng_skip; k++) st = bl_xorshift(st);
+  int first = 0;
+  if (xtc && cut >= 2) {
+    const float chance = bl_rng_f32(&st);
+    if (chance <= sp.xtc_probability) {
+      /* the sum of the probabilities before the cut, then the last of the leading run at or above the
+       * threshold (candidates past the materialised list are below it, by the candidate span) */
+      const int64_t lim = cut < n ? cut : n;
+      float xs = 0.0f;
+      for (int64_t i = 0; i < lim; i++) xs += ser_e[i] / sum_exp;
+      int64_t pos_last = 0;
+      for (int64_t i = 0; i < lim && (ser_e[i] / sum_exp) / xs >= sp.xtc_threshold; i++) pos_last = i;
+      if (pos_last > 0 && cut - pos_last >= keep) first = (int)pos_last;
+    }
+  }
+  const int n_eff = (int)(cut < n ? cut : n);
+  if (first > 0) {
+    /* the draw's terms from the new first candidate */
+    const float vf = ser_v[first], T = sp.temperature;
+    for (int j = first; j < n_eff; j++) {
+      const float dd = ser_v[j] - vf;
+      const float q = dd / T;
+      ser_r[j] = SEL_EXPF(q);
+    }
+  }
+  float S = 0.0f;
+  for (int j = first; j < n_eff; j++) S += ser_r[j];
   const float target = bl_rng_f32(&st) * S;
   float run = 0.0f;
   int64_t f = -1;
-  for (int j = 0; j < n_eff; j++) {
+  for (int j = first; j < n_eff; j++) {
     run += ser_r[j];
     if (run >= target) {
       f = j;
@@ -1116,39 +1150,53 @@ __device__ int ranked_serial(const bl_slot_dev &sp, int n, int64_t n_logical, in
     }
   }
   *rng_out = st;
-  return unsup ? -2 : (int)(f >= 0 ? f : cut - 1);
+  sel_draw r;
+  r.pos = unsup ? -2 : (int)(f >= 0 ? f : cut - 1);
+  r.first = first;
+  r.cut = (int)cut;
+  r.S = S;
+  return r;
 }
 
 /*
  * A long ranked list (more than BL_SERIAL_MAX entries) by the whole block: the sequential sums of
  * sample_candidates_with_probs (src/sampling.br:490-607) through the exact-sum records. n_list entries are
  * materialised; n_logical >= n_list is the reference's candidate count, the entries past n_list being too
- * small to change any float32 sum. Returns the chosen position, or -1 with `status` set.
+ * small to change any float32 sum. Returns the draw (pos -1 with `status` set on failure); `tbuf` then
+ * holds the draw's terms from its first candidate (tbuf[j - first]).
  */
 template <class ValF>
-__device__ int sample_ranked_long(const bl_slot_dev &sp, ValF val, int64_t n_list, int64_t n_logical, int64_t keep,
-                                  uint64_t &rng, int rng_skip, bl_grec *recs, double *gsum, float *tbuf,
-                                  sel_shared &sh, int &status) {
+__device__ sel_draw sample_ranked_long(const bl_slot_dev &sp, ValF val, int64_t n_list, int64_t n_logical,
+                                      int64_t keep, uint64_t &rng, int rng_skip, bl_grec *recs, double *gsum,
+                                      float *tbuf, sel_shared &sh, int &status) {
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   const float T = sp.temperature;
   const float v0 = val(0);
+  const bool xtc = bl_xtc_on(sp);
   int64_t cutoff = n_logical;
-  if (sp.top_p < 1.0f || sp.min_p > 0.0f) {
+  float sum_exp = 1.0f;
+  auto termPv = [&](float v) { return SEL_EXPF(v - v0) / sum_exp; };
+  auto termS = [&](int64_t j) { return tbuf[j]; };
+  sel_draw out;
+  out.pos = -1;
+  out.first = 0;
+  out.cut = 0;
+  out.S = 0.0f;
+  if (bl_probs_on(sp)) {
     block_records(n_list, val, [&](float v) { return SEL_EXPF(v - v0); }, recs, gsum, tbuf);
     if (w == 0) {
       float S;
-      bl_seq_walk(n_list, [&](int64_t j) { return tbuf[j]; }, [&](int64_t g) { return recs[g]; }, false, 0.0f, 0, S, lane);
+      bl_seq_walk(n_list, termS, [&](int64_t g) { return recs[g]; }, false, 0.0f, 0, S, lane);
       if (lane == 0) sh.fres[0] = S;
     }
     __syncthreads();
-    const float sum_exp = sh.fres[0];
+    sum_exp = sh.fres[0];
     __syncthreads();
-    auto termP = [&](int64_t j) { return SEL_EXPF(val(j) - v0) / sum_exp; };
     if (sp.top_p < 1.0f) {
-      block_records(n_list, val, [&](float v) { return SEL_EXPF(v - v0) / sum_exp; }, recs, gsum, tbuf);
+      block_records(n_list, val, termPv, recs, gsum, tbuf);
       if (w == 0) {
         float S;
-        int f = bl_seq_walk(n_list, [&](int64_t j) { return tbuf[j]; }, [&](int64_t g) { return recs[g]; }, true, sp.top_p, keep - 1, S, lane);
+        int f = bl_seq_walk(n_list, termS, [&](int64_t g) { return recs[g]; }, true, sp.top_p, keep - 1, S, lane);
         if (lane == 0) sh.ires[0] = f;
       }
       __syncthreads();
@@ -1156,14 +1204,14 @@ __device__ int sample_ranked_long(const bl_slot_dev &sp, ValF val, int64_t n_lis
       __syncthreads();
     }
     if (sp.min_p > 0.0f) {
-      const float p0 = termP(0);
+      const float p0 = termPv(v0);
       const float threshold = p0 * sp.min_p;
       /* first j in [keep, cutoff) with probs[j] < threshold */
       if (t == 0) sh.ires[1] = 0x7fffffff;
       __syncthreads();
       int64_t lim = cutoff < n_list ? cutoff : n_list;
       for (int64_t j = keep + t; j < lim; j += blockDim.x)
-        if (termP(j) < threshold) atomicMin(&sh.ires[1], (int)j);
+        if (termPv(val(j)) < threshold) atomicMin(&sh.ires[1], (int)j);
       __syncthreads();
       int64_t first_small = sh.ires[1];
       if (first_small == 0x7fffffff) {
@@ -1179,26 +1227,56 @@ __device__ int sample_ranked_long(const bl_slot_dev &sp, ValF val, int64_t n_lis
       __syncthreads();
     }
   }
-  if (status) return -1;
+  if (status) return out;
+  /* the RNG after the rows drawn before this one, then XTC's chance (every thread) */
+  uint64_t st = rng;
+  for (int k = 0; k < rng_skip; k++) st = bl_xorshift(st);
+  int64_t first = 0;
+  if (xtc && cutoff >= 2) {
+    const float chance = bl_rng_f32(&st);
+    if (chance <= sp.xtc_probability) {
+      /* the sum of the probabilities before the cut (candidates past the list add nothing), then the
+       * last of the leading run at or above the threshold (past the list all are below it) */
+      const int64_t nx = cutoff < n_list ? cutoff : n_list;
+      block_records(nx, val, termPv, recs, gsum, tbuf);
+      if (w == 0) {
+        float S;
+        bl_seq_walk(nx, termS, [&](int64_t g) { return recs[g]; }, false, 0.0f, 0, S, lane);
+        if (lane == 0) {
+          sh.fres[2] = S;
+          sh.ires[1] = 0x7fffffff;
+        }
+      }
+      __syncthreads();
+      const float xs = sh.fres[2];
+      for (int64_t j = t; j < nx; j += blockDim.x)
+        if (!(tbuf[j] / xs >= sp.xtc_threshold)) atomicMin(&sh.ires[1], (int)j);
+      __syncthreads();
+      const int64_t ff = sh.ires[1] == 0x7fffffff ? nx : sh.ires[1];
+      const int64_t pos_last = ff > 0 ? ff - 1 : 0;
+      if (pos_last > 0 && cutoff - pos_last >= keep) first = pos_last;
+      __syncthreads();
+    }
+  }
   const int64_t n_eff = cutoff < n_list ? cutoff : n_list;
+  const int64_t m = n_eff - first;
+  const float vf = val(first);
+  auto valF = [&](int64_t j) { return val(first + j); };
   auto termRv = [&](float v) {
-    float dd = v - v0;
+    float dd = v - vf;
     float q = dd / T;
     return SEL_EXPF(q);
   };
-  block_records(n_eff, val, termRv, recs, gsum, tbuf);
-  auto termT = [&](int64_t j) { return tbuf[j]; };
+  block_records(m, valF, termRv, recs, gsum, tbuf);
   if (w == 0) {
     float S;
-    bl_seq_walk(n_eff, termT, [&](int64_t g) { return recs[g]; }, false, 0.0f, 0, S, lane);
-    uint64_t st = rng;
-    for (int k = 0; k < rng_skip; k++) st = bl_xorshift(st);
+    bl_seq_walk(m, termS, [&](int64_t g) { return recs[g]; }, false, 0.0f, 0, S, lane);
     float r01 = bl_rng_f32(&st);
     float target = r01 * S;
     float S2;
-    int f = bl_seq_walk(n_eff, termT, [&](int64_t g) { return recs[g]; }, true, target, 0, S2, lane);
+    int f = bl_seq_walk(m, termS, [&](int64_t g) { return recs[g]; }, true, target, 0, S2, lane);
     if (lane == 0) {
-      sh.ires[2] = f >= 0 ? f : (int)(cutoff - 1);
+      sh.ires[2] = f >= 0 ? (int)(first + f) : (int)(cutoff - 1);
       sh.fres[1] = S;
       sh.rng_out = st;
     }
@@ -1206,12 +1284,16 @@ __device__ int sample_ranked_long(const bl_slot_dev &sp, ValF val, int64_t n_lis
   __syncthreads();
   int chosen = sh.ires[2];
   rng = sh.rng_out;
+  out.S = sh.fres[1];
   __syncthreads();
+  out.first = (int)first;
+  out.cut = (int)cutoff;
   if (chosen >= n_list) {
     status |= BL_SE_UNSUPPORTED;
-    return -1;
+    return out;
   }
-  return chosen;
+  out.pos = chosen;
+  return out;
 }
 
 /* wavefront-level resolution of the terms [start, 64) of one 64-term group from state (e, N): the group
@@ -1687,7 +1769,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
     const float *fv = d.full_v + (int64_t)row * NB * BL_EB;
     const int32_t *fi = d.full_i + (int64_t)row * NB * BL_EB;
     int *boff = reinterpret_cast<int *>(&sh.n); /* [NB + 1]; the normaliser's LDS is free until norm_prep */
-    const bool filt = sp.top_p < 1.0f || sp.min_p > 0.0f;
+    const bool filt = bl_probs_on(sp);
     int nf = 0;
     double s_ap = 0.0; /* the exponent blocks' approximate tempered sum (unfiltered rows) */
     for (int b0 = 0; b0 < NB; b0 += BL_SEL_THREADS) {
@@ -1753,7 +1835,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
        * lower buckets, equal values in one bucket), scattered by bucket, then ranked by counting within
        * each bucket, one LDS tile of the bucketed list at a time */
       const float T = sp.temperature;
-      float thr = M - 17.5f * (filt && T < 1.0f ? 1.0f : T); /* the exponent pass's candidate span */
+      float thr = M - bl_cand_span(sp); /* the exponent pass's candidates */
       if (!filt) {
         /* the draw adds exp((v - M) / T) in descending order. With u = 2^-24 and m <= V terms, the float
          * running sum past every term >= 2^(k-24) is at least (1 - g) (S - V 2^(k-24)), g = m u / (1 - m u)
@@ -1901,7 +1983,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
   const bool short_list = n_list <= BL_SERIAL_MAX;
   if (sampled) {
     if (!ranked_supported(sp, n_list, n_logical, keep)) status |= BL_SE_UNSUPPORTED;
-    if (!status && short_list) ranked_terms(sp, val, n_list, sh.ser_e, sh.ser_r, sh);
+    if (!status && short_list) ranked_terms(sp, val, n_list, sh);
   }
 
   if (gram) {
@@ -1945,13 +2027,20 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
   __syncthreads();
   if (lp_row && w == 0) norm_chain(d, row, M, sh);
   if (sampled && !status && short_list && w == 1 && lane == 0)
-    sh.ires[2] = ranked_serial(sp, (int)n_list, n_logical, keep, rng, skip, sh.ser_e, sh.ser_r, &sh.rng_out);
+    sh.draw = ranked_serial(sp, (int)n_list, n_logical, keep, rng, skip, sh, &sh.rng_out);
   __syncthreads();
   const float S_norm = sh.n.S; /* the normaliser's LDS is scratch from here on (heap ties) */
+  sel_draw dr;
+  dr.pos = -1;
+  dr.first = dr.cut = 0;
+  dr.S = 0.0f;
+  const float *dterm = sh.ser_r; /* the draw's term of position j: dterm[j - dshift] */
+  int64_t dshift = 0;
   if (sampled && !status) {
     int pos;
     if (short_list) {
-      pos = sh.ires[2];
+      dr = sh.draw;
+      pos = dr.pos;
       if (pos == -2 || pos >= n_list) {
         status |= BL_SE_UNSUPPORTED;
         pos = -1;
@@ -1966,8 +2055,12 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
         gsum = d.gsum + (int64_t)row * (V / 64 + 64);
       }
       float *tbuf = reinterpret_cast<float *>(d.sortk + (int64_t)row * 2 * V); /* free once the list is sorted */
-      pos = sample_ranked_long(sp, val, n_list, n_logical, keep, rng, skip, recs, gsum, tbuf, sh, status);
+      dr = sample_ranked_long(sp, val, n_list, n_logical, keep, rng, skip, recs, gsum, tbuf, sh, status);
+      pos = dr.pos;
+      dterm = tbuf;
+      dshift = dr.first;
     }
+    dr.pos = pos;
     if (pos >= 0) {
       const uint64_t kp = keys[pos];
       tok = kp ? ckey_i(kp) : 0;
@@ -1986,6 +2079,52 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
     }
   }
 
+  /* post-sampling probabilities (src/server.br:1015-1025): the drawn token's and those of the first
+   * n_probs candidates of the drawn range, each its term over the range's sum (src/sampling.br:600-607);
+   * a greedy row has the one probability 1 (src/sampling.br:753-755), a grammar row none. Equal values
+   * next to the listed positions of a full-vocabulary rank stand in the heap's order: reported as a tie */
+  const bool psp_row = (mode & BL_M_PSP) && rows.lp;
+  const int n_alt = sp.n_probs < rows.top_stride ? sp.n_probs : rows.top_stride;
+  int psp_n = 0;
+  float psp_tok = 0.0f;
+  if (psp_row) {
+    if (sampled) {
+      if (!status) {
+        const int64_t avail = (int64_t)dr.cut - dr.first;
+        psp_n = (int)(avail < n_alt ? avail : n_alt);
+        if (dr.first + psp_n > n_list) status |= BL_SE_UNSUPPORTED;
+      }
+      if (t == 0) sh.ires[6] = 0;
+      __syncthreads();
+      if (!status && (mode & BL_M_FULL) && t <= psp_n) {
+        const int64_t j = dr.first + t;
+        if (j >= 1 && j < n_list && val(j - 1) == val(j)) sh.ires[6] = 1;
+      }
+      __syncthreads();
+      if (sh.ires[6]) status |= BL_SE_TIE;
+      if (!status) psp_tok = dterm[dr.pos - dshift] / dr.S;
+    } else if (!gram) {
+      psp_n = n_alt > 0 ? 1 : 0;
+      psp_tok = 1.0f;
+    }
+    if (t < n_alt) {
+      int32_t id = -1;
+      float pv = 0.0f;
+      if (t < psp_n && !status) {
+        if (sampled) {
+          const int64_t j = dr.first + t;
+          id = keys[j] ? ckey_i(keys[j]) : 0;
+          pv = dterm[j - dshift] / dr.S;
+        } else {
+          id = tok;
+          pv = 1.0f;
+        }
+      }
+      rows.top_ids[(int64_t)row * rows.top_stride + t] = id;
+      rows.top_lp[(int64_t)row * rows.top_stride + t] = pv;
+    }
+  }
+
   /* outputs, logprobs (src/server.br:1027-1035): alternatives = the first n_probs of the merged list */
   const float lse = lp_row ? (float)log((double)S_norm) : 0.0f;
   if (lp_row) {
@@ -2001,6 +2140,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
     rows.tok[row] = tok;
     if (rows.status) rows.status[row] = status;
     if (lp_row) rows.lp[row] = (tokv - M) - lse;
+    if (psp_row) rows.lp[row] = psp_tok;
     bool is_eog = false;
     for (int k = 0; k < n_eog; k++) is_eog |= (k < BL_EOG_LDS ? sh.eog[k] : d.eog[k]) == tok;
     if (rows.commit && status == 0) {

@@ -17,6 +17,14 @@ CASES = [
     dict(temperature=1.0, top_k=10, logprobs=1, n_probs=12, ignore_eos=1),
     dict(temperature=2.0, top_k=0, logprobs=1, n_probs=3, final_softcap=5.0),
     dict(temperature=0.6, top_k=30, logit_mul=0.5, logprobs=1, n_probs=1),
+    # XTC (src/sampling.br:552-572) and post-sampling probabilities (src/server.br:1015-1025)
+    dict(temperature=0.9, top_k=40, xtc_probability=0.6, xtc_threshold=0.1, logprobs=1, n_probs=6,
+         post_sampling_probs=1),
+    dict(temperature=1.1, top_k=0, top_p=0.95, xtc_probability=0.5, xtc_threshold=0.05),
+    dict(temperature=0.8, top_k=0, xtc_probability=0.7, xtc_threshold=0.2, min_keep=2, logprobs=1, n_probs=4,
+         post_sampling_probs=1),
+    dict(temperature=0.0, logprobs=1, n_probs=3, post_sampling_probs=1),
+    dict(temperature=1.2, top_k=0, min_p=0.05, logprobs=1, n_probs=8, post_sampling_probs=1),
 ]
 SMALL_V = 5003
 EOS, EOGS = 7, [11, 13]

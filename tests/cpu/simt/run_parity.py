@@ -105,7 +105,7 @@ def run_small(BL, case, steps, coarse=False, ramp=False, quant=None):
             buf.upload(x)
             tok, lp, ti, tl = ctx.sample_step([1], buf.ptr, SMALL_V, top_stride=max(n_probs, 1))
             ot, olp = np.zeros(1, np.int32), np.zeros(1, np.float32)
-            oti, otl = np.zeros(max(n_probs, 1), np.int32), np.zeros(max(n_probs, 1), np.float32)
+            oti, otl = np.full(max(n_probs, 1), -1, np.int32), np.zeros(max(n_probs, 1), np.float32)
             eog = O.C.c_int()
             assert L.orc_slot_step(h, O.fp(x), SMALL_V, wants, 1, O.ip(ot), O.fp(olp), O.ip(oti), O.fp(otl),
                                    O.C.byref(eog)) == 0
@@ -250,7 +250,7 @@ def run_pair(BL, ca, cb, steps):
             tok, lp, ti, tl = ctx.sample_step([0, 1], buf.ptr, SMALL_V, top_stride=stride)
             for r in range(2):
                 ot, olp = np.zeros(1, np.int32), np.zeros(1, np.float32)
-                oti, otl = np.zeros(stride, np.int32), np.zeros(stride, np.float32)
+                oti, otl = np.full(stride, -1, np.int32), np.zeros(stride, np.float32)
                 eg = O.C.c_int()
                 assert L.orc_slot_step(hs[r], O.fp(xs[r]), SMALL_V, wants[r][0], 1, O.ip(ot), O.fp(olp), O.ip(oti),
                                        O.fp(otl), O.C.byref(eg)) == 0

@@ -165,6 +165,7 @@ inline int __clz(int x) { return x ? __builtin_clz((unsigned)x) : 32; }
 inline int __clzll(long long x) { return x ? __builtin_clzll((unsigned long long)x) : 64; }
 inline uint64_t __umul64hi(uint64_t a, uint64_t b) { return (uint64_t)(((unsigned __int128)a * b) >> 64); }
 inline float __expf(float x) { return expf(x); }
+inline float __logf(float x) { return logf(x); }
 using std::max;
 using std::min;
 

@@ -218,7 +218,7 @@ def test_small_vocab_cases(cuda, case):
             tok, lp, ti, tl = ctx.sample_step([1], buf.data_ptr(), V, top_stride=max(n_probs, 1))
             ot = np.zeros(1, np.int32)
             olp = np.zeros(1, np.float32)
-            oti = np.zeros(max(n_probs, 1), np.int32)
+            oti = np.full(max(n_probs, 1), -1, np.int32)  # no alternative: -1, as the library writes
             otl = np.zeros(max(n_probs, 1), np.float32)
             eog = O.C.c_int()
             assert L.orc_slot_step(h, O.fp(x), V, wants, 1, O.ip(ot), O.fp(olp), O.ip(oti), O.fp(otl),
