@@ -31,9 +31,11 @@ enum {
   BL_EGRAMMAR_DEAD = -5,   /* "the reply no longer matches the grammar" (src/server.br:320) */
   BL_EGRAMMAR_REJECT = -6, /* "the grammar rejected every vocabulary token" (src/server.br:361) */
   BL_EGRAMMAR_AMBIG = -7,  /* "grammar is left-recursive or too ambiguous to match" (src/grammar.br:354) */
-  BL_EUNSUPPORTED = -8,    /* a sampler stage this library does not run on the device yet */
+  BL_EUNSUPPORTED = -8,    /* a sampler stage this library does not run on the device yet: top_n_sigma,
+                              typical_p, dynatemp, DRY (rejected by bl_slot_reset), XTC on speculative rows */
   BL_ETIE = -9             /* a draw on equal logits whose heap order is past the device simulation (more than
-                              8192 values at or above the tied one), or equal allowed maxima of a grammar row */
+                              8192 values at or above the tied one), equal allowed maxima of a grammar row, or
+                              post-sampling alternatives of a full-vocabulary rank that meet equal values */
 };
 
 /* SamplingParams (src/model.br:1565-1584) + the per-request server fields (src/server.br:665-760).
@@ -47,7 +49,7 @@ typedef struct {
   float typical_p;
   float top_p;
   float min_p;
-  float xtc_probability;
+  float xtc_probability;   /* XTC (src/sampling.br:552-572): on when > 0 and xtc_threshold <= 0.5 */
   float xtc_threshold;
   int32_t min_keep;
   float repeat_penalty;    /* 1: off */
@@ -60,7 +62,9 @@ typedef struct {
   float presence_penalty;
   int32_t logprobs;        /* 1: return the chosen token's logprob (wants_logprobs) */
   int32_t n_probs;         /* alternatives returned with logprobs (0..256) */
-  int32_t post_sampling_probs;
+  int32_t post_sampling_probs; /* with logprobs: the draw's probabilities instead (src/server.br:1015-1025): the
+                                  chosen token's probability and those of the first n_probs candidates of the
+                                  drawn range; alternatives past the range read id -1, probability 0 */
   int32_t ignore_eos;
   float final_softcap;     /* model tail (src/model.br:973-984): 0 = off */
   float logit_mul;         /* model tail: 1 = off */
