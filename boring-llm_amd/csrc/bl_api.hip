@@ -381,9 +381,8 @@ static int configure(const bl_ctx *c, const bl_params *p, bl_slot_dev &s) {
   if (p->temperature > 0.0f && p->top_n_sigma > 0.0f) return fail(BL_EUNSUPPORTED, "top_n_sigma is not supported on the device");
   if (p->dry_multiplier != 0.0f && p->dry_base >= 1.0f && p->dry_penalty_last_n != 0)
     return fail(BL_EUNSUPPORTED, "DRY is not supported on the device");
-  if (p->temperature > 0.0f && p->typical_p < 1.0f) return fail(BL_EUNSUPPORTED, "typical_p is not supported on the device");
-  if (p->temperature > 0.0f && p->dynatemp_range > 0.0f)
-    return fail(BL_EUNSUPPORTED, "dynamic temperature is not supported on the device");
+  if (p->temperature > 0.0f && p->dynatemp_range > 0.0f && p->dynatemp_exponent != 1.0f)
+    return fail(BL_EUNSUPPORTED, "dynamic temperature with an exponent other than 1 is not supported on the device");
   if (k > BL_KSEL_MAX)
     return fail(BL_EUNSUPPORTED, "top_k/n_probs of %d exceeds the device selection limit", k);
   if (p->repeat_last_n > BL_WCAP) return fail(BL_EUNSUPPORTED, "repeat_last_n above %d", BL_WCAP);
@@ -900,7 +899,7 @@ int bl_workload_drafts(int64_t seed, int64_t step, int seq, const int32_t *argma
 }
 
 int bl_math_digest(bl_ctx *c, int fn, uint32_t first_block, int n_blocks, uint64_t *out) {
-  if (!c || (fn != 0 && fn != 1) || n_blocks <= 0 || (uint64_t)first_block + n_blocks > 4096 || !out)
+  if (!c || fn < 0 || fn > 2 || n_blocks <= 0 || (uint64_t)first_block + n_blocks > 4096 || !out)
     return fail(BL_EPARAM, "bl_math_digest: invalid arguments");
   hipSetDevice(c->device);
   unsigned long long *d = nullptr;

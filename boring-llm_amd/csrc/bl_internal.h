@@ -160,20 +160,27 @@ __device__ __forceinline__ int bl_row_slot(const bl_rows &r, int row) {
 __device__ __forceinline__ bool bl_xtc_on(const bl_slot_dev &sp) {
   return sp.xtc_probability > 0.0f && sp.xtc_threshold <= 0.5f;
 }
-/* the untempered softmax is formed (top-p, min-p or XTC read it) */
+/* the untempered softmax is formed (top-p, min-p, XTC, the dynamic temperature or the typical filter
+ * read it) */
 __device__ __forceinline__ bool bl_probs_on(const bl_slot_dev &sp) {
-  return sp.top_p < 1.0f || sp.min_p > 0.0f || bl_xtc_on(sp);
+  return sp.top_p < 1.0f || sp.min_p > 0.0f || bl_xtc_on(sp) || sp.dynatemp_range > 0.0f || sp.typical_p < 1.0f;
 }
 /* A full-vocabulary rank's candidates: every value within this span of the row maximum. Past it a term
  * exp(v - v0) (untempered, when formed) or exp((v - v0) / T) of the draw is below 2^-25 of the first
  * term, too small to change a float32 sum that holds the first term (17.5 > 25 ln 2). The span is
  * 17.5 max(T, 1) when the untempered softmax is formed and 17.5 T otherwise. XTC may start the draw at a
  * later candidate v_first, whose probability, at least the threshold, puts it within -ln(threshold)
- * (+0.05 for the rounding of the probabilities and their sum) of the maximum: the span grows by that. */
+ * (+0.05 for the rounding of the probabilities and their sum) of the maximum: the span grows by that.
+ * The dynamic temperature draws at most at T + range. */
 __device__ __forceinline__ float bl_cand_span(const bl_slot_dev &sp) {
-  const float T = sp.temperature;
+  const float T = sp.dynatemp_range > 0.0f ? sp.temperature + sp.dynatemp_range : sp.temperature;
   float span = 17.5f * (bl_probs_on(sp) && T < 1.0f ? 1.0f : T);
   if (bl_xtc_on(sp)) span = sp.xtc_threshold > 1.0e-30f ? span + (-__logf(sp.xtc_threshold) + 0.05f) : 3.0e38f;
+  /* without a top-p or min-p cut the dynamic temperature's entropy runs over every candidate, where
+   * terms -q ln q far below the draw's reach still count: every value is a candidate */
+  if (sp.dynatemp_range > 0.0f && !(sp.top_p < 1.0f || sp.min_p > 0.0f)) span = 3.0e38f;
+  /* the typical filter needs the whole candidate list */
+  if (sp.typical_p < 1.0f) span = 3.0e38f;
   return span;
 }
 

@@ -1028,6 +1028,7 @@ struct sel_shared {
   float ser_e[BL_SERIAL_MAX];          /* short-list terms exp(v - v0) */
   float ser_r[BL_SERIAL_MAX];          /* short-list terms exp((v - v0) / T), from the draw's first candidate */
   float ser_v[BL_SERIAL_MAX];          /* short-list values */
+  int16_t ser_o[BL_SERIAL_MAX];        /* after the typical filter: a kept candidate's list position */
   sel_draw draw;                        /* the draw's range and sum */
   float fres[8];
   int ires[8];
@@ -1045,7 +1046,7 @@ __device__ __forceinline__ bool ranked_supported(const bl_slot_dev &sp, int64_t 
                                                  int64_t &keep) {
   keep = sp.min_keep > 1 ? sp.min_keep : 1;
   if (keep > n_logical) keep = n_logical;
-  return !(sp.typical_p < 1.0f || sp.dynatemp_range > 0.0f || keep > n_list);
+  return !(keep > n_list);
 }
 
 /* a short ranked list (n_list <= BL_SERIAL_MAX), by every thread: the values, the terms exp(v - v0) of
@@ -1069,7 +1070,7 @@ __device__ void ranked_terms(const bl_slot_dev &sp, ValF val, int64_t n_list, se
  * prefix, min-p cut, XTC, tempered sum and the draw (src/sampling.br:505-607); *rng_out = the state after
  * the draw */
 __device__ sel_draw ranked_serial(const bl_slot_dev &sp, int n, int64_t n_logical, int64_t keep, uint64_t rng,
-                                 int rng_skip, sel_shared &sh, uint64_t *rng_out) {
+                                 int rng_skip, bool pre, sel_shared &sh, uint64_t *rng_out) {
   const float *ser_e = sh.ser_e, *ser_v = sh.ser_v;
   float *ser_r = sh.ser_r;
   const bool xtc = bl_xtc_on(sp);
@@ -1078,7 +1079,10 @@ __device__ sel_draw ranked_serial(const bl_slot_dev &sp, int n, int64_t n_logica
   bool unsup = false;
   float sum_exp = 0.0f;
   if (filt) {
-    for (int j = 0; j < n; j++) sum_exp += ser_e[j];
+    /* `pre`: ser_e already holds the probabilities (after the typical filter), divided here by 1 */
+    if (pre) sum_exp = 1.0f;
+    else
+      for (int j = 0; j < n; j++) sum_exp += ser_e[j];
     if (sp.top_p < 1.0f) {
       float cum = 0.0f;
       for (int j = 0; j < n; j++) {
@@ -1128,12 +1132,44 @@ __device__ sel_draw ranked_serial(const bl_slot_dev &sp, int n, int64_t n_logica
     }
   }
   const int n_eff = (int)(cut < n ? cut : n);
-  if (first > 0) {
-    /* the draw's terms from the new first candidate */
-    const float vf = ser_v[first], T = sp.temperature;
+  /* dynamic_temperature (src/sampling.br:467-488), exponent 1 (powf(x, 1) = x): the entropy of the
+   * renormalised probabilities over [first, cut) against that of a uniform choice */
+  float Teff = sp.temperature;
+  if (sp.dynatemp_range > 0.0f && cut - first > 1) {
+    if (cut > n) {
+      unsup = true; /* the entropy would need candidates past the materialised list */
+    } else {
+      float ss = 0.0f;
+      for (int i = first; i < n_eff; i++) ss += ser_e[i] / sum_exp;
+      float ent = 0.0f;
+      for (int i = first; i < n_eff; i++) {
+        const float q = (ser_e[i] / sum_exp) / ss;
+        if (q > 0.0f) ent -= q * bl_logf(q);
+      }
+      const float maxe = bl_logf((float)(cut - first));
+      const float ne = ent / maxe;
+      const float T = sp.temperature, rg = sp.dynatemp_range;
+      const float tmin = T > rg ? T - rg : 0.0f, tmax = T + rg;
+      Teff = tmin + (tmax - tmin) * ne;
+    }
+  }
+  sel_draw r;
+  if (!(Teff > 0.0f)) {
+    /* no draw: the first candidate, probability 1 (src/sampling.br:581-582) */
+    ser_r[first] = 1.0f;
+    *rng_out = st;
+    r.pos = unsup ? -2 : first;
+    r.first = first;
+    r.cut = first + 1;
+    r.S = 1.0f;
+    return r;
+  }
+  if (first > 0 || Teff != sp.temperature) {
+    /* the draw's terms from the first candidate at the effective temperature */
+    const float vf = ser_v[first];
     for (int j = first; j < n_eff; j++) {
       const float dd = ser_v[j] - vf;
-      const float q = dd / T;
+      const float q = dd / Teff;
       ser_r[j] = SEL_EXPF(q);
     }
   }
@@ -1150,12 +1186,104 @@ __device__ sel_draw ranked_serial(const bl_slot_dev &sp, int n, int64_t n_logica
     }
   }
   *rng_out = st;
-  sel_draw r;
   r.pos = unsup ? -2 : (int)(f >= 0 ? f : cut - 1);
   r.first = first;
   r.cut = (int)cut;
   r.S = S;
   return r;
+}
+
+/*
+ * typical_filter (src/sampling.br:424-465) on a complete short list, by the block. The probabilities
+ * p = e / sum_exp and the entropy -sum p ln p are the reference's float loops (the sums by one thread,
+ * in order); candidates are taken by distance |-ln p - entropy|, ties by position (the loop's strict
+ * `<`), until their probabilities, added in that order, reach typical_p and min_keep is met. The kept
+ * candidates, in list order, replace the short list: values, probabilities in ser_e (ranked_serial then
+ * divides by 1: the later stages read the unrenormalised probabilities) and the draw's terms from the
+ * new first value; ser_o maps a kept position to its list position. Returns the kept count. On a
+ * full-vocabulary rank a cut between equal distances picks among equal values by the heap's order:
+ * reported as a tie.
+ */
+__device__ int typical_filter(const bl_slot_dev &sp, int n, bool full, sel_shared &sh, int &status) {
+  const int t = threadIdx.x;
+  float *tp = reinterpret_cast<float *>(&sh.n); /* the normaliser's LDS is free until norm_prep */
+  float *tq = tp + BL_SERIAL_MAX;
+  float *tl = tq + BL_SERIAL_MAX;
+  uint64_t *tk = reinterpret_cast<uint64_t *>(tl + BL_SERIAL_MAX);
+  int *ord = reinterpret_cast<int *>(tk + BL_SERIAL_MAX);
+  __syncthreads(); /* the short list's terms */
+  if (t == 0) {
+    float se = 0.0f;
+    for (int j = 0; j < n; j++) se += sh.ser_e[j];
+    sh.fres[4] = se;
+  }
+  __syncthreads();
+  const float se = sh.fres[4];
+  for (int j = t; j < n; j += BL_SEL_THREADS) {
+    const float p = sh.ser_e[j] / se;
+    const float l = p > 0.0f ? bl_logf(p) : 0.0f;
+    tp[j] = p;
+    tl[j] = l;
+    tq[j] = p * l;
+  }
+  __syncthreads();
+  if (t == 0) {
+    float ent = 0.0f;
+    for (int j = 0; j < n; j++)
+      if (tp[j] > 0.0f) ent -= tq[j];
+    sh.fres[5] = ent;
+  }
+  __syncthreads();
+  const float ent = sh.fres[5];
+  for (int j = t; j < n; j += BL_SEL_THREADS) {
+    const float dist = fabsf(-tl[j] - ent);
+    tk[j] = (uint64_t)(tp[j] > 0.0f ? bl_f2u(dist) : 0xffffffffu) << 32 | (uint32_t)j;
+  }
+  __syncthreads();
+  for (int j = t; j < n; j += BL_SEL_THREADS) {
+    const uint64_t k = tk[j];
+    int r = 0;
+    for (int q = 0; q < n; q++) r += tk[q] < k ? 1 : 0;
+    ord[r] = j;
+  }
+  __syncthreads();
+  if (t == 0) {
+    const int req = sp.min_keep > 1 ? sp.min_keep : 1;
+    float cum = 0.0f;
+    int m = 0;
+    while (m < n && (cum < sp.typical_p || m < req)) {
+      const int j = ord[m];
+      if (!(tp[j] > 0.0f)) break; /* nothing selectable is left */
+      cum += tp[j];
+      m++;
+    }
+    sh.ires[7] = m;
+  }
+  __syncthreads();
+  const int m = sh.ires[7];
+  const uint64_t klast = tk[ord[m - 1]];
+  if (full && m < n && (uint32_t)(tk[ord[m]] >> 32) == (uint32_t)(klast >> 32)) status |= BL_SE_TIE; /* uniform */
+  /* compaction in list order (one candidate per thread: n <= BL_SERIAL_MAX < the block) */
+  const bool sel = t < n && tk[t] <= klast;
+  int ni = 0;
+  if (sel)
+    for (int q = 0; q < t; q++) ni += tk[q] <= klast ? 1 : 0;
+  const float v = t < n ? sh.ser_v[t] : 0.0f, p = t < n ? tp[t] : 0.0f;
+  __syncthreads();
+  if (sel) {
+    sh.ser_v[ni] = v;
+    sh.ser_e[ni] = p;
+    sh.ser_o[ni] = (int16_t)t;
+  }
+  __syncthreads();
+  const float v0 = sh.ser_v[0], T = sp.temperature;
+  for (int j = t; j < m; j += BL_SEL_THREADS) {
+    const float dd = sh.ser_v[j] - v0;
+    const float q = dd / T;
+    sh.ser_r[j] = SEL_EXPF(q);
+  }
+  __syncthreads();
+  return m;
 }
 
 /*
@@ -1262,9 +1390,55 @@ __device__ sel_draw sample_ranked_long(const bl_slot_dev &sp, ValF val, int64_t 
   const int64_t m = n_eff - first;
   const float vf = val(first);
   auto valF = [&](int64_t j) { return val(first + j); };
+  /* dynamic_temperature (src/sampling.br:467-488), exponent 1: the surviving probabilities' sum, then
+   * the entropy of the renormalised ones (entropy -= q ln q adds the non-negative -(q ln q)) */
+  float Teff = T;
+  if (sp.dynatemp_range > 0.0f && cutoff - first > 1) {
+    if (cutoff > n_list) { /* the entropy would need candidates past the materialised list */
+      status |= BL_SE_UNSUPPORTED;
+      return out;
+    }
+    block_records(m, valF, termPv, recs, gsum, tbuf);
+    if (w == 0) {
+      float S;
+      bl_seq_walk(m, termS, [&](int64_t g) { return recs[g]; }, false, 0.0f, 0, S, lane);
+      if (lane == 0) sh.fres[3] = S;
+    }
+    __syncthreads();
+    const float ss = sh.fres[3];
+    __syncthreads();
+    block_records(m, valF, [&](float v) {
+      const float q = termPv(v) / ss;
+      return q > 0.0f ? -(q * bl_logf(q)) : 0.0f;
+    }, recs, gsum, tbuf);
+    if (w == 0) {
+      float S;
+      bl_seq_walk(m, termS, [&](int64_t g) { return recs[g]; }, false, 0.0f, 0, S, lane);
+      if (lane == 0) sh.fres[3] = S;
+    }
+    __syncthreads();
+    const float ent = sh.fres[3];
+    __syncthreads();
+    const float maxe = bl_logf((float)(cutoff - first));
+    const float ne = ent / maxe;
+    const float rg = sp.dynatemp_range;
+    const float tmin = T > rg ? T - rg : 0.0f, tmax = T + rg;
+    Teff = tmin + (tmax - tmin) * ne;
+  }
+  if (!(Teff > 0.0f)) {
+    /* no draw: the first candidate, probability 1 (src/sampling.br:581-582) */
+    if (t == 0) tbuf[0] = 1.0f;
+    __syncthreads();
+    rng = st;
+    out.pos = (int)first;
+    out.first = (int)first;
+    out.cut = (int)first + 1;
+    out.S = 1.0f;
+    return out;
+  }
   auto termRv = [&](float v) {
     float dd = v - vf;
-    float q = dd / T;
+    float q = dd / Teff;
     return SEL_EXPF(q);
   };
   block_records(m, valF, termRv, recs, gsum, tbuf);
@@ -1985,6 +2159,22 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
     if (!ranked_supported(sp, n_list, n_logical, keep)) status |= BL_SE_UNSUPPORTED;
     if (!status && short_list) ranked_terms(sp, val, n_list, sh);
   }
+  /* the typical filter (complete short lists; the candidate span keeps every value for it) */
+  bool typ = false;
+  int n_draw = (int)n_list;
+  int64_t nlog_draw = n_logical;
+  if (sampled && !status && sp.typical_p < 1.0f && n_logical > 1) {
+    if (!short_list || n_list != n_logical) {
+      status |= BL_SE_UNSUPPORTED;
+    } else {
+      typ = true;
+      n_draw = typical_filter(sp, (int)n_list, (mode & BL_M_FULL) != 0, sh, status);
+      nlog_draw = n_draw;
+      if (keep > n_draw) keep = n_draw;
+    }
+  }
+  /* a draw position -> its list position */
+  auto lpos = [&](int64_t j) -> int64_t { return typ ? (int64_t)sh.ser_o[j] : j; };
 
   if (gram) {
     /* sample_grammar_token, greedy (src/server.br:308-361): the frontier's status, then the first
@@ -2027,7 +2217,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
   __syncthreads();
   if (lp_row && w == 0) norm_chain(d, row, M, sh);
   if (sampled && !status && short_list && w == 1 && lane == 0)
-    sh.draw = ranked_serial(sp, (int)n_list, n_logical, keep, rng, skip, sh, &sh.rng_out);
+    sh.draw = ranked_serial(sp, n_draw, nlog_draw, keep, rng, skip, typ, sh, &sh.rng_out);
   __syncthreads();
   const float S_norm = sh.n.S; /* the normaliser's LDS is scratch from here on (heap ties) */
   sel_draw dr;
@@ -2041,11 +2231,12 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
     if (short_list) {
       dr = sh.draw;
       pos = dr.pos;
-      if (pos == -2 || pos >= n_list) {
+      if (pos == -2 || pos >= n_draw) {
         status |= BL_SE_UNSUPPORTED;
-        pos = -1;
+        pos = dr.pos = -1;
       } else {
         rng = sh.rng_out;
+        pos = (int)lpos(pos);
       }
     } else {
       bl_grec *recs = sh.c.recs;
@@ -2060,7 +2251,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
       dterm = tbuf;
       dshift = dr.first;
     }
-    dr.pos = pos;
+    /* dr.pos stays a draw position; pos is the list position */
     if (pos >= 0) {
       const uint64_t kp = keys[pos];
       tok = kp ? ckey_i(kp) : 0;
@@ -2092,13 +2283,13 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
       if (!status) {
         const int64_t avail = (int64_t)dr.cut - dr.first;
         psp_n = (int)(avail < n_alt ? avail : n_alt);
-        if (dr.first + psp_n > n_list) status |= BL_SE_UNSUPPORTED;
+        if (dr.first + psp_n > (typ ? n_draw : n_list)) status |= BL_SE_UNSUPPORTED;
       }
       if (t == 0) sh.ires[6] = 0;
       __syncthreads();
       if (!status && (mode & BL_M_FULL) && t <= psp_n) {
         const int64_t j = dr.first + t;
-        if (j >= 1 && j < n_list && val(j - 1) == val(j)) sh.ires[6] = 1;
+        if (j >= 1 && j < (typ ? n_draw : n_list) && val(lpos(j - 1)) == val(lpos(j))) sh.ires[6] = 1;
       }
       __syncthreads();
       if (sh.ires[6]) status |= BL_SE_TIE;
@@ -2112,8 +2303,8 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
       float pv = 0.0f;
       if (t < psp_n && !status) {
         if (sampled) {
-          const int64_t j = dr.first + t;
-          id = keys[j] ? ckey_i(keys[j]) : 0;
+          const int64_t j = dr.first + t, lj = lpos(j);
+          id = keys[lj] ? ckey_i(keys[lj]) : 0;
           pv = dterm[j - dshift] / dr.S;
         } else {
           id = tok;
@@ -2228,7 +2419,7 @@ __global__ void bl_k_math_digest(int fn, uint32_t first_block, unsigned long lon
   for (int k = 0; k < 16; k++) {
     uint32_t u = base + (uint32_t)(blockIdx.x * 4096 + k * 256 + threadIdx.x);
     float x = bl_u2f(u);
-    float y = fn == 0 ? bl_expf(x) : bl_tanhf(x);
+    float y = fn == 0 ? bl_expf(x) : fn == 1 ? bl_tanhf(x) : bl_logf(x);
     uint32_t yb = y != y ? 0x7fc00000u : bl_f2u(y); /* NaN payloads are not part of the path */
     h += bl_splitmix(((uint64_t)u << 32) | yb);
   }

@@ -10,6 +10,7 @@
  *              every float in [-104, 89] (2.24e9 inputs) and at the special values.
  *   bl_tanhf — fdlibm's float tanh built on fdlibm's float expm1 (glibc sysdeps/ieee754/flt-32),
  *              evaluated in float arithmetic. Exhaustively equal to host glibc tanhf on all 2^32 inputs.
+ *   bl_logf  — the table-driven log of ARM optimized-routines as shipped in glibc (below).
  * The table below is 2^(i/32) rounded to double minus (i << 47); it is derived, not copied: the test
  * suite recomputes it from high-precision arithmetic.
  *
@@ -109,6 +110,46 @@ BL_FN float bl_expf_tab(float x, Tab tab) {
 
 BL_FN float bl_expf(float x) {
   return bl_expf_tab(x, [](uint32_t i) { return bl_exp2_tab[i]; });
+}
+
+/* ---------------- logf ---------------- */
+/* ARM optimized-routines logf (as in glibc >= 2.28): x = 2^k z with z in [0x1.66p-1, 0x1.66p0) split
+ * by the top 4 mantissa bits into 16 subintervals; log(x) = log1p(z/c - 1) + log(c) + k ln2 with
+ * (1/c, log c) from the table, log1p by a cubic in double, one rounding to float at the end.
+ * Equal to host glibc logf on every positive float (CPU, tests/cpu/check_exact.cpp samples it) and on
+ * all 2^32 bit patterns on the device (tests/golden/math_digest.bin). */
+BL_FN float bl_logf(float x) {
+  const double invc[16] = {0x1.661ec79f8f3bep+0, 0x1.571ed4aaf883dp+0, 0x1.49539f0f010bp+0,  0x1.3c995b0b80385p+0,
+                           0x1.30d190c8864a5p+0, 0x1.25e227b0b8eap+0,  0x1.1bb4a4a1a343fp+0, 0x1.12358f08ae5bap+0,
+                           0x1.0953f419900a7p+0, 0x1p+0,               0x1.e608cfd9a47acp-1, 0x1.ca4b31f026aap-1,
+                           0x1.b2036576afce6p-1, 0x1.9c2d163a1aa2dp-1, 0x1.886e6037841edp-1, 0x1.767dcf5534862p-1};
+  const double logc[16] = {-0x1.57bf7808caadep-2, -0x1.2bef0a7c06ddbp-2, -0x1.01eae7f513a67p-2, -0x1.b31d8a68224e9p-3,
+                           -0x1.6574f0ac07758p-3, -0x1.1aa2bc79c81p-3,   -0x1.a4e76ce8c0e5ep-4, -0x1.1973c5a611cccp-4,
+                           -0x1.252f438e10c1ep-5, 0x0p+0,                0x1.aa5aa5df25984p-5,  0x1.c5e53aa362eb4p-4,
+                           0x1.526e57720db08p-3,  0x1.bc2860d22477p-3,   0x1.1058bc8a07ee1p-2,  0x1.4043057b6ee09p-2};
+  const double LN2 = 0x1.62e42fefa39efp-1, A0 = -0x1.00ea348b88334p-2, A1 = 0x1.5575b0be00b6ap-2,
+               A2 = -0x1.ffffef20a4123p-2;
+  uint32_t ix = bl_f2u(x);
+  if (ix == 0x3f800000u) return 0.0f;
+  if (ix - 0x00800000u >= 0x7f800000u - 0x00800000u) {
+    if (ix * 2u == 0u) return bl_u2f(0xff800000u); /* -inf */
+    if (ix == 0x7f800000u) return x;
+    if ((ix & 0x80000000u) || ix * 2u >= 0xff000000u) return bl_u2f(0x7fc00000u); /* NaN */
+    ix = bl_f2u(x * 0x1p23f); /* subnormal: normalise */
+    ix -= 23u << 23;
+  }
+  const uint32_t tmp = ix - 0x3f330000u;
+  const int i = (int)((tmp >> 19) % 16u);
+  const int k = (int32_t)tmp >> 23;
+  const uint32_t iz = ix - (tmp & 0xff800000u);
+  const double z = (double)bl_u2f(iz);
+  const double r = z * invc[i] - 1.0;
+  const double y0 = logc[i] + (double)k * LN2;
+  const double r2 = r * r;
+  double y = A1 * r + A2;
+  y = A0 * r2 + y;
+  y = y * r2 + (y0 + r);
+  return (float)y;
 }
 
 /* ---------------- expm1f / tanhf (float arithmetic) ---------------- */

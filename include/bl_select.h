@@ -174,7 +174,7 @@ int bl_workload_bias(int cfg, int64_t seed, int row, int n, int vocab, float lo,
 int bl_workload_c3_vocab(int64_t seed, int vocab, uint8_t *blob, size_t blob_cap, uint32_t *offsets, int32_t *eos_id);
 int bl_workload_drafts(int64_t seed, int64_t step, int seq, const int32_t *argmax, int k, int vocab, int32_t *out);
 
-/* Self-test (no reference counterpart): digests of the device expf (fn 0) / tanhf (fn 1) over
+/* Self-test (no reference counterpart): digests of the device expf (fn 0) / tanhf (fn 1) / logf (fn 2) over
  * input bit-pattern blocks [b*2^20, (b+1)*2^20), b = first_block .. first_block+n_blocks-1; each digest
  * is the wrapping sum of splitmix64(u << 32 | bits(f(u))) with NaN results canonicalised to 0x7fc00000.
  * Compared with host-glibc fixtures. */

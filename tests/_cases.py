@@ -25,6 +25,14 @@ CASES = [
          post_sampling_probs=1),
     dict(temperature=0.0, logprobs=1, n_probs=3, post_sampling_probs=1),
     dict(temperature=1.2, top_k=0, min_p=0.05, logprobs=1, n_probs=8, post_sampling_probs=1),
+    # dynamic temperature, exponent 1 (src/sampling.br:467-488)
+    dict(temperature=0.9, top_k=30, dynatemp_range=0.5, logprobs=1, n_probs=4, post_sampling_probs=1),
+    dict(temperature=1.0, top_k=0, min_p=0.05, dynatemp_range=0.8),
+    dict(temperature=0.4, top_k=0, dynatemp_range=0.6, xtc_probability=0.5, xtc_threshold=0.15),
+    # the typical filter (src/sampling.br:424-465) on top-k lists
+    dict(temperature=0.9, top_k=50, typical_p=0.6, logprobs=1, n_probs=5, post_sampling_probs=1),
+    dict(temperature=1.1, top_k=120, typical_p=0.9, min_keep=4, top_p=0.95, min_p=0.02, xtc_probability=0.4,
+         xtc_threshold=0.1, dynatemp_range=0.3),
 ]
 SMALL_V = 5003
 EOS, EOGS = 7, [11, 13]

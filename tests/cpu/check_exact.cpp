@@ -88,16 +88,24 @@ int main() {
     }
   }
   printf("exact-sum mismatches: %ld of %ld\n", bad, trials);
-  // 2) glibc-identical expf / tanhf on a strided sample of all float bit patterns
-  long me = 0, mt = 0, n = 0;
+  // 2) glibc-identical expf / tanhf / logf on a strided sample of all float bit patterns (logf: NaN
+  // results compared as NaN, the payload is not part of the path)
+  long me = 0, mt = 0, ml = 0, n = 0;
   for (uint64_t u = 0; u <= 0xffffffffull; u += 4093) {
     float x = bl_u2f((uint32_t)u);
     if (x != x) continue;
     n++;
     if (bl_f2u(bl_expf(x)) != bl_f2u(expf(x))) me++;
     if (bl_f2u(bl_tanhf(x)) != bl_f2u(tanhf(x))) mt++;
+    const float la = bl_logf(x), lb = logf(x);
+    if (!(la != la && lb != lb) && bl_f2u(la) != bl_f2u(lb)) ml++;
   }
-  printf("expf mismatches %ld, tanhf mismatches %ld, of %ld sampled inputs\n", me, mt, n);
+  // logf densely over (0, 1], the probabilities it is applied to (every 3rd pattern)
+  for (uint32_t u = 1; u <= 0x3f800000u; u += 3) {
+    const float x = bl_u2f(u);
+    if (bl_f2u(bl_logf(x)) != bl_f2u(logf(x))) ml++;
+  }
+  printf("expf mismatches %ld, tanhf mismatches %ld, logf mismatches %ld, of %ld sampled inputs\n", me, mt, ml, n);
   // 3) u64 -> f32 rounding against the C conversion
   long mc = 0;
   for (int i = 0; i < 2000000; i++) {
@@ -105,5 +113,5 @@ int main() {
     if (bl_f2u(bl_u64_to_f32(v)) != bl_f2u((float)v)) mc++;
   }
   printf("u64->f32 mismatches %ld\n", mc);
-  return (bad || me || mt || mc) ? 1 : 0;
+  return (bad || me || mt || ml || mc) ? 1 : 0;
 }

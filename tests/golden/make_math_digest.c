@@ -1,5 +1,5 @@
-/* Writes tests/golden/math_digest.bin: per 2^20-input block digests of the host glibc expf and tanhf
- * over all 2^32 float bit patterns (4096 uint64 for expf, then 4096 for tanhf, little endian).
+/* Writes tests/golden/math_digest.bin: per 2^20-input block digests of the host glibc expf, tanhf and
+ * logf over all 2^32 float bit patterns (4096 uint64 for each, in that order, little endian).
  * Digest of a block = wrapping sum over its inputs u of splitmix64(u << 32 | bits(f(u))), NaN results
  * canonicalised to 0x7fc00000.
  * Build: gcc -O2 -ffp-contract=off -fopenmp make_math_digest.c -lm -o /tmp/mmd && /tmp/mmd out.bin */
@@ -17,14 +17,14 @@ static uint64_t splitmix(uint64_t x) {
 static uint32_t bits(float f) { uint32_t u; memcpy(&u, &f, 4); return f != f ? 0x7fc00000u : u; }
 static float fl(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
 int main(int argc, char **argv) {
-  static uint64_t dig[2][4096];
-  for (int fn = 0; fn < 2; fn++) {
+  static uint64_t dig[3][4096];
+  for (int fn = 0; fn < 3; fn++) {
     #pragma omp parallel for schedule(dynamic, 16)
     for (int b = 0; b < 4096; b++) {
       uint64_t h = 0;
       for (uint32_t k = 0; k < (1u << 20); k++) {
         uint32_t u = ((uint32_t)b << 20) | k;
-        float y = fn == 0 ? expf(fl(u)) : tanhf(fl(u));
+        float y = fn == 0 ? expf(fl(u)) : fn == 1 ? tanhf(fl(u)) : logf(fl(u));
         h += splitmix(((uint64_t)u << 32) | bits(y));
       }
       dig[fn][b] = h;

@@ -41,10 +41,10 @@ def lp_close(a, b):
 
 # ------------------------------------------------------------------ device math, exhaustive
 def test_math_exhaustive(cuda):
-    say("math digest: expf/tanhf over all 2^32 inputs")
-    want = np.fromfile(os.path.join(GOLDEN, "math_digest.bin"), dtype="<u8").reshape(2, 4096)
+    say("math digest: expf/tanhf/logf over all 2^32 inputs")
+    want = np.fromfile(os.path.join(GOLDEN, "math_digest.bin"), dtype="<u8").reshape(3, 4096)
     ctx = BL.Context(1024, 1, 1)
-    for fn, name in ((0, "expf"), (1, "tanhf")):
+    for fn, name in ((0, "expf"), (1, "tanhf"), (2, "logf")):
         got = np.array(ctx.math_digest(fn, 0, 4096), dtype=np.uint64)
         bad = np.nonzero(got != want[fn])[0]
         assert len(bad) == 0, f"{name}: {len(bad)} blocks differ, first {bad[:8]}"
@@ -238,7 +238,16 @@ def test_small_vocab_cases(cuda, case):
 def test_errors_are_reported(cuda):
     ctx = BL.Context(1000, 2, 2)
     with pytest.raises(BL.BLError) as e:
-        ctx.slot_reset(0, BL.Params(temperature=1.0, typical_p=0.5), 1)
+        ctx.slot_reset(0, BL.Params(temperature=1.0, top_n_sigma=1.5), 1)
+    assert e.value.code == BL.BL_EUNSUPPORTED
+    with pytest.raises(BL.BLError) as e:
+        ctx.slot_reset(0, BL.Params(temperature=1.0, dynatemp_range=0.5, dynatemp_exponent=2.0), 1)
+    assert e.value.code == BL.BL_EUNSUPPORTED
+    # the typical filter over a full-vocabulary list longer than the short-list path: reported at the step
+    ctx.slot_reset(0, BL.Params(temperature=1.0, typical_p=0.5), 1)
+    row = torch.randn(1000, device=cuda)
+    with pytest.raises(BL.BLError) as e:
+        ctx.sample_step([0], row.data_ptr(), 1000)
     assert e.value.code == BL.BL_EUNSUPPORTED
     with pytest.raises(BL.BLError) as e:
         ctx.slot_reset(0, BL.Params(), 1, bias={5000: 1.0})

@@ -41,8 +41,8 @@ def _run(lib, items, env_extra=None, timeout=600):
 
 
 def test_small_cases_random_thread_order(simt_lib):
-    out = _run(simt_lib, ["small:0-15:4"], {"SIMT_ORDER": "rand"})
-    assert out.count("ok   small case") == 16
+    out = _run(simt_lib, ["small:0-20:4"], {"SIMT_ORDER": "rand"})
+    assert out.count("ok   small case") == 21
 
 
 def test_coarse_and_ramp_logits(simt_lib):
@@ -96,5 +96,5 @@ def test_small_cases_address_sanitizer():
         assert os.path.isabs(p) and os.path.exists(p), f"{rt} not found"
         pre.append(p)
     env = {"LD_PRELOAD": " ".join(pre), "ASAN_OPTIONS": "detect_leaks=0", "UBSAN_OPTIONS": "print_stacktrace=1"}
-    out = _run(os.path.join(SIMT, "_build", "libbl_simt_asan.so"), ["small:0-15:3", "coarse:1,5:3", "ramp:8:2", "grammar:0-6:20", "q4:2,9:4"], env)
+    out = _run(os.path.join(SIMT, "_build", "libbl_simt_asan.so"), ["small:0-20:3", "coarse:1,5:3", "ramp:8:2", "grammar:0-6:20", "q4:2,9:4"], env)
     assert "ERROR: AddressSanitizer" not in out and "runtime error" not in out
