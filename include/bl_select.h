@@ -32,7 +32,8 @@ enum {
   BL_EGRAMMAR_REJECT = -6, /* "the grammar rejected every vocabulary token" (src/server.br:361) */
   BL_EGRAMMAR_AMBIG = -7,  /* "grammar is left-recursive or too ambiguous to match" (src/grammar.br:354) */
   BL_EUNSUPPORTED = -8,    /* a sampler stage this library does not run on the device yet: top_n_sigma,
-                              typical_p, dynatemp, DRY (rejected by bl_slot_reset), XTC on speculative rows */
+                              DRY, a dynatemp exponent other than 1 (rejected by bl_slot_reset); XTC on
+                              speculative rows; typical_p over a full-vocabulary list above 512 candidates */
   BL_ETIE = -9             /* a draw on equal logits whose heap order is past the device simulation (more than
                               8192 values at or above the tied one), equal allowed maxima of a grammar row, or
                               post-sampling alternatives of a full-vocabulary rank that meet equal values */
