@@ -34,6 +34,7 @@ class Params(C.Structure):
         ("dry_penalty_last_n", C.c_int32), ("frequency_penalty", C.c_float), ("presence_penalty", C.c_float),
         ("logprobs", C.c_int32), ("n_probs", C.c_int32), ("post_sampling_probs", C.c_int32),
         ("ignore_eos", C.c_int32), ("final_softcap", C.c_float), ("logit_mul", C.c_float),
+        ("mirostat", C.c_int32), ("mirostat_tau", C.c_float), ("mirostat_eta", C.c_float),
     ]
 
     def __init__(self, **kw):

@@ -187,6 +187,9 @@ void bl_params_default(bl_params *p) {
   p->min_p = 0.0f;
   p->xtc_probability = 0.0f;
   p->xtc_threshold = 0.1f;
+  p->mirostat = 0;
+  p->mirostat_tau = 5.0f;
+  p->mirostat_eta = 0.1f;
   p->min_keep = 0;
   p->repeat_penalty = 1.0f;
   p->repeat_last_n = 64;
@@ -372,6 +375,17 @@ static int configure(const bl_ctx *c, const bl_params *p, bl_slot_dev &s) {
   else mode |= BL_M_FULL;
   /* logprobs: the effective logits' normaliser and top n_probs, or the draw's own probabilities */
   if (p->logprobs) mode |= p->post_sampling_probs ? BL_M_PSP : BL_M_LOGPROBS;
+  /* mirostat replaces the sampler chain (src/server.br:964-976); a greedy row stays greedy */
+  if (p->mirostat < 0 || p->mirostat > 2 || !(p->mirostat_tau >= 0.0f) || !(p->mirostat_eta >= 0.0f))
+    return fail(BL_EPARAM, "`mirostat` must be 0, 1, or 2 with non-negative tau and eta");
+  if (p->mirostat != 0 && p->post_sampling_probs && p->logprobs)
+    return fail(BL_EPARAM, "post_sampling_probs require the standard unconstrained sampling chain");
+  if (p->mirostat == 1) return fail(BL_EUNSUPPORTED, "mirostat v1 is not supported on the device");
+  s.mirostat = p->mirostat;
+  s.mirostat_tau = p->mirostat_tau;
+  s.mirostat_eta = p->mirostat_eta;
+  s.mu = 2.0f * p->mirostat_tau;
+  if (p->mirostat == 2 && p->temperature > 0.0f) mode = (mode & ~(BL_M_TOPK | BL_M_FULL)) | BL_M_FULL | BL_M_MIRO;
   s.mode = mode;
   int k = 0;
   if (mode & BL_M_TOPK) k = p->top_k;
@@ -562,6 +576,8 @@ int bl_slot_grammar(bl_ctx *c, int slot, const char *gbnf, size_t len) {
     s.mode &= ~BL_M_GRAMMAR;
   } else {
     if (c->voff.empty()) return fail(BL_EPARAM, "bl_slot_grammar: the vocabulary pieces are not set (bl_set_vocab)");
+    if (s.mirostat != 0)
+      return fail(BL_EPARAM, "stateful adaptive sampling cannot be combined with constrained decoding");
     if (s.temperature > 0.0f)
       return fail(BL_EUNSUPPORTED, "grammar-constrained sampling with temperature > 0 is not supported on the device");
     bl_ctx::gram_entry *e = nullptr;
@@ -813,6 +829,8 @@ int bl_spec_verify(bl_ctx *c, const int32_t *slots, int B, int k, const float *d
     /* each row's draw starts at its position in the RNG chain; an XTC chance draw would shift the rest */
     if (k > 0 && s.temperature > 0.0f && s.xtc_probability > 0.0f && s.xtc_threshold <= 0.5f)
       return fail(BL_EUNSUPPORTED, "speculative rows with XTC are not supported on the device");
+    if (k > 0 && (s.mode & BL_M_MIRO))
+      return fail(BL_EUNSUPPORTED, "speculative rows with mirostat are not supported on the device");
   }
   hipSetDevice(c->device);
   for (int b = 0; b < B; b++)

@@ -49,6 +49,7 @@
 #define BL_M_LOGPROBS 8
 #define BL_M_GRAMMAR 16
 #define BL_M_PSP 32 /* logprobs as post-sampling probabilities (src/server.br:1015-1025) */
+#define BL_M_MIRO 64 /* the draw is mirostat v2's */
 
 /* grammar mask kernel: tokens per workgroup */
 #define BL_GM_THREADS 256
@@ -89,6 +90,9 @@ struct bl_slot_dev {
   /* grammar (src/server.br:309-362): position of the reply in the slot's automaton */
   bl_gram_pos gpos;
   int32_t g_on, pad2;
+  /* mirostat v2 (src/sampling.br:663-674): tau, eta and the running mu */
+  int32_t mirostat;
+  float mirostat_tau, mirostat_eta, mu;
 };
 
 struct bl_dev {
@@ -173,6 +177,8 @@ __device__ __forceinline__ bool bl_probs_on(const bl_slot_dev &sp) {
  * (+0.05 for the rounding of the probabilities and their sum) of the maximum: the span grows by that.
  * The dynamic temperature draws at most at T + range. */
 __device__ __forceinline__ float bl_cand_span(const bl_slot_dev &sp) {
+  /* mirostat's terms exp(v/T - v0/T) (the span allows for the rounding of the two quotients) */
+  if (sp.mode & BL_M_MIRO) return 17.6f * sp.temperature;
   const float T = sp.dynatemp_range > 0.0f ? sp.temperature + sp.dynatemp_range : sp.temperature;
   float span = 17.5f * (bl_probs_on(sp) && T < 1.0f ? 1.0f : T);
   if (bl_xtc_on(sp)) span = sp.xtc_threshold > 1.0e-30f ? span + (-__logf(sp.xtc_threshold) + 0.05f) : 3.0e38f;

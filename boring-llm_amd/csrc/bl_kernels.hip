@@ -1470,6 +1470,88 @@ __device__ sel_draw sample_ranked_long(const bl_slot_dev &sp, ValF val, int64_t 
   return out;
 }
 
+/*
+ * sample_mirostat_v2 (src/sampling.br:663-674, draw_mirostat_prefix :643-659) over the full-vocabulary
+ * list, by the block: scaled values v/T, the softmax of exp(v/T - v0/T) over every candidate (the terms
+ * past the list are below half an ulp of the sum), the prefix whose surprise -ln p / ln 2 stays within
+ * mu, the softmax and draw over that prefix, and mu - eta (surprise - tau) for the slot (sh.fres[6]).
+ */
+template <class ValF>
+__device__ sel_draw sample_mirostat(const bl_slot_dev &sp, ValF val, int64_t n_list, int64_t n_logical,
+                                    uint64_t &rng, int rng_skip, bl_grec *recs, double *gsum, float *tbuf,
+                                    sel_shared &sh, int &status) {
+  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+  const float T = sp.temperature;
+  const float s0 = val(0) / T;
+  auto termE = [&](float v) { return SEL_EXPF(v / T - s0); };
+  auto termS = [&](int64_t j) { return tbuf[j]; };
+  sel_draw out;
+  out.pos = -1;
+  out.first = 0;
+  out.cut = 0;
+  out.S = 0.0f;
+  /* softmax_prefix over the whole rank */
+  block_records(n_list, val, termE, recs, gsum, tbuf);
+  if (w == 0) {
+    float S;
+    bl_seq_walk(n_list, termS, [&](int64_t g) { return recs[g]; }, false, 0.0f, 0, S, lane);
+    if (lane == 0) {
+      sh.fres[0] = S;
+      sh.ires[1] = 0x7fffffff;
+    }
+  }
+  __syncthreads();
+  const float total = sh.fres[0];
+  const float ln2 = bl_logf(2.0f), mu = sp.mu;
+  /* the cutoff: the first candidate whose surprise exceeds mu */
+  for (int64_t j = t; j < n_list; j += BL_SEL_THREADS) {
+    const float p = tbuf[j] / total;
+    if (!((-bl_logf(p)) / ln2 <= mu)) atomicMin(&sh.ires[1], (int)j);
+  }
+  __syncthreads();
+  const bool past = sh.ires[1] == 0x7fffffff && n_list < n_logical; /* the prefix runs past the list */
+  int64_t cut = sh.ires[1] == 0x7fffffff ? n_list : sh.ires[1];
+  if (cut == 0) cut = 1;
+  __syncthreads();
+  /* softmax_prefix over the cut, then the draw (draw_mirostat_prefix) */
+  block_records(cut, val, termE, recs, gsum, tbuf);
+  if (w == 0) {
+    float S;
+    bl_seq_walk(cut, termS, [&](int64_t g) { return recs[g]; }, false, 0.0f, 0, S, lane);
+    if (lane == 0) sh.fres[2] = S;
+  }
+  __syncthreads();
+  const float total2 = sh.fres[2];
+  __syncthreads();
+  block_records(cut, val, [&](float v) { return termE(v) / total2; }, recs, gsum, tbuf);
+  uint64_t st = rng;
+  for (int k = 0; k < rng_skip; k++) st = bl_xorshift(st);
+  const float draw = bl_rng_f32(&st);
+  if (w == 0) {
+    float S2;
+    const int f = bl_seq_walk(cut, termS, [&](int64_t g) { return recs[g]; }, true, draw, 0, S2, lane);
+    if (lane == 0) sh.ires[2] = f;
+  }
+  __syncthreads();
+  const int f = sh.ires[2];
+  __syncthreads();
+  if (f < 0 && past) { /* the default, last candidate of the prefix lies past the list */
+    status |= BL_SE_UNSUPPORTED;
+    return out;
+  }
+  const int64_t sel = f >= 0 ? f : cut - 1;
+  const float nl = -bl_logf(tbuf[sel]);
+  const float surprise = nl / ln2;
+  const float dd = surprise - sp.mirostat_tau;
+  const float tt = sp.mirostat_eta * dd;
+  if (t == 0) sh.fres[6] = mu - tt;
+  rng = st;
+  out.pos = (int)sel;
+  out.cut = (int)cut;
+  out.S = 1.0f;
+  return out;
+}
+
 /* wavefront-level resolution of the terms [start, 64) of one 64-term group from state (e, N): the group
  * crosses a binade (or its prediction failed), so its terms are added one at a time in float32 from the
  * exact running sum, as the reference's loop does (src/sampling.br:262-264). `a` is this lane's term and
@@ -1943,7 +2025,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
     const float *fv = d.full_v + (int64_t)row * NB * BL_EB;
     const int32_t *fi = d.full_i + (int64_t)row * NB * BL_EB;
     int *boff = reinterpret_cast<int *>(&sh.n); /* [NB + 1]; the normaliser's LDS is free until norm_prep */
-    const bool filt = bl_probs_on(sp);
+    const bool filt = bl_probs_on(sp) || (mode & BL_M_MIRO) != 0; /* the draw-aware cut: plain draws only */
     int nf = 0;
     double s_ap = 0.0; /* the exponent blocks' approximate tempered sum (unfiltered rows) */
     for (int b0 = 0; b0 < NB; b0 += BL_SEL_THREADS) {
@@ -2154,8 +2236,9 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
   __syncthreads();
   auto val = [&](int64_t j) -> float { return keys[j] ? ckey_v(keys[j]) : -1.0e30f; };
   int64_t keep = 1;
-  const bool short_list = n_list <= BL_SERIAL_MAX;
-  if (sampled) {
+  const bool miro = sampled && (mode & BL_M_MIRO) != 0;
+  const bool short_list = !miro && n_list <= BL_SERIAL_MAX;
+  if (sampled && !miro) {
     if (!ranked_supported(sp, n_list, n_logical, keep)) status |= BL_SE_UNSUPPORTED;
     if (!status && short_list) ranked_terms(sp, val, n_list, sh);
   }
@@ -2163,7 +2246,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
   bool typ = false;
   int n_draw = (int)n_list;
   int64_t nlog_draw = n_logical;
-  if (sampled && !status && sp.typical_p < 1.0f && n_logical > 1) {
+  if (sampled && !miro && !status && sp.typical_p < 1.0f && n_logical > 1) {
     if (!short_list || n_list != n_logical) {
       status |= BL_SE_UNSUPPORTED;
     } else {
@@ -2246,7 +2329,8 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
         gsum = d.gsum + (int64_t)row * (V / 64 + 64);
       }
       float *tbuf = reinterpret_cast<float *>(d.sortk + (int64_t)row * 2 * V); /* free once the list is sorted */
-      dr = sample_ranked_long(sp, val, n_list, n_logical, keep, rng, skip, recs, gsum, tbuf, sh, status);
+      dr = miro ? sample_mirostat(sp, val, n_list, n_logical, rng, skip, recs, gsum, tbuf, sh, status)
+                : sample_ranked_long(sp, val, n_list, n_logical, keep, rng, skip, recs, gsum, tbuf, sh, status);
       pos = dr.pos;
       dterm = tbuf;
       dshift = dr.first;
@@ -2364,6 +2448,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
         if (g_on) grammar_commit(d, sp, d.gram[slot], tok);
       }
       sp.rng = rng;
+      if (mode & BL_M_MIRO) sp.mu = sh.fres[6];
     }
     if (status) sp.err |= status;
   }

@@ -69,6 +69,10 @@ typedef struct {
   int32_t ignore_eos;
   float final_softcap;     /* model tail (src/model.br:973-984): 0 = off */
   float logit_mul;         /* model tail: 1 = off */
+  int32_t mirostat;        /* server extras (src/server.br:684-686): 0 off, 2 = sample_mirostat_v2
+                              (src/sampling.br:663-674) on the device; 1 (needs powf) is BL_EUNSUPPORTED */
+  float mirostat_tau;      /* target surprise; the slot's mu starts at 2 tau (src/server.br:936) */
+  float mirostat_eta;
 } bl_params;
 
 void bl_params_default(bl_params *p);

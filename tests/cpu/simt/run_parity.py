@@ -222,6 +222,44 @@ def run_unfiltered(BL, steps, rows=None):
     return None
 
 
+MIRO_ROWS = [(1.0, 5.0, 0.1), (0.7, 3.0, 0.5), (1.5, 8.0, 0.2)]
+
+
+def run_mirostat(BL, steps):
+    """Mirostat v2 rows (temperature, tau, eta) on the small vocabulary's logits (planted ties: the heap's
+    order) against the oracle's sample_mirostat_v2, the running mu carried by both; the final RNG states."""
+    L = O.lib()
+    L.orc_mirostat.restype = O.C.c_int32
+    L.orc_mirostat.argtypes = [O.C.c_int, O.C.POINTER(O.C.c_uint64), O.C.POINTER(O.C.c_float), O.C.c_int64,
+                               O.C.c_float, O.C.c_float, O.C.c_float, O.C.POINTER(O.C.c_float)]
+    R = len(MIRO_ROWS)
+    ctx = BL.Context(SMALL_V, R, R)
+    rng = np.random.default_rng(77)
+    states, mus = [], []
+    for r, (T, tau, eta) in enumerate(MIRO_ROWS):
+        ctx.slot_reset(r, BL.Params(temperature=T, mirostat=2, mirostat_tau=tau, mirostat_eta=eta), BL.seed_rng(300 + r))
+        states.append(O.C.c_uint64(BL.seed_rng(300 + r)))
+        mus.append(O.C.c_float(2.0 * tau))
+    buf = MEM.zeros(R * SMALL_V, np.float32)
+    try:
+        for t in range(steps):
+            xs = [small_case_logits(rng) for _ in range(R)]
+            buf.upload(np.concatenate(xs))
+            tok = ctx.sample_step(list(range(R)), buf.ptr, SMALL_V)[0]
+            for r, (T, tau, eta) in enumerate(MIRO_ROWS):
+                x = np.ascontiguousarray(xs[r])
+                ot = L.orc_mirostat(2, O.C.byref(states[r]), x.ctypes.data_as(O.C.POINTER(O.C.c_float)), SMALL_V, T,
+                                    tau, eta, O.C.byref(mus[r]))
+                if tok[r] != ot:
+                    return f"step {t} row {r}: token {tok[r]} vs {ot} (mu {mus[r].value})"
+        for r in range(R):
+            if ctx.slot_rng(r) != states[r].value:
+                return f"row {r}: final RNG state differs"
+    finally:
+        ctx.close()
+    return None
+
+
 def run_pair(BL, ca, cb, steps):
     """Two small cases stepped together in one call (rows 0 and 1 of an odd-length vocabulary: row 1 starts
     at a 4-byte but not 16-byte aligned address)."""
@@ -605,6 +643,8 @@ def main():
             results.append((f"rows {f[1]} + {f[2]}", run_pair(BL, int(f[1]), int(f[2]), int(f[3]) if len(f) > 3 else 10)))
         elif kind == "bigties":
             results.append(("bf16 ties at V=151936", run_bigties(BL, int(f[1]))))
+        elif kind == "miro":
+            results.append(("mirostat v2 rows", run_mirostat(BL, int(f[1]))))
         elif kind == "unfilt":
             rows = [int(v) for v in f[2].split(",")] if len(f) > 2 else None
             results.append(("unfiltered rows at V=151936", run_unfiltered(BL, int(f[1]), rows)))

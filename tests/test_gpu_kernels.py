@@ -77,6 +77,12 @@ def test_unfiltered_full_vocabulary_rows():
     assert err is None, err
 
 
+def test_mirostat_v2_rows():
+    print("three mirostat v2 rows, V=5003: 40 steps", flush=True)
+    err = RP.run_mirostat(BL, 40)
+    assert err is None, err
+
+
 def test_async_step_equals_sync():
     print("bound rows, asynchronous step: 4 steps", flush=True)
     err = RP.run_async(BL, 4)

@@ -243,6 +243,12 @@ def test_errors_are_reported(cuda):
     with pytest.raises(BL.BLError) as e:
         ctx.slot_reset(0, BL.Params(temperature=1.0, dynatemp_range=0.5, dynatemp_exponent=2.0), 1)
     assert e.value.code == BL.BL_EUNSUPPORTED
+    with pytest.raises(BL.BLError) as e:
+        ctx.slot_reset(0, BL.Params(temperature=1.0, mirostat=1), 1)
+    assert e.value.code == BL.BL_EUNSUPPORTED
+    with pytest.raises(BL.BLError) as e:
+        ctx.slot_reset(0, BL.Params(temperature=1.0, mirostat=2, logprobs=1, post_sampling_probs=1), 1)
+    assert e.value.code == BL.BL_EPARAM and "standard unconstrained sampling chain" in str(e.value)
     # the typical filter over a full-vocabulary list longer than the short-list path: reported at the step
     ctx.slot_reset(0, BL.Params(temperature=1.0, typical_p=0.5), 1)
     row = torch.randn(1000, device=cuda)

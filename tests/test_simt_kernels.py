@@ -63,6 +63,13 @@ def test_heap_tie_order(simt_lib):
     assert "ok   bf16 ties at V=151936" in out
 
 
+def test_mirostat_v2(simt_lib):
+    """Mirostat v2 rows over the full-vocabulary rank with planted ties, the running mu carried across
+    steps, against the oracle's sample_mirostat_v2."""
+    out = _run(simt_lib, ["miro:12"], {"SIMT_ORDER": "rand"})
+    assert "ok   mirostat v2 rows" in out
+
+
 def test_unfiltered_candidate_cut(simt_lib):
     """Full-vocabulary rows without top-p or min-p at V=151936: the candidates cut at half an ulp of the
     draw's running sum (six rows, 12 steps; the bfloat16 row's draws on equal values include one whose heap
