@@ -2401,7 +2401,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
   }
 
   /* outputs, logprobs (src/server.br:1027-1035): alternatives = the first n_probs of the merged list */
-  const float lse = lp_row ? (float)log((double)S_norm) : 0.0f;
+  const float lse = lp_row ? bl_logf(S_norm) : 0.0f; /* sum_exp.ln(), glibc's logf (src/sampling.br:265) */
   if (lp_row) {
     const int n = sp.n_probs < rows.top_stride ? sp.n_probs : rows.top_stride;
     if (t < n) {
