@@ -56,7 +56,7 @@ def cpu_baseline(target_s):
         sec = us.value / 1e6
         if sec >= target_s or steps >= 4096:
             break
-        steps = min(4096, max(steps * 2, int(steps * target_s / max(sec, 1e-3)) + 1))
+        steps = min(4096, steps * 4, max(steps * 2, int(steps * target_s / max(sec, 1e-3)) + 1))
     return {"value": steps / sec, "unit": "steps/s", "cores": 1, "kind": "port",
             "sample": f"first {steps} steps of the workload, 8 rows each, oracle (oracle/liboracle.so) on one "
                       f"host core ({platform.processor() or platform.machine()}, nproc {os.cpu_count()}); "
@@ -78,7 +78,8 @@ def measured_traffic():
 
 
 def cpu_sample(run, target_s, unit_steps=1):
-    """Doubles the oracle's step count until its own timer passes target_s; returns (steps, seconds)."""
+    """Grows the oracle's step count (at most 4x per run: a step's cost can grow with the history, as the
+    grammar path's whole-reply re-decode does) until its own timer passes target_s; returns (steps, seconds)."""
     import ctypes
     steps = 2
     while True:
@@ -87,7 +88,7 @@ def cpu_sample(run, target_s, unit_steps=1):
         sec = us.value / 1e6
         if sec >= target_s or steps >= 4096:
             return steps, sec
-        steps = min(4096, max(steps * 2, int(steps * target_s / max(sec, 1e-3)) + 1))
+        steps = min(4096, steps * 4, max(steps * 2, int(steps * target_s / max(sec, 1e-3)) + 1))
 
 
 def bench_workload(args, wl):

@@ -14,7 +14,7 @@ LIB_PATH = os.path.join(HERE, "libbl_select.so")
 
 BL_OK, BL_EPARAM, BL_EDEVICE, BL_EEMPTY = 0, -1, -2, -3
 BL_EGRAMMAR, BL_EGRAMMAR_DEAD, BL_EGRAMMAR_REJECT, BL_EGRAMMAR_AMBIG = -4, -5, -6, -7
-BL_EUNSUPPORTED, BL_ETIE = -8, -9
+BL_EUNSUPPORTED, BL_ETIE, BL_ESCHEMA = -8, -9, -10
 
 
 class BLError(RuntimeError):
@@ -50,7 +50,7 @@ EXPORTS = [
     "bl_spec_verify", "bl_synth_logits", "bl_math_digest", "bl_workload_ids", "bl_workload_bias",
     "bl_workload_drafts", "bl_set_timing", "bl_get_timing", "bl_set_vocab", "bl_slot_grammar", "bl_grammar_mask",
     "bl_workload_c3_vocab", "bl_step_graph_create", "bl_step_graph_launch", "bl_step_graph_destroy",
-    "bl_stream_sync",
+    "bl_stream_sync", "bl_json_schema_to_gbnf", "bl_slot_schema",
 ]
 
 _lib = None
@@ -97,6 +97,9 @@ def lib():
         L.bl_workload_drafts.argtypes = [C.c_int64, C.c_int64, C.c_int, i32p, C.c_int, C.c_int, i32p]
         L.bl_set_vocab.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int]
         L.bl_slot_grammar.argtypes = [C.c_void_p, C.c_int, C.c_char_p, C.c_size_t]
+        L.bl_json_schema_to_gbnf.argtypes = [C.c_char_p, C.c_size_t, C.c_char_p, C.c_size_t,
+                                             C.POINTER(C.c_size_t)]
+        L.bl_slot_schema.argtypes = [C.c_void_p, C.c_int, C.c_char_p, C.c_size_t]
         L.bl_grammar_mask.argtypes = [C.c_void_p, C.c_int, C.c_void_p, i32p]
         L.bl_workload_c3_vocab.argtypes = [C.c_int64, C.c_int, C.c_void_p, C.c_size_t, C.c_void_p, i32p]
         _lib = L
@@ -230,6 +233,14 @@ class Context:
             t = gbnf.encode() if isinstance(gbnf, str) else bytes(gbnf)
             _check(lib().bl_slot_grammar(self.h, slot, t, len(t)))
 
+    def slot_schema(self, slot, schema):
+        """Attach the grammar of a JSON schema (its JSON text) to `slot` (None detaches)."""
+        if schema is None:
+            _check(lib().bl_slot_schema(self.h, slot, None, 0))
+        else:
+            t = schema.encode() if isinstance(schema, str) else bytes(schema)
+            _check(lib().bl_slot_schema(self.h, slot, t, len(t)))
+
     def grammar_mask(self, slot, d_mask_ptr):
         """Writes ceil(V/32) mask words to device memory; returns forced_eos."""
         f = C.c_int32()
@@ -282,3 +293,14 @@ def seed_rng(seed):
     """seed_rng of src/sampling.br:35-40 (the initial xorshift state for a request seed)."""
     K = 88172645463325252
     return K if seed == 0 else (seed & 0xFFFFFFFFFFFFFFFF) ^ K
+
+
+def json_schema_to_gbnf(schema):
+    """GBNF text of a JSON schema (json_schema_to_gbnf, src/schema_grammar.br:313-337); raises BLError
+    (code BL_ESCHEMA) with the reference's message."""
+    t = schema.encode() if isinstance(schema, str) else bytes(schema)
+    n = C.c_size_t(0)
+    _check(lib().bl_json_schema_to_gbnf(t, len(t), None, 0, C.byref(n)))
+    buf = C.create_string_buffer(n.value + 1)
+    _check(lib().bl_json_schema_to_gbnf(t, len(t), buf, n.value + 1, None))
+    return buf.raw[:n.value].decode()

@@ -16,6 +16,7 @@
 #include "bl_grammar.h"
 #include "bl_internal.h"
 #include "bl_math.h"
+#include "bl_schema.h"
 #include "bl_workload.h"
 
 void bl_launch_step(const bl_dev &d, const float *logits, int64_t ld, const bl_rows &rows, int B, bool need_pass2,
@@ -601,6 +602,33 @@ int bl_slot_grammar(bl_ctx *c, int slot, const char *gbnf, size_t len) {
   HIPCHK(hipMemcpy(c->d.slots + slot, &s, sizeof s, hipMemcpyHostToDevice));
   c->host_slots[slot] = s;
   return BL_OK;
+}
+
+int bl_json_schema_to_gbnf(const char *schema, size_t len, char *out, size_t cap, size_t *out_len) {
+  if (!schema) return fail(BL_EPARAM, "bl_json_schema_to_gbnf: no schema text");
+  std::string gbnf, err;
+  if (bl_schema_to_gbnf(schema, len, gbnf, err)) {
+    g_err = err;
+    return BL_ESCHEMA;
+  }
+  if (out_len) *out_len = gbnf.size();
+  if (out) {
+    if (cap < gbnf.size() + 1)
+      return fail(BL_EPARAM, "bl_json_schema_to_gbnf: the grammar needs %zu bytes, the buffer holds %zu",
+                  gbnf.size() + 1, cap);
+    memcpy(out, gbnf.c_str(), gbnf.size() + 1);
+  }
+  return BL_OK;
+}
+
+int bl_slot_schema(bl_ctx *c, int slot, const char *schema, size_t len) {
+  if (!schema) return bl_slot_grammar(c, slot, nullptr, 0);
+  std::string gbnf, err;
+  if (bl_schema_to_gbnf(schema, len, gbnf, err)) {
+    g_err = "the JSON schema is not supported: " + err; /* the 400 body of src/server.br:738-741 */
+    return BL_ESCHEMA;
+  }
+  return bl_slot_grammar(c, slot, gbnf.data(), gbnf.size());
 }
 
 int bl_grammar_mask(bl_ctx *c, int slot, uint32_t *d_mask_out, int32_t *forced_eos) {

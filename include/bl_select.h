@@ -34,9 +34,11 @@ enum {
   BL_EUNSUPPORTED = -8,    /* a sampler stage this library does not run on the device yet: top_n_sigma,
                               DRY, a dynatemp exponent other than 1 (rejected by bl_slot_reset); XTC on
                               speculative rows; typical_p over a full-vocabulary list above 512 candidates */
-  BL_ETIE = -9             /* a draw on equal logits whose heap order is past the device simulation (more than
+  BL_ETIE = -9,            /* a draw on equal logits whose heap order is past the device simulation (more than
                               8192 values at or above the tied one), equal allowed maxima of a grammar row, or
                               post-sampling alternatives of a full-vocabulary rank that meet equal values */
+  BL_ESCHEMA = -10         /* a JSON schema that does not parse (src/json.br json_parse messages) or that
+                              json_schema_to_gbnf rejects (src/schema_grammar.br messages) */
 };
 
 /* SamplingParams (src/model.br:1565-1584) + the per-request server fields (src/server.br:665-760).
@@ -114,6 +116,18 @@ int bl_set_vocab(bl_ctx *ctx, const uint8_t *blob, const uint32_t *offsets, int 
  * BL_EGRAMMAR_AMBIG, BL_EUNSUPPORTED (temperature > 0, or a grammar whose reachable automaton exceeds
  * 65536 states: a recursive one). */
 int bl_slot_grammar(bl_ctx *ctx, int slot, const char *gbnf, size_t len);
+
+/* JSON Schema -> GBNF (json_schema_to_gbnf, src/schema_grammar.br:313-337, over the schema text parsed as
+ * src/json.br's json_parse does; the text must be UTF-8). Writes the NUL-terminated grammar into `out`
+ * (`cap` bytes) and its length into *out_len (either may be NULL: out = NULL only reports the length).
+ * BL_ESCHEMA with the reference's message; BL_EPARAM when `cap` is too small. */
+int bl_json_schema_to_gbnf(const char *schema, size_t len, char *out, size_t cap, size_t *out_len);
+
+/* Attach the grammar of a JSON schema to a slot: a request's response_format json_schema (src/server.br:733-745:
+ * the schema is compiled to GBNF, then parsed as the slot's grammar), with bl_slot_grammar's rules and errors.
+ * BL_ESCHEMA reads "the JSON schema is not supported: <message>" (src/server.br:738-741). schema = NULL
+ * detaches. */
+int bl_slot_schema(bl_ctx *ctx, int slot, const char *schema, size_t len);
 
 /* The slot's allow-bitmask for the next token (the `allowed` predicate of src/server.br:334-350 over
  * every vocabulary id, including the EOG rule): ceil(vocab/32) words into device memory, bit t of

@@ -452,8 +452,10 @@ def run_bigk(BL, steps):
 GOLDEN = os.path.join(ROOT, "tests", "golden")
 
 
-def run_w3(BL, steps, check_masks=True):
-    """Workload 3: greedy decode under the config-3 JSON-Schema grammar, masks and tokens per step."""
+def run_w3(BL, steps, check_masks=True, schema=None):
+    """Workload 3: greedy decode under the config-3 JSON-Schema grammar, masks and tokens per step. With
+    `schema` (the schema's JSON text) the slot is constrained through bl_slot_schema instead of the
+    committed GBNF text."""
     V, seed = 151936, 3
     L = O.lib()
     L.orc_set_eog_tokens(O.ip(O.i32([0])), 0, -1)
@@ -469,7 +471,10 @@ def run_w3(BL, steps, check_masks=True):
 
     def restart():
         ctx.slot_reset(0, BL.Params(), BL.seed_rng(seed))
-        ctx.slot_grammar(0, gbnf)
+        if schema is None:
+            ctx.slot_grammar(0, gbnf)
+        else:
+            ctx.slot_schema(0, schema)
 
     restart()
     buf = MEM.zeros(V, np.float32)
@@ -652,6 +657,11 @@ def main():
             results.append(("large top-k / n_probs", run_bigk(BL, int(f[1]))))
         elif kind == "w3":
             results.append(("workload 3", run_w3(BL, int(f[1]))))
+        elif kind == "w3schema":  # the same decode with the slot constrained through bl_slot_schema
+            schema = ('{"type":"object","properties":{"name":{"type":"string","pattern":"^[a-z_]+$"},'
+                      '"count":{"type":"integer"},"tags":{"type":"array","items":{"type":"string"}}},'
+                      '"required":["name","count","tags"]}')
+            results.append(("workload 3 via the schema entry point", run_w3(BL, int(f[1]), schema=schema)))
         elif kind == "grammar":
             for c in parse_range(f[1]):
                 results.append((f"grammar case {c}", run_grammar_case(BL, c, int(f[2]) if len(f) > 2 else 30)))

@@ -44,6 +44,39 @@ def test_workload3_masks_and_tokens():
     assert err is None, err
 
 
+def test_workload3_through_the_schema_entry_point():
+    # response_format json_schema (src/server.br:733-745): the schema text itself, compiled by the library
+    from test_oracle_grammar import C3_SCHEMA
+    say("workload 3 via bl_slot_schema: 64 greedy grammar steps, masks and tokens")
+    err = RP.run_w3(BL, 64, schema=C3_SCHEMA)
+    assert err is None, err
+
+
+def test_schema_errors_on_a_slot():
+    say("schema errors on a slot")
+    blob, off, eos = RP.grammar_vocab(np.random.default_rng(1), 50)
+    V = len(off) - 1
+    ctx = BL.Context(V, 1, 1)
+    ctx.set_eog(eos, [])
+    ctx.set_vocab(blob, off)
+    ctx.slot_reset(0, BL.Params(), 1)
+    with pytest.raises(BL.BLError) as e:
+        ctx.slot_schema(0, '{"type":"tuple"}')
+    assert e.value.code == BL.BL_ESCHEMA
+    assert "the JSON schema is not supported: unsupported schema type 'tuple'" in str(e.value)
+    with pytest.raises(BL.BLError) as e:  # a recursive schema has no finite automaton
+        ctx.slot_schema(0, '{"$ref":"#/$defs/n","$defs":{"n":{"type":"object","properties":'
+                           '{"next":{"anyOf":[{"$ref":"#/$defs/n"},{"type":"null"}]}}}}}')
+    assert e.value.code == BL.BL_EUNSUPPORTED
+    ctx.slot_schema(0, '{"enum":["{", "{}"]}')  # a valid schema attaches
+    x = np.full(V, -1.0, np.float32)
+    x[ord("}")] = 7.0
+    x[ord('"')] = 5.0
+    buf = torch.from_numpy(x).to("cuda:0")
+    assert ctx.sample_step([0], buf.data_ptr(), V)[0][0] == ord('"')
+    ctx.close()
+
+
 @pytest.mark.parametrize("case", range(len(RP.GRAMMAR_CASES)))
 def test_grammar_cases(case):
     say(f"grammar case {case}: {RP.GRAMMAR_CASES[case]!r}")

@@ -91,8 +91,9 @@ def test_grammar_masks_and_tokens(simt_lib):
     """The grammar path (GBNF automaton tables, per-token mask walk, masked greedy, on-device commit of
     the reply position) against the oracle's whole-reply re-decode: workload 3 and seven adversarial
     byte-level vocabularies."""
-    out = _run(simt_lib, ["w3:3", "grammar:0-6:40"], {"SIMT_ORDER": "rand"})
-    assert "ok   workload 3" in out and out.count("ok   grammar case") == 7
+    out = _run(simt_lib, ["w3:3", "w3schema:3", "grammar:0-6:40"], {"SIMT_ORDER": "rand"})
+    assert "ok   workload 3\n" in out and "ok   workload 3 via the schema entry point" in out
+    assert out.count("ok   grammar case") == 7
 
 
 def test_small_cases_address_sanitizer():
