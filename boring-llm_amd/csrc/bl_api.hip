@@ -8,6 +8,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <chrono>
 #include <string>
 #include <unordered_map>
 #include <vector>
@@ -26,6 +27,17 @@ void bl_launch_synth(float *out, int64_t ld, int cfg, int64_t seed, int64_t step
 void bl_launch_math_digest(int fn, uint32_t first_block, int n_blocks, unsigned long long *out, hipStream_t s);
 
 static thread_local std::string g_err;
+
+/* Waits for the stream's work: polls it for up to 2 ms (a step completes within tens of microseconds, and
+ * a blocking wait adds the interrupt's wake-up to its latency), then blocks. */
+static hipError_t wait_stream(hipStream_t s) {
+  const auto until = std::chrono::steady_clock::now() + std::chrono::milliseconds(2);
+  for (;;) {
+    const hipError_t e = hipStreamQuery(s);
+    if (e != hipErrorNotReady) return e;
+    if (std::chrono::steady_clock::now() >= until) return hipStreamSynchronize(s);
+  }
+}
 
 static int fail(int code, const char *fmt, ...) {
   char buf[512];
@@ -54,6 +66,9 @@ struct bl_ctx {
   float *d_lp = nullptr, *d_top_lp = nullptr;
   int32_t *h_slot = nullptr, *h_tok = nullptr, *h_status = nullptr, *h_top_ids = nullptr, *h_skip = nullptr;
   float *h_lp = nullptr, *h_top_lp = nullptr;
+  /* the synchronous step's outputs packed in one block per side: tokens, statuses, logprobs, top ids, top
+   * logprobs of the call's B rows back to back, so one copy brings them to the host */
+  int32_t *d_out = nullptr, *h_out = nullptr;
   int32_t *d_commit_toks = nullptr;
   int32_t *d_mslot = nullptr; /* row table of bl_grammar_mask */
   int32_t *d_bslot = nullptr, *d_acc = nullptr, *h_acc = nullptr; /* speculative verification: slots, accepted */
@@ -278,6 +293,7 @@ int bl_create(int device, int max_slots, int max_rows, int vocab, bl_ctx **out) 
   ALLOC(c->d_mslot, 1);
   ALLOC(c->d_bslot, R);
   ALLOC(c->d_acc, R);
+  ALLOC(c->d_out, R * (3 + 2 * 256));
 #undef ALLOC
   d.n_eog = 0;
   if (hipHostMalloc((void **)&c->h_slot, R * sizeof(int32_t)) != hipSuccess ||
@@ -287,7 +303,8 @@ int bl_create(int device, int max_slots, int max_rows, int vocab, bl_ctx **out) 
       hipHostMalloc((void **)&c->h_lp, R * sizeof(float)) != hipSuccess ||
       hipHostMalloc((void **)&c->h_top_ids, R * 256 * sizeof(int32_t)) != hipSuccess ||
       hipHostMalloc((void **)&c->h_top_lp, R * 256 * sizeof(float)) != hipSuccess ||
-      hipHostMalloc((void **)&c->h_acc, R * sizeof(int32_t)) != hipSuccess) {
+      hipHostMalloc((void **)&c->h_acc, R * sizeof(int32_t)) != hipSuccess ||
+      hipHostMalloc((void **)&c->h_out, R * (3 + 2 * 256) * sizeof(int32_t)) != hipSuccess) {
     bl_destroy(c);
     return fail(BL_EDEVICE, "hipHostMalloc failed");
   }
@@ -315,7 +332,7 @@ void bl_destroy(bl_ctx *c) {
   }
   if (c->d_vblob) hipFree(c->d_vblob);
   if (c->d_voff) hipFree(c->d_voff);
-  void *hp[] = {c->h_slot, c->h_skip, c->h_tok, c->h_status, c->h_lp, c->h_top_ids, c->h_top_lp, c->h_acc};
+  void *hp[] = {c->h_slot, c->h_skip, c->h_tok, c->h_status, c->h_lp, c->h_top_ids, c->h_top_lp, c->h_acc, c->h_out};
   for (void *p : hp)
     if (p) hipHostFree(p);
   for (hipEvent_t e : c->ev)
@@ -720,25 +737,30 @@ int bl_sample_step(bl_ctx *c, const int32_t *slots, int B, const float *d_logits
   if (top_stride < 0 || top_stride > 256) return fail(BL_EPARAM, "top_stride must be in 0..256");
   hipSetDevice(c->device);
   memcpy(c->h_slot, slots, B * sizeof(int32_t));
-  HIPCHK(hipMemcpyAsync(c->d_slot, c->h_slot, B * sizeof(int32_t), hipMemcpyHostToDevice, c->stream));
+  /* rows past the inline slot indices read the device table */
+  if (B > BL_ROWS_INLINE)
+    HIPCHK(hipMemcpyAsync(c->d_slot, c->h_slot, B * sizeof(int32_t), hipMemcpyHostToDevice, c->stream));
   bl_rows rows = make_rows(c, false, 1, top_stride > 0 ? top_stride : 1);
+  const int ts = top_stride;
+  rows.tok = c->d_out;
+  rows.status = c->d_out + B;
+  rows.lp = reinterpret_cast<float *>(c->d_out + 2 * B);
+  if (ts > 0) {
+    rows.top_ids = c->d_out + 3 * B;
+    rows.top_lp = reinterpret_cast<float *>(c->d_out + 3 * B + B * ts);
+  }
   mark_stepped(c, slots, B);
   bl_launch_step(c->d, d_logits, ld, rows, B, needs_pass2(c, slots, B), needs_gram(c, slots, B), c->stream, nullptr);
   HIPCHK(hipGetLastError());
-  HIPCHK(hipMemcpyAsync(c->h_tok, c->d_tok, B * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));
-  HIPCHK(hipMemcpyAsync(c->h_status, c->d_status, B * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));
-  HIPCHK(hipMemcpyAsync(c->h_lp, c->d_lp, B * sizeof(float), hipMemcpyDeviceToHost, c->stream));
-  if (top_stride > 0) {
-    HIPCHK(hipMemcpyAsync(c->h_top_ids, c->d_top_ids, (size_t)B * top_stride * 4, hipMemcpyDeviceToHost, c->stream));
-    HIPCHK(hipMemcpyAsync(c->h_top_lp, c->d_top_lp, (size_t)B * top_stride * 4, hipMemcpyDeviceToHost, c->stream));
-  }
-  HIPCHK(hipStreamSynchronize(c->stream));
+  HIPCHK(hipMemcpyAsync(c->h_out, c->d_out, (size_t)(3 * B + 2 * B * ts) * 4, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(wait_stream(c->stream));
+  const int32_t *h = c->h_out;
   int st = 0;
-  for (int i = 0; i < B; i++) st |= c->h_status[i];
-  memcpy(tokens, c->h_tok, B * sizeof(int32_t));
-  if (logprobs) memcpy(logprobs, c->h_lp, B * sizeof(float));
-  if (top_ids && top_stride > 0) memcpy(top_ids, c->h_top_ids, (size_t)B * top_stride * 4);
-  if (top_logprobs && top_stride > 0) memcpy(top_logprobs, c->h_top_lp, (size_t)B * top_stride * 4);
+  for (int i = 0; i < B; i++) st |= h[B + i];
+  memcpy(tokens, h, B * sizeof(int32_t));
+  if (logprobs) memcpy(logprobs, h + 2 * B, B * sizeof(float));
+  if (top_ids && ts > 0) memcpy(top_ids, h + 3 * B, (size_t)B * ts * 4);
+  if (top_logprobs && ts > 0) memcpy(top_logprobs, h + 3 * B + B * ts, (size_t)B * ts * 4);
   return status_error(st);
 }
 
@@ -822,7 +844,7 @@ int bl_step_graph_destroy(void *graph) {
 
 int bl_stream_sync(bl_ctx *c) {
   if (!c) return fail(BL_EPARAM, "null context");
-  HIPCHK(hipStreamSynchronize(c->stream));
+  HIPCHK(wait_stream(c->stream));
   return BL_OK;
 }
 
@@ -880,7 +902,7 @@ int bl_spec_verify(bl_ctx *c, const int32_t *slots, int B, int k, const float *d
   HIPCHK(hipMemcpyAsync(c->h_tok, c->d_tok, R * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));
   HIPCHK(hipMemcpyAsync(c->h_status, c->d_status, R * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));
   HIPCHK(hipMemcpyAsync(c->h_acc, c->d_acc, B * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));
-  HIPCHK(hipStreamSynchronize(c->stream));
+  HIPCHK(wait_stream(c->stream));
   int st = 0;
   for (int i = 0; i < R; i++) st |= c->h_status[i];
   memcpy(tokens, c->h_tok, R * sizeof(int32_t));

@@ -159,13 +159,20 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass(bl_dev d, const fl
   const int c = blockIdx.x, row = blockIdx.y, t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int slot = bl_row_slot(rows, row);
   const bl_slot_dev &sp = slot_of(d, slot);
-  __shared__ float xs[BL_CH];
-  __shared__ uint32_t hist[2048];
+  /* LDS kept under 20 KB so that eight workgroups fit a CU. The chunk's values (logprob sums, then the
+   * radix fallback) and the compacted keys (the counting rank) are never live together. */
+  __shared__ union {
+    float xs[BL_CH];
+    uint64_t tkeys[BL_TK_CAP]; /* keys at or above the bound */
+  } lds;
+  static_assert(BL_TK_CAP * 8 <= BL_CH * 4, "the key list fits in the value area");
+  float *const xs = lds.xs;
+  uint64_t *const tkeys = lds.tkeys;
+  __shared__ uint32_t hist[256];
   __shared__ float red_m[4];
   __shared__ int red_i[4];
   __shared__ uint32_t sel[4];
   __shared__ int out_n;
-  __shared__ uint64_t tkeys[BL_TK_CAP];      /* keys at or above the bound */
   __shared__ uint32_t tk_wb[BL_RP_THREADS / 64];
   __shared__ int tk_n;
 
@@ -293,7 +300,7 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass(bl_dev d, const fl
     for (int k = 1; k < BL_RP_THREADS / 64; k++) argmax_merge(cm, ci, red_m[k], red_i[k]);
     const int64_t o = (int64_t)row * nc + c;
     if (sp.mode & BL_M_LOGPROBS) {
-      float *red_s = xs; /* [BL_SUBS][BL_RP_THREADS]; xs is free until the radix fallback */
+      float *red_s = xs; /* [BL_SUBS][BL_RP_THREADS]; the value area is free until the key list */
 #pragma unroll
       for (int j = 0; j < NV; j++) {
         float sj = 0.0f;
@@ -402,9 +409,9 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass(bl_dev d, const fl
   uint32_t prefix = 0u, pmask = 0u;
   int need = K;
   bool take_all = false;
-  for (int pass = 0; pass < 3; pass++) {
-    const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
-    const int nb = pass == 2 ? 1024 : 2048;
+  for (int pass = 0; pass < 4; pass++) { /* 8 bits of the order key per pass, from the top */
+    const int shift = 24 - 8 * pass;
+    constexpr int nb = 256;
     for (int b = t; b < nb; b += BL_RP_THREADS) hist[b] = 0u;
     __syncthreads();
     for (int i = t; i < cnt; i += BL_RP_THREADS) {

@@ -249,6 +249,8 @@ inline hipError_t hipStreamCreateWithFlags(hipStream_t *s, unsigned) {
 }
 inline hipError_t hipStreamDestroy(hipStream_t) { return hipSuccess; }
 inline hipError_t hipStreamSynchronize(hipStream_t) { return hipSuccess; }
+enum { hipErrorNotReady = 600 };
+inline hipError_t hipStreamQuery(hipStream_t) { return hipSuccess; } /* launches run to completion */
 inline hipError_t hipEventCreate(hipEvent_t *e) {
   *e = (hipEvent_t)0x1;
   return hipSuccess;
