@@ -519,13 +519,12 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass(bl_dev d, const fl
  * Keys stay in registers when the lists hold at most BL_MERGE_REG per thread, and are re-read from memory
  * per pass otherwise. Returns the K-th key of the merged prefixes (0 when they hold fewer than K).
  */
-#define BL_MERGE_REG 16
+#define BL_MERGE_REG 8 /* keys per thread held in registers: 8 keeps the exponent pass at 50 VGPRs (8 waves/SIMD) */
 #define BL_MERGE_CAP 512
 #define BL_MERGE_L 16      /* keys per list of the first, prefix-only merge */
 #define BL_MERGE_PREFIX 1024 /* the prefix merge's key budget (nc * L) */
 static_assert(BL_MERGE_CAP >= BL_KSEL_MAX, "the last radix pass leaves exactly K keys");
-template <class KF>
-__device__ uint64_t merge_lists(const bl_dev &d, int row, KF get_k, int L, int &K_out, int *cut_out) {
+__device__ uint64_t merge_lists(const bl_dev &d, int row, int K, int L, int cap) {
   constexpr int NT = BL_RP_THREADS;
   const int nc = d.nc, t = threadIdx.x;
   const int total = nc * L;
@@ -535,43 +534,25 @@ __device__ uint64_t merge_lists(const bl_dev &d, int row, KF get_k, int L, int &
   __shared__ uint64_t surv[BL_MERGE_CAP];
   __shared__ int s_cnt;
   __shared__ uint64_t s_kth;
-  /* the id and the value are loaded together (no load waits on another), for every key in registers
-   * before the row's K is read */
   auto load_key = [&](int i) -> uint64_t {
     const int ch = i / L, q = i - ch * L;
     const int64_t o = ((int64_t)row * nc + ch) * BL_KSEL_MAX + q;
     const int32_t id = d.cand_i[o];
-    const float v = d.cand_v[o];
-    return id >= 0 ? ckey(v, id) : 0ull;
+    return id >= 0 ? ckey(d.cand_v[o], id) : 0ull;
   };
   const bool inreg = total <= NT * BL_MERGE_REG;
   uint64_t kr[BL_MERGE_REG];
 #pragma unroll
   for (int j = 0; j < BL_MERGE_REG; j++) {
     const int i = t + j * NT;
-    kr[j] = 0ull;
-    if (inreg && j * NT < total) { /* uniform: loads of every j are in flight together */
-      const uint64_t k = load_key(i < total ? i : total - 1);
-      kr[j] = i < total ? k : 0ull;
-    }
-  }
-  /* the row pass wrote K keys per list: positions past K are not this step's */
-  const int K = get_k();
-  K_out = K;
-  if (K <= 0) return 0ull;
-  const int cap = K <= 96 ? 128 : BL_MERGE_CAP;
-  auto listed = [&](int i) { return i - (i / L) * L < K; };
-  if (inreg && K < L) {
-#pragma unroll
-    for (int j = 0; j < BL_MERGE_REG; j++)
-      if (!listed(t + j * NT)) kr[j] = 0ull;
+    kr[j] = inreg && i < total ? load_key(i) : 0ull;
   }
   auto each = [&](auto f) {
     if (inreg) {
 #pragma unroll
       for (int j = 0; j < BL_MERGE_REG; j++) f(kr[j]);
     } else {
-      for (int i = t; i < total; i += NT) f(listed(i) ? load_key(i) : 0ull);
+      for (int i = t; i < total; i += NT) f(load_key(i));
     }
   };
   /* valid keys */
@@ -621,12 +602,8 @@ __device__ uint64_t merge_lists(const bl_dev &d, int row, KF get_k, int L, int &
   for (int i = t; i < ns; i += NT) {
     const uint64_t k = surv[i];
     int r = 0, j = 0;
-    for (; j + 8 <= ns; j += 8) {
-      int r8 = 0;
-#pragma unroll
-      for (int u = 0; u < 8; u++) r8 += surv[j + u] > k ? 1 : 0;
-      r += r8;
-    }
+    for (; j + 4 <= ns; j += 4)
+      r += (surv[j] > k ? 1 : 0) + (surv[j + 1] > k ? 1 : 0) + (surv[j + 2] > k ? 1 : 0) + (surv[j + 3] > k ? 1 : 0);
     for (; j < ns; j++) r += surv[j] > k ? 1 : 0;
     if (r < K) out[r] = k;
     if (r == K - 1) s_kth = k;
@@ -634,51 +611,32 @@ __device__ uint64_t merge_lists(const bl_dev &d, int row, KF get_k, int L, int &
   for (int q = ns + t; q < K; q += NT) out[q] = 0ull;
   __syncthreads();
   const uint64_t kth = s_kth;
-  if (cut_out) {
-    /* a list cut above the K-th key: its L-th key (the last one read) ranks above it */
-    __shared__ int s_cut;
-    if (t == 0) s_cut = 0;
-    __syncthreads();
-    int mine_cut = 0;
-    if (inreg) {
-#pragma unroll
-      for (int j = 0; j < BL_MERGE_REG; j++) {
-        const int i = t + j * NT;
-        if (i < total && i - (i / L) * L == L - 1 && kr[j] != 0ull && kr[j] > kth) mine_cut = 1;
-      }
-    } else {
-      for (int ch = t; ch < nc; ch += NT) {
-        const uint64_t k = load_key(ch * L + L - 1);
-        if (k != 0ull && k > kth) mine_cut = 1;
-      }
-    }
-    if (mine_cut) s_cut = 1;
-    __syncthreads();
-    *cut_out = s_cut;
-  }
   __syncthreads();
   return kth;
 }
 
-/* The merge from the first L keys of every list (loaded while the row's K is still being read) is the row's
- * exact top K when K <= L (each list's top K lies in its first L keys), and otherwise unless some list was
- * cut while its last key read is above the K-th key found (then its unread keys could rank in the top K):
- * that case merges the whole lists. */
-template <class KF>
-__device__ void merge_topk(const bl_dev &d, int row, KF get_k) {
+/* The merge from the first L keys of every list is the row's exact top K unless some list was cut while its
+ * last key read is above the K-th key found (then its unread keys could rank in the top K): that case, and
+ * K <= L, merge the whole lists. */
+__device__ void merge_topk(const bl_dev &d, int row, int K) {
   const int nc = d.nc, t = threadIdx.x;
   const int L = min(BL_MERGE_L, BL_MERGE_PREFIX / nc);
-  int K = 0;
-  if (L < 1) {
-    K = get_k();
-    if (K <= 0) return;
-  } else {
-    int cut = 0;
-    merge_lists(d, row, get_k, L, K, &cut);
-    if (K <= L || !cut) return;
+  if (L >= 1 && L < K) {
+    __shared__ int s_cut;
+    const uint64_t kth = merge_lists(d, row, K, L, K <= 96 ? 128 : BL_MERGE_CAP);
+    if (t == 0) s_cut = 0;
+    __syncthreads();
+    for (int ch = t; ch < nc; ch += BL_RP_THREADS) {
+      const int64_t o = ((int64_t)row * nc + ch) * BL_KSEL_MAX + (L - 1);
+      const int32_t id = d.cand_i[o];
+      if (id >= 0 && ckey(d.cand_v[o], id) > kth) s_cut = 1;
+    }
+    __syncthreads();
+    const int cut = s_cut;
+    __syncthreads();
+    if (!cut) return;
   }
-  int K2;
-  merge_lists(d, row, [K] { return K; }, K, K2, nullptr);
+  merge_lists(d, row, K, K, BL_MERGE_CAP);
 }
 
 /* grid (1 + ceil(V / BL_EB), B) x 256. The first B workgroups in dispatch order merge the top-K candidates
@@ -697,7 +655,7 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_exppass(bl_dev d, bl_rows 
   const bl_slot_dev &sp = slot_of(d, slot);
   const int mode = sp.mode;
   if (merger) {
-    merge_topk(d, row, [&] { return sp.k_sel; });
+    if (sp.k_sel > 0) merge_topk(d, row, sp.k_sel);
     return;
   }
   if (!(mode & (BL_M_LOGPROBS | BL_M_FULL))) return;
