@@ -72,6 +72,8 @@ struct bl_ctx {
   int32_t *d_commit_toks = nullptr;
   int32_t *d_mslot = nullptr; /* row table of bl_grammar_mask */
   int32_t *d_bslot = nullptr, *d_acc = nullptr, *h_acc = nullptr; /* speculative verification: slots, accepted */
+  bl_sdelta *d_delta = nullptr; /* speculative rows' count corrections [rows][BL_SPEC_DCAP] */
+  int32_t *d_delta_n = nullptr;
   int bound_B = 0;
   std::vector<void *> allocs;
   bool timing = false;
@@ -180,6 +182,35 @@ __global__ void bl_k_spec_commit(bl_dev d, const int32_t *slots, const int32_t *
   commit_one(d, sp, slot, tb[a]);
   if (sp.temperature > 0.0f)
     for (int q = 0; q <= a; q++) sp.rng = bl_xorshift(sp.rng);
+}
+
+/*
+ * Count corrections of speculative rows: row i of sequence b is sampled as if drafts[0..i) had been pushed
+ * to tokens and reply_tokens (src/server.br:1173-1216), as commit_one would push them: each draft adds one
+ * to its reply count and, while it is still in the repeat window, to its window count; once the window holds
+ * repeat_last_n tokens each push evicts the oldest ring entry. One thread per row.
+ */
+__global__ void bl_k_spec_delta(bl_dev d, const int32_t *slots, const int32_t *drafts, int k, bl_sdelta *delta,
+                                int32_t *delta_n) {
+  const int b = blockIdx.x, i = threadIdx.x;
+  if (i > k) return;
+  const int slot = slots[b];
+  const bl_slot_dev &sp = d.slots[slot];
+  const int32_t *db = drafts + (int64_t)b * k;
+  bl_sdelta *out = delta + ((int64_t)b * (k + 1) + i) * BL_SPEC_DCAP;
+  const int rl = sp.repeat_last_n;
+  int n = 0;
+  for (int j = 0; j < i; j++) {
+    const int dc = sp.fp_on ? 1 : 0;
+    const int dw = sp.rep_on && (rl < 0 || j >= i - rl) ? 1 : 0;
+    if (dc || dw) out[n++] = bl_sdelta{db[j], (int16_t)dc, (int16_t)dw};
+  }
+  if (sp.rep_on && rl > 0) {
+    const int leave = min(max(sp.win_len + i - rl, 0), sp.win_len);
+    const int32_t *ring = d.ring + (int64_t)slot * BL_WCAP;
+    for (int m = 0; m < leave; m++) out[n++] = bl_sdelta{ring[(sp.win_head + m) % rl], 0, -1};
+  }
+  delta_n[(int64_t)b * (k + 1) + i] = n;
 }
 
 __global__ void bl_k_bump(float *out, const int32_t *ids, int n, float add) {
@@ -294,6 +325,8 @@ int bl_create(int device, int max_slots, int max_rows, int vocab, bl_ctx **out) 
   ALLOC(c->d_bslot, R);
   ALLOC(c->d_acc, R);
   ALLOC(c->d_out, R * (3 + 2 * 256));
+  ALLOC(c->d_delta, R * BL_SPEC_DCAP);
+  ALLOC(c->d_delta_n, R);
 #undef ALLOC
   d.n_eog = 0;
   if (hipHostMalloc((void **)&c->h_slot, R * sizeof(int32_t)) != hipSuccess ||
@@ -871,10 +904,18 @@ int bl_spec_verify(bl_ctx *c, const int32_t *slots, int B, int k, const float *d
   if (k < 0 || R > c->d.max_rows || !d_rows || !tokens || !accepted || ld < c->d.vocab || (k > 0 && !drafts) ||
       (int64_t)B * k > 4096)
     return fail(BL_EPARAM, "bl_spec_verify: invalid arguments (B %d, k %d)", B, k);
+  bool pen = false; /* a sequence whose rows' penalties depend on the drafts before them */
   for (int b = 0; b < B; b++) {
     const bl_slot_dev &s = c->host_slots[slots[b]];
-    if (k > 0 && (s.fp_on || s.rep_on))
-      return fail(BL_EUNSUPPORTED, "speculative rows with history-dependent penalties are not supported on the device");
+    if (k > 0 && (s.fp_on || s.rep_on)) {
+      if (2 * k > BL_SPEC_DCAP)
+        return fail(BL_EUNSUPPORTED, "speculative rows with history-dependent penalties take at most %d drafts",
+                    BL_SPEC_DCAP / 2);
+      for (int i = 0; i < k; i++)
+        if (drafts[b * k + i] < 0 || drafts[b * k + i] >= c->d.vocab)
+          return fail(BL_EPARAM, "bl_spec_verify: draft token %d is outside the vocabulary", drafts[b * k + i]);
+      pen = true;
+    }
     if (s.g_on) return fail(BL_EUNSUPPORTED, "speculative rows of a grammar-constrained slot are not supported on the device");
     /* each row's draw starts at its position in the RNG chain; an XTC chance draw would shift the rest */
     if (k > 0 && s.temperature > 0.0f && s.xtc_probability > 0.0f && s.xtc_threshold <= 0.5f)
@@ -894,6 +935,13 @@ int bl_spec_verify(bl_ctx *c, const int32_t *slots, int B, int k, const float *d
   HIPCHK(hipMemcpyAsync(c->d_bslot, slots, B * sizeof(int32_t), hipMemcpyHostToDevice, c->stream));
   bl_rows rows = make_rows(c, true, 0, 1);
   rows.lp = nullptr; /* no logprobs are returned for speculative rows */
+  if (pen) {
+    hipLaunchKernelGGL(bl_k_spec_delta, dim3(B), dim3(64), 0, c->stream, c->d, c->d_bslot, c->d_commit_toks, k,
+                       c->d_delta, c->d_delta_n);
+    HIPCHK(hipGetLastError());
+    rows.delta = c->d_delta;
+    rows.delta_n = c->d_delta_n;
+  }
   mark_stepped(c, slots, B);
   bl_launch_step(c->d, d_rows, ld, rows, R, needs_pass2(c, slots, B), false, c->stream, nullptr);
   hipLaunchKernelGGL(bl_k_spec_commit, dim3(B), dim3(64), 0, c->stream, c->d, c->d_bslot, c->d_commit_toks, k,

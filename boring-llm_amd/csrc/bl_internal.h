@@ -76,6 +76,16 @@ struct alignas(16) bl_tok {
   uint32_t flags; /* BL_TF_* */
 };
 
+/* A speculative row's correction to one token's counts: row i of a sequence is sampled with the drafts
+ * before it appended to the history (src/server.br:1173-1216), so each such draft adds to its reply count
+ * and window count, and window entries the drafts push out subtract from theirs. */
+#define BL_SPEC_DCAP 64 /* corrections per row: drafts before the row plus the entries they evict */
+struct bl_sdelta {
+  int32_t tok;
+  int16_t dcnt;  /* reply count */
+  int16_t dwcnt; /* repeat-window count */
+};
+
 struct bl_slot_dev {
   /* parameters (SamplingParams, src/model.br:1565-1584, and server extras) */
   float temperature, dynatemp_range, dynatemp_exponent, top_n_sigma;
@@ -153,6 +163,8 @@ struct bl_rows {
   float *top_lp;
   int32_t top_stride;
   int32_t *status;         /* [B] */
+  const bl_sdelta *delta;  /* [B][BL_SPEC_DCAP] speculative rows' count corrections, or null */
+  const int32_t *delta_n;  /* [B] corrections of each row */
 };
 
 #if defined(__HIPCC__)

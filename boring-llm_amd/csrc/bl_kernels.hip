@@ -153,8 +153,11 @@ __device__ double block_excl_scan_d(double x, double *sd, double *total) {
 }
 
 /* ------------------------------------------------------------------ K1: row pass */
-__global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass(bl_dev d, const float *__restrict__ logits, int64_t ld,
-                                                              bl_rows rows) {
+/* SPEC: the row may carry speculative count corrections (compiled separately: the correction loops
+ * cost the ordinary row pass registers) */
+template <bool SPEC>
+__device__ __forceinline__ void rowpass_body(const bl_dev &d, const float *__restrict__ logits, int64_t ld,
+                                             const bl_rows &rows) {
   const int V = d.vocab, nc = d.nc;
   const int c = blockIdx.x, row = blockIdx.y, t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int slot = bl_row_slot(rows, row);
@@ -230,6 +233,16 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass(bl_dev d, const fl
       tb[j] = p < cnt ? (tw[(i0 + p) >> 5] >> ((i0 + p) & 31)) & 0xFu : 0u;
       any |= tb[j] != 0u;
     }
+    /* a speculative row's count corrections: bit k of dm marks this thread's position k */
+    const int nd = SPEC && rows.delta ? rows.delta_n[row] : 0;
+    const bl_sdelta *dl = SPEC && rows.delta ? rows.delta + (int64_t)row * BL_SPEC_DCAP : nullptr;
+    uint32_t dm = 0u;
+    for (int e = 0; e < nd; e++) {
+      const int p = dl[e].tok - i0;
+      if (p >= 0 && p < cnt && ((p & (4 * BL_RP_THREADS - 1)) >> 2) == t)
+        dm |= 1u << ((p / (4 * BL_RP_THREADS)) * 4 + (p & 3));
+    }
+    any |= dm != 0u;
     if (any) {
       const int64_t so = (int64_t)slot * V + i0;
       const bool fp = sp.fp_on && sp.n_reply > 0;
@@ -239,7 +252,7 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass(bl_dev d, const fl
       int32_t cc[4 * NV], wc[4 * NV];
 #pragma unroll
       for (int k = 0; k < 4 * NV; k++) {
-        const bool on = (tb[k >> 2] >> (k & 3)) & 1u;
+        const bool on = ((tb[k >> 2] >> (k & 3)) & 1u) || ((dm >> k) & 1u);
         const bl_tok r = on ? d.tokst[so + pos_of(k)] : bl_tok{0.0f, 0, 0, 0u};
         f[k] = r.flags;
         bv[k] = r.bias;
@@ -248,7 +261,17 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass(bl_dev d, const fl
       }
 #pragma unroll
       for (int k = 0; k < 4 * NV; k++) {
-        if (!((tb[k >> 2] >> (k & 3)) & 1u)) continue;
+        if (!((tb[k >> 2] >> (k & 3)) & 1u) && !((dm >> k) & 1u)) continue;
+        if (SPEC && ((dm >> k) & 1u)) {
+          int dc = 0, dw = 0;
+          for (int e = 0; e < nd; e++)
+            if (dl[e].tok == i0 + pos_of(k)) {
+              dc += dl[e].dcnt;
+              dw += dl[e].dwcnt;
+            }
+          if (sp.fp_on) cc[k] += dc;
+          if (sp.rep_on) wc[k] += dw;
+        }
         float v = x[k];
         if (f[k] & BL_TF_BIAS) v = v + bv[k];
         if (f[k] & BL_TF_SUPPRESS) v = -1000000000.0f;
@@ -506,6 +529,15 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass(bl_dev d, const fl
     d.cand_v[cbase + p] = BL_NEG_INF;
     d.cand_i[cbase + p] = -1;
   }
+}
+
+__global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass(bl_dev d, const float *__restrict__ logits, int64_t ld,
+                                                              bl_rows rows) {
+  rowpass_body<false>(d, logits, ld, rows);
+}
+__global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass_spec(bl_dev d, const float *__restrict__ logits,
+                                                                   int64_t ld, bl_rows rows) {
+  rowpass_body<true>(d, logits, ld, rows);
 }
 
 /* ------------------------------------------------------------------ K2: exponent pass + top-K merge */
@@ -2477,7 +2509,10 @@ void bl_launch_step(const bl_dev &d, const float *logits, int64_t ld, const bl_r
                     bool need_gram, hipStream_t s, hipEvent_t *ev) {
   dim3 g1(d.nc, B);
   if (ev) (void)hipEventRecord(ev[0], s);
-  hipLaunchKernelGGL(bl_k_rowpass, g1, dim3(BL_RP_THREADS), 0, s, d, logits, ld, rows);
+  if (rows.delta)
+    hipLaunchKernelGGL(bl_k_rowpass_spec, g1, dim3(BL_RP_THREADS), 0, s, d, logits, ld, rows);
+  else
+    hipLaunchKernelGGL(bl_k_rowpass, g1, dim3(BL_RP_THREADS), 0, s, d, logits, ld, rows);
   if (ev) (void)hipEventRecord(ev[1], s);
   if (need_gram) hipLaunchKernelGGL(bl_k_gmask, dim3(d.gm_blocks, B), dim3(BL_GM_THREADS), 0, s, d, rows, 1);
   if (need_pass2)

@@ -32,8 +32,9 @@ enum {
   BL_EGRAMMAR_REJECT = -6, /* "the grammar rejected every vocabulary token" (src/server.br:361) */
   BL_EGRAMMAR_AMBIG = -7,  /* "grammar is left-recursive or too ambiguous to match" (src/grammar.br:354) */
   BL_EUNSUPPORTED = -8,    /* a sampler stage this library does not run on the device yet: top_n_sigma,
-                              DRY, a dynatemp exponent other than 1 (rejected by bl_slot_reset); XTC on
-                              speculative rows; typical_p over a full-vocabulary list above 512 candidates */
+                              DRY, a dynatemp exponent other than 1 (rejected by bl_slot_reset); XTC, mirostat
+                              or a grammar on speculative rows, or more than 32 drafts with history-dependent
+                              penalties; typical_p over a full-vocabulary list above 512 candidates */
   BL_ETIE = -9,            /* a draw on equal logits whose heap order is past the device simulation (more than
                               8192 values at or above the tied one), equal allowed maxima of a grammar row, or
                               post-sampling alternatives of a full-vocabulary rank that meet equal values */
@@ -173,7 +174,10 @@ int bl_get_timing(bl_ctx *ctx, double *ms_total3, int64_t *steps);
 /* Speculative verification (src/server.br:1173-1216): for each of the B slots, rows
  * d_rows[b*(k+1) + i] (i = 0..k) are the target logits after feeding drafts[b*k .. b*k+i). Row i is
  * sampled with the slot's RNG advanced by i draws; accepted[b] = number of leading rows whose token
- * equals its draft; the slot commits drafts[0..accepted) and tokens[b*(k+1)+accepted].
+ * equals its draft; the slot commits drafts[0..accepted) and tokens[b*(k+1)+accepted]. With frequency,
+ * presence or repeat penalties, row i counts drafts[0..i) in the reply and the repeat window (and drops the
+ * window entries they evict), as the reference's loop does after pushing them; drafts must then be
+ * vocabulary ids and k at most 32.
  * `tokens` receives every row's token (row i as if drafts[0..i) were accepted). */
 int bl_spec_verify(bl_ctx *ctx, const int32_t *slots, int B, int k, const float *d_rows, int64_t ld,
                    const int32_t *drafts, int32_t *tokens, int32_t *accepted);

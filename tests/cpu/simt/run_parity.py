@@ -394,6 +394,61 @@ def run_w5(BL, steps):
     return None
 
 
+def run_spec_penalties(BL, rounds):
+    """Speculative verification of rows with frequency/presence/repeat penalties (row i sees the drafts before
+    it in its history and reply): every row's token, the accepted length and, at the end, the RNG state equal
+    the oracle's spec_verify over the same rows, round after round (the device commits in between). Drafts
+    repeat a few hot tokens so that the penalties decide rows; a 3-token window makes drafts leave it."""
+    V, K = 997, 6
+    confs = [dict(temperature=0.0, repeat_penalty=1.3, repeat_last_n=3, frequency_penalty=0.4, presence_penalty=0.2),
+             dict(temperature=0.8, top_k=0, repeat_penalty=1.2, repeat_last_n=8, frequency_penalty=0.3,
+                  presence_penalty=0.1),
+             dict(temperature=0.0, repeat_penalty=1.5, repeat_last_n=-1),
+             dict(temperature=0.7, top_k=20, frequency_penalty=0.8, presence_penalty=0.5)]
+    S = len(confs)
+    rng = np.random.default_rng(21)
+    hot = [int(x) for x in rng.choice(V, 6, replace=False)]
+    L = O.lib()
+    L.orc_set_eog_tokens(O.ip(O.i32([0])), 0, -1)
+    ctx = BL.Context(V, S, S * (K + 1))
+    hs = []
+    buf = MEM.zeros(S * (K + 1) * V, np.float32)
+    try:
+        for b, kw in enumerate(confs):
+            hist = [int(x) for x in rng.choice(hot + [int(y) for y in rng.integers(0, V, 6)], 12)]
+            ctx.slot_reset(b, BL.Params(**kw), BL.seed_rng(300 + b), history=hist, reply=hist)
+            op = O.params(**kw)
+            hh = O.i32(hist)
+            hs.append(L.orc_slot_new(O.C.byref(op), BL.seed_rng(300 + b), O.ip(hh), len(hist), O.ip(hh), len(hist),
+                                     None, None, 0))
+        for t in range(rounds):
+            rows = (rng.standard_normal((S * (K + 1), V)) * 2.0).astype(np.float32)
+            rows[:, hot] += np.float32(5.0)
+            drafts = []
+            for b in range(S):
+                for i in range(K):
+                    r = rows[b * (K + 1) + i]
+                    drafts.append(int(np.argmax(r)) if rng.random() < 0.7 else hot[int(rng.integers(0, len(hot)))])
+            buf.upload(rows.reshape(-1))
+            toks, acc = ctx.spec_verify(list(range(S)), K, buf.ptr, V, drafts)
+            for b in range(S):
+                ot = np.zeros(K + 1, np.int32)
+                oa = O.C.c_int32()
+                assert L.orc_slot_spec_verify(hs[b], O.fp(rows[b * (K + 1):(b + 1) * (K + 1)].reshape(-1)), V,
+                                              O.ip(O.i32(drafts[b * K:(b + 1) * K])), K, O.ip(ot), O.C.byref(oa)) == 0
+                if toks[b * (K + 1):(b + 1) * (K + 1)] != list(ot) or acc[b] != oa.value:
+                    return (f"round {t} sequence {b} ({confs[b]}): tokens {toks[b * (K + 1):(b + 1) * (K + 1)]} "
+                            f"vs {list(ot)}, accepted {acc[b]} vs {oa.value}")
+        for b in range(S):
+            if ctx.slot_rng(b) != L.orc_slot_rng(hs[b]):
+                return f"sequence {b}: final RNG state differs"
+    finally:
+        for h in hs:
+            L.orc_slot_free(h)
+        ctx.close()
+    return None
+
+
 def run_async(BL, steps):
     """bl_bind_rows + bl_sample_step_async into caller buffers equals the synchronous step."""
     V, seed, B = 151936, 2, 8
@@ -642,6 +697,8 @@ def main():
             results.append(("workload 4", run_w4(BL, int(f[1]), int(f[2]) if len(f) > 2 else 32)))
         elif kind == "w5":
             results.append(("workload 5", run_w5(BL, int(f[1]))))
+        elif kind == "specpen":
+            results.append(("speculative rows with penalties", run_spec_penalties(BL, int(f[1]))))
         elif kind == "async":
             results.append(("asynchronous step", run_async(BL, int(f[1]))))
         elif kind == "pair":

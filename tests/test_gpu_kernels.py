@@ -87,3 +87,10 @@ def test_async_step_equals_sync():
     print("bound rows, asynchronous step: 4 steps", flush=True)
     err = RP.run_async(BL, 4)
     assert err is None, err
+
+
+def test_spec_verify_with_penalties():
+    # src/server.br:1173-1216 with frequency/presence/repeat penalties: row i's counts include the drafts before it
+    print("speculative rows with penalties: 12 rounds x 4 sequences x 7 rows", flush=True)
+    err = RP.run_spec_penalties(BL, 12)
+    assert err is None, err

@@ -87,6 +87,13 @@ def test_full_vocabulary_workloads(simt_lib):
     assert "ok   rows 3 + 8" in out and "ok   large top-k" in out
 
 
+def test_spec_verify_with_penalties(simt_lib):
+    """Speculative rows whose frequency/presence/repeat penalties count the drafts before them (and the window
+    entries those drafts evict) against the oracle's spec_verify, over rounds of device commits."""
+    out = _run(simt_lib, ["specpen:8"], {"SIMT_ORDER": "rand"})
+    assert "ok   speculative rows with penalties" in out
+
+
 def test_grammar_masks_and_tokens(simt_lib):
     """The grammar path (GBNF automaton tables, per-token mask walk, masked greedy, on-device commit of
     the reply position) against the oracle's whole-reply re-decode: workload 3 and seven adversarial
