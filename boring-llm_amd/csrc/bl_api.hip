@@ -263,6 +263,12 @@ int bl_create(int device, int max_slots, int max_rows, int vocab, bl_ctx **out) 
   d.nc = (vocab + BL_CH - 1) / BL_CH;
   d.max_slots = max_slots;
   d.max_rows = max_rows;
+  {
+    int n_cu = 0;
+    if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || n_cu <= 0)
+      n_cu = 256;
+    d.rp_resident = 5 * n_cu;
+  }
   d.words = (vocab + 31) / 32;
   const size_t V = (size_t)vocab, S = (size_t)max_slots, R = (size_t)max_rows;
   const size_t G = V / 64 + 64;

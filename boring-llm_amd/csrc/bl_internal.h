@@ -107,6 +107,8 @@ struct bl_slot_dev {
 
 struct bl_dev {
   int vocab, nc, max_slots, max_rows;
+  int rp_resident; /* row-pass workgroups the chip holds at once (5 per CU); larger grids take the
+                      two-half instance, which fits 8 per CU */
   int64_t words; /* V/32 rounded up */
   bl_slot_dev *slots;
   uint32_t *touched; /* [slots][words] */

@@ -154,8 +154,10 @@ __device__ double block_excl_scan_d(double x, double *sd, double *total) {
 
 /* ------------------------------------------------------------------ K1: row pass */
 /* SPEC: the row may carry speculative count corrections (compiled separately: the correction loops
- * cost the ordinary row pass registers) */
-template <bool SPEC>
+ * cost the ordinary row pass registers). HALVES: the touched tokens' records are gathered and applied in
+ * two halves of the thread's positions (one more dependent load, fewer registers: more workgroups per CU
+ * for grids that do not fit the chip at once) */
+template <bool SPEC, bool HALVES>
 __device__ __forceinline__ void rowpass_body(const bl_dev &d, const float *__restrict__ logits, int64_t ld,
                                              const bl_rows &rows) {
   const int V = d.vocab, nc = d.nc;
@@ -247,41 +249,48 @@ __device__ __forceinline__ void rowpass_body(const bl_dev &d, const float *__res
       const int64_t so = (int64_t)slot * V + i0;
       const bool fp = sp.fp_on && sp.n_reply > 0;
       const bool rp = sp.rep_on && sp.n_tokens > 0;
-      uint32_t f[4 * NV];
-      float bv[4 * NV];
-      int32_t cc[4 * NV], wc[4 * NV];
+      constexpr int NH = HALVES ? 2 : 1, KH = 4 * NV / NH; /* positions per half */
 #pragma unroll
-      for (int k = 0; k < 4 * NV; k++) {
-        const bool on = ((tb[k >> 2] >> (k & 3)) & 1u) || ((dm >> k) & 1u);
-        const bl_tok r = on ? d.tokst[so + pos_of(k)] : bl_tok{0.0f, 0, 0, 0u};
-        f[k] = r.flags;
-        bv[k] = r.bias;
-        cc[k] = fp ? r.cnt : 0;
-        wc[k] = rp ? r.wcnt : 0;
-      }
-#pragma unroll
-      for (int k = 0; k < 4 * NV; k++) {
-        if (!((tb[k >> 2] >> (k & 3)) & 1u) && !((dm >> k) & 1u)) continue;
-        if (SPEC && ((dm >> k) & 1u)) {
-          int dc = 0, dw = 0;
-          for (int e = 0; e < nd; e++)
-            if (dl[e].tok == i0 + pos_of(k)) {
-              dc += dl[e].dcnt;
-              dw += dl[e].dwcnt;
-            }
-          if (sp.fp_on) cc[k] += dc;
-          if (sp.rep_on) wc[k] += dw;
+      for (int h = 0; h < NH; h++) {
+        if (HALVES && h > 0) asm volatile("" ::: "memory"); /* the second half's loads stay after the first's use */
+        uint32_t f[KH];
+        float bv[KH];
+        int32_t cc[KH], wc[KH];
+  #pragma unroll
+        for (int kk = 0; kk < KH; kk++) {
+          const int k = h * KH + kk;
+          const bool on = ((tb[k >> 2] >> (k & 3)) & 1u) || ((dm >> k) & 1u);
+          const bl_tok r = on ? d.tokst[so + pos_of(k)] : bl_tok{0.0f, 0, 0, 0u};
+          f[kk] = r.flags;
+          bv[kk] = r.bias;
+          cc[kk] = fp ? r.cnt : 0;
+          wc[kk] = rp ? r.wcnt : 0;
         }
-        float v = x[k];
-        if (f[k] & BL_TF_BIAS) v = v + bv[k];
-        if (f[k] & BL_TF_SUPPRESS) v = -1000000000.0f;
-        if (cc[k] > 0) {
-          float tcf = (float)cc[k] * sp.frequency_penalty;
-          v = v - tcf;
-          v = v - sp.presence_penalty;
+  #pragma unroll
+        for (int kk = 0; kk < KH; kk++) {
+          const int k = h * KH + kk;
+          if (!((tb[k >> 2] >> (k & 3)) & 1u) && !((dm >> k) & 1u)) continue;
+          if (SPEC && ((dm >> k) & 1u)) {
+            int dc = 0, dw = 0;
+            for (int e = 0; e < nd; e++)
+              if (dl[e].tok == i0 + pos_of(k)) {
+                dc += dl[e].dcnt;
+                dw += dl[e].dwcnt;
+              }
+            if (sp.fp_on) cc[kk] += dc;
+            if (sp.rep_on) wc[kk] += dw;
+          }
+          float v = x[k];
+          if (f[kk] & BL_TF_BIAS) v = v + bv[kk];
+          if (f[kk] & BL_TF_SUPPRESS) v = -1000000000.0f;
+          if (cc[kk] > 0) {
+            float tcf = (float)cc[kk] * sp.frequency_penalty;
+            v = v - tcf;
+            v = v - sp.presence_penalty;
+          }
+          if (wc[kk] > 0) v = v > 0.0f ? v / sp.repeat_penalty : v * sp.repeat_penalty;
+          x[k] = v;
         }
-        if (wc[k] > 0) v = v > 0.0f ? v / sp.repeat_penalty : v * sp.repeat_penalty;
-        x[k] = v;
       }
     }
   }
@@ -533,11 +542,15 @@ __device__ __forceinline__ void rowpass_body(const bl_dev &d, const float *__res
 
 __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass(bl_dev d, const float *__restrict__ logits, int64_t ld,
                                                               bl_rows rows) {
-  rowpass_body<false>(d, logits, ld, rows);
+  rowpass_body<false, false>(d, logits, ld, rows);
+}
+__global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass_wide(bl_dev d, const float *__restrict__ logits,
+                                                                   int64_t ld, bl_rows rows) {
+  rowpass_body<false, true>(d, logits, ld, rows);
 }
 __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass_spec(bl_dev d, const float *__restrict__ logits,
                                                                    int64_t ld, bl_rows rows) {
-  rowpass_body<true>(d, logits, ld, rows);
+  rowpass_body<true, false>(d, logits, ld, rows);
 }
 
 /* ------------------------------------------------------------------ K2: exponent pass + top-K merge */
@@ -2511,6 +2524,8 @@ void bl_launch_step(const bl_dev &d, const float *logits, int64_t ld, const bl_r
   if (ev) (void)hipEventRecord(ev[0], s);
   if (rows.delta)
     hipLaunchKernelGGL(bl_k_rowpass_spec, g1, dim3(BL_RP_THREADS), 0, s, d, logits, ld, rows);
+  else if ((int64_t)d.nc * B > d.rp_resident)
+    hipLaunchKernelGGL(bl_k_rowpass_wide, g1, dim3(BL_RP_THREADS), 0, s, d, logits, ld, rows);
   else
     hipLaunchKernelGGL(bl_k_rowpass, g1, dim3(BL_RP_THREADS), 0, s, d, logits, ld, rows);
   if (ev) (void)hipEventRecord(ev[1], s);
