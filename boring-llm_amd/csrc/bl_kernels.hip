@@ -256,7 +256,7 @@ __device__ __forceinline__ void rowpass_body(const bl_dev &d, const float *__res
         uint32_t f[KH];
         float bv[KH];
         int32_t cc[KH], wc[KH];
-  #pragma unroll
+#pragma unroll
         for (int kk = 0; kk < KH; kk++) {
           const int k = h * KH + kk;
           const bool on = ((tb[k >> 2] >> (k & 3)) & 1u) || ((dm >> k) & 1u);
@@ -266,7 +266,7 @@ __device__ __forceinline__ void rowpass_body(const bl_dev &d, const float *__res
           cc[kk] = fp ? r.cnt : 0;
           wc[kk] = rp ? r.wcnt : 0;
         }
-  #pragma unroll
+#pragma unroll
         for (int kk = 0; kk < KH; kk++) {
           const int k = h * KH + kk;
           if (!((tb[k >> 2] >> (k & 3)) & 1u) && !((dm >> k) & 1u)) continue;
