@@ -139,3 +139,99 @@ def test_invalid_utf8_and_buffer_size():
     assert BL.lib().bl_json_schema_to_gbnf(t, len(t), None, 0, C.byref(n)) == 0 and n.value > 0
     small = C.create_string_buffer(n.value)  # no room for the NUL
     assert BL.lib().bl_json_schema_to_gbnf(t, len(t), small, n.value, None) == BL.BL_EPARAM
+
+
+def _random_schema(rng, depth=0):
+    """A random schema over the keywords json_schema_to_gbnf reads (seeded: the cases are fixed)."""
+    import json
+    def lit():
+        return rng.choice([0, -3, 2.5, 1e21, "s", "a\"b", "é", True, False, None, [1, "x"], {"k": [None]}])
+    keys = ["alpha", "b-c", "d e", "ü", "", "x1"]
+    kind = rng.randrange(12 if depth < 3 else 7)
+    if kind == 0:
+        return {"type": rng.choice(["string", "integer", "number", "boolean", "null"])}
+    if kind == 1:
+        return {"const": lit()}
+    if kind == 2:
+        return {"enum": [lit() for _ in range(rng.randrange(1, 4))]}
+    if kind == 3:
+        s = {"type": "string"}
+        if rng.random() < 0.7:
+            s["minLength"] = rng.choice([0, 1, 3, 2.0])
+        if rng.random() < 0.6:
+            s["maxLength"] = rng.choice([0, 4, 9, 5.0])
+        return s
+    if kind == 4:
+        return rng.choice([True, False, {}])
+    if kind == 5:
+        return {"type": [rng.choice(["string", "integer", "boolean", "null", "number"]) for _ in range(2)]}
+    if kind == 6:
+        return {"$ref": "#/$defs/" + rng.choice(["n", "m"])}
+    if kind in (7, 8):
+        props = {k: _random_schema(rng, depth + 1) for k in rng.sample(keys, rng.randrange(0, 4))}
+        s = {"type": "object", "properties": props}
+        if props and rng.random() < 0.6:
+            s["required"] = rng.sample(list(props), rng.randrange(0, len(props) + 1))
+        if rng.random() < 0.4:
+            s["additionalProperties"] = rng.choice([True, False, {"type": "integer"}, {}])
+        return s
+    if kind == 9:
+        s = {"type": "array"}
+        if rng.random() < 0.7:
+            s["items"] = _random_schema(rng, depth + 1)
+        lo = rng.choice([None, 0, 1, 2, 3])
+        hi = rng.choice([None, 0, 1, 2, 4])
+        if lo is not None:
+            s["minItems"] = lo
+        if hi is not None and (lo is None or hi >= lo):
+            s["maxItems"] = hi
+        return s
+    key = rng.choice(["anyOf", "oneOf"])
+    return {key: [_random_schema(rng, depth + 1) for _ in range(rng.randrange(1, 4))]}
+
+
+def test_random_schemas_match_oracle():
+    import json
+    import random
+    rng = random.Random(1234)
+    for case in range(400):
+        root = _random_schema(rng)
+        if isinstance(root, dict) and rng.random() < 0.5:
+            root = dict(root)
+            root["$defs"] = {"n": _random_schema(rng, 2), "m": {"type": "integer"}}
+        text = json.dumps(root, ensure_ascii=rng.random() < 0.5)
+        try:
+            want = O.json_schema_to_gbnf(text)
+        except ValueError as e:
+            with pytest.raises(BL.BLError) as got:
+                lib_gbnf(text)
+            assert str(got.value) == f"{e} (code {BL.BL_ESCHEMA})", (case, text)
+            continue
+        assert lib_gbnf(text) == want, (case, text)
+
+
+def test_mutated_schema_texts_match_oracle():
+    # byte-level mutations of valid schema texts exercise json_parse's error paths and positions
+    import random
+    rng = random.Random(99)
+    alphabet = '{}[]":,\\ \n\tu0123456789abcdefé-+.eEtrnl'
+    for case in range(1500):
+        base = rng.choice(REFERENCE_SCHEMAS + EDGE_SCHEMAS[:20])
+        s = list(base)
+        for _ in range(rng.randrange(1, 4)):
+            op, i = rng.randrange(3), rng.randrange(len(s) + 1)
+            if op == 0 and s:
+                del s[min(i, len(s) - 1)]
+            elif op == 1:
+                s.insert(i, rng.choice(alphabet))
+            elif s:
+                s[min(i, len(s) - 1)] = rng.choice(alphabet)
+        text = "".join(s)
+        try:
+            want = O.json_schema_to_gbnf(text)
+        except ValueError as e:
+            with pytest.raises(BL.BLError) as got:
+                lib_gbnf(text)
+            assert str(got.value) == f"{e} (code {BL.BL_ESCHEMA})", (case, text)
+            continue
+        assert lib_gbnf(text) == want, (case, text)
