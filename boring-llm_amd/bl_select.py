@@ -50,7 +50,7 @@ EXPORTS = [
     "bl_spec_verify", "bl_synth_logits", "bl_math_digest", "bl_workload_ids", "bl_workload_bias",
     "bl_workload_drafts", "bl_set_timing", "bl_get_timing", "bl_set_vocab", "bl_slot_grammar", "bl_grammar_mask",
     "bl_workload_c3_vocab", "bl_step_graph_create", "bl_step_graph_launch", "bl_step_graph_destroy",
-    "bl_stream_sync", "bl_json_schema_to_gbnf", "bl_slot_schema",
+    "bl_stream_sync", "bl_json_schema_to_gbnf", "bl_slot_schema", "bl_slot_status",
 ]
 
 _lib = None
@@ -75,6 +75,7 @@ def lib():
         L.bl_slot_reset.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_uint64, i32p, C.c_int, i32p, C.c_int,
                                     i32p, f32p, C.c_int]
         L.bl_slot_rng.argtypes = [C.c_void_p, C.c_int, u64p]
+        L.bl_slot_status.argtypes = [C.c_void_p, C.c_int]
         L.bl_slot_commit.argtypes = [C.c_void_p, C.c_int, i32p, C.c_int]
         L.bl_sample_step.argtypes = [C.c_void_p, i32p, C.c_int, C.c_void_p, C.c_int64, i32p, f32p, i32p, f32p, C.c_int]
         L.bl_bind_rows.argtypes = [C.c_void_p, i32p, C.c_int]
@@ -166,6 +167,10 @@ class Context:
         s = C.c_uint64()
         _check(lib().bl_slot_rng(self.h, slot, C.byref(s)))
         return s.value
+
+    def slot_status(self, slot):
+        """Raises BLError with the failure of the slot's rows since the last call (bl_slot_status)."""
+        _check(lib().bl_slot_status(self.h, slot))
 
     def commit(self, slot, toks):
         a, n = _arr(C.c_int32, toks)

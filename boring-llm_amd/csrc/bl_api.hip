@@ -28,16 +28,10 @@ void bl_launch_math_digest(int fn, uint32_t first_block, int n_blocks, unsigned 
 
 static thread_local std::string g_err;
 
-/* Waits for the stream's work: polls it for up to 2 ms (a step completes within tens of microseconds, and
- * a blocking wait adds the interrupt's wake-up to its latency), then blocks. */
-static hipError_t wait_stream(hipStream_t s) {
-  const auto until = std::chrono::steady_clock::now() + std::chrono::milliseconds(2);
-  for (;;) {
-    const hipError_t e = hipStreamQuery(s);
-    if (e != hipErrorNotReady) return e;
-    if (std::chrono::steady_clock::now() >= until) return hipStreamSynchronize(s);
-  }
-}
+/* Waits for the stream's work. hipStreamSynchronize spins on the completion signal before it blocks; on
+ * MI355X it returns 9.4 us after the launch of an empty kernel, where a loop of hipStreamQuery calls
+ * (each one a runtime round trip) takes 28 us (median of 500, ROCm 7.2). */
+static hipError_t wait_stream(hipStream_t s) { return hipStreamSynchronize(s); }
 
 static int fail(int code, const char *fmt, ...) {
   char buf[512];
@@ -65,6 +59,9 @@ struct bl_ctx {
   int32_t *d_slot = nullptr, *d_skip = nullptr, *d_tok = nullptr, *d_status = nullptr, *d_top_ids = nullptr;
   float *d_lp = nullptr, *d_top_lp = nullptr;
   int32_t *h_slot = nullptr, *h_tok = nullptr, *h_status = nullptr, *h_top_ids = nullptr, *h_skip = nullptr;
+  /* the rows of bl_bind_rows: read only by the asynchronous step and graphs, written only by bl_bind_rows
+   * (the synchronous step and speculative verification build their own row table in d_slot/h_slot) */
+  int32_t *d_bound = nullptr, *h_bound = nullptr;
   float *h_lp = nullptr, *h_top_lp = nullptr;
   /* the synchronous step's outputs packed in one block per side: tokens, statuses, logprobs, top ids, top
    * logprobs of the call's B rows back to back, so one copy brings them to the host */
@@ -320,6 +317,7 @@ int bl_create(int device, int max_slots, int max_rows, int vocab, bl_ctx **out) 
   ALLOC(d.gm_eq, R * d.gm_blocks);
   d.eos_id = -1;
   ALLOC(c->d_slot, R);
+  ALLOC(c->d_bound, R);
   ALLOC(c->d_skip, R);
   ALLOC(c->d_tok, R);
   ALLOC(c->d_status, R);
@@ -334,8 +332,16 @@ int bl_create(int device, int max_slots, int max_rows, int vocab, bl_ctx **out) 
   ALLOC(c->d_delta, R * BL_SPEC_DCAP);
   ALLOC(c->d_delta_n, R);
 #undef ALLOC
+  /* slot records and grammar views start zeroed: a slot is only stepped or committed after bl_slot_reset, and
+   * nothing reads uninitialised state even when a caller breaks that rule */
+  if (hipMemset(d.slots, 0, S * sizeof(bl_slot_dev)) != hipSuccess || hipMemset(d.gram, 0, S * sizeof(bl_gram_view)) != hipSuccess ||
+      hipDeviceSynchronize() != hipSuccess) {
+    bl_destroy(c);
+    return fail(BL_EDEVICE, "hipMemset failed");
+  }
   d.n_eog = 0;
   if (hipHostMalloc((void **)&c->h_slot, R * sizeof(int32_t)) != hipSuccess ||
+      hipHostMalloc((void **)&c->h_bound, R * sizeof(int32_t)) != hipSuccess ||
       hipHostMalloc((void **)&c->h_skip, R * sizeof(int32_t)) != hipSuccess ||
       hipHostMalloc((void **)&c->h_tok, R * sizeof(int32_t)) != hipSuccess ||
       hipHostMalloc((void **)&c->h_status, R * sizeof(int32_t)) != hipSuccess ||
@@ -371,7 +377,7 @@ void bl_destroy(bl_ctx *c) {
   }
   if (c->d_vblob) hipFree(c->d_vblob);
   if (c->d_voff) hipFree(c->d_voff);
-  void *hp[] = {c->h_slot, c->h_skip, c->h_tok, c->h_status, c->h_lp, c->h_top_ids, c->h_top_lp, c->h_acc, c->h_out};
+  void *hp[] = {c->h_slot, c->h_bound, c->h_skip, c->h_tok, c->h_status, c->h_lp, c->h_top_ids, c->h_top_lp, c->h_acc, c->h_out};
   for (void *p : hp)
     if (p) hipHostFree(p);
   for (hipEvent_t e : c->ev)
@@ -531,6 +537,7 @@ int bl_slot_reset(bl_ctx *c, int slot, const bl_params *p, uint64_t rng_state, c
 
 int bl_slot_rng(bl_ctx *c, int slot, uint64_t *state) {
   if (!c || slot < 0 || slot >= c->d.max_slots || !state) return fail(BL_EPARAM, "bl_slot_rng: invalid arguments");
+  if (!c->slot_ready[slot]) return fail(BL_EPARAM, "slot %d is not set up", slot);
   hipSetDevice(c->device);
   bl_slot_dev s;
   HIPCHK(hipStreamSynchronize(c->stream));
@@ -540,7 +547,9 @@ int bl_slot_rng(bl_ctx *c, int slot, uint64_t *state) {
 }
 
 int bl_slot_commit(bl_ctx *c, int slot, const int32_t *toks, int n) {
-  if (!c || slot < 0 || slot >= c->d.max_slots || n < 0 || n > 4096) return fail(BL_EPARAM, "bl_slot_commit: invalid arguments");
+  if (!c || slot < 0 || slot >= c->d.max_slots || n < 0 || n > 4096 || (n > 0 && !toks))
+    return fail(BL_EPARAM, "bl_slot_commit: invalid arguments");
+  if (!c->slot_ready[slot]) return fail(BL_EPARAM, "slot %d is not set up", slot);
   if (n == 0) return BL_OK;
   for (int i = 0; i < n; i++)
     if (toks[i] >= 0 && toks[i] < c->d.vocab) {
@@ -753,10 +762,24 @@ static int status_error(int st) {
   return BL_OK;
 }
 
-static bl_rows make_rows(bl_ctx *c, bool with_skip, int commit, int top_stride) {
+int bl_slot_status(bl_ctx *c, int slot) {
+  if (!c || slot < 0 || slot >= c->d.max_slots) return fail(BL_EPARAM, "bl_slot_status: invalid arguments");
+  if (!c->slot_ready[slot]) return fail(BL_EPARAM, "slot %d is not set up", slot);
+  hipSetDevice(c->device);
+  int32_t err = 0;
+  const int32_t zero = 0;
+  int32_t *dp = &c->d.slots[slot].err;
+  HIPCHK(hipStreamSynchronize(c->stream));
+  HIPCHK(hipMemcpy(&err, dp, sizeof err, hipMemcpyDeviceToHost));
+  HIPCHK(hipMemcpy(dp, &zero, sizeof zero, hipMemcpyHostToDevice));
+  return status_error(err);
+}
+
+static bl_rows make_rows(bl_ctx *c, bool with_skip, int commit, int top_stride, bool bound = false) {
   bl_rows r{};
-  r.slot = c->d_slot;
-  for (int i = 0; i < BL_ROWS_INLINE && i < c->d.max_rows; i++) r.slot_inline[i] = (int16_t)c->h_slot[i];
+  const int32_t *h = bound ? c->h_bound : c->h_slot;
+  r.slot = bound ? c->d_bound : c->d_slot;
+  for (int i = 0; i < BL_ROWS_INLINE && i < c->d.max_rows; i++) r.slot_inline[i] = (int16_t)h[i];
   r.rng_skip = with_skip ? c->d_skip : nullptr;
   r.commit = commit;
   r.tok = c->d_tok;
@@ -807,8 +830,9 @@ int bl_bind_rows(bl_ctx *c, const int32_t *slots, int B) {
   int rc = check_rows(c, slots, B);
   if (rc) return rc;
   hipSetDevice(c->device);
-  HIPCHK(hipMemcpy(c->d_slot, slots, B * sizeof(int32_t), hipMemcpyHostToDevice));
-  memcpy(c->h_slot, slots, B * sizeof(int32_t));
+  HIPCHK(hipStreamSynchronize(c->stream)); /* a step in flight may still read the previous table */
+  HIPCHK(hipMemcpy(c->d_bound, slots, B * sizeof(int32_t), hipMemcpyHostToDevice));
+  memcpy(c->h_bound, slots, B * sizeof(int32_t));
   c->bound_B = B;
   mark_stepped(c, slots, B);
   return BL_OK;
@@ -819,7 +843,7 @@ int bl_sample_step_async(bl_ctx *c, int B, const float *d_logits, int64_t ld, in
   if (!c || B != c->bound_B || B <= 0) return fail(BL_EPARAM, "bl_sample_step_async: rows not bound (bl_bind_rows)");
   if (!d_logits || !d_tokens || ld < c->d.vocab || top_stride < 0 || top_stride > 256)
     return fail(BL_EPARAM, "bl_sample_step_async: invalid buffers");
-  bl_rows rows = make_rows(c, false, 1, top_stride > 0 ? top_stride : 1);
+  bl_rows rows = make_rows(c, false, 1, top_stride > 0 ? top_stride : 1, true);
   rows.tok = d_tokens;
   rows.lp = d_logprobs;
   rows.top_ids = d_top_ids ? d_top_ids : c->d_top_ids;
@@ -830,7 +854,7 @@ int bl_sample_step_async(bl_ctx *c, int B, const float *d_logits, int64_t ld, in
       for (int k = 0; k < 4; k++) HIPCHK(hipEventCreate(&c->ev[k]));
     ev = c->ev;
   }
-  bl_launch_step(c->d, d_logits, ld, rows, B, needs_pass2(c, c->h_slot, B), needs_gram(c, c->h_slot, B), c->stream,
+  bl_launch_step(c->d, d_logits, ld, rows, B, needs_pass2(c, c->h_bound, B), needs_gram(c, c->h_bound, B), c->stream,
                  ev);
   HIPCHK(hipGetLastError());
   if (ev) {
@@ -928,6 +952,10 @@ int bl_spec_verify(bl_ctx *c, const int32_t *slots, int B, int k, const float *d
       return fail(BL_EUNSUPPORTED, "speculative rows with XTC are not supported on the device");
     if (k > 0 && (s.mode & BL_M_MIRO))
       return fail(BL_EUNSUPPORTED, "speculative rows with mirostat are not supported on the device");
+    /* with dynatemp_range >= temperature the effective temperature can reach 0, and such a row makes no draw
+     * (src/sampling.br:576-582): the rows after it would start one draw early in the RNG chain */
+    if (k > 0 && s.temperature > 0.0f && s.dynatemp_range > 0.0f && s.dynatemp_range >= s.temperature)
+      return fail(BL_EUNSUPPORTED, "speculative rows with dynatemp_range >= temperature are not supported on the device");
   }
   hipSetDevice(c->device);
   for (int b = 0; b < B; b++)

@@ -256,15 +256,18 @@ __device__ __forceinline__ void rowpass_body(const bl_dev &d, const float *__res
         uint32_t f[KH];
         float bv[KH];
         int32_t cc[KH], wc[KH];
+        /* every load is issued unconditionally (a position that is not touched reads the chunk's first
+         * record, a line all of them share, and discards it), so the gathers are in flight together
+         * instead of one branch and one round trip each */
 #pragma unroll
         for (int kk = 0; kk < KH; kk++) {
           const int k = h * KH + kk;
           const bool on = ((tb[k >> 2] >> (k & 3)) & 1u) || ((dm >> k) & 1u);
-          const bl_tok r = on ? d.tokst[so + pos_of(k)] : bl_tok{0.0f, 0, 0, 0u};
-          f[kk] = r.flags;
+          const bl_tok r = d.tokst[so + (on ? pos_of(k) : 0)];
+          f[kk] = on ? r.flags : 0u;
           bv[kk] = r.bias;
-          cc[kk] = fp ? r.cnt : 0;
-          wc[kk] = rp ? r.wcnt : 0;
+          cc[kk] = fp && on ? r.cnt : 0;
+          wc[kk] = rp && on ? r.wcnt : 0;
         }
 #pragma unroll
         for (int kk = 0; kk < KH; kk++) {
@@ -735,16 +738,20 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_exppass(bl_dev d, bl_rows 
   if (mode & BL_M_LOGPROBS) {
     /* approximate sum before this block, from the row pass's sums per BL_EB positions (every
      * wavefront computes the same value) */
+    /* lane k: chunk k's sub-blocks before this block, scaled by the hardware exponential (a prediction:
+     * its error, ~1e-7 relative, is far inside the 2^-20 margin of the critical-group test, and a wrong
+     * binade is caught on the exact state) */
+    static_assert(BL_SUBS == 4, "one float4 of sub-block sums per chunk");
     const int nsub = i0 / BL_EB;
     double part = 0.0;
-    for (int k = lane; k * BL_SUBS < nsub; k += 64) { /* lane k: chunk k's sub-blocks before this block */
+    for (int k = lane; k * BL_SUBS < nsub; k += 64) {
       const float cm = d.c_max[(int64_t)row * nc + k];
+      const float4 cb = *reinterpret_cast<const float4 *>(d.c_bsum + ((int64_t)row * nc + k) * BL_SUBS);
       if (cm > BL_NEG_INF) {
-        double cs = 0.0;
-#pragma unroll
-        for (int j = 0; j < BL_SUBS; j++)
-          if (k * BL_SUBS + j < nsub) cs += (double)d.c_bsum[((int64_t)row * nc + k) * BL_SUBS + j];
-        part += cs * exp((double)cm - (double)M);
+        const int lim = nsub - k * BL_SUBS;
+        const double cs = (double)cb.x + (lim > 1 ? (double)cb.y : 0.0) + (lim > 2 ? (double)cb.z : 0.0) +
+                          (lim > 3 ? (double)cb.w : 0.0);
+        part += cs * (double)__expf(cm - M);
       }
     }
     const double S0 = bl_wave_sum_d(part);
@@ -2464,7 +2471,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
     }
   }
   if (t == 0) {
-    rows.tok[row] = tok;
+    rows.tok[row] = status ? -1 : tok; /* a failed row has no token; its status stays sticky in the slot */
     if (rows.status) rows.status[row] = status;
     if (lp_row) rows.lp[row] = (tokv - M) - lse;
     if (psp_row) rows.lp[row] = psp_tok;

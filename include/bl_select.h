@@ -100,8 +100,13 @@ int bl_slot_reset(bl_ctx *ctx, int slot, const bl_params *p, uint64_t rng_state,
 /* The slot's current xorshift64 state (Rng.state, src/sampling.br:18-19). */
 int bl_slot_rng(bl_ctx *ctx, int slot, uint64_t *state);
 /* Append tokens chosen elsewhere to the slot history (tokens.push / reply_tokens.push,
- * src/server.br:1004, :1037). */
+ * src/server.br:1004, :1037). BL_EPARAM for a slot that bl_slot_reset has not set up. */
 int bl_slot_commit(bl_ctx *ctx, int slot, const int32_t *toks, int n);
+/* The failures of the slot's rows since the previous call or its reset (the error a synchronous step would
+ * have returned for them, with its message), cleared by the call: how a caller of bl_sample_step_async or
+ * of a step graph learns why a row's token came back as -1. Replaces the `throws` of the reference's
+ * sampler calls (src/sampling.br:495, src/server.br:318-361) for steps that do not return to the host. */
+int bl_slot_status(bl_ctx *ctx, int slot);
 
 /* Vocabulary pieces for grammar-constrained slots: token t's bytes are blob[offsets[t] .. offsets[t+1]),
  * n_tokens = the context's vocabulary (Tokenizer.decode / piece_bytes, src/tokenizer.br:122-151,
@@ -145,7 +150,10 @@ int bl_sample_step(bl_ctx *ctx, const int32_t *slots, int B, const float *d_logi
                    float *logprobs, int32_t *top_ids, float *top_logprobs, int top_stride);
 
 /* The same step with device-memory outputs and no host synchronisation, on the context stream
- * (capturable in a HIP graph once bl_bind_rows has fixed the row table). */
+ * (capturable in a HIP graph once bl_bind_rows has fixed the row table). A row that fails (an error the
+ * synchronous step would return) gets token -1 and commits nothing; bl_slot_status reports the error.
+ * bl_bind_rows keeps its own row table: synchronous steps and speculative verification on other slots
+ * in between do not change the bound rows. */
 int bl_bind_rows(bl_ctx *ctx, const int32_t *slots, int B);
 int bl_sample_step_async(bl_ctx *ctx, int B, const float *d_logits, int64_t ld, int32_t *d_tokens, float *d_logprobs,
                          int32_t *d_top_ids, float *d_top_logprobs, int top_stride);

@@ -114,6 +114,12 @@ int32_t orc_sample_greedy(const float *logits, int64_t n) { return sample_greedy
 void orc_logprob_normalizer(const float *logits, int64_t n, float *mx, float *lse) {
   logprob_normalizer(Row(logits, logits + n), n, *mx, *lse);
 }
+/* the normaliser's float32 sum itself (sum_exp before its logf) */
+float orc_logprob_sum(const float *logits, int64_t n) {
+  float mx, lse, sum;
+  logprob_normalizer(Row(logits, logits + n), n, mx, lse, &sum);
+  return sum;
+}
 float orc_token_logprob(const float *logits, int64_t n, int32_t tok) { return token_logprob(Row(logits, logits + n), n, tok); }
 /* writes min(k, n) entries */
 void orc_top_k_select(const float *logits, int64_t n, int64_t k, float *vals, int32_t *ids) {
@@ -132,6 +138,27 @@ void orc_all_candidates_sorted(const float *logits, int64_t n, float *vals, int3
 }
 
 /* ---------------- candidate sampling ---------------- */
+/* the running sums of one sample_candidates_with_probs call: out_f = {sum_exp, temperature, renorm_sum, target},
+ * out_i = {cutoff, first, chosen}; returns the token or -1 */
+int32_t orc_sample_candidates_trace(uint64_t rng, const float *vals, const int32_t *ids, int64_t n, float temperature,
+                                    float top_p, float min_p, int64_t min_keep, float *out_f, int64_t *out_i) {
+  try {
+    CandTrace tr{};
+    CandResult r = sample_candidates_with_probs(Rng{rng}, Row(vals, vals + n), Ids(ids, ids + n), temperature, 0.0f,
+                                                1.0f, 1.0f, top_p, min_p, 0.0f, 0.1f, min_keep, &tr);
+    out_f[0] = tr.sum_exp;
+    out_f[1] = tr.temperature;
+    out_f[2] = tr.renorm_sum;
+    out_f[3] = tr.target;
+    out_i[0] = tr.cutoff;
+    out_i[1] = tr.first;
+    out_i[2] = tr.chosen;
+    return r.token;
+  } catch (const std::exception &e) {
+    g_err = e.what();
+    return -1;
+  }
+}
 /* returns the token (or -1 on error); probs/ids receive the post-sampling list (cap entries at most) */
 int32_t orc_sample_candidates(uint64_t *rng, const float *vals, const int32_t *ids, int64_t n, float temperature,
                               float dyn_range, float dyn_exp, float typical_p, float top_p, float min_p, float xtc_p,

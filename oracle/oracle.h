@@ -27,22 +27,30 @@
  *                                 determinism tests (test/test_sampling.br:7-13, :29-39)
  *   bias, penalties, greedy,      the reference's known answers (test/test_sampling.br:16, :42-61,
  *   top-k, heap rank (distinct)   :187-264) and lexsort/brute-force rankings on random rows
- *   candidate sampling            known answers typical->8, XTC->9, min_p=1 (:112-122, :163-167,
- *                                 :268-272), min_keep/top-p cut properties, a chi-square check of the
- *                                 draw distribution against the float64 softmax
- *   logprobs                      the reference's approximate known answers (:19-26) and a float64
- *                                 log-sum-exp within float32 rounding
- *   soft-cap                      float64 closed form within float32 rounding (test/test_arch.br)
+ *   heap rank among equal values  numpy's heapsort (same bottom-up max-heap and extraction), reversed, on
+ *                                 1,200 tied arrays and a bfloat16 row of 151,936 (test_oracle_pinning.py)
+ *   logprob normaliser            np.cumsum (a sequential float32 sum) over glibc expf terms, bit for bit,
+ *                                 at V up to 262,144, then glibc logf; the reference's approximate known
+ *                                 answers (:19-26)
+ *   candidate sampling            sum_exp, the top-p running probability, the min-p cut, the tempered sum,
+ *                                 the draw target and position restated with numpy sequential sums and glibc
+ *                                 expf, bit for bit (full-vocabulary lists of 151,936 and 150 short lists);
+ *                                 known answers typical->8, XTC->9, min_p=1 (:112-122, :163-167, :268-272);
+ *                                 a chi-square check of the draw distribution
+ *   soft-cap                      float64 closed form within float32 rounding (test/test_arch.br); the device
+ *                                 tanhf equals glibc's over all 2^32 inputs
  *   grammar, schema, UTF-8,       transliterations of test/test_grammar.br, test_schema_grammar.br,
  *   n-gram drafts                 test_tokenizer.br:52-58, test_speculative.br; the workload-3 GBNF
  *                                 against its hand derivation; the carry form of a candidate piece
  *                                 against the literal whole-reply re-decode
+ *   full-vocabulary masks         by composition of pinned parts: each bit is grammar_advance_text over
+ *                                 the candidate's piece, the piece is bytes_to_str of the carry form, and the
+ *                                 carry form equals the literal whole-reply re-decode (test_oracle_grammar.py)
  *   speculative verification      sequential decoding of the same rows (CHANGELOG.md:92's invariant)
- * Parity unpinned (the restatement is the only authority, no reference vector or closed form fixes it):
- *   - the order of equal values in the heap rank (all_candidates_sorted, src/sampling.br:301-365);
- *   - the float32 bits of the sequential sums and of expf/logf/tanhf beyond the glibc the oracle links
- *     (the Boring compiler's lowering to Rust f32 -> glibc is assumed, not vendored);
- *   - full-vocabulary grammar masks beyond the language tests above.
+ * Every check above fails against a build with a planted mistake where one is listed in oracle/Makefile
+ * (`mutants`: sift tie direction, pairwise normaliser, reversed softmax sum, split tempered sum).
+ * Assumed, not pinned: that the external `boring` compiler lowers float32 exp/ln/tanh/powf to Rust f32 and
+ * so to glibc (it is not vendored); the oracle and the device follow glibc 2.35 exactly.
  */
 #ifndef BL_ORACLE_H
 #define BL_ORACLE_H
@@ -81,7 +89,8 @@ int32_t turn_close_token(int32_t eos_id);
 Row suppress_eog_tokens(const Row &logits, int32_t eos_id);
 Row suppress_token(const Row &logits, int32_t token);
 int32_t sample_greedy(const Row &logits, int64_t vocab);
-void logprob_normalizer(const Row &logits, int64_t vocab, float &maximum, float &log_sum_exp);
+void logprob_normalizer(const Row &logits, int64_t vocab, float &maximum, float &log_sum_exp,
+                        float *sum_out = nullptr);
 float normalized_token_logprob(const Row &logits, int32_t token, float maximum, float log_sum_exp);
 float token_logprob(const Row &logits, int64_t vocab, int32_t token);
 void top_k_select(const Row &logits, int64_t vocab, int64_t k, Row &top_val, Ids &top_idx);
@@ -99,10 +108,21 @@ struct CandResult {
   Row probs;
   Ids ids;
 };
+/* the float32 running sums of one call, for the checks that pin them (tests/test_oracle_pinning.py) */
+struct CandTrace {
+  float sum_exp;      /* untempered softmax denominator, rank order */
+  int64_t cutoff;     /* after top-p and min-p */
+  int64_t first;      /* after XTC */
+  float temperature;  /* effective (dynamic) temperature */
+  float renorm_sum;   /* tempered sum over [first, cutoff) */
+  float target;       /* r01 * renorm_sum */
+  int64_t chosen;     /* drawn list position */
+};
 /* throws std::runtime_error("sample_candidates: empty or mismatched candidates") */
 CandResult sample_candidates_with_probs(Rng rng, const Row &top_val, const Ids &top_idx, float temperature,
                                         float dynatemp_range, float dynatemp_exponent, float typical_p, float top_p,
-                                        float min_p, float xtc_probability, float xtc_threshold, int64_t min_keep);
+                                        float min_p, float xtc_probability, float xtc_threshold, int64_t min_keep,
+                                        CandTrace *trace = nullptr);
 int32_t sample_candidates(Rng &rng, const Row &top_val, const Ids &top_idx, float temperature, float dynatemp_range,
                           float dynatemp_exponent, float typical_p, float top_p, float min_p, float xtc_probability,
                           float xtc_threshold, int64_t min_keep);

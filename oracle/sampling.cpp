@@ -212,14 +212,23 @@ int32_t sample_greedy(const Row &logits, int64_t vocab) {
 }
 
 /* :254-266 sequential float32 sum in index order */
-void logprob_normalizer(const Row &logits, int64_t vocab, float &maximum, float &log_sum_exp) {
+void logprob_normalizer(const Row &logits, int64_t vocab, float &maximum, float &log_sum_exp, float *sum_out) {
   float mx = logits[0];
   for (int64_t i = 1; i < vocab; i++)
     if (logits[i] > mx) mx = logits[i];
   float sum_exp = 0.0f;
+#if ORC_MUTANT == 2 /* planted mistake (tests only): a pairwise sum instead of the sequential one */
+  Row t(vocab);
+  for (int64_t i = 0; i < vocab; i++) t[i] = expf(logits[i] - mx);
+  for (int64_t w = 1; w < vocab; w *= 2)
+    for (int64_t i = 0; i + w < vocab; i += 2 * w) t[i] += t[i + w];
+  sum_exp = t[0];
+#else
   for (int64_t i = 0; i < vocab; i++) sum_exp += expf(logits[i] - mx);
+#endif
   maximum = mx;
   log_sum_exp = logf(sum_exp);
+  if (sum_out) *sum_out = sum_exp;
 }
 
 /* :268-269 */
@@ -265,7 +274,11 @@ static void sift_down(Row &hv, Ids &hi, int64_t root, int64_t size) {
     } else {
       int64_t child = left;
       int64_t right = left + 1;
+#if ORC_MUTANT == 1 /* planted mistake (tests only): ties go to the right child */
+      if (right < size && hv[right] >= hv[left]) child = right;
+#else
       if (right < size && hv[right] > hv[left]) child = right;
+#endif
       if (hv[child] <= hv[root]) {
         placed = true;
       } else {
@@ -419,7 +432,8 @@ float dynamic_temperature(const Row &probs, int64_t first, int64_t cutoff, float
 /* :490-607 */
 CandResult sample_candidates_with_probs(Rng rng, const Row &top_val, const Ids &top_idx, float temperature,
                                         float dynatemp_range, float dynatemp_exponent, float typical_p, float top_p,
-                                        float min_p, float xtc_probability, float xtc_threshold, int64_t min_keep) {
+                                        float min_p, float xtc_probability, float xtc_threshold, int64_t min_keep,
+                                        CandTrace *trace) {
   if (!(top_val.size() > 0 && top_val.size() == top_idx.size()))
     throw std::runtime_error("sample_candidates: empty or mismatched candidates");
   if (temperature <= 0.0f) return CandResult{top_idx[0], rng, Row{1.0f}, Ids{top_idx[0]}};
@@ -433,8 +447,13 @@ CandResult sample_candidates_with_probs(Rng rng, const Row &top_val, const Ids &
   for (int64_t i = 0; i < n; i++) {
     float e = expf(top_val[i] - top_val[0]);
     probs[i] = e;
+#if ORC_MUTANT != 3
     sum_exp += e;
+#endif
   }
+#if ORC_MUTANT == 3 /* planted mistake (tests only): the softmax sum in reverse rank order */
+  for (int64_t i = n - 1; i >= 0; i--) sum_exp += probs[i];
+#endif
   for (int64_t i = 0; i < n; i++) probs[i] = probs[i] / sum_exp;
 
   Row tprobs, tvalues;
@@ -487,6 +506,7 @@ CandResult sample_candidates_with_probs(Rng rng, const Row &top_val, const Ids &
   }
   float effective_temperature =
       dynamic_temperature(probs, first, cutoff, temperature, dynatemp_range, dynatemp_exponent);
+  if (trace) *trace = CandTrace{sum_exp, cutoff, first, effective_temperature, 0.0f, 0.0f, first};
   if (effective_temperature <= 0.0f)
     return CandResult{candidate_idx[first], sample_rng, Row{1.0f}, Ids{candidate_idx[first]}};
 
@@ -496,8 +516,19 @@ CandResult sample_candidates_with_probs(Rng rng, const Row &top_val, const Ids &
     float d = candidate_values[i] - candidate_values[first];
     float q = d / effective_temperature;
     probs[i] = expf(q);
+#if ORC_MUTANT != 4
     renorm_sum += probs[i];
+#endif
   }
+#if ORC_MUTANT == 4 /* planted mistake (tests only): the tempered sum as two halves added at the end */
+  {
+    float a = 0.0f, b = 0.0f;
+    const int64_t mid = first + (cutoff - first) / 2;
+    for (int64_t i = first; i < mid; i++) a += probs[i];
+    for (int64_t i = mid; i < cutoff; i++) b += probs[i];
+    renorm_sum = a + b;
+  }
+#endif
   /* draw (:586-598) */
   Rng new_rng = sample_rng;
   float r01 = rng_next_f32(new_rng);
@@ -513,6 +544,11 @@ CandResult sample_candidates_with_probs(Rng rng, const Row &top_val, const Ids &
       slot_found = true;
     }
     s += 1;
+  }
+  if (trace) {
+    trace->renorm_sum = renorm_sum;
+    trace->target = target;
+    trace->chosen = chosen_slot;
   }
   CandResult r{candidate_idx[chosen_slot], new_rng, Row{}, Ids{}};
   for (int64_t i = first; i < cutoff; i++) {

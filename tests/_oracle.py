@@ -49,7 +49,20 @@ def lib():
     if _lib is None:
         if not os.path.exists(LIB):
             subprocess.check_call(["make", "-s", "-C", os.path.join(ROOT, "oracle")])
-        L = C.CDLL(LIB)
+        _lib = _configure(C.CDLL(LIB))
+    return _lib
+
+
+def mutant(k):
+    """The oracle built with planted mistake k (oracle/Makefile `mutants`): the checks that pin the oracle
+    must fail against it."""
+    path = os.path.join(ROOT, "oracle", f"liboracle_mut{k}.so")
+    subprocess.check_call(["make", "-s", "-C", os.path.join(ROOT, "oracle"), f"liboracle_mut{k}.so"])
+    return _configure(C.CDLL(path))
+
+
+def _configure(L):
+    if True:
         L.orc_last_error.restype = C.c_char_p
         L.orc_seed_rng.restype = C.c_uint64
         L.orc_seed_rng.argtypes = [i64]
@@ -126,8 +139,12 @@ def lib():
         L.orc_c3_vocab.argtypes = [i64, C.c_char_p, i64, u32p, i32p]
         L.orc_crc32.restype = C.c_uint32
         L.orc_crc32.argtypes = [C.c_void_p, C.c_size_t]
-        _lib = L
-    return _lib
+        L.orc_logprob_sum.restype = C.c_float
+        L.orc_logprob_sum.argtypes = [f32p, i64]
+        L.orc_sample_candidates_trace.restype = C.c_int32
+        L.orc_sample_candidates_trace.argtypes = [C.c_uint64, f32p, i32p, i64, C.c_float, C.c_float, C.c_float, i64,
+                                                  f32p, C.POINTER(i64)]
+    return L
 
 
 def fp(a):

@@ -1,0 +1,211 @@
+"""Pins the oracle parts that no reference vector fixes, against independent library routines, and shows
+that each check fails against an oracle with a planted mistake (oracle/Makefile `mutants`).
+
+  heap rank order among equal values (all_candidates_sorted, src/sampling.br:301-365): numpy's heapsort
+      (the same bottom-up max-heap with strict-greater child choice and extraction of the root), reversed;
+  the index-order normaliser (logprob_normalizer, src/sampling.br:254-266): np.cumsum over float32 terms
+      (a sequential float32 sum, checked here against a plain loop) of glibc's expf, called through ctypes;
+  the rank-order sums of sample_candidates_with_probs (src/sampling.br:506-598): sum_exp, the top-p running
+      probability, the min-p cut, the tempered sum and the draw's running sum, the same way, with the RNG
+      draw from the xorshift closed form.
+The planted mistakes: ties sent to the right child in the sift (1), a pairwise normaliser sum (2), the
+softmax sum in reverse rank order (3), the tempered sum as two halves (4).
+"""
+import ctypes
+from fractions import Fraction
+
+import numpy as np
+import pytest
+
+import _oracle as O
+
+F = np.float32
+MASK = (1 << 64) - 1
+_m = ctypes.CDLL("libm.so.6")
+_m.expf.restype = ctypes.c_float
+_m.expf.argtypes = [ctypes.c_float]
+_m.logf.restype = ctypes.c_float
+_m.logf.argtypes = [ctypes.c_float]
+_vexpf = np.frompyfunc(_m.expf, 1, 1)
+
+
+def gexpf(a):
+    """glibc expf elementwise (float32 in, float32 out)."""
+    return np.asarray(_vexpf(np.asarray(a, F)), dtype=F)
+
+
+def seq_sum(a):
+    """Sequential float32 sum, left to right."""
+    return F(np.cumsum(np.asarray(a, F), dtype=F)[-1]) if len(a) else F(0.0)
+
+
+def test_cumsum_is_a_sequential_float32_sum():
+    x = (np.random.default_rng(1).standard_normal(4000) * 3).astype(F)
+    s = F(0.0)
+    run = []
+    for v in x:
+        s = F(s + v)
+        run.append(s)
+    assert np.array_equal(np.cumsum(x, dtype=F), np.array(run, F))
+    assert np.sum(x) != s  # numpy's sum is pairwise, the reason it is not used here
+
+
+# ---------------------------------------------------------------- heap rank order
+
+def tied_arrays(seed, n_arrays):
+    rng = np.random.default_rng(seed)
+    for _ in range(n_arrays):
+        n = int(rng.integers(2, 700))
+        kind = int(rng.integers(0, 3))
+        if kind == 0:
+            yield rng.integers(0, int(rng.integers(1, 8)), n).astype(F)
+        elif kind == 1:
+            yield (rng.integers(-12, 12, n) * 0.25).astype(F)
+        else:  # bfloat16-rounded normals
+            x = (rng.standard_normal(n) * 3).astype(F)
+            yield (x.view(np.uint32) & 0xFFFF0000).view(F)
+
+
+def heap_mismatches(L, arrays):
+    bad = 0
+    for x in arrays:
+        v = np.zeros(len(x), F)
+        i = np.zeros(len(x), np.int32)
+        L.orc_all_candidates_sorted(O.fp(x), len(x), O.fp(v), O.ip(i))
+        bad += not np.array_equal(i, np.argsort(x, kind="heapsort")[::-1])
+    return bad
+
+
+def test_heap_tie_order_equals_numpy_heapsort():
+    assert heap_mismatches(O.lib(), tied_arrays(7, 1200)) == 0
+
+
+def test_heap_tie_order_full_vocabulary():
+    rng = np.random.default_rng(11)
+    x = (rng.standard_normal(151936) * 3).astype(F)
+    x = (x.view(np.uint32) & 0xFFFF0000).view(F)  # bfloat16: thousands of equal values
+    assert heap_mismatches(O.lib(), [x]) == 0
+
+
+def test_heap_check_fails_on_planted_mistake():
+    assert heap_mismatches(O.mutant(1), tied_arrays(7, 200)) > 0
+
+
+# ---------------------------------------------------------------- index-order normaliser
+
+def normaliser_rows():
+    rng = np.random.default_rng(21)
+    rows = [(rng.standard_normal(151936) * s).astype(F) for s in (3.0, 4.0)]
+    rows.append((rng.standard_normal(262144) * 10).astype(F))
+    for _ in range(30):
+        n = int(rng.integers(1, 6000))
+        rows.append((rng.standard_normal(n) * float(rng.uniform(0.1, 12))).astype(F))
+    rows.append((np.arange(5000) % 7).astype(F))  # ties and exact crossings
+    return rows
+
+
+def normaliser_mismatches(L, rows):
+    bad = 0
+    for x in rows:
+        mx = x.max()
+        want = seq_sum(gexpf(x - mx))
+        bad += L.orc_logprob_sum(O.fp(x), len(x)) != want
+        m, lse = ctypes.c_float(), ctypes.c_float()
+        L.orc_logprob_normalizer(O.fp(x), len(x), ctypes.byref(m), ctypes.byref(lse))
+        bad += m.value != mx or lse.value != _m.logf(float(want))
+    return bad
+
+
+def test_normaliser_is_the_sequential_glibc_sum():
+    assert normaliser_mismatches(O.lib(), normaliser_rows()) == 0
+
+
+def test_normaliser_check_fails_on_planted_mistake():
+    assert normaliser_mismatches(O.mutant(2), normaliser_rows()) > 0
+
+
+# ---------------------------------------------------------------- rank-order sums of the draw
+
+def xorshift(x):
+    x ^= (x << 13) & MASK
+    x ^= x >> 7
+    x ^= (x << 17) & MASK
+    return x
+
+
+def u64_to_f32(x):
+    if x == 0:
+        return 0.0
+    e = x.bit_length() - 1
+    sh = max(e - 23, 0)
+    m = Fraction(x, 1 << sh)
+    q = m.numerator // m.denominator
+    r = m - q
+    if r > Fraction(1, 2) or (r == Fraction(1, 2) and q & 1):
+        q += 1
+    return float(F(q * (1 << sh)))
+
+
+def draw_trace(state, v, T, top_p, min_p, min_keep):
+    """sample_candidates_with_probs' float32 sums for a ranked list v (no typical, XTC or dynatemp),
+    restated with numpy sequential sums and glibc expf."""
+    n = len(v)
+    keep = min(max(min_keep, 1), n)
+    e = gexpf(v - v[0])
+    sum_exp = seq_sum(e)
+    p = (e / sum_exp).astype(F)
+    cutoff = n
+    if top_p < 1.0:
+        cum = np.cumsum(p, dtype=F)
+        hit = np.nonzero((cum >= F(top_p)) & (np.arange(1, n + 1) >= keep))[0]
+        if len(hit):
+            cutoff = int(hit[0]) + 1
+    if min_p > 0.0:
+        thr = F(p[0] * F(min_p))
+        mc = keep
+        while mc < cutoff and p[mc] >= thr:
+            mc += 1
+        cutoff = mc
+    r = gexpf(((v[:cutoff] - v[0]).astype(F) / F(T)).astype(F))
+    renorm = seq_sum(r)
+    r01 = F(u64_to_f32(xorshift(state)) / 2.0 ** 64)
+    target = F(r01 * renorm)
+    run = np.cumsum(r, dtype=F)
+    hit = np.nonzero(run >= target)[0]
+    chosen = int(hit[0]) if len(hit) else cutoff - 1
+    return [sum_exp, F(T), renorm, target], [cutoff, 0, chosen]
+
+
+def ranked_cases():
+    rng = np.random.default_rng(31)
+    cases = []
+    for s, T, tp, mp in ((4.0, 0.7, 0.9, 0.0), (3.0, 1.0, 1.0, 0.0), (4.0, 0.8, 0.95, 0.05)):
+        x = (rng.standard_normal(151936) * s).astype(F)
+        cases.append((np.sort(x)[::-1].copy(), T, tp, mp, 1, int(rng.integers(1, 1 << 62))))
+    for _ in range(150):
+        n = int(rng.integers(1, 600))
+        x = np.sort((rng.standard_normal(n) * float(rng.uniform(0.2, 6))).astype(F))[::-1].copy()
+        cases.append((x, float(rng.choice([0.3, 0.7, 1.0, 1.5])), float(rng.choice([1.0, 0.9, 0.5])),
+                      float(rng.choice([0.0, 0.05, 0.2])), int(rng.integers(0, 4)), int(rng.integers(1, 1 << 62))))
+    return cases
+
+
+def trace_mismatches(L, cases):
+    bad = 0
+    for v, T, tp, mp, mk, st in cases:
+        ids = np.arange(len(v), dtype=np.int32)
+        of = np.zeros(4, F)
+        oi = (ctypes.c_int64 * 3)()
+        tok = L.orc_sample_candidates_trace(st, O.fp(v), O.ip(ids), len(v), T, tp, mp, mk, O.fp(of), oi)
+        wf, wi = draw_trace(st, v, T, tp, mp, mk)
+        bad += (not np.array_equal(of, np.array(wf, F))) or list(oi) != wi or tok != wi[2]
+    return bad
+
+
+def test_rank_order_sums_are_sequential_glibc_sums():
+    assert trace_mismatches(O.lib(), ranked_cases()) == 0
+
+
+@pytest.mark.parametrize("k", [3, 4])
+def test_rank_order_check_fails_on_planted_mistake(k):
+    assert trace_mismatches(O.mutant(k), ranked_cases()) > 0

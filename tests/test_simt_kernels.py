@@ -113,3 +113,25 @@ def test_small_cases_address_sanitizer():
     env = {"LD_PRELOAD": " ".join(pre), "ASAN_OPTIONS": "detect_leaks=0", "UBSAN_OPTIONS": "print_stacktrace=1"}
     out = _run(os.path.join(SIMT, "_build", "libbl_simt_asan.so"), ["small:0-20:3", "coarse:1,5:3", "ramp:8:2", "grammar:0-6:20", "q4:2,9:4"], env)
     assert "ERROR: AddressSanitizer" not in out and "runtime error" not in out
+
+
+def test_unready_slot_is_rejected_without_a_launch(simt_lib):
+    """bl_slot_commit, bl_slot_rng and bl_slot_status on a slot that bl_slot_reset never set up return
+    BL_EPARAM before any kernel runs (slot state is zeroed at creation either way)."""
+    import ctypes as C
+    L = C.CDLL(simt_lib)
+    L.bl_create.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_void_p)]
+    L.bl_slot_commit.argtypes = [C.c_void_p, C.c_int, C.POINTER(C.c_int32), C.c_int]
+    L.bl_slot_rng.argtypes = [C.c_void_p, C.c_int, C.POINTER(C.c_uint64)]
+    L.bl_slot_status.argtypes = [C.c_void_p, C.c_int]
+    L.bl_destroy.argtypes = [C.c_void_p]
+    L.bl_last_error.restype = C.c_char_p
+    h = C.c_void_p()
+    assert L.bl_create(0, 4, 4, 4096, C.byref(h)) == 0
+    toks = (C.c_int32 * 2)(5, 6)
+    assert L.bl_slot_commit(h, 1, toks, 2) == -1
+    assert b"not set up" in L.bl_last_error()
+    st = C.c_uint64()
+    assert L.bl_slot_rng(h, 1, C.byref(st)) == -1
+    assert L.bl_slot_status(h, 1) == -1
+    L.bl_destroy(h)
