@@ -102,12 +102,10 @@ static hipError_t dalloc(bl_ctx *c, T **p, size_t n) {
 
 /* ------------------------------------------------------------------ commit kernels */
 /* tokens.push / reply_tokens.push of one token (src/server.br:1004, :1037): repeat window, reply counts,
- * touched bits, grammar position; one thread */
+ * grammar position; one thread */
 __device__ void commit_one(const bl_dev &d, bl_slot_dev &sp, int slot, int32_t tok) {
   const int V = d.vocab;
   if (tok < 0 || tok >= V) return;
-  const int64_t so = (int64_t)slot * V;
-  uint32_t *tw = d.touched + (int64_t)slot * d.words;
   bool is_eog = false;
   for (int k = 0; k < d.n_eog; k++) is_eog |= d.eog[k] == tok;
   sp.n_tokens += 1;
@@ -117,7 +115,7 @@ __device__ void commit_one(const bl_dev &d, bl_slot_dev &sp, int slot, int32_t t
       int32_t *ring = d.ring + (int64_t)slot * BL_WCAP;
       if (sp.win_len == rl) {
         int32_t old = ring[sp.win_head];
-        d.tokst[so + old].wcnt -= 1;
+        bl_rec_get(d, slot, old)->wf -= 1u;
         ring[sp.win_head] = tok;
         sp.win_head = (sp.win_head + 1) % rl;
       } else {
@@ -125,15 +123,11 @@ __device__ void commit_one(const bl_dev &d, bl_slot_dev &sp, int slot, int32_t t
         sp.win_len += 1;
       }
     }
-    d.tokst[so + tok].wcnt += 1;
-    tw[tok >> 5] |= 1u << (tok & 31);
+    bl_rec_get(d, slot, tok)->wf += 1u;
   }
   if (!is_eog) {
     sp.n_reply += 1;
-    if (sp.fp_on) {
-      d.tokst[so + tok].cnt += 1;
-      tw[tok >> 5] |= 1u << (tok & 31);
-    }
+    if (sp.fp_on) bl_rec_get(d, slot, tok)->cnt += 1;
     if (sp.g_on) grammar_commit(d, sp, d.gram[slot], tok);
   }
 }
@@ -260,13 +254,6 @@ int bl_create(int device, int max_slots, int max_rows, int vocab, bl_ctx **out) 
   d.nc = (vocab + BL_CH - 1) / BL_CH;
   d.max_slots = max_slots;
   d.max_rows = max_rows;
-  {
-    int n_cu = 0;
-    if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || n_cu <= 0)
-      n_cu = 256;
-    d.rp_resident = 5 * n_cu;
-  }
-  d.words = (vocab + 31) / 32;
   const size_t V = (size_t)vocab, S = (size_t)max_slots, R = (size_t)max_rows;
   const size_t G = V / 64 + 64;
 #define ALLOC(p, n)                                   \
@@ -277,11 +264,12 @@ int bl_create(int device, int max_slots, int max_rows, int vocab, bl_ctx **out) 
     }                                                 \
   } while (0)
   ALLOC(d.slots, S);
-  ALLOC(d.touched, S * d.words);
-  ALLOC(d.tokst, S * V);
+  d.nb = (vocab + BL_EB - 1) / BL_EB;
+  ALLOC(d.rec, S * d.nb * BL_EB);
+  ALLOC(d.rcnt, S * d.nb);
+  ALLOC(d.ridx, S * V);
   ALLOC(d.ring, S * BL_WCAP);
   ALLOC(d.eog, 1024);
-  ALLOC(d.eff, R * V);
   ALLOC(d.c_max, R * d.nc);
   ALLOC(d.c_arg, R * d.nc);
   ALLOC(d.c_bsum, R * d.nc * BL_SUBS);
@@ -292,15 +280,14 @@ int bl_create(int device, int max_slots, int max_rows, int vocab, bl_ctx **out) 
     ALLOC(g, R * 2 * G * 32);
     d.grec = g;
   }
-  d.nb = (vocab + BL_EB - 1) / BL_EB;
   ALLOC(d.full_v, R * d.nb * BL_EB);
   ALLOC(d.full_i, R * d.nb * BL_EB);
   ALLOC(d.full_cnt, R * d.nb);
   ALLOC(d.full_s, R * d.nb);
   ALLOC(d.sortk, R * 2 * V);
   ALLOC(d.gsum, R * G);
-  ALLOC(d.gapx, R * G);
-  ALLOC(d.mkey, (size_t)R * BL_KSEL_MAX);
+  ALLOC(d.crit, R * BL_CRIT_MAX);
+  ALLOC(d.ncrit, R);
   {
     char *b = nullptr;
     ALLOC(b, R * d.nb * 16);
@@ -481,36 +468,31 @@ int bl_slot_reset(bl_ctx *c, int slot, const bl_params *p, uint64_t rng_state, c
   for (int i = 0; i < n_bias; i++)
     if (bias_ids[i] < 0 || bias_ids[i] >= V)
       return fail(BL_EPARAM, "logit_bias token id %d is outside the vocabulary", bias_ids[i]);
-  std::vector<uint32_t> touched(c->d.words, 0u);
-  std::vector<bl_tok> tk(V, bl_tok{0.0f, 0, 0, 0u});
+  /* the slot's records: one per modified token, packed per bucket in first-touch order */
+  const int NB = c->d.nb;
+  std::vector<bl_rec> rec((size_t)NB * BL_EB, bl_rec{0, 0.0f, 0, 0u});
+  std::vector<int32_t> rcnt(NB, 0);
+  std::vector<int16_t> ridx(V, (int16_t)-1);
   std::vector<int32_t> ring(BL_WCAP, 0);
-  auto touch = [&](int32_t id) { touched[id >> 5] |= 1u << (id & 31); };
+  auto rec_of = [&](int32_t id) -> bl_rec & {
+    const int b = id / BL_EB;
+    if (ridx[id] < 0) {
+      ridx[id] = (int16_t)rcnt[b];
+      rec[(size_t)b * BL_EB + rcnt[b]++] = bl_rec{id, 0.0f, 0, 0u};
+    }
+    return rec[(size_t)b * BL_EB + ridx[id]];
+  };
   for (int i = 0; i < n_bias; i++) {
-    tk[bias_ids[i]].flags |= BL_TF_BIAS;
-    tk[bias_ids[i]].bias = bias_vals[i]; /* a repeated id keeps the last value, as a JSON object would */
-    touch(bias_ids[i]);
-  }
-  if (p->ignore_eos) {
-    std::vector<int32_t> eog(c->d.n_eog);
-    if (c->d.n_eog) HIPCHK(hipMemcpy(eog.data(), c->d.eog, eog.size() * sizeof(int32_t), hipMemcpyDeviceToHost));
-    for (int32_t id : eog)
-      if (id >= 0 && id < V) {
-        tk[id].flags |= BL_TF_SUPPRESS;
-        touch(id);
-      }
+    bl_rec &r = rec_of(bias_ids[i]);
+    r.wf |= BL_TF_BIAS << BL_WF_SHIFT;
+    r.bias = bias_vals[i]; /* a repeated id keeps the last value, as a JSON object would */
   }
   if (s.fp_on)
-    for (int i = 0; i < n_reply; i++) {
-      tk[reply[i]].cnt += 1;
-      touch(reply[i]);
-    }
+    for (int i = 0; i < n_reply; i++) rec_of(reply[i]).cnt += 1;
   if (s.rep_on) {
     int rl = p->repeat_last_n;
     int win = (rl > 0 && n_hist > rl) ? rl : n_hist;
-    for (int i = n_hist - win; i < n_hist; i++) {
-      tk[history[i]].wcnt += 1;
-      touch(history[i]);
-    }
+    for (int i = n_hist - win; i < n_hist; i++) rec_of(history[i]).wf += 1u;
     if (rl > 0) {
       for (int i = 0; i < win; i++) ring[i] = history[n_hist - win + i];
       s.win_len = win;
@@ -524,10 +506,10 @@ int bl_slot_reset(bl_ctx *c, int slot, const bl_params *p, uint64_t rng_state, c
   c->reply[slot].assign(reply, reply + n_reply);
   c->stepped[slot] = 0;
   hipSetDevice(c->device);
-  const size_t so = (size_t)slot * V;
   HIPCHK(hipStreamSynchronize(c->stream));
-  HIPCHK(hipMemcpy(c->d.touched + (size_t)slot * c->d.words, touched.data(), touched.size() * 4, hipMemcpyHostToDevice));
-  HIPCHK(hipMemcpy(c->d.tokst + so, tk.data(), (size_t)V * sizeof(bl_tok), hipMemcpyHostToDevice));
+  HIPCHK(hipMemcpy(c->d.rec + (size_t)slot * NB * BL_EB, rec.data(), rec.size() * sizeof(bl_rec), hipMemcpyHostToDevice));
+  HIPCHK(hipMemcpy(c->d.rcnt + (size_t)slot * NB, rcnt.data(), NB * sizeof(int32_t), hipMemcpyHostToDevice));
+  HIPCHK(hipMemcpy(c->d.ridx + (size_t)slot * V, ridx.data(), (size_t)V * sizeof(int16_t), hipMemcpyHostToDevice));
   HIPCHK(hipMemcpy(c->d.ring + (size_t)slot * BL_WCAP, ring.data(), BL_WCAP * 4, hipMemcpyHostToDevice));
   HIPCHK(hipMemcpy(c->d.slots + slot, &s, sizeof s, hipMemcpyHostToDevice));
   c->host_slots[slot] = s;
@@ -741,11 +723,11 @@ static void mark_stepped(bl_ctx *c, const int32_t *slots, int B) {
   for (int i = 0; i < B; i++) c->stepped[slots[i]] = 1;
 }
 
-/* the exponent pass runs when a row has logprobs, a full-vocabulary rank or top-K candidates to merge */
+/* the exponent pass runs when a row has logprobs or a full-vocabulary rank */
 static bool needs_pass2(bl_ctx *c, const int32_t *slots, int B) {
   for (int i = 0; i < B; i++) {
     const bl_slot_dev &s = c->host_slots[slots[i]];
-    if ((s.mode & (BL_M_LOGPROBS | BL_M_FULL)) || s.k_sel > 0) return true;
+    if (s.mode & (BL_M_LOGPROBS | BL_M_FULL)) return true;
   }
   return false;
 }

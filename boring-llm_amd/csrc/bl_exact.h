@@ -356,7 +356,7 @@ __device__ int bl_seq_walk(int64_t n, TermF term, RecF rec, bool thr_on, float t
     if (valid) {
       bl_grec r = rec(gl);
       int k = e - (r.E - 1);
-      if (k >= 0 && k <= 2 && e >= BL_E_MIN) f = r.v[k];
+      if (k >= 0 && k <= 2 && e >= BL_E_MIN) f = k == 0 ? r.v[0] : (k == 1 ? r.v[1] : r.v[2]); /* selects: no dynamic index into private memory */
       else valid = false;
     }
     bl_inc sc = bl_wave_scan(f, lane);

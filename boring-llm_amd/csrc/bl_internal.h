@@ -3,13 +3,15 @@
  *
  * Per slot (one request's sampler state, all in HBM, owned by the context):
  *   bl_slot_dev            sampling parameters + scalar state (RNG, history lengths, window ring head)
- *   touched[V/32]          bit t set when token t's logit is modified by the step (logit_bias,
- *                          ignore_eos suppression, a reply count, a repeat-window count)
- *   tokst[V]               bl_tok, 16 bytes per token: logit_bias value, reply count (frequency /
- *                          presence penalties), repeat-window count, flags (bias present, suppressed)
+ *   rec[nb][BL_EB]         the tokens the server stages modify (a logit_bias value, a reply count for the
+ *                          frequency / presence penalties, a repeat-window count), one 16-byte bl_rec each,
+ *                          grouped by 1024-token bucket and packed at the front of the bucket's area
+ *   rcnt[nb]               records in each bucket
+ *   ridx[V]                a token's record index within its bucket, or -1 (used by commits only)
  *   ring[WCAP]             the last repeat_last_n tokens, for window eviction
- * The row pass reads `touched` densely (V/8 bytes per row, ~3% of the logits traffic) and the token
- * records only at set bits, one cache line each. Committing a token is O(1) writes.
+ * A pass over a chunk of the row reads its buckets' counts, then their records contiguously (coalesced, no
+ * per-token gather) and applies them in LDS. Committing a token is O(1) writes. ignore_eos suppression
+ * reads the context's end-of-generation registry at every step.
  *
  * Per step workspace, rows = B: transformed rows, per-chunk statistics and top-K candidates,
  * sequential-sum group records, full-vocabulary candidate lists and sort scratch.
@@ -19,6 +21,7 @@
 
 #include <stdint.h>
 
+#include "bl_exact.h"
 #include "bl_gwalk.h"
 
 #define BL_CH 4096          /* vocabulary chunk per workgroup in the row passes */
@@ -38,9 +41,10 @@
 #define BL_NBUCKET 8192     /* value buckets of the sort of longer lists (more than BL_LDS_SORT) */
 #define BL_EOG_LDS 64       /* end-of-generation ids the selection keeps in LDS */
 
-/* per-token flags */
+/* record flags (bl_rec.wf above BL_WF_SHIFT) */
 #define BL_TF_BIAS 1u
-#define BL_TF_SUPPRESS 2u
+#define BL_WF_SHIFT 16
+#define BL_WF_WMASK 0xFFFFu /* repeat-window count (at most BL_WCAP) */
 
 /* row modes */
 #define BL_M_GREEDY 1
@@ -68,12 +72,13 @@
 #define BL_SE_GREJECT 32
 #define BL_SE_GAMBIG 64
 
-/* one token's server-stage inputs in one slot (src/server.br:940-944, src/sampling.br:65-107, :175-237) */
-struct alignas(16) bl_tok {
-  float bias;     /* logit_bias value (flags & BL_TF_BIAS) */
-  int32_t cnt;    /* occurrences in the reply */
-  int32_t wcnt;   /* occurrences in the repeat window */
-  uint32_t flags; /* BL_TF_* */
+/* one modified token's server-stage inputs in one slot (src/server.br:940-944, src/sampling.br:65-107,
+ * :175-188) */
+struct alignas(16) bl_rec {
+  int32_t tok;  /* token id */
+  float bias;   /* logit_bias value (BL_TF_BIAS) */
+  int32_t cnt;  /* occurrences in the reply */
+  uint32_t wf;  /* occurrences in the repeat window (low 16 bits), BL_TF_* flags above */
 };
 
 /* A speculative row's correction to one token's counts: row i of a sequence is sampled with the drafts
@@ -84,6 +89,19 @@ struct bl_sdelta {
   int32_t tok;
   int16_t dcnt;  /* reply count */
   int16_t dwcnt; /* repeat-window count */
+};
+
+/* One critical 64-term group of a row's index-order normaliser (the running sum may cross a power of two
+ * inside it), written by the exponent pass: the exact terms, cp[l] = the composition of terms 0..l at the
+ * binade e0 of the group's approximate start, cs[l] = that of terms l..63 at the binade e1 of its approximate
+ * end, and the group records of its block (ng groups), from which the selection composes the runs between
+ * critical groups. */
+struct bl_crit {
+  int32_t g, e0, e1, ng;
+  float terms[64];
+  bl_inc cp[64];
+  bl_inc cs[64];
+  bl_grec1 blk[BL_EB / 64];
 };
 
 struct bl_slot_dev {
@@ -107,17 +125,14 @@ struct bl_slot_dev {
 
 struct bl_dev {
   int vocab, nc, max_slots, max_rows;
-  int rp_resident; /* row-pass workgroups the chip holds at once (5 per CU); larger grids take the
-                      two-half instance, which fits 8 per CU */
-  int64_t words; /* V/32 rounded up */
   bl_slot_dev *slots;
-  uint32_t *touched; /* [slots][words] */
-  bl_tok *tokst;     /* [slots][V] */
+  bl_rec *rec;       /* [slots][nb][BL_EB] */
+  int32_t *rcnt;     /* [slots][nb] */
+  int16_t *ridx;     /* [slots][V] */
   int32_t *ring;     /* [slots][WCAP] */
   int32_t *eog;      /* [n_eog] end-of-generation ids */
   int32_t n_eog;
   /* workspace for up to max_rows rows */
-  float *eff;       /* [rows][V] transformed row */
   float *c_max;     /* [rows][nc] */
   int32_t *c_arg;   /* [rows][nc] */
   float *c_bsum;    /* [rows][nc][BL_SUBS] approximate sums of exp(x - c_max) over each BL_EB positions */
@@ -130,8 +145,8 @@ struct bl_dev {
   double *full_s;    /* [rows][nb] approximate tempered sum over each region (rows without top-p/min-p) */
   uint64_t *sortk;  /* [rows][2V]: bucketed keys, then the sorted list; the draw's terms in the first half */
   double *gsum;     /* [rows][V/64 + 64] */
-  float *gapx;      /* [rows][V/64 + 64] approximate index-order sum before each 64-term group, then the total */
-  uint64_t *mkey;   /* [rows][KSEL_MAX] the row's top K order keys, sorted (0: unfilled) */
+  bl_crit *crit;    /* [rows][BL_CRIT_MAX] the normaliser's critical groups, in order of arrival */
+  int32_t *ncrit;   /* [rows] critical groups found (entries past BL_CRIT_MAX are not stored) */
   void *brec;       /* [rows][nb] bl_grec1 per BL_EB terms: the block's binade and composed automaton, or
                        BL_E_NONE when it holds a critical group or two binades */
   uint32_t *bcrit;  /* [rows][nb] the block's critical groups (bit i: group 16 b + i) */
@@ -202,6 +217,21 @@ __device__ __forceinline__ float bl_cand_span(const bl_slot_dev &sp) {
   /* the typical filter needs the whole candidate list */
   if (sp.typical_p < 1.0f) span = 3.0e38f;
   return span;
+}
+
+/* the record of `tok` in `slot`, created (zeroed) when the token has none; one thread (commits) */
+__device__ inline bl_rec *bl_rec_get(const bl_dev &d, int slot, int32_t tok) {
+  const int64_t sb = (int64_t)slot * d.nb + tok / BL_EB;
+  int16_t *ri = d.ridx + (int64_t)slot * d.vocab + tok;
+  bl_rec *base = d.rec + sb * BL_EB;
+  int i = *ri;
+  if (i < 0) {
+    i = d.rcnt[sb];
+    d.rcnt[sb] = i + 1;
+    *ri = (int16_t)i;
+    base[i] = bl_rec{tok, 0.0f, 0, 0u};
+  }
+  return base + i;
 }
 
 /* appends token `tok`'s bytes to the slot's grammar position (reply_tokens.push of a non-EOG token,

@@ -2,7 +2,7 @@
  * bl_kernels.hip — HIP kernels of one token-selection step for B slots (gfx950, wave64).
  *
  *   bl_k_rowpass  grid (chunks, B) x 256: reads each logits row once (float4), applies the model tail
- *                 (logit_mul, soft-cap), then the server's per-token stages at the touched bits
+ *                 (logit_mul, soft-cap), then the server's per-token stages at the chunk's records
  *                 (logit_bias -> ignore_eos suppression -> frequency/presence -> repeat penalty,
  *                 src/server.br:940-944, src/sampling.br:65-107,175-237), writes the transformed
  *                 row, and per chunk: max + first argmax, an approximate exp-sum, and the chunk's
@@ -49,7 +49,7 @@ __device__ __forceinline__ void argmax_merge(float &m, int &mi, float m2, int mi
 }
 
 template <int NT>
-__device__ void block_argmax(float &m, int &mi, float *sm, int *si) {
+__device__ __forceinline__ void block_argmax(float &m, int &mi, float *sm, int *si) {
   int t = threadIdx.x, lane = t & 63, w = t >> 6;
 #pragma unroll
   for (int k = 32; k >= 1; k >>= 1) {
@@ -74,7 +74,7 @@ __device__ void block_argmax(float &m, int &mi, float *sm, int *si) {
 }
 
 template <int NT>
-__device__ double block_sum_d(double x, double *sd) {
+__device__ __forceinline__ double block_sum_d(double x, double *sd) {
   int t = threadIdx.x, lane = t & 63, w = t >> 6;
   x = bl_wave_sum_d(x);
   if (lane == 0) sd[w] = x;
@@ -152,12 +152,163 @@ __device__ double block_excl_scan_d(double x, double *sd, double *total) {
   return base + ex;
 }
 
+/* ------------------------------------------------------------------ server stages */
+/* frequency/presence over the reply count, then the repeat penalty over the window count
+ * (src/sampling.br:91-107, :65-85) */
+__device__ __forceinline__ float stage_counts(const bl_slot_dev &sp, float v, int cc, int wc) {
+  if (cc > 0) {
+    const float tcf = (float)cc * sp.frequency_penalty;
+    v = v - tcf;
+    v = v - sp.presence_penalty;
+  }
+  if (wc > 0) v = v > 0.0f ? v / sp.repeat_penalty : v * sp.repeat_penalty;
+  return v;
+}
+
+/*
+ * The decode loop's per-token stages (src/server.br:940-944: logit_bias, ignore_eos suppression,
+ * frequency/presence, then sampling_logits' repeat penalty, src/sampling.br:65-107, :175-237) over the
+ * row positions [lo, lo + n) held in LDS `vals` (lo a multiple of BL_EB, n <= BL_CH), by the whole
+ * workgroup. The buckets' records are read contiguously; the end-of-generation registry is read live.
+ * A speculative row (SPEC) adds its count corrections: a corrected token with a record is handled with it,
+ * one without by the first correction that names it. The caller writes `vals` before and reads them after.
+ */
+template <bool SPEC>
+__device__ void apply_stages(const bl_dev &d, const bl_slot_dev &sp, const bl_rows &rows, int row, int slot, int lo,
+                             int n, float *vals, uint32_t *sup, uint32_t *done) {
+  const int t = threadIdx.x, NT = (int)blockDim.x;
+  const int b0 = lo / BL_EB, nbk = (n + BL_EB - 1) / BL_EB;
+  int pre[BL_SUBS + 1];
+  pre[0] = 0;
+#pragma unroll
+  for (int q = 0; q < BL_SUBS; q++) pre[q + 1] = pre[q] + (q < nbk ? d.rcnt[(int64_t)slot * d.nb + b0 + q] : 0);
+  const int nrec = pre[BL_SUBS];
+  const bool eog_on = sp.ignore_eos && d.n_eog > 0;
+  const int nd = SPEC && rows.delta ? rows.delta_n[row] : 0;
+  /* the model tail (src/model.br:973-984) first: logit_mul, then the final soft-cap cap * tanh(x / cap) */
+  const float lmul = sp.logit_mul, cap = sp.final_softcap;
+  const bool tail = lmul != 1.0f || cap > 0.0f;
+  if (nrec == 0 && !eog_on && nd == 0 && !tail) return; /* uniform: nothing in this range changes */
+  const bl_sdelta *dl = SPEC && rows.delta ? rows.delta + (int64_t)row * BL_SPEC_DCAP : nullptr;
+  const bool fp = sp.fp_on && sp.n_reply > 0, rp = sp.rep_on && sp.n_tokens > 0;
+  const int nw = (n + 31) / 32;
+  for (int i = t; i < nw; i += NT) {
+    sup[i] = 0u;
+    if (SPEC) done[i] = 0u;
+  }
+  __syncthreads(); /* the caller's values and the cleared marks */
+  if (tail) {
+#pragma unroll 1
+    for (int p = t; p < n; p += NT) {
+      float x = vals[p];
+      if (lmul != 1.0f) x = x * lmul;
+      if (cap > 0.0f) {
+        const float q = x / cap;
+        x = cap * bl_tanhf(q);
+      }
+      vals[p] = x;
+    }
+    __syncthreads();
+  }
+  if (eog_on) {
+    for (int e = t; e < d.n_eog; e += NT) {
+      const int p = d.eog[e] - lo;
+      if (p >= 0 && p < n) {
+        vals[p] = -1000000000.0f; /* suppress_token (src/sampling.br:236) */
+        atomicOr(&sup[p >> 5], 1u << (p & 31));
+      }
+    }
+    __syncthreads();
+  }
+  const bl_rec *rb = d.rec + ((int64_t)slot * d.nb + b0) * BL_EB;
+  constexpr int RU = 4; /* records in flight per thread */
+  for (int base = t; base < nrec; base += RU * NT) {
+    bl_rec rr[RU];
+#pragma unroll
+    for (int u = 0; u < RU; u++) {
+      const int i = base + u * NT;
+      const int q = (i >= pre[1] ? 1 : 0) + (i >= pre[2] ? 1 : 0) + (i >= pre[3] ? 1 : 0);
+      rr[u] = i < nrec ? rb[(int64_t)q * BL_EB + (i - pre[q])] : bl_rec{lo, 0.0f, 0, 0u};
+    }
+#pragma unroll
+    for (int u = 0; u < RU; u++) {
+    if (base + u * NT >= nrec) break;
+    const bl_rec r = rr[u];
+    const int p = r.tok - lo;
+    int cc = fp ? r.cnt : 0, wc = rp ? (int)(r.wf & BL_WF_WMASK) : 0;
+    if (SPEC) {
+      for (int e = 0; e < nd; e++)
+        if (dl[e].tok == r.tok) {
+          if (sp.fp_on) cc += dl[e].dcnt;
+          if (sp.rep_on) wc += dl[e].dwcnt;
+        }
+      atomicOr(&done[p >> 5], 1u << (p & 31));
+    }
+    float v = vals[p];
+    if (!((sup[p >> 5] >> (p & 31)) & 1u) && ((r.wf >> BL_WF_SHIFT) & BL_TF_BIAS)) v = v + r.bias;
+    vals[p] = stage_counts(sp, v, cc, wc);
+    }
+  }
+  if (SPEC && nd > 0) {
+    __syncthreads(); /* record marks */
+    for (int e = t; e < nd; e += NT) {
+      const int32_t tok = dl[e].tok;
+      const int p = tok - lo;
+      if (p < 0 || p >= n || ((done[p >> 5] >> (p & 31)) & 1u)) continue;
+      bool first = true;
+      int cc = 0, wc = 0;
+      for (int e2 = 0; e2 < nd; e2++)
+        if (dl[e2].tok == tok) {
+          first = first && e2 >= e;
+          cc += dl[e2].dcnt;
+          wc += dl[e2].dwcnt;
+        }
+      if (first) vals[p] = stage_counts(sp, vals[p], sp.fp_on ? cc : 0, sp.rep_on ? wc : 0);
+    }
+  }
+  __syncthreads(); /* before the caller reads `vals` back */
+}
+
+/* One token's value after the model tail and the server stages: apply_stages' arithmetic for a single
+ * token, its record found through the slot's token index. For the places that need a handful of tokens (the
+ * normaliser's fallback walk, grammar maxima, the forced end-of-sequence token). */
+__device__ __forceinline__ float bl_row_value(const bl_dev &d, const bl_slot_dev &sp, const bl_rows &rows, int row, int slot,
+                              const float *logits, int64_t ld, int32_t tok) {
+  float x = logits[(int64_t)row * ld + tok];
+  const float lmul = sp.logit_mul, cap = sp.final_softcap;
+  if (lmul != 1.0f) x = x * lmul;
+  if (cap > 0.0f) {
+    const float q = x / cap;
+    x = cap * bl_tanhf(q);
+  }
+  bool sup = false;
+  if (sp.ignore_eos)
+    for (int k = 0; k < d.n_eog; k++) sup |= d.eog[k] == tok;
+  if (sup) x = -1000000000.0f;
+  const bool fp = sp.fp_on && sp.n_reply > 0, rp = sp.rep_on && sp.n_tokens > 0;
+  int cc = 0, wc = 0;
+  const int ri = d.ridx[(int64_t)slot * d.vocab + tok];
+  if (ri >= 0) {
+    const bl_rec r = d.rec[((int64_t)slot * d.nb + tok / BL_EB) * BL_EB + ri];
+    if (!sup && ((r.wf >> BL_WF_SHIFT) & BL_TF_BIAS)) x = x + r.bias;
+    cc = fp ? r.cnt : 0;
+    wc = rp ? (int)(r.wf & BL_WF_WMASK) : 0;
+  }
+  if (rows.delta) {
+    const int nd = rows.delta_n[row];
+    const bl_sdelta *dl = rows.delta + (int64_t)row * BL_SPEC_DCAP;
+    for (int e = 0; e < nd; e++)
+      if (dl[e].tok == tok) {
+        if (sp.fp_on) cc += dl[e].dcnt;
+        if (sp.rep_on) wc += dl[e].dwcnt;
+      }
+  }
+  return stage_counts(sp, x, cc, wc);
+}
+
 /* ------------------------------------------------------------------ K1: row pass */
-/* SPEC: the row may carry speculative count corrections (compiled separately: the correction loops
- * cost the ordinary row pass registers). HALVES: the touched tokens' records are gathered and applied in
- * two halves of the thread's positions (one more dependent load, fewer registers: more workgroups per CU
- * for grids that do not fit the chip at once) */
-template <bool SPEC, bool HALVES>
+/* SPEC: the rows may carry speculative count corrections (compiled separately) */
+template <bool SPEC>
 __device__ __forceinline__ void rowpass_body(const bl_dev &d, const float *__restrict__ logits, int64_t ld,
                                              const bl_rows &rows) {
   const int V = d.vocab, nc = d.nc;
@@ -180,6 +331,7 @@ __device__ __forceinline__ void rowpass_body(const bl_dev &d, const float *__res
   __shared__ int out_n;
   __shared__ uint32_t tk_wb[BL_RP_THREADS / 64];
   __shared__ int tk_n;
+  __shared__ uint32_t st_sup[BL_CH / 32], st_done[SPEC ? BL_CH / 32 : 1];
 
   const int i0 = c * BL_CH;
   const int cnt = min(BL_CH, V - i0);
@@ -187,18 +339,8 @@ __device__ __forceinline__ void rowpass_body(const bl_dev &d, const float *__res
   if (c == 0 && t == 0) {
     /* consumed by the kernels that run after this one */
     d.gamb[row] = 0;
+    d.ncrit[row] = 0;
   }
-  /* model tail (src/model.br:973-984), applied in registers by the thread that loads the value */
-  const float lmul = sp.logit_mul, cap = sp.final_softcap;
-  const bool tail = lmul != 1.0f || cap > 0.0f;
-  auto finish = [&](float x) {
-    if (lmul != 1.0f) x = x * lmul;
-    if (cap > 0.0f) {
-      float q = x / cap;
-      x = cap * bl_tanhf(q);
-    }
-    return x;
-  };
   /* thread t owns the chunk positions j*1024 + 4t + q (j, q < 4): one float4 per 1024; positions past
    * the row hold -inf */
   constexpr int NV = BL_CH / (4 * BL_RP_THREADS);
@@ -218,96 +360,20 @@ __device__ __forceinline__ void rowpass_body(const bl_dev &d, const float *__res
 #pragma unroll
     for (int k = 0; k < 4 * NV; k++) x[k] = pos_of(k) < cnt ? src[pos_of(k)] : BL_NEG_INF;
   }
-  if (tail) {
-#pragma unroll
-    for (int k = 0; k < 4 * NV; k++)
-      if (pos_of(k) < cnt) x[k] = finish(x[k]);
-  }
-  /* server stages at the touched tokens among this thread's positions: each 4-position group lies in
-   * one word of the touched bitmap; every touched token's table entries are loaded before any is used */
+  /* model tail and server stages at the chunk's modified tokens, in LDS (thread t's positions keep their
+   * float4 layout) */
   {
-    const uint32_t *tw = d.touched + (int64_t)slot * d.words;
-    uint32_t tb[NV];
-    bool any = false;
+    float4 *xv = reinterpret_cast<float4 *>(xs);
+#pragma unroll
+    for (int j = 0; j < NV; j++) xv[j * BL_RP_THREADS + t] = make_float4(x[4 * j], x[4 * j + 1], x[4 * j + 2], x[4 * j + 3]);
+    apply_stages<SPEC>(d, sp, rows, row, slot, i0, cnt, xs, st_sup, st_done);
 #pragma unroll
     for (int j = 0; j < NV; j++) {
-      const int p = j * (4 * BL_RP_THREADS) + 4 * t;
-      tb[j] = p < cnt ? (tw[(i0 + p) >> 5] >> ((i0 + p) & 31)) & 0xFu : 0u;
-      any |= tb[j] != 0u;
-    }
-    /* a speculative row's count corrections: bit k of dm marks this thread's position k */
-    const int nd = SPEC && rows.delta ? rows.delta_n[row] : 0;
-    const bl_sdelta *dl = SPEC && rows.delta ? rows.delta + (int64_t)row * BL_SPEC_DCAP : nullptr;
-    uint32_t dm = 0u;
-    for (int e = 0; e < nd; e++) {
-      const int p = dl[e].tok - i0;
-      if (p >= 0 && p < cnt && ((p & (4 * BL_RP_THREADS - 1)) >> 2) == t)
-        dm |= 1u << ((p / (4 * BL_RP_THREADS)) * 4 + (p & 3));
-    }
-    any |= dm != 0u;
-    if (any) {
-      const int64_t so = (int64_t)slot * V + i0;
-      const bool fp = sp.fp_on && sp.n_reply > 0;
-      const bool rp = sp.rep_on && sp.n_tokens > 0;
-      constexpr int NH = HALVES ? 2 : 1, KH = 4 * NV / NH; /* positions per half */
-#pragma unroll
-      for (int h = 0; h < NH; h++) {
-        if (HALVES && h > 0) asm volatile("" ::: "memory"); /* the second half's loads stay after the first's use */
-        uint32_t f[KH];
-        float bv[KH];
-        int32_t cc[KH], wc[KH];
-        /* every load is issued unconditionally (a position that is not touched reads the chunk's first
-         * record, a line all of them share, and discards it), so the gathers are in flight together
-         * instead of one branch and one round trip each */
-#pragma unroll
-        for (int kk = 0; kk < KH; kk++) {
-          const int k = h * KH + kk;
-          const bool on = ((tb[k >> 2] >> (k & 3)) & 1u) || ((dm >> k) & 1u);
-          const bl_tok r = d.tokst[so + (on ? pos_of(k) : 0)];
-          f[kk] = on ? r.flags : 0u;
-          bv[kk] = r.bias;
-          cc[kk] = fp && on ? r.cnt : 0;
-          wc[kk] = rp && on ? r.wcnt : 0;
-        }
-#pragma unroll
-        for (int kk = 0; kk < KH; kk++) {
-          const int k = h * KH + kk;
-          if (!((tb[k >> 2] >> (k & 3)) & 1u) && !((dm >> k) & 1u)) continue;
-          if (SPEC && ((dm >> k) & 1u)) {
-            int dc = 0, dw = 0;
-            for (int e = 0; e < nd; e++)
-              if (dl[e].tok == i0 + pos_of(k)) {
-                dc += dl[e].dcnt;
-                dw += dl[e].dwcnt;
-              }
-            if (sp.fp_on) cc[kk] += dc;
-            if (sp.rep_on) wc[kk] += dw;
-          }
-          float v = x[k];
-          if (f[kk] & BL_TF_BIAS) v = v + bv[kk];
-          if (f[kk] & BL_TF_SUPPRESS) v = -1000000000.0f;
-          if (cc[kk] > 0) {
-            float tcf = (float)cc[kk] * sp.frequency_penalty;
-            v = v - tcf;
-            v = v - sp.presence_penalty;
-          }
-          if (wc[kk] > 0) v = v > 0.0f ? v / sp.repeat_penalty : v * sp.repeat_penalty;
-          x[k] = v;
-        }
-      }
-    }
-  }
-  /* transformed row */
-  {
-    float *dst = d.eff + (int64_t)row * V + i0;
-    if (vec && (((uintptr_t)dst) & 15) == 0) {
-#pragma unroll
-      for (int j = 0; j < NV; j++)
-        reinterpret_cast<float4 *>(dst)[j * BL_RP_THREADS + t] = make_float4(x[4 * j], x[4 * j + 1], x[4 * j + 2], x[4 * j + 3]);
-    } else {
-#pragma unroll
-      for (int k = 0; k < 4 * NV; k++)
-        if (pos_of(k) < cnt) dst[pos_of(k)] = x[k];
+      const float4 v = xv[j * BL_RP_THREADS + t];
+      x[4 * j] = v.x;
+      x[4 * j + 1] = v.y;
+      x[4 * j + 2] = v.z;
+      x[4 * j + 3] = v.w;
     }
   }
   /* max and first argmax; then, for logprob rows, approximate sums of exp(x - chunk max) over each BL_EB
@@ -545,180 +611,53 @@ __device__ __forceinline__ void rowpass_body(const bl_dev &d, const float *__res
 
 __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass(bl_dev d, const float *__restrict__ logits, int64_t ld,
                                                               bl_rows rows) {
-  rowpass_body<false, false>(d, logits, ld, rows);
-}
-__global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass_wide(bl_dev d, const float *__restrict__ logits,
-                                                                   int64_t ld, bl_rows rows) {
-  rowpass_body<false, true>(d, logits, ld, rows);
+  rowpass_body<false>(d, logits, ld, rows);
 }
 __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass_spec(bl_dev d, const float *__restrict__ logits,
                                                                    int64_t ld, bl_rows rows) {
-  rowpass_body<true, false>(d, logits, ld, rows);
+  rowpass_body<true>(d, logits, ld, rows);
 }
 
-/* ------------------------------------------------------------------ K2: exponent pass + top-K merge */
+/* ------------------------------------------------------------------ K2: exponent pass */
 /*
- * The row's top K keys (value desc, index asc; top_k_select, src/sampling.br:280-296) from the chunks'
- * lists of the row pass (each sorted, K long), into d.mkey[row][0..K) (0 = unfilled: the row holds fewer
- * than K values above -1e30). merge_lists takes the first L keys of every list: a radix selection over the
- * 64-bit order keys, 8 bits per pass from the top, narrows them until the keys at or above the current
- * bound number at most `cap` (at the last pass the bound is the K-th key itself, so exactly K remain);
- * those are ranked by counting. The keys are distinct (they carry the index), so ranks are a permutation.
- * Keys stay in registers when the lists hold at most BL_MERGE_REG per thread, and are re-read from memory
- * per pass otherwise. Returns the K-th key of the merged prefixes (0 when they hold fewer than K).
+ * grid (ceil(V / BL_EB), B) x 256, rows with logprobs or a full-vocabulary rank: thread t holds the block's
+ * positions 4t..4t+3 (one float4 of the logits), a 64-term group is 16 threads. The block re-reads its
+ * logits, applies the model tail and the server stages at its bucket's records (the row pass's values,
+ * recomputed: no transformed row is stored), then writes
+ *   - per 64-term group, the exact terms' composed automaton at the binade of the group's approximate start
+ *     (bl_grec1), and per block a summary (bl_grec1 + a mask of critical groups);
+ *   - per critical group (the sum may cross a power of two inside it), an entry of the row's critical list:
+ *     the terms, their prefix compositions at the start binade, suffix compositions at the end binade, and
+ *     the block's group records, so that the selection resolves the crossing without re-deriving anything;
+ *   - the candidates of a full-vocabulary rank (within bl_cand_span of the row maximum).
+ * The critical list is appended with one device-scope atomic per critical group (a few per row); no
+ * workgroup waits for another: the selection kernel, a later launch, reads the list.
  */
-#define BL_MERGE_REG 8 /* keys per thread held in registers: 8 keeps the exponent pass at 50 VGPRs (8 waves/SIMD) */
-#define BL_MERGE_CAP 512
-#define BL_MERGE_L 16      /* keys per list of the first, prefix-only merge */
-#define BL_MERGE_PREFIX 1024 /* the prefix merge's key budget (nc * L) */
-static_assert(BL_MERGE_CAP >= BL_KSEL_MAX, "the last radix pass leaves exactly K keys");
-__device__ uint64_t merge_lists(const bl_dev &d, int row, int K, int L, int cap) {
-  constexpr int NT = BL_RP_THREADS;
-  const int nc = d.nc, t = threadIdx.x;
-  const int total = nc * L;
-  __shared__ uint32_t hist[256];
-  __shared__ uint32_t res[4];
-  __shared__ uint32_t wsum[NT / 64];
-  __shared__ uint64_t surv[BL_MERGE_CAP];
-  __shared__ int s_cnt;
-  __shared__ uint64_t s_kth;
-  auto load_key = [&](int i) -> uint64_t {
-    const int ch = i / L, q = i - ch * L;
-    const int64_t o = ((int64_t)row * nc + ch) * BL_KSEL_MAX + q;
-    const int32_t id = d.cand_i[o];
-    return id >= 0 ? ckey(d.cand_v[o], id) : 0ull;
-  };
-  const bool inreg = total <= NT * BL_MERGE_REG;
-  uint64_t kr[BL_MERGE_REG];
-#pragma unroll
-  for (int j = 0; j < BL_MERGE_REG; j++) {
-    const int i = t + j * NT;
-    kr[j] = inreg && i < total ? load_key(i) : 0ull;
-  }
-  auto each = [&](auto f) {
-    if (inreg) {
-#pragma unroll
-      for (int j = 0; j < BL_MERGE_REG; j++) f(kr[j]);
-    } else {
-      for (int i = t; i < total; i += NT) f(load_key(i));
-    }
-  };
-  /* valid keys */
-  int mine = 0;
-  each([&](uint64_t k) { mine += k != 0ull ? 1 : 0; });
-  if (t == 0) {
-    s_cnt = 0;
-    s_kth = 0ull;
-  }
-  __syncthreads();
-  if (mine) atomicAdd(&s_cnt, mine);
-  __syncthreads();
-  const int n_valid = s_cnt;
-  uint64_t lo = 1ull; /* survivors: keys >= lo (every valid key when the lists hold at most K) */
-  if (n_valid > K) {
-    uint64_t prefix = 0ull, pmask = 0ull;
-    int need = K;
-    for (int shift = 56; shift >= 0; shift -= 8) {
-      static_assert(NT == 256, "one histogram bin per thread");
-      hist[t] = 0u;
-      __syncthreads();
-      each([&](uint64_t k) {
-        if (k != 0ull && (k & pmask) == prefix) atomicAdd(&hist[(uint32_t)(k >> shift) & 255u], 1u);
-      });
-      __syncthreads();
-      block_find_bin<NT>(hist, 256, (uint32_t)need, res, wsum);
-      const uint32_t bin = res[0], above = res[1], inbin = res[2];
-      prefix |= (uint64_t)bin << shift;
-      pmask |= 0xFFull << shift;
-      lo = prefix;
-      if ((K - need) + (int)(above + inbin) <= cap) break;
-      need -= (int)above;
-    }
-  }
-  __syncthreads();
-  if (t == 0) s_cnt = 0;
-  __syncthreads();
-  each([&](uint64_t k) {
-    if (k != 0ull && k >= lo) {
-      const int p = atomicAdd(&s_cnt, 1);
-      if (p < cap) surv[p] = k;
-    }
-  });
-  __syncthreads();
-  const int ns = min(s_cnt, cap);
-  uint64_t *out = d.mkey + (int64_t)row * BL_KSEL_MAX;
-  for (int i = t; i < ns; i += NT) {
-    const uint64_t k = surv[i];
-    int r = 0, j = 0;
-    for (; j + 4 <= ns; j += 4)
-      r += (surv[j] > k ? 1 : 0) + (surv[j + 1] > k ? 1 : 0) + (surv[j + 2] > k ? 1 : 0) + (surv[j + 3] > k ? 1 : 0);
-    for (; j < ns; j++) r += surv[j] > k ? 1 : 0;
-    if (r < K) out[r] = k;
-    if (r == K - 1) s_kth = k;
-  }
-  for (int q = ns + t; q < K; q += NT) out[q] = 0ull;
-  __syncthreads();
-  const uint64_t kth = s_kth;
-  __syncthreads();
-  return kth;
-}
-
-/* The merge from the first L keys of every list is the row's exact top K unless some list was cut while its
- * last key read is above the K-th key found (then its unread keys could rank in the top K): that case, and
- * K <= L, merge the whole lists. */
-__device__ void merge_topk(const bl_dev &d, int row, int K) {
-  const int nc = d.nc, t = threadIdx.x;
-  const int L = min(BL_MERGE_L, BL_MERGE_PREFIX / nc);
-  if (L >= 1 && L < K) {
-    __shared__ int s_cut;
-    const uint64_t kth = merge_lists(d, row, K, L, K <= 96 ? 128 : BL_MERGE_CAP);
-    if (t == 0) s_cut = 0;
-    __syncthreads();
-    for (int ch = t; ch < nc; ch += BL_RP_THREADS) {
-      const int64_t o = ((int64_t)row * nc + ch) * BL_KSEL_MAX + (L - 1);
-      const int32_t id = d.cand_i[o];
-      if (id >= 0 && ckey(d.cand_v[o], id) > kth) s_cut = 1;
-    }
-    __syncthreads();
-    const int cut = s_cut;
-    __syncthreads();
-    if (!cut) return;
-  }
-  merge_lists(d, row, K, K, BL_MERGE_CAP);
-}
-
-/* grid (1 + ceil(V / BL_EB), B) x 256. The first B workgroups in dispatch order merge the top-K candidates
- * of rows that have them (sampling or logprob alternatives); the others serve the rows with logprobs or a
- * full-vocabulary rank: thread t holds the block's terms 4t..4t+3, a 64-term group is 16 threads */
-__global__ __launch_bounds__(BL_RP_THREADS) void bl_k_exppass(bl_dev d, bl_rows rows) {
+template <bool SPEC>
+__device__ __forceinline__ void exppass_body(const bl_dev &d, const float *__restrict__ logits, int64_t ld,
+                                             const bl_rows &rows) {
   const int V = d.vocab, nc = d.nc;
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-  /* linear workgroup ids 0..B-1 (dispatched first) merge; the rest are row-major exponent blocks */
-  const int nrows = (int)gridDim.y, nbx = (int)gridDim.x - 1;
-  const int lin = (int)blockIdx.y * (int)gridDim.x + (int)blockIdx.x;
-  const bool merger = lin < nrows;
-  const int row = merger ? lin : (lin - nrows) / nbx;
-  const int b = merger ? 0 : (lin - nrows) - row * nbx;
+  const int b = blockIdx.x, row = blockIdx.y;
   const int slot = bl_row_slot(rows, row);
   const bl_slot_dev &sp = slot_of(d, slot);
   const int mode = sp.mode;
-  if (merger) {
-    if (sp.k_sel > 0) merge_topk(d, row, sp.k_sel);
-    return;
-  }
   if (!(mode & (BL_M_LOGPROBS | BL_M_FULL))) return;
   __shared__ uint64_t s_tab[BL_EXP2_N]; /* expf's 2^(i/32) table */
+  __shared__ float vals[BL_EB];
+  __shared__ uint32_t st_sup[BL_EB / 32], st_done[SPEC ? BL_EB / 32 : 1];
   __shared__ double wtot[BL_RP_THREADS / 64];
   __shared__ uint32_t bs_crit[BL_RP_THREADS / 64];
   __shared__ int bs_E[BL_RP_THREADS / 64];
   __shared__ bool bs_same[BL_RP_THREADS / 64];
   __shared__ bl_inc bs_v[BL_RP_THREADS / 64];
+  __shared__ bl_grec1 s_grp[BL_EB / 64];
   if (t < BL_EXP2_N) s_tab[t] = bl_exp2_tab[t];
   const int i0 = b * BL_EB;
   const int cnt = min(BL_EB, V - i0);
   const int j0 = 4 * t;
   float x[4];
-  const float *src = d.eff + (int64_t)row * V + i0 + j0;
+  const float *src = logits + (int64_t)row * ld + i0 + j0;
   if (j0 + 4 <= cnt && (((uintptr_t)src) & 15) == 0) {
     const float4 v = *reinterpret_cast<const float4 *>(src);
     x[0] = v.x;
@@ -733,11 +672,19 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_exppass(bl_dev d, bl_rows 
   float M = BL_NEG_INF;
   int Mi = 0x7fffffff;
   for (int k = lane; k < nc; k += 64) argmax_merge(M, Mi, d.c_max[(int64_t)row * nc + k], d.c_arg[(int64_t)row * nc + k]);
+  /* model tail and server stages, as the row pass applied them */
+  *reinterpret_cast<float4 *>(vals + j0) = make_float4(x[0], x[1], x[2], x[3]);
+  apply_stages<SPEC>(d, sp, rows, row, slot, i0, cnt, vals, st_sup, st_done);
+  {
+    const float4 v = *reinterpret_cast<const float4 *>(vals + j0);
+    x[0] = v.x;
+    x[1] = v.y;
+    x[2] = v.z;
+    x[3] = v.w;
+  }
   bl_wargmax(M, Mi, lane);
 
   if (mode & BL_M_LOGPROBS) {
-    /* approximate sum before this block, from the row pass's sums per BL_EB positions (every
-     * wavefront computes the same value) */
     /* lane k: chunk k's sub-blocks before this block, scaled by the hardware exponential (a prediction:
      * its error, ~1e-7 relative, is far inside the 2^-20 margin of the critical-group test, and a wrong
      * binade is caught on the exact state) */
@@ -766,40 +713,39 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_exppass(bl_dev d, bl_rows 
     const double ex = bl_wave_excl_scan_d(sa, lane);
     if (lane == 63) wtot[w] = ex + sa;
     __syncthreads();
-    double before = S0 + ex, tot = 0.0;
-    for (int q = 0; q < BL_RP_THREADS / 64; q++) {
+    double before = S0 + ex;
+    for (int q = 0; q < BL_RP_THREADS / 64; q++)
       if (q < w) before += wtot[q];
-      tot += wtot[q];
-    }
     /* group of 64 terms = 16 threads (one row of the wavefront); its approximate start is its first
      * thread's prefix, raised to the exact floor 1.0 once the row maximum's term exp(0) = 1 is behind it.
      * The row's last lane holds the group's composed automaton (row scan) and its approximate end (its own
      * inclusive prefix), and writes the record. */
+    const int gl = lane & ~15, tail_l = gl | 15, r16 = lane & 15;
     const int gs = i0 + 4 * (t & ~15);
     const double floor1 = gs > Mi ? 1.0 : 0.0;
-    const double gs0 = __shfl(before, lane & ~15, 64);
+    const double gs0 = __shfl(before, gl, 64);
     const double gstart = gs0 > floor1 ? gs0 : floor1;
     const int E = bl_binade_of(gstart);
-    const bl_inc gv = bl_row_scan(bl_thread_compose<4>(a, E), lane);
-    const bool tail = (lane & 15) == 15;
+    const bl_inc tc = bl_thread_compose<4>(a, E);
+    const bl_inc gv = bl_row_scan(tc, lane);
+    const bool tail = r16 == 15;
     const bool gex = 4 * (t & ~15) < cnt;
-    const int g = (i0 + 4 * (t & ~15)) >> 6;
+    const int g = gs >> 6;
     bl_grec1 *rec = reinterpret_cast<bl_grec1 *>(reinterpret_cast<bl_grec *>(d.grec) + (int64_t)row * 2 * (V / 64 + 64));
-    float *apx = d.gapx + (int64_t)row * (V / 64 + 64);
+    const double gend = before + sa;
+    const double gend_f = gend > floor1 ? gend : floor1;
+    const bool crit = gex && bl_group_critical((float)gstart, (float)gend_f, E, floor1);
     if (tail && gex) {
       bl_grec1 r;
       r.E = E;
       r.pad = 0;
       r.v = gv;
       rec[g] = r;
-      apx[g] = (float)gstart;
+      s_grp[g & 15] = r;
     }
-    if (i0 + BL_EB >= V && t == BL_RP_THREADS - 1) apx[(V + 63) / 64] = (float)(S0 + tot); /* the row's total */
     /* block summary for the normaliser: the critical groups (approximate start or end not safely inside
      * the predicted binade), and, when there is none and every group has the same binade, the block's
      * automaton composed in order (wavefront w holds groups 4w..4w+3) */
-    const double gend = before + sa;
-    const bool crit = gex && bl_group_critical((float)gstart, (float)(gend > floor1 ? gend : floor1), E, floor1);
     const unsigned long long cb = __ballot(crit && tail);
     const unsigned long long eb = __ballot(gex && tail);
     const int E0 = (int)bl_bcast((uint32_t)E, 15);
@@ -814,7 +760,7 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_exppass(bl_dev d, bl_rows 
       bs_same[w] = db == 0ull;
       bs_v[w] = f;
     }
-    __syncthreads();
+    __syncthreads(); /* summaries and s_grp */
     if (t == 0) {
       uint32_t mask = 0u;
       const int Eb = bs_E[0];
@@ -833,11 +779,63 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_exppass(bl_dev d, bl_rows 
       reinterpret_cast<bl_grec1 *>(d.brec)[(int64_t)row * d.nb + b] = br;
       d.bcrit[(int64_t)row * d.nb + b] = mask;
     }
+    /* critical groups: an entry of the row's critical list each (wavefront-uniform branch; the lanes of
+     * other groups compute alongside and write nothing) */
+    if (cb) {
+      const bool gcrit = __shfl(crit ? 1 : 0, tail_l, 64) != 0;
+      const int e1 = bl_binade_of(__shfl(gend_f, tail_l, 64));
+      int slot_i = 0;
+      if (gcrit && tail) slot_i = atomicAdd(&d.ncrit[row], 1);
+      slot_i = __shfl(slot_i, tail_l, 64);
+      /* prefix compositions at E: the row scan's exclusive prefix (identity at the row's first lane), then
+       * the thread's own terms */
+      const uint32_t x0 = bl_dpp<BL_DPP_ROW_SHR(1), 0xF>(0u, gv.d0), x1 = bl_dpp<BL_DPP_ROW_SHR(1), 0xF>(0u, gv.d1);
+      bl_inc px = r16 == 0 ? bl_inc_ident() : bl_inc{x0, x1};
+      bl_inc cp[4];
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        px = bl_compose(px, bl_term_inc(a[q], E));
+        cp[q] = px;
+      }
+      /* suffix compositions at e1: the thread's own suffixes, then the following threads of the group in
+       * order (a reversed scan over the row's 16 lanes) */
+      bl_inc sfx[4];
+      bl_inc acc = bl_inc_ident();
+#pragma unroll
+      for (int q = 3; q >= 0; q--) {
+        acc = bl_compose(bl_term_inc(a[q], e1), acc);
+        sfx[q] = acc;
+      }
+      bl_inc rv = acc; /* composition of this thread's four terms at e1, then those after it */
+#pragma unroll
+      for (int k = 1; k < 16; k <<= 1) {
+        const bl_inc o = bl_inc{(uint32_t)__shfl_down((int)rv.d0, k, 64), (uint32_t)__shfl_down((int)rv.d1, k, 64)};
+        if (r16 + k < 16) rv = bl_compose(rv, o);
+      }
+      const bl_inc nx = bl_inc{(uint32_t)__shfl_down((int)rv.d0, 1, 64), (uint32_t)__shfl_down((int)rv.d1, 1, 64)};
+      const bl_inc after = r16 == 15 ? bl_inc_ident() : nx;
+      if (gcrit && slot_i < BL_CRIT_MAX) {
+        bl_crit &ce = d.crit[(int64_t)row * BL_CRIT_MAX + slot_i];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          ce.terms[4 * r16 + q] = a[q];
+          ce.cp[4 * r16 + q] = cp[q];
+          ce.cs[4 * r16 + q] = bl_compose(sfx[q], after);
+        }
+        ce.blk[r16] = s_grp[r16];
+        if (tail) {
+          ce.g = g;
+          ce.e0 = E;
+          ce.e1 = e1;
+          ce.ng = min(BL_EB / 64, (cnt + 63) / 64);
+        }
+      }
+    }
   }
   if (mode & BL_M_FULL) {
     /* candidates of a full-vocabulary rank (within bl_cand_span of the maximum). The block writes them
      * in index order to its own BL_EB-entry region, and their count: no counter is shared between
-     * workgroups (one would serialise device-scope atomics across XCDs) */
+     * workgroups */
     __shared__ int f_w[BL_RP_THREADS / 64];
     const float T = sp.temperature;
     const bool filt = bl_probs_on(sp);
@@ -885,17 +883,28 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_exppass(bl_dev d, bl_rows 
   }
 }
 
+__global__ __launch_bounds__(BL_RP_THREADS) void bl_k_exppass(bl_dev d, const float *__restrict__ logits, int64_t ld,
+                                                              bl_rows rows) {
+  exppass_body<false>(d, logits, ld, rows);
+}
+__global__ __launch_bounds__(BL_RP_THREADS) void bl_k_exppass_spec(bl_dev d, const float *__restrict__ logits,
+                                                                   int64_t ld, bl_rows rows) {
+  exppass_body<true>(d, logits, ld, rows);
+}
+
 /* ------------------------------------------------------------------ K2g: grammar allow-mask */
 /*
  * grid (ceil(V/256), B) x 256 over the rows of grammar slots; one lane per token. The allowed
  * predicate of sample_grammar_token (src/server.br:334-350): an end-of-generation token when the
  * frontier is complete and ignore_eos is off, any other token when grammar_advance_text(frontier,
  * piece) is not empty. Writes the packed allow-bitmask (a __ballot per wavefront), the frontier's
- * status (src/server.br:311-321), and, with `with_values`, each block's allowed maximum of the
- * transformed row with its lowest index and the number of allowed tokens equal to it (the first
- * allowed candidate in rank order of a greedy step, src/server.br:351-356).
+ * status (src/server.br:311-321), and, with `with_values`, each block's allowed maximum of the row after
+ * the model tail and server stages (bl_row_value of the allowed tokens: a grammar leaves few) with its
+ * lowest index and the number of allowed tokens equal to it (the first allowed candidate in rank order of
+ * a greedy step, src/server.br:351-356).
  */
-__global__ __launch_bounds__(BL_GM_THREADS) void bl_k_gmask(bl_dev d, bl_rows rows, int with_values) {
+__global__ __launch_bounds__(BL_GM_THREADS) void bl_k_gmask(bl_dev d, const float *__restrict__ logits, int64_t ld,
+                                                            bl_rows rows, int with_values) {
   const int V = d.vocab, row = blockIdx.y, t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int slot = bl_row_slot(rows, row);
   const bl_slot_dev &sp = d.slots[slot];
@@ -944,7 +953,7 @@ __global__ __launch_bounds__(BL_GM_THREADS) void bl_k_gmask(bl_dev d, bl_rows ro
   /* allowed maximum of this block, lowest index, and its multiplicity */
   float m = BL_NEG_INF;
   int mi = 0x7fffffff;
-  const float v = allowed ? d.eff[(int64_t)row * V + tok] : BL_NEG_INF;
+  const float v = allowed ? bl_row_value(d, sp, rows, row, slot, logits, ld, (int32_t)tok) : BL_NEG_INF;
   if (allowed) {
     m = v;
     mi = (int)tok;
@@ -968,7 +977,7 @@ __global__ __launch_bounds__(BL_GM_THREADS) void bl_k_gmask(bl_dev d, bl_rows ro
 #define SEL_NW (BL_SEL_THREADS / 64)
 
 
-__device__ void bitonic_desc(uint64_t *s, int P) {
+__device__ __forceinline__ void bitonic_desc(uint64_t *s, int P) {
   for (int k = 2; k <= P; k <<= 1)
     for (int j = k >> 1; j > 0; j >>= 1) {
       for (int i = threadIdx.x; i < P; i += blockDim.x) {
@@ -991,7 +1000,7 @@ __device__ void bitonic_desc(uint64_t *s, int P) {
  * float running sum before its group, g*64 terms, is within g*64*2^-24 (recursive summation bound, with
  * a 1% margin) of the approximate prefix and that interval lies in one binade. */
 template <class ValF, class TermF>
-__device__ void block_records(int64_t n, ValF val, TermF term, bl_grec *recs, double *gsum, float *tbuf) {
+__device__ __forceinline__ void block_records(int64_t n, ValF val, TermF term, bl_grec *recs, double *gsum, float *tbuf) {
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int64_t G = (n + 63) / 64;
   /* each loop loads the next group's inputs before this group's stores: global stores share the
@@ -1047,9 +1056,11 @@ struct sel_norm {
   int32_t bE[BL_STAGE_B];              /* each block's binade, BL_E_NONE when not composable as a whole */
   bl_inc bV[BL_STAGE_B];               /* each block's composed automaton */
   float terms[BL_CRIT_MAX * 64];       /* the critical groups' terms */
-  bl_inc cp[BL_CRIT_MAX * 64];         /* their prefix scans at the predicted start binade */
-  bl_inc cs[BL_CRIT_MAX * 65];         /* their suffix scans at the predicted end binade (+ identity) */
+  bl_inc cp[BL_CRIT_MAX * 64];         /* their prefix compositions at the predicted start binade */
+  bl_inc cs[BL_CRIT_MAX * 64];         /* their suffix compositions at the predicted end binade */
+  bl_grec1 blk[BL_CRIT_MAX * (BL_EB / 64)]; /* the group records of each critical group's block */
   int ce0[BL_CRIT_MAX], ce1[BL_CRIT_MAX]; /* those binades */
+  int eg[BL_CRIT_MAX], epos[BL_CRIT_MAX]; /* the entries' groups, and their positions in group order */
   int crit[BL_CRIT_MAX];               /* critical groups, ascending */
   int r_E[BL_CRIT_MAX + 1];            /* runs between them: predicted binade */
   int r_st[BL_CRIT_MAX + 1];           /* 0 empty, 1 composed in one binade, 2 not composable */
@@ -1094,6 +1105,9 @@ struct sel_shared {
   float red_m[SEL_NW];
   int red_i[SEL_NW];
   int32_t eog[BL_EOG_LDS];             /* the first end-of-generation ids */
+  uint64_t mkeys[BL_KSEL_MAX];         /* the merged top-K keys */
+  uint64_t mtau;                       /* the merge's lower bound on the K-th key */
+  int mcnt;                            /* the merge's survivors */
   uint64_t etab[BL_EXP2_N];            /* expf's 2^(i/32) table (a global table read is a dependent load) */
 };
 /* expf through the selection's LDS copy of the table */
@@ -1111,7 +1125,7 @@ __device__ __forceinline__ bool ranked_supported(const bl_slot_dev &sp, int64_t 
 /* a short ranked list (n_list <= BL_SERIAL_MAX), by every thread: the values, the terms exp(v - v0) of
  * the untempered softmax (when formed) and exp((v - v0) / T) of the draw */
 template <class ValF>
-__device__ void ranked_terms(const bl_slot_dev &sp, ValF val, int64_t n_list, sel_shared &sh) {
+__device__ __forceinline__ void ranked_terms(const bl_slot_dev &sp, ValF val, int64_t n_list, sel_shared &sh) {
   const float T = sp.temperature;
   const bool filt = bl_probs_on(sp);
   const float v0 = val(0);
@@ -1128,7 +1142,7 @@ __device__ void ranked_terms(const bl_slot_dev &sp, ValF val, int64_t n_list, se
 /* ... then the reference's sequential float32 loops over those terms, by one thread: softmax sum, top-p
  * prefix, min-p cut, XTC, tempered sum and the draw (src/sampling.br:505-607); *rng_out = the state after
  * the draw */
-__device__ sel_draw ranked_serial(const bl_slot_dev &sp, int n, int64_t n_logical, int64_t keep, uint64_t rng,
+__device__ __forceinline__ sel_draw ranked_serial(const bl_slot_dev &sp, int n, int64_t n_logical, int64_t keep, uint64_t rng,
                                  int rng_skip, bool pre, sel_shared &sh, uint64_t *rng_out) {
   const float *ser_e = sh.ser_e, *ser_v = sh.ser_v;
   float *ser_r = sh.ser_r;
@@ -1263,7 +1277,7 @@ __device__ sel_draw ranked_serial(const bl_slot_dev &sp, int n, int64_t n_logica
  * full-vocabulary rank a cut between equal distances picks among equal values by the heap's order:
  * reported as a tie.
  */
-__device__ int typical_filter(const bl_slot_dev &sp, int n, bool full, sel_shared &sh, int &status) {
+__device__ __forceinline__ int typical_filter(const bl_slot_dev &sp, int n, bool full, sel_shared &sh, int &status) {
   const int t = threadIdx.x;
   float *tp = reinterpret_cast<float *>(&sh.n); /* the normaliser's LDS is free until norm_prep */
   float *tq = tp + BL_SERIAL_MAX;
@@ -1353,7 +1367,7 @@ __device__ int typical_filter(const bl_slot_dev &sp, int n, bool full, sel_share
  * holds the draw's terms from its first candidate (tbuf[j - first]).
  */
 template <class ValF>
-__device__ sel_draw sample_ranked_long(const bl_slot_dev &sp, ValF val, int64_t n_list, int64_t n_logical,
+__device__ __forceinline__ sel_draw sample_ranked_long(const bl_slot_dev &sp, ValF val, int64_t n_list, int64_t n_logical,
                                       int64_t keep, uint64_t &rng, int rng_skip, bl_grec *recs, double *gsum,
                                       float *tbuf, sel_shared &sh, int &status) {
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
@@ -1536,7 +1550,7 @@ __device__ sel_draw sample_ranked_long(const bl_slot_dev &sp, ValF val, int64_t 
  * mu, the softmax and draw over that prefix, and mu - eta (surprise - tau) for the slot (sh.fres[6]).
  */
 template <class ValF>
-__device__ sel_draw sample_mirostat(const bl_slot_dev &sp, ValF val, int64_t n_list, int64_t n_logical,
+__device__ __forceinline__ sel_draw sample_mirostat(const bl_slot_dev &sp, ValF val, int64_t n_list, int64_t n_logical,
                                     uint64_t &rng, int rng_skip, bl_grec *recs, double *gsum, float *tbuf,
                                     sel_shared &sh, int &status) {
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
@@ -1641,7 +1655,7 @@ __device__ void walk_groups(int64_t g_lo, int64_t g_hi, int64_t n, TermF term, R
     if (valid) {
       const bl_grec r = rec(gl);
       const int k = e - (r.E - 1);
-      if (k >= 0 && k <= 2 && e >= BL_E_MIN) f = r.v[k];
+      if (k >= 0 && k <= 2 && e >= BL_E_MIN) f = k == 0 ? r.v[0] : (k == 1 ? r.v[1] : r.v[2]); /* selects: no dynamic index into private memory */
       else valid = false;
     }
     const uint32_t Nend = bl_apply(bl_wave_scan(f, lane), N);
@@ -1660,28 +1674,43 @@ __device__ void walk_groups(int64_t g_lo, int64_t g_hi, int64_t n, TermF term, R
 }
 
 /*
- * Exact index-order sum of exp(eff[j] - M), j < V (logprob_normalizer, src/sampling.br:254-266), by the
- * whole block (norm_prep) and one wavefront (norm_chain). The exponent pass left, per 64-term group, the composed automaton at the binade of its
- * approximate start, and per 1024-term block the groups where the sum may cross a power of two
- * ("critical") and, for a block without them, the block's composed automaton. The groups between two
- * critical groups form a run in one binade; the wavefronts compose the runs (edge groups, then whole
- * blocks) and, for each critical group, its terms and, for the binades predicted at its start and end,
- * a prefix scan and a suffix scan of their automata. One wavefront then chains runs and critical groups:
- * a run applies at once when the exact state is in its binade and stays there; a critical group needs
- * one ballot for the crossing, one real float add and the suffix. Every prediction is checked on the
- * exact state, and a run or group whose prediction fails is walked group by group and element by
- * element instead.
+ * Exact index-order sum of exp(x[j] - M), j < V (logprob_normalizer, src/sampling.br:254-266), by the whole
+ * block (norm_prep) and one wavefront (norm_chain). The exponent pass left, per 64-term group, the composed
+ * automaton at the binade of its approximate start, per 1024-term block the groups where the sum may cross a
+ * power of two ("critical") and, for a block without them, the block's composed automaton, and for each
+ * critical group an entry with its terms, prefix compositions at the binade of its start, suffix
+ * compositions at the binade of its end and its block's group records. The groups between two critical
+ * groups form a run in one binade; the wavefronts compose the runs (edge groups from the entries, whole
+ * blocks from the summaries). One wavefront then chains runs and critical groups: a run applies at once when
+ * the exact state is in its binade and stays there; a critical group needs one ballot for the crossing, one
+ * real float add and the suffix. Every prediction is checked on the exact state; a run or group whose
+ * prediction fails is walked group by group and element by element (terms recomputed from the logits).
+ * With more critical groups than BL_CRIT_MAX the whole row is walked that way.
  */
-__device__ void norm_prep(const bl_dev &d, int row, float M, sel_shared &sh, uint32_t m_pre, bl_grec1 br_pre) {
+__device__ __forceinline__ void norm_prep(const bl_dev &d, int row, float M, sel_shared &sh, uint32_t m_pre, bl_grec1 br_pre,
+                          int n_ent) {
   const int V = d.vocab, t = threadIdx.x, w = t >> 6, lane = t & 63;
   const int G = (V + 63) / 64, NB = d.nb;
   const bl_grec1 *rec =
       reinterpret_cast<const bl_grec1 *>(reinterpret_cast<const bl_grec *>(d.grec) + (int64_t)row * 2 * (V / 64 + 64));
   const bl_grec1 *brec = reinterpret_cast<const bl_grec1 *>(d.brec) + (int64_t)row * NB;
   const uint32_t *bcrit = d.bcrit + (int64_t)row * NB;
-  const float *apx = d.gapx + (int64_t)row * (V / 64 + 64);
-  const float *eff = d.eff + (int64_t)row * V;
+  const bl_crit *ent = d.crit + (int64_t)row * BL_CRIT_MAX;
   sel_norm &nm = sh.n;
+  /* the entries to LDS in their order of arrival (slot i); nm.epos maps a critical group's rank to its slot */
+  const int ne = n_ent < BL_CRIT_MAX ? n_ent : BL_CRIT_MAX;
+  for (int idx = t; idx < ne * 64; idx += BL_SEL_THREADS) {
+    const int i = idx >> 6, l = idx & 63;
+    nm.terms[idx] = ent[i].terms[l];
+    nm.cp[idx] = ent[i].cp[l];
+    nm.cs[idx] = ent[i].cs[l];
+    if (l < BL_EB / 64) nm.blk[i * (BL_EB / 64) + l] = ent[i].blk[l];
+    if (l == 0) {
+      nm.eg[i] = ent[i].g;
+      nm.ce0[i] = ent[i].e0;
+      nm.ce1[i] = ent[i].e1;
+    }
+  }
   /* 1. critical groups in order (a block-wide scan of the per-block counts); block summaries to LDS */
   int ncrit_all = 0;
   for (int b0 = 0; b0 < NB; b0 += BL_SEL_THREADS) {
@@ -1713,68 +1742,68 @@ __device__ void norm_prep(const bl_dev &d, int row, float M, sel_shared &sh, uin
     ncrit_all += tot;
     __syncthreads();
   }
-  /* past BL_CRIT_MAX critical groups the last run holds the rest (its blocks are not composable) */
-  const int ncrit = ncrit_all < BL_CRIT_MAX ? ncrit_all : BL_CRIT_MAX;
+  /* every critical group has its entry when they number at most BL_CRIT_MAX; past that the row is walked */
+  const bool have = ncrit_all <= BL_CRIT_MAX && ne == ncrit_all;
+  const int ncrit = have ? ncrit_all : 0;
+  /* 2. the slot of each critical group's entry (its rank among the entries' groups) */
+  if (have) {
+    if (t < ncrit) {
+      const int g = nm.eg[t];
+      int p = 0;
+      for (int j = 0; j < ncrit; j++) p += nm.eg[j] < g ? 1 : 0;
+      nm.epos[p] = t;
+    }
+    __syncthreads();
+  }
   auto run_lo = [&](int r) { return r == 0 ? 0 : nm.crit[r - 1] + 1; };
   auto run_hi = [&](int r) { return r == ncrit ? G : nm.crit[r]; };
   auto blk_E = [&](int b) -> int { return b < BL_STAGE_B ? nm.bE[b] : brec[b].E; };
   auto blk_v = [&](int b) -> bl_inc { return b < BL_STAGE_B ? nm.bV[b] : brec[b].v; };
-  /* 2. runs (edge groups and whole blocks) and critical groups, one per wavefront at a time */
+  /* a group record of a block holding critical group r (from its entry) */
+  auto edge = [&](int r, int g) -> bl_grec1 { return nm.blk[nm.epos[r] * (BL_EB / 64) + (g & (BL_EB / 64 - 1))]; };
+  /* 3. runs (edge groups and whole blocks), one per wavefront at a time */
   const int nrun = ncrit + 1;
-  for (int it = w; it < nrun + ncrit; it += SEL_NW) {
-    if (it < nrun) {
-      const int lo = run_lo(it), hi = run_hi(it);
-      int st = 0, Er = BL_E_NONE;
-      bl_inc acc = bl_inc_ident();
-      if (lo < hi) {
-        Er = rec[lo].E;
-        const int gb0 = min((lo + 15) & ~15, hi), gb1 = max(hi & ~15, gb0);
-        const int npre = gb0 - lo, nblk = (gb1 - gb0) >> 4, nit = npre + nblk + (hi - gb1);
-        bool bad = false;
-        for (int i0 = 0; i0 < nit; i0 += 64) {
-          const int i = i0 + lane;
-          bl_inc f = bl_inc_ident();
-          if (i < nit) {
-            int Ei;
-            if (i < npre || i >= npre + nblk) {
-              const bl_grec1 gr = rec[i < npre ? lo + i : gb1 + (i - npre - nblk)];
-              Ei = gr.E;
-              f = gr.v;
-            } else {
-              const int bb = (gb0 >> 4) + (i - npre);
-              Ei = blk_E(bb);
-              f = blk_v(bb);
-            }
-            bad |= Ei != Er;
+  for (int it = w; it < nrun; it += SEL_NW) {
+    const int lo = run_lo(it), hi = run_hi(it);
+    int st = 0, Er = BL_E_NONE;
+    bl_inc acc = bl_inc_ident();
+    if (lo < hi) {
+      const int gb0 = min((lo + 15) & ~15, hi), gb1 = max(hi & ~15, gb0);
+      const int npre = gb0 - lo, nblk = (gb1 - gb0) >> 4, nit = npre + nblk + (hi - gb1);
+      /* a group of a critical group's block from that entry; others (the row's trailing partial block) from
+       * the exponent pass's records */
+      auto grp = [&](int g) -> bl_grec1 {
+        const int bg = g >> 4;
+        if (it > 0 && (nm.crit[it - 1] >> 4) == bg) return edge(it - 1, g);
+        if (it < ncrit && (nm.crit[it] >> 4) == bg) return edge(it, g);
+        return rec[g];
+      };
+      Er = npre > 0 ? grp(lo).E : (nblk > 0 ? blk_E(gb0 >> 4) : grp(gb1).E);
+      bool bad = false;
+      for (int i0 = 0; i0 < nit; i0 += 64) {
+        const int i = i0 + lane;
+        bl_inc f = bl_inc_ident();
+        if (i < nit) {
+          int Ei;
+          if (i < npre || i >= npre + nblk) {
+            const bl_grec1 gr = grp(i < npre ? lo + i : gb1 + (i - npre - nblk));
+            Ei = gr.E;
+            f = gr.v;
+          } else {
+            const int bb = (gb0 >> 4) + (i - npre);
+            Ei = blk_E(bb);
+            f = blk_v(bb);
           }
-          acc = bl_compose(acc, bl_wave_reduce(f, lane));
+          bad |= Ei != Er;
         }
-        st = __ballot(bad) ? 2 : 1;
+        acc = bl_compose(acc, bl_wave_reduce(f, lane));
       }
-      if (lane == 0) {
-        nm.r_E[it] = Er;
-        nm.r_st[it] = st;
-        nm.r_f[it] = acc;
-      }
-    } else {
-      const int ci = it - nrun;
-      const int g = nm.crit[ci];
-      const int64_t j = (int64_t)g * 64 + lane;
-      const bool in = j < V;
-      const float a = in ? SEL_EXPF(eff[j] - M) : 0.0f;
-      const int e0 = rec[g].E, e1 = bl_binade_of((double)apx[g + 1]);
-      nm.terms[ci * 64 + lane] = a;
-      nm.cp[ci * 64 + lane] = bl_wave_scan(in ? bl_term_inc(a, e0) : bl_inc_ident(), lane);
-      /* suffixes: lane l takes term 63 - l, and the reversed scan leaves in it the composition of terms
-       * 63 - l .. 63 in order */
-      const float ar = __shfl(a, 63 - lane, 64);
-      const bool inr = (int64_t)g * 64 + (63 - lane) < V;
-      nm.cs[ci * 65 + (63 - lane)] = bl_wave_scan<true>(inr ? bl_term_inc(ar, e1) : bl_inc_ident(), lane);
-      if (lane == 0) {
-        nm.cs[ci * 65 + 64] = bl_inc_ident();
-        nm.ce0[ci] = e0;
-        nm.ce1[ci] = e1;
-      }
+      st = __ballot(bad) ? 2 : 1;
+    }
+    if (lane == 0) {
+      nm.r_E[it] = Er;
+      nm.r_st[it] = st;
+      nm.r_f[it] = acc;
     }
   }
   if (t == 0) nm.ncrit = ncrit;
@@ -1784,15 +1813,15 @@ __device__ void norm_prep(const bl_dev &d, int row, float M, sel_shared &sh, uin
 /*
  * The chain of the index-order normaliser, by one whole wavefront after norm_prep; nm.S = the sum. Lane r
  * holds run r's composed automaton and critical group r's index and predicted binades, so the walk reads
- * them with readlane; a critical group's per-lane term, prefix scan and suffix scan (lane c holds the
- * suffix after c) are loaded one group ahead.
+ * them with readlane; a critical group's per-lane term, prefix and suffix compositions are read one group
+ * ahead. `term(j)` recomputes term j for the fallback walks.
  */
-__device__ void norm_chain(const bl_dev &d, int row, float M, sel_shared &sh) {
+template <class TermF>
+__device__ __forceinline__ void norm_chain(const bl_dev &d, int row, sel_shared &sh, TermF term) {
   const int V = d.vocab, lane = threadIdx.x & 63;
   const int G = (V + 63) / 64;
   const bl_grec1 *rec =
       reinterpret_cast<const bl_grec1 *>(reinterpret_cast<const bl_grec *>(d.grec) + (int64_t)row * 2 * (V / 64 + 64));
-  const float *eff = d.eff + (int64_t)row * V;
   const sel_norm &nm = sh.n;
   const int ncrit = nm.ncrit, nrun = ncrit + 1;
   static_assert(BL_CRIT_MAX + 1 <= 64, "one lane per run and per critical group");
@@ -1800,32 +1829,39 @@ __device__ void norm_chain(const bl_dev &d, int row, float M, sel_shared &sh) {
   const int rE = nm.r_E[rl], rst = nm.r_st[rl];
   const bl_inc rf = nm.r_f[rl];
   const int cl = lane < ncrit ? lane : 0;
-  const int cg = nm.crit[cl], ce0 = nm.ce0[cl], ce1 = nm.ce1[cl];
+  const int cslot = lane < ncrit ? nm.epos[cl] : 0; /* critical group cl's entry slot (none without entries) */
+  const int cg = nm.crit[cl], ce0 = nm.ce0[cslot], ce1 = nm.ce1[cslot];
+  auto slot_of_r = [&](int r) { return (int)bl_bcast((uint32_t)cslot, r); };
   auto crit_of = [&](int r) { return (int)bl_bcast((uint32_t)cg, r); };
   auto run_lo = [&](int r) { return r == 0 ? 0 : crit_of(r - 1) + 1; };
   auto run_hi = [&](int r) { return r == ncrit ? G : crit_of(r); };
   int e = BL_E_MIN;
   uint32_t N = 0u;
-  auto term = [&](int64_t j) { return SEL_EXPF(eff[j] - M); };
   /* a record holds its own binade only: a neighbouring binade reads as saturated (element level) */
   auto recf = [&](int64_t g) {
     const bl_grec1 r1 = rec[g];
     return bl_grec{r1.E, 0u, {bl_inc{BL_SAT, BL_SAT}, r1.v, bl_inc{BL_SAT, BL_SAT}}};
   };
+  /* lane c holds term c, the composition of terms 0..c, and that of the terms after c */
+  auto cs_after = [&](int r) {
+    const int sr = slot_of_r(r); /* the broadcast runs in every lane */
+    return lane < 63 ? nm.cs[sr * 64 + lane + 1] : bl_inc_ident();
+  };
   float a = 0.0f;
   bl_inc cp = bl_inc_ident(), cs = bl_inc_ident();
   if (ncrit > 0) {
-    a = nm.terms[lane];
-    cp = nm.cp[lane];
-    cs = nm.cs[lane + 1];
+    a = nm.terms[slot_of_r(0) * 64 + lane];
+    cp = nm.cp[slot_of_r(0) * 64 + lane];
+    cs = cs_after(0);
   }
   for (int r = 0; r <= ncrit; r++) {
     float a_nx = 0.0f;
     bl_inc cp_nx = bl_inc_ident(), cs_nx = bl_inc_ident();
     if (r + 1 < ncrit) {
-      a_nx = nm.terms[(r + 1) * 64 + lane];
-      cp_nx = nm.cp[(r + 1) * 64 + lane];
-      cs_nx = nm.cs[(r + 1) * 65 + lane + 1];
+      const int sn = slot_of_r(r + 1);
+      a_nx = nm.terms[sn * 64 + lane];
+      cp_nx = nm.cp[sn * 64 + lane];
+      cs_nx = cs_after(r + 1);
     }
     const int st = (int)bl_bcast((uint32_t)rst, r);
     if (st != 0) {
@@ -1887,7 +1923,7 @@ static_assert(BL_NBUCKET % BL_SEL_THREADS == 0, "whole buckets per thread");
 static_assert((BL_TIE_HASH & (BL_TIE_HASH - 1)) == 0, "table size is a power of two");
 __device__ __forceinline__ uint32_t tie_slot(int p) { return ((uint32_t)p * 2654435761u) >> 22 & (BL_TIE_HASH - 1); }
 template <class KeyF>
-__device__ int heap_tie_id(KeyF key, bool keys_in_lds, int64_t n_list, int64_t pos, int V, int32_t *occ_g,
+__device__ __forceinline__ int heap_tie_id(KeyF key, bool keys_in_lds, int64_t n_list, int64_t pos, int V, int32_t *occ_g,
                            sel_shared &sh) {
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   const float vp = ckey_v(key(pos));
@@ -2019,7 +2055,127 @@ __device__ int heap_tie_id(KeyF key, bool keys_in_lds, int64_t n_list, int64_t p
  * src/server.br:1027-1035) and the history commit (src/server.br:1004, :1037): counts and bitmap bits by
  * atomics that nothing waits for, the slot's scalar state read at the start.
  */
-__global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows rows) {
+/*
+ * The row's top K keys in (value desc, index asc) order (top_k_select, src/sampling.br:280-296) from the row
+ * pass's chunk lists (each sorted, K long, unfilled entries id -1), into sh.mkeys[0..K) (0 = unfilled), by
+ * the block. The lists are staged in LDS. The first L = ceil(K/nc) keys of all the lists hold at least K keys;
+ * their K-th largest, tau, is at most the row's K-th key, so the row's top K are among the keys >= tau: in
+ * each list a prefix, whose length one thread per list finds by binary search. The prefixes are packed by a
+ * prefix sum of their lengths and ranked by counting (keys are distinct: they carry the index). Lists too
+ * large to stage find the K-th key itself by bisection over the key bits (a slower path).
+ */
+__device__ __forceinline__ void sel_merge(const bl_dev &d, int row, int K, sel_shared &sh) {
+  constexpr int NT = BL_SEL_THREADS;
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6, nc = d.nc;
+  const int L = (K + nc - 1) / nc, nu = nc * L, total = nc * K;
+  auto gkey = [&](int i) -> uint64_t {
+    const int c = i / K, q = i - c * K;
+    const int64_t o = ((int64_t)row * nc + c) * BL_KSEL_MAX + q;
+    const int32_t id = d.cand_i[o];
+    return id >= 0 ? ckey(d.cand_v[o], id) : 0ull;
+  };
+  uint64_t *stage = sh.c.keys, *ua = sh.c.tmp;
+  uint64_t *surv = reinterpret_cast<uint64_t *>(&sh.n); /* the normaliser's LDS is free until norm_prep */
+  int *lc = reinterpret_cast<int *>(sh.c.tmp);         /* per-list prefix lengths, after the first selection */
+  static_assert(sizeof(sel_norm) >= BL_LDS_SORT * sizeof(uint64_t), "survivors fit the normaliser's LDS");
+  static_assert(BL_RANK_MAX * 2 >= BL_MAX_CHUNKS + 1, "per-list lengths fit the rank area");
+  const bool fits = total <= BL_LDS_SORT && nu <= BL_RANK_MAX;
+  if (t == 0) {
+    sh.mtau = 1ull; /* every valid key, when fewer than K exist */
+    sh.mcnt = 0;
+  }
+  if (fits) {
+    for (int i = t; i < total; i += NT) {
+      const uint64_t k = gkey(i);
+      stage[i] = k;
+      const int c = i / K, q = i - c * K;
+      if (q < L) ua[c * L + q] = k;
+    }
+    __syncthreads();
+    for (int i = t; i < nu; i += NT) {
+      const uint64_t k = ua[i];
+      if (!k) continue;
+      int r = 0;
+      for (int j = 0; j < nu; j++) r += ua[j] > k ? 1 : 0;
+      if (r == K - 1) sh.mtau = k;
+    }
+    __syncthreads();
+    const uint64_t tau = sh.mtau;
+    /* list c's keys >= tau: a prefix (lists are sorted, unfilled keys 0 < tau); offsets by a block scan */
+    for (int c0 = 0; c0 < nc; c0 += NT) {
+      const int c = c0 + t;
+      int n = 0;
+      if (c < nc) {
+        int lo = 0, hi = K;
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if (stage[c * K + mid] >= tau) lo = mid + 1;
+          else hi = mid;
+        }
+        n = lo;
+      }
+      const int incl = bl_wscan_add(n, lane);
+      if (lane == 63) sh.red_i[w] = incl;
+      __syncthreads();
+      int off = sh.mcnt + incl - n, tot = 0;
+      for (int q = 0; q < NT / 64; q++) {
+        if (q < w) off += sh.red_i[q];
+        tot += sh.red_i[q];
+      }
+      if (c < nc) {
+        lc[2 * c] = off;
+        lc[2 * c + 1] = n;
+      }
+      __syncthreads();
+      if (t == 0) sh.mcnt += tot;
+      __syncthreads();
+    }
+    for (int i = t; i < total; i += NT) {
+      const int c = i / K, q = i - c * K;
+      if (q < lc[2 * c + 1]) surv[lc[2 * c] + q] = stage[i];
+    }
+  } else {
+    /* bisection: the largest tau with at least K keys >= tau */
+    uint64_t tau = 0ull;
+    for (int bit = 63; bit >= 0; bit--) {
+      const uint64_t cand = tau | (1ull << bit);
+      int c = 0;
+      for (int i = t; i < total; i += NT) c += gkey(i) >= cand ? 1 : 0;
+      c = bl_wscan_add(c, lane);
+      if (lane == 63) sh.red_i[w] = c;
+      __syncthreads();
+      int tot = 0;
+      for (int q = 0; q < NT / 64; q++) tot += sh.red_i[q];
+      __syncthreads();
+      if (tot >= K) tau = cand;
+    }
+    if (t == 0 && tau) sh.mtau = tau;
+    __syncthreads();
+    const uint64_t tau2 = sh.mtau;
+    for (int i = t; i < total; i += NT) {
+      const uint64_t k = gkey(i);
+      if (k && k >= tau2) {
+        const int p = atomicAdd(&sh.mcnt, 1);
+        if (p < BL_LDS_SORT) surv[p] = k;
+      }
+    }
+  }
+  __syncthreads();
+  const int C = min(sh.mcnt, BL_LDS_SORT);
+  for (int i = t; i < C; i += NT) {
+    const uint64_t k = surv[i];
+    int r = 0, j = 0;
+    for (; j + 4 <= C; j += 4)
+      r += (surv[j] > k ? 1 : 0) + (surv[j + 1] > k ? 1 : 0) + (surv[j + 2] > k ? 1 : 0) + (surv[j + 3] > k ? 1 : 0);
+    for (; j < C; j++) r += surv[j] > k ? 1 : 0;
+    if (r < K) sh.mkeys[r] = k;
+  }
+  for (int q = C + t; q < K; q += NT) sh.mkeys[q] = 0ull;
+  __syncthreads();
+}
+
+__global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const float *__restrict__ logits, int64_t ld,
+                                                              bl_rows rows) {
   const int V = d.vocab, nc = d.nc;
   const int row = blockIdx.x, t = threadIdx.x, w = t >> 6, lane = t & 63;
   __shared__ sel_shared sh;
@@ -2035,9 +2191,9 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
       sh.red_i[0] = Mi;
     }
   }
-  const uint64_t mk = t < BL_KSEL_MAX ? d.mkey[(int64_t)row * BL_KSEL_MAX + t] : 0ull; /* used when K > t */
   uint32_t m_pre = 0u; /* the normaliser's first block flags and summaries (used by logprob rows) */
   bl_grec1 br_pre{};
+  const int n_ent = d.ncrit[row]; /* the normaliser's critical-group entries */
   if (t < d.nb) {
     m_pre = d.bcrit[(int64_t)row * d.nb + t];
     br_pre = reinterpret_cast<const bl_grec1 *>(d.brec)[(int64_t)row * d.nb + t];
@@ -2060,8 +2216,10 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
   M = sh.red_m[0];
   Mi = sh.red_i[0];
   if (Mi == 0x7fffffff) Mi = 0;
+  /* the row's top K keys: thread t keeps the t-th (used when K > t) */
+  if (K > 0) sel_merge(d, row, K, sh);
+  const uint64_t mk = t < K ? sh.mkeys[t] : 0ull;
 
-  const float *eff = d.eff + (int64_t)row * V;
   int status = 0;
   uint64_t rng = sp.rng;
   const int skip = rows.rng_skip ? rows.rng_skip[row] : 0;
@@ -2329,7 +2487,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
       status |= BL_SE_GDEAD;
     } else if (gst & BL_GR_FORCED) {
       tok = d.eos_id;
-      tokv = eff[tok];
+      tokv = bl_row_value(d, sp, rows, row, slot, logits, ld, tok);
     } else if (d.gamb[row]) {
       status |= BL_SE_GAMBIG;
     } else {
@@ -2355,9 +2513,10 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
 
   /* the normaliser, prepared by every wavefront; then wavefront 0 chains it while wavefront 1 runs the
    * short list's sequential loops */
-  if (lp_row) norm_prep(d, row, M, sh, m_pre, br_pre);
+  if (lp_row) norm_prep(d, row, M, sh, m_pre, br_pre, n_ent);
   __syncthreads();
-  if (lp_row && w == 0) norm_chain(d, row, M, sh);
+  if (lp_row && w == 0)
+    norm_chain(d, row, sh, [&](int64_t j) { return SEL_EXPF(bl_row_value(d, sp, rows, row, slot, logits, ld, (int32_t)j) - M); });
   if (sampled && !status && short_list && w == 1 && lane == 0)
     sh.draw = ranked_serial(sp, n_draw, nlog_draw, keep, rng, skip, typ, sh, &sh.rng_out);
   __syncthreads();
@@ -2398,7 +2557,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
     if (pos >= 0) {
       const uint64_t kp = keys[pos];
       tok = kp ? ckey_i(kp) : 0;
-      tokv = kp ? ckey_v(kp) : eff[tok];
+      tokv = kp ? ckey_v(kp) : bl_row_value(d, sp, rows, row, slot, logits, ld, tok);
       /* the heap rank orders equal values its own way (src/sampling.br:310-364): a draw on a tie takes
        * the heap's token (or reports the tie when the simulation does not fit) */
       if (mode & BL_M_FULL) {
@@ -2479,15 +2638,12 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
     for (int k = 0; k < n_eog; k++) is_eog |= (k < BL_EOG_LDS ? sh.eog[k] : d.eog[k]) == tok;
     if (rows.commit && status == 0) {
       /* tokens.push (src/server.br:1004): repeat window; reply_tokens.push unless EOG (:1037) */
-      const int64_t so = (int64_t)slot * V;
-      uint32_t *tw = d.touched + (int64_t)slot * d.words + (tok >> 5);
-      const uint32_t bit = 1u << (tok & 31);
       sp.n_tokens = n_tokens0 + 1;
       if (rep_on) {
         if (rl > 0) {
           int32_t *ring = d.ring + (int64_t)slot * BL_WCAP;
           if (ring_full) {
-            atomicAdd(&d.tokst[so + ring_old].wcnt, -1);
+            bl_rec_get(d, slot, ring_old)->wf -= 1u;
             ring[win_head] = tok;
             sp.win_head = (win_head + 1) % rl;
           } else {
@@ -2495,15 +2651,11 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, bl_rows 
             sp.win_len = win_len + 1;
           }
         }
-        atomicAdd(&d.tokst[so + tok].wcnt, 1);
-        atomicOr(tw, bit);
+        bl_rec_get(d, slot, tok)->wf += 1u;
       }
       if (!is_eog) {
         sp.n_reply = n_reply0 + 1;
-        if (fp_on) {
-          atomicAdd(&d.tokst[so + tok].cnt, 1);
-          atomicOr(tw, bit);
-        }
+        if (fp_on) bl_rec_get(d, slot, tok)->cnt += 1;
         if (g_on) grammar_commit(d, sp, d.gram[slot], tok);
       }
       sp.rng = rng;
@@ -2531,16 +2683,18 @@ void bl_launch_step(const bl_dev &d, const float *logits, int64_t ld, const bl_r
   if (ev) (void)hipEventRecord(ev[0], s);
   if (rows.delta)
     hipLaunchKernelGGL(bl_k_rowpass_spec, g1, dim3(BL_RP_THREADS), 0, s, d, logits, ld, rows);
-  else if ((int64_t)d.nc * B > d.rp_resident)
-    hipLaunchKernelGGL(bl_k_rowpass_wide, g1, dim3(BL_RP_THREADS), 0, s, d, logits, ld, rows);
   else
     hipLaunchKernelGGL(bl_k_rowpass, g1, dim3(BL_RP_THREADS), 0, s, d, logits, ld, rows);
   if (ev) (void)hipEventRecord(ev[1], s);
-  if (need_gram) hipLaunchKernelGGL(bl_k_gmask, dim3(d.gm_blocks, B), dim3(BL_GM_THREADS), 0, s, d, rows, 1);
-  if (need_pass2)
-    hipLaunchKernelGGL(bl_k_exppass, dim3(1 + (d.vocab + BL_EB - 1) / BL_EB, B), dim3(BL_RP_THREADS), 0, s, d, rows);
+  if (need_gram) hipLaunchKernelGGL(bl_k_gmask, dim3(d.gm_blocks, B), dim3(BL_GM_THREADS), 0, s, d, logits, ld, rows, 1);
+  if (need_pass2) {
+    if (rows.delta)
+      hipLaunchKernelGGL(bl_k_exppass_spec, dim3(d.nb, B), dim3(BL_RP_THREADS), 0, s, d, logits, ld, rows);
+    else
+      hipLaunchKernelGGL(bl_k_exppass, dim3(d.nb, B), dim3(BL_RP_THREADS), 0, s, d, logits, ld, rows);
+  }
   if (ev) (void)hipEventRecord(ev[2], s);
-  hipLaunchKernelGGL(bl_k_select, dim3(B), dim3(BL_SEL_THREADS), 0, s, d, rows);
+  hipLaunchKernelGGL(bl_k_select, dim3(B), dim3(BL_SEL_THREADS), 0, s, d, logits, ld, rows);
   if (ev) (void)hipEventRecord(ev[3], s);
 }
 
@@ -2551,7 +2705,8 @@ __global__ void bl_k_gclear(bl_dev d) {
 }
 void bl_launch_gmask(const bl_dev &d, const bl_rows &rows, hipStream_t s) {
   hipLaunchKernelGGL(bl_k_gclear, dim3(1), dim3(64), 0, s, d);
-  hipLaunchKernelGGL(bl_k_gmask, dim3(d.gm_blocks, 1), dim3(BL_GM_THREADS), 0, s, d, rows, 0);
+  hipLaunchKernelGGL(bl_k_gmask, dim3(d.gm_blocks, 1), dim3(BL_GM_THREADS), 0, s, d, (const float *)nullptr, (int64_t)0,
+                     rows, 0);
 }
 
 void bl_launch_synth(float *out, int64_t ld, int cfg, int64_t seed, int64_t step, int rows, int V, hipStream_t s) {
