@@ -209,6 +209,34 @@ __global__ void bl_k_bump(float *out, const int32_t *ids, int n, float add) {
   if (i < n) out[ids[i]] = out[ids[i]] + add;
 }
 
+/* The device buffers of a step (bl_dev) for S slots, R rows and a vocabulary of V tokens, in this order, each
+ * from take(pointer, element count); false when one could not be had. */
+template <class Take>
+static bool dev_layout(bl_dev &d, size_t S, size_t R, int vocab, Take take) {
+  const size_t V = (size_t)vocab, G = V / 64 + 64;
+  d.vocab = vocab;
+  d.nc = (vocab + BL_CH - 1) / BL_CH;
+  d.nb = (vocab + BL_EB - 1) / BL_EB;
+  d.gm_blocks = (vocab + BL_GM_THREADS - 1) / BL_GM_THREADS;
+  d.max_slots = (int)S;
+  d.max_rows = (int)R;
+  d.eos_id = -1;
+  d.n_eog = 0;
+  char *grec = nullptr, *brec = nullptr;
+  const bool ok = take(d.slots, S) && take(d.rec, S * d.nb * BL_EB) && take(d.rcnt, S * d.nb) && take(d.ridx, S * V) &&
+                  take(d.ring, S * BL_WCAP) && take(d.eog, 1024) && take(d.c_max, R * d.nc) && take(d.c_arg, R * d.nc) &&
+                  take(d.c_bsum, R * d.nc * BL_SUBS) && take(d.cand_v, R * d.nc * BL_KSEL_MAX) &&
+                  take(d.cand_i, R * d.nc * BL_KSEL_MAX) && take(grec, R * 2 * G * 32) && take(d.full_v, R * d.nb * BL_EB) &&
+                  take(d.full_i, R * d.nb * BL_EB) && take(d.full_cnt, R * d.nb) && take(d.full_s, R * d.nb) &&
+                  take(d.sortk, R * 2 * V) && take(d.gsum, R * G) && take(d.crit, R * BL_CRIT_MAX) && take(d.ncrit, R) &&
+                  take(brec, R * d.nb * 16) && take(d.bcrit, R * d.nb) && take(d.gram, S) &&
+                  take(d.gmask, R * 2 * ((V + 63) / 64)) && take(d.gstat, R) && take(d.gamb, R) &&
+                  take(d.gm_max, R * d.gm_blocks) && take(d.gm_arg, R * d.gm_blocks) && take(d.gm_eq, R * d.gm_blocks);
+  d.grec = grec;
+  d.brec = brec;
+  return ok;
+}
+
 extern "C" {
 
 const char *bl_last_error(void) { return g_err.c_str(); }
@@ -250,12 +278,7 @@ int bl_create(int device, int max_slots, int max_rows, int vocab, bl_ctx **out) 
     return fail(BL_EDEVICE, "hipSetDevice(%d): %s", device, hipGetErrorString(e));
   }
   bl_dev &d = c->d;
-  d.vocab = vocab;
-  d.nc = (vocab + BL_CH - 1) / BL_CH;
-  d.max_slots = max_slots;
-  d.max_rows = max_rows;
-  const size_t V = (size_t)vocab, S = (size_t)max_slots, R = (size_t)max_rows;
-  const size_t G = V / 64 + 64;
+  const size_t R = (size_t)max_rows;
 #define ALLOC(p, n)                                   \
   do {                                                \
     if (dalloc(c, &(p), (n)) != hipSuccess) {         \
@@ -263,46 +286,10 @@ int bl_create(int device, int max_slots, int max_rows, int vocab, bl_ctx **out) 
       return fail(BL_EDEVICE, "hipMalloc failed (%s)", #p); \
     }                                                 \
   } while (0)
-  ALLOC(d.slots, S);
-  d.nb = (vocab + BL_EB - 1) / BL_EB;
-  ALLOC(d.rec, S * d.nb * BL_EB);
-  ALLOC(d.rcnt, S * d.nb);
-  ALLOC(d.ridx, S * V);
-  ALLOC(d.ring, S * BL_WCAP);
-  ALLOC(d.eog, 1024);
-  ALLOC(d.c_max, R * d.nc);
-  ALLOC(d.c_arg, R * d.nc);
-  ALLOC(d.c_bsum, R * d.nc * BL_SUBS);
-  ALLOC(d.cand_v, R * d.nc * BL_KSEL_MAX);
-  ALLOC(d.cand_i, R * d.nc * BL_KSEL_MAX);
-  {
-    char *g = nullptr;
-    ALLOC(g, R * 2 * G * 32);
-    d.grec = g;
+  if (!dev_layout(d, max_slots, max_rows, vocab, [&](auto *&p, size_t n) { return dalloc(c, &p, n) == hipSuccess; })) {
+    bl_destroy(c);
+    return fail(BL_EDEVICE, "hipMalloc failed (step workspace)");
   }
-  ALLOC(d.full_v, R * d.nb * BL_EB);
-  ALLOC(d.full_i, R * d.nb * BL_EB);
-  ALLOC(d.full_cnt, R * d.nb);
-  ALLOC(d.full_s, R * d.nb);
-  ALLOC(d.sortk, R * 2 * V);
-  ALLOC(d.gsum, R * G);
-  ALLOC(d.crit, R * BL_CRIT_MAX);
-  ALLOC(d.ncrit, R);
-  {
-    char *b = nullptr;
-    ALLOC(b, R * d.nb * 16);
-    d.brec = b;
-  }
-  ALLOC(d.bcrit, R * d.nb);
-  d.gm_blocks = (vocab + BL_GM_THREADS - 1) / BL_GM_THREADS;
-  ALLOC(d.gram, S);
-  ALLOC(d.gmask, R * 2 * ((V + 63) / 64));
-  ALLOC(d.gstat, R);
-  ALLOC(d.gamb, R);
-  ALLOC(d.gm_max, R * d.gm_blocks);
-  ALLOC(d.gm_arg, R * d.gm_blocks);
-  ALLOC(d.gm_eq, R * d.gm_blocks);
-  d.eos_id = -1;
   ALLOC(c->d_slot, R);
   ALLOC(c->d_bound, R);
   ALLOC(c->d_skip, R);
@@ -321,12 +308,12 @@ int bl_create(int device, int max_slots, int max_rows, int vocab, bl_ctx **out) 
 #undef ALLOC
   /* slot records and grammar views start zeroed: a slot is only stepped or committed after bl_slot_reset, and
    * nothing reads uninitialised state even when a caller breaks that rule */
-  if (hipMemset(d.slots, 0, S * sizeof(bl_slot_dev)) != hipSuccess || hipMemset(d.gram, 0, S * sizeof(bl_gram_view)) != hipSuccess ||
+  if (hipMemset(d.slots, 0, max_slots * sizeof(bl_slot_dev)) != hipSuccess ||
+      hipMemset(d.gram, 0, max_slots * sizeof(bl_gram_view)) != hipSuccess ||
       hipDeviceSynchronize() != hipSuccess) {
     bl_destroy(c);
     return fail(BL_EDEVICE, "hipMemset failed");
   }
-  d.n_eog = 0;
   if (hipHostMalloc((void **)&c->h_slot, R * sizeof(int32_t)) != hipSuccess ||
       hipHostMalloc((void **)&c->h_bound, R * sizeof(int32_t)) != hipSuccess ||
       hipHostMalloc((void **)&c->h_skip, R * sizeof(int32_t)) != hipSuccess ||
@@ -345,10 +332,10 @@ int bl_create(int device, int max_slots, int max_rows, int vocab, bl_ctx **out) 
     return fail(BL_EDEVICE, "hipStreamCreate failed");
   }
   c->stream = c->own;
-  c->host_slots.assign(S, bl_slot_dev{});
-  c->slot_ready.assign(S, false);
-  c->reply.assign(S, {});
-  c->stepped.assign(S, 0);
+  c->host_slots.assign(max_slots, bl_slot_dev{});
+  c->slot_ready.assign(max_slots, false);
+  c->reply.assign(max_slots, {});
+  c->stepped.assign(max_slots, 0);
   *out = c;
   return BL_OK;
 }
@@ -393,8 +380,7 @@ int bl_set_eog(bl_ctx *c, int32_t eos_id, const int32_t *eog_ids, int n_eog) {
 }
 
 /* mode and unsupported-stage checks for one slot's parameters */
-static int configure(const bl_ctx *c, const bl_params *p, bl_slot_dev &s) {
-  const int V = c->d.vocab;
+static int configure(int V, const bl_params *p, bl_slot_dev &s) {
   if (p->temperature != p->temperature || p->top_p != p->top_p) return fail(BL_EPARAM, "NaN sampling parameter");
   if (p->n_probs < 0 || p->n_probs > 256) return fail(BL_EPARAM, "n_probs must be in 0..256 (got %d)", p->n_probs);
   s.temperature = p->temperature;
@@ -459,7 +445,7 @@ int bl_slot_reset(bl_ctx *c, int slot, const bl_params *p, uint64_t rng_state, c
     return fail(BL_EPARAM, "bl_slot_reset: invalid arguments");
   const int V = c->d.vocab;
   bl_slot_dev s{};
-  int rc = configure(c, p, s);
+  int rc = configure(V, p, s);
   if (rc) return rc;
   for (int i = 0; i < n_hist; i++)
     if (history[i] < 0 || history[i] >= V) return fail(BL_EPARAM, "history token %d outside the vocabulary", history[i]);

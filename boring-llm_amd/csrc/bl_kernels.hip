@@ -2629,11 +2629,15 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
       rows.top_lp[(int64_t)row * rows.top_stride + t] = (v - M) - lse;
     }
   }
+  /* the rest of the row's alternatives (past its n_probs, or all of a row without logprobs): id -1, 0 */
+  if (rows.lp && t < rows.top_stride && !(lp_row && t < sp.n_probs) && !(psp_row && t < n_alt)) {
+    rows.top_ids[(int64_t)row * rows.top_stride + t] = -1;
+    rows.top_lp[(int64_t)row * rows.top_stride + t] = 0.0f;
+  }
   if (t == 0) {
     rows.tok[row] = status ? -1 : tok; /* a failed row has no token; its status stays sticky in the slot */
     if (rows.status) rows.status[row] = status;
-    if (lp_row) rows.lp[row] = (tokv - M) - lse;
-    if (psp_row) rows.lp[row] = psp_tok;
+    if (rows.lp) rows.lp[row] = lp_row ? (tokv - M) - lse : psp_row ? psp_tok : 0.0f;
     bool is_eog = false;
     for (int k = 0; k < n_eog; k++) is_eog |= (k < BL_EOG_LDS ? sh.eog[k] : d.eog[k]) == tok;
     if (rows.commit && status == 0) {

@@ -145,7 +145,8 @@ int bl_grammar_mask(bl_ctx *ctx, int slot, uint32_t *d_mask_out, int32_t *forced
  * frequency/presence, then sample() = sampling_logits + greedy | rank + sample_candidates, then
  * logprob_normalizer + top_k_select for logprobs). `d_logits` is a device pointer to B rows of
  * `ld` floats. The chosen tokens are appended to each slot's history. Host outputs; `logprobs`,
- * `top_ids`, `top_logprobs` may be NULL; `top_stride` entries per row. */
+ * `top_ids`, `top_logprobs` may be NULL; `top_stride` entries per row. A row without logprobs reads
+ * logprob 0; alternatives past a row's n_probs (all of them without logprobs) read id -1, logprob 0. */
 int bl_sample_step(bl_ctx *ctx, const int32_t *slots, int B, const float *d_logits, int64_t ld, int32_t *tokens,
                    float *logprobs, int32_t *top_ids, float *top_logprobs, int top_stride);
 
