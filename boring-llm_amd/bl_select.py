@@ -50,8 +50,10 @@ EXPORTS = [
     "bl_spec_verify", "bl_synth_logits", "bl_math_digest", "bl_workload_ids", "bl_workload_bias",
     "bl_workload_drafts", "bl_set_timing", "bl_get_timing", "bl_set_vocab", "bl_slot_grammar", "bl_grammar_mask",
     "bl_workload_c3_vocab", "bl_step_graph_create", "bl_step_graph_launch", "bl_step_graph_destroy",
-    "bl_stream_sync", "bl_json_schema_to_gbnf", "bl_slot_schema", "bl_slot_status",
+    "bl_stream_sync", "bl_json_schema_to_gbnf", "bl_slot_schema", "bl_slot_status", "bl_sample_rows_noalloc",
 ]
+NOALLOC_BYTES = 64 << 20
+NOALLOC_ROWS = 16
 
 _lib = None
 
@@ -103,6 +105,8 @@ def lib():
         L.bl_slot_schema.argtypes = [C.c_void_p, C.c_int, C.c_char_p, C.c_size_t]
         L.bl_grammar_mask.argtypes = [C.c_void_p, C.c_int, C.c_void_p, i32p]
         L.bl_workload_c3_vocab.argtypes = [C.c_int64, C.c_int, C.c_void_p, C.c_size_t, C.c_void_p, i32p]
+        L.bl_sample_rows_noalloc.argtypes = [C.c_int, C.c_void_p, C.c_void_p, u64p, C.c_int, C.c_void_p, C.c_int64,
+                                             C.c_int, i32p, f32p, i32p, f32p, C.c_int]
         _lib = L
     return _lib
 
@@ -259,6 +263,23 @@ class Context:
         out = (C.c_uint64 * n_blocks)()
         _check(lib().bl_math_digest(self.h, fn, first_block, n_blocks, out))
         return list(out)
+
+
+def sample_rows_noalloc(params, rng_states, d_logits_ptr, ld, vocab, top_stride=0, device=0, stream=0):
+    """bl_sample_rows_noalloc: one stateless step of len(params) rows, no device allocation. Returns
+    (tokens, logprobs, top_ids, top_logprobs, advanced RNG states) as Python lists."""
+    B = len(params)
+    ps = (Params * max(B, 1))(*params)
+    rng = (C.c_uint64 * max(B, 1))(*rng_states)
+    tok = (C.c_int32 * max(B, 1))()
+    lp = (C.c_float * max(B, 1))()
+    ti = (C.c_int32 * max(B * top_stride, 1))()
+    tl = (C.c_float * max(B * top_stride, 1))()
+    _check(lib().bl_sample_rows_noalloc(device, C.c_void_p(stream), ps, rng, B, C.c_void_p(d_logits_ptr), ld, vocab,
+                                        tok, lp, ti, tl, top_stride))
+    tops = [list(ti[b * top_stride:(b + 1) * top_stride]) for b in range(B)]
+    tlps = [list(tl[b * top_stride:(b + 1) * top_stride]) for b in range(B)]
+    return list(tok[:B]), list(lp[:B]), tops, tlps, list(rng[:B])
 
 
 def workload_ids(kind, cfg, seed, row, n, vocab):

@@ -9,7 +9,9 @@
 
 #include <algorithm>
 #include <chrono>
+#include <mutex>
 #include <string>
+#include <type_traits>
 #include <unordered_map>
 #include <vector>
 
@@ -210,7 +212,8 @@ __global__ void bl_k_bump(float *out, const int32_t *ids, int n, float add) {
 }
 
 /* The device buffers of a step (bl_dev) for S slots, R rows and a vocabulary of V tokens, in this order, each
- * from take(pointer, element count); false when one could not be had. */
+ * from take(pointer, element count); false when one could not be had. A context takes them from hipMalloc,
+ * the allocation-free step from its fixed array. */
 template <class Take>
 static bool dev_layout(bl_dev &d, size_t S, size_t R, int vocab, Take take) {
   const size_t V = (size_t)vocab, G = V / 64 + 64;
@@ -792,6 +795,108 @@ int bl_sample_step(bl_ctx *c, const int32_t *slots, int B, const float *d_logits
   if (top_ids && ts > 0) memcpy(top_ids, h + 3 * B, (size_t)B * ts * 4);
   if (top_logprobs && ts > 0) memcpy(top_logprobs, h + 3 * B + B * ts, (size_t)B * ts * 4);
   return status_error(st);
+}
+
+/* ------------------------------------------------------------------ allocation-free step */
+/* The allocation-free step's slot state and workspace. Each device that runs the call holds its own copy
+ * for the life of the process; host code takes its device address from hipGetSymbolAddress, once per
+ * device, and never passes the name itself to a kernel or a copy. */
+static __device__ __align__(256) unsigned char scratch[BL_NOALLOC_BYTES];
+#define BL_MAX_DEVICES 64
+static std::mutex g_scratch_mu;
+static unsigned char *g_scratch[BL_MAX_DEVICES];
+
+/* the device address of `scratch` on the current device `dev` */
+static int scratch_of(int dev, unsigned char **out) {
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void *p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(BL_EDEVICE, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+    g_scratch[dev] = (unsigned char *)p;
+  }
+  *out = g_scratch[dev];
+  return BL_OK;
+}
+
+int bl_sample_rows_noalloc(int device, void *stream, const bl_params *params, uint64_t *rng_states, int B,
+                           const float *d_logits, int64_t ld, int vocab, int32_t *tokens, float *logprobs,
+                           int32_t *top_ids, float *top_logprobs, int top_stride) {
+  if (device < 0 || device >= BL_MAX_DEVICES || !params || !rng_states || !d_logits || !tokens)
+    return fail(BL_EPARAM, "bl_sample_rows_noalloc: invalid arguments");
+  if (B <= 0 || B > BL_NOALLOC_ROWS)
+    return fail(BL_EPARAM, "bl_sample_rows_noalloc: %d rows (1..%d)", B, BL_NOALLOC_ROWS);
+  if (vocab <= 0 || vocab > BL_MAX_CHUNKS * BL_CH || ld < vocab)
+    return fail(BL_EPARAM, "bl_sample_rows_noalloc: invalid vocabulary %d (ld %lld)", vocab, (long long)ld);
+  if (top_stride < 0 || top_stride > 256) return fail(BL_EPARAM, "top_stride must be in 0..256");
+  bl_slot_dev hs[BL_NOALLOC_ROWS];
+  int32_t tbl[BL_NOALLOC_ROWS];
+  for (int i = 0; i < B; i++) {
+    hs[i] = bl_slot_dev{};
+    int rc = configure(vocab, params + i, hs[i]);
+    if (rc) return rc;
+    hs[i].rng = rng_states[i];
+    tbl[i] = i;
+  }
+  HIPCHK(hipSetDevice(device));
+  unsigned char *base = nullptr;
+  int rc = scratch_of(device, &base);
+  if (rc) return rc;
+  /* carve a context's buffers for B slots and rows out of the array, then the row table and outputs */
+  size_t off = 0;
+  auto take = [&](auto *&p, size_t n) {
+    using T = std::remove_reference_t<decltype(*p)>;
+    off = (off + 255) & ~(size_t)255;
+    const size_t bytes = n * sizeof(T) + 16;
+    if (off + bytes > BL_NOALLOC_BYTES) return false;
+    p = reinterpret_cast<T *>(base + off);
+    off += bytes;
+    return true;
+  };
+  bl_dev d{};
+  int32_t *d_tbl = nullptr, *d_out = nullptr;
+  const int ts = top_stride, tsa = ts > 0 ? ts : 1; /* rows with logprobs write one alternative at stride 0 */
+  if (!dev_layout(d, B, B, vocab, take) || !take(d_tbl, B) || !take(d_out, (size_t)B * (3 + 2 * tsa)))
+    return fail(BL_EPARAM, "bl_sample_rows_noalloc: %d rows of %d tokens need more than the %u bytes of its array", B,
+                vocab, (unsigned)BL_NOALLOC_BYTES);
+  hipStream_t st = (hipStream_t)stream;
+  /* the array keeps the previous call's contents: slot state and records start afresh (no records, no
+   * token has one, an empty window) */
+  HIPCHK(hipMemcpyAsync(d.slots, hs, B * sizeof(bl_slot_dev), hipMemcpyHostToDevice, st));
+  HIPCHK(hipMemcpyAsync(d_tbl, tbl, B * sizeof(int32_t), hipMemcpyHostToDevice, st));
+  HIPCHK(hipMemsetAsync(d.rcnt, 0, (size_t)B * d.nb * sizeof(int32_t), st));
+  HIPCHK(hipMemsetAsync(d.ridx, 0xFF, (size_t)B * vocab * sizeof(int16_t), st));
+  bl_rows rows{};
+  rows.slot = d_tbl;
+  for (int i = 0; i < B; i++) rows.slot_inline[i] = (int16_t)i;
+  rows.commit = 1; /* the commit is what stores the advanced RNG state */
+  rows.tok = d_out;
+  rows.status = d_out + B;
+  rows.lp = reinterpret_cast<float *>(d_out + 2 * B);
+  rows.top_stride = tsa;
+  rows.top_ids = d_out + 3 * B;
+  rows.top_lp = reinterpret_cast<float *>(d_out + 3 * B + B * tsa);
+  bool pass2 = false;
+  for (int i = 0; i < B; i++) pass2 |= (hs[i].mode & (BL_M_LOGPROBS | BL_M_FULL)) != 0;
+  bl_launch_step(d, d_logits, ld, rows, B, pass2, false, st, nullptr);
+  HIPCHK(hipGetLastError());
+  int32_t status[BL_NOALLOC_ROWS];
+  HIPCHK(hipMemcpyAsync(tokens, d_out, B * sizeof(int32_t), hipMemcpyDeviceToHost, st));
+  HIPCHK(hipMemcpyAsync(status, d_out + B, B * sizeof(int32_t), hipMemcpyDeviceToHost, st));
+  if (logprobs) HIPCHK(hipMemcpyAsync(logprobs, d_out + 2 * B, B * sizeof(float), hipMemcpyDeviceToHost, st));
+  if (top_ids && ts > 0)
+    HIPCHK(hipMemcpyAsync(top_ids, d_out + 3 * B, (size_t)B * ts * 4, hipMemcpyDeviceToHost, st));
+  if (top_logprobs && ts > 0)
+    HIPCHK(hipMemcpyAsync(top_logprobs, d_out + 3 * B + B * ts, (size_t)B * ts * 4, hipMemcpyDeviceToHost, st));
+  HIPCHK(hipMemcpyAsync(hs, d.slots, B * sizeof(bl_slot_dev), hipMemcpyDeviceToHost, st));
+  HIPCHK(wait_stream(st));
+  int err = 0;
+  for (int i = 0; i < B; i++) {
+    err |= status[i];
+    rng_states[i] = hs[i].rng;
+  }
+  return status_error(err);
 }
 
 int bl_bind_rows(bl_ctx *c, const int32_t *slots, int B) {

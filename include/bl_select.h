@@ -159,6 +159,23 @@ int bl_bind_rows(bl_ctx *ctx, const int32_t *slots, int B);
 int bl_sample_step_async(bl_ctx *ctx, int B, const float *d_logits, int64_t ld, int32_t *d_tokens, float *d_logprobs,
                          int32_t *d_top_ids, float *d_top_logprobs, int top_stride);
 
+/* Allocation-free step: no counterpart in the reference; for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). Row i of d_logits
+ * (B rows of `ld` floats, `vocab` tokens, on `device`) is sampled as bl_sample_step samples a slot reset with
+ * params[i], RNG state rng_states[i] and no history, reply or logit_bias, in a context without
+ * end-of-generation ids; rng_states (host) are advanced in place and the outputs are bl_sample_step's. The
+ * slot state and step workspace live in one fixed device array of BL_NOALLOC_BYTES, which each device that
+ * runs the call holds until the process ends; no device memory is allocated or freed. Limits: B up to
+ * BL_NOALLOC_ROWS, and the workspace (about 44 bytes per row and vocabulary entry, e.g. B = 8 at V = 151936)
+ * within the array, else BL_EPARAM. Work is ordered on `stream` (a hipStream_t; NULL: the null stream) and
+ * the call returns when results are in host memory. Calls that overlap on one device (threads or streams)
+ * race on the array. */
+#define BL_NOALLOC_BYTES (64u << 20)
+#define BL_NOALLOC_ROWS 16
+int bl_sample_rows_noalloc(int device, void *stream, const bl_params *params, uint64_t *rng_states, int B,
+                           const float *d_logits, int64_t ld, int vocab, int32_t *tokens, float *logprobs,
+                           int32_t *top_ids, float *top_logprobs, int top_stride);
+
 /* A serving loop's step without host work (no reference counterpart; the reference samples on the host):
  * bl_step_graph_create captures one bl_sample_step_async of the bound rows, with these buffers, into an
  * instantiated HIP graph (*graph_out, a hipGraphExec_t); bl_step_graph_launch replays it on the context

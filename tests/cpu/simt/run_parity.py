@@ -472,6 +472,46 @@ def run_async(BL, steps):
     return None
 
 
+NOALLOC_ROWS = [
+    dict(temperature=0.0, logprobs=1, n_probs=10),
+    dict(temperature=0.7, top_k=20, frequency_penalty=0.5, presence_penalty=0.3, logprobs=1, n_probs=10),
+    dict(temperature=1.0, top_p=0.9, logprobs=1, n_probs=10),
+    dict(temperature=0.8, top_k=64, min_p=0.05, repeat_penalty=1.1),
+    dict(temperature=1.0, mirostat=2, mirostat_tau=5.0, mirostat_eta=0.1),
+    dict(temperature=0.9, top_p=0.95, logprobs=1, n_probs=5, post_sampling_probs=1),
+    dict(temperature=1.0, top_k=40, xtc_probability=0.5, xtc_threshold=0.1),
+    dict(temperature=0.6, logprobs=1, n_probs=3, frequency_penalty=0.2),
+]
+
+
+def run_noalloc(BL):
+    """bl_sample_rows_noalloc, twice in a row (the second call smaller), equals bl_sample_step over fresh
+    slots with the same parameters and RNG states."""
+    seed = 5
+    for B, V, ld, step in ((8, 151936, 151936, 0), (3, 50000, 50048, 1)):
+        buf = MEM.zeros(B * ld, np.float32)
+        gen = BL.Context(V, 1, 1)
+        gen.synth_logits(buf.ptr, ld, 2, seed, step, B, V)
+        gen.close()
+        params = [BL.Params(**NOALLOC_ROWS[(r + step) % len(NOALLOC_ROWS)]) for r in range(B)]
+        rngs = [BL.seed_rng(seed * 100 + 10 * step + r) for r in range(B)]
+        got = BL.sample_rows_noalloc(params, rngs, buf.ptr, ld, V, top_stride=10)
+        ctx = BL.Context(V, B, B)
+        for r in range(B):
+            ctx.slot_reset(r, params[r], rngs[r])
+        want = list(ctx.sample_step(list(range(B)), buf.ptr, ld, top_stride=10)) + [[ctx.slot_rng(r) for r in range(B)]]
+        ctx.close()
+        if got[0] != want[0]:
+            return f"B={B} V={V}: tokens {got[0]} vs {want[0]}"
+        if not all(lp_close(a, b) for a, b in zip(got[1], want[1])):
+            return f"B={B} V={V}: logprobs differ"
+        if got[2] != want[2] or not all(lp_close(a, b) for x, y in zip(got[3], want[3]) for a, b in zip(x, y)):
+            return f"B={B} V={V}: alternatives differ"
+        if got[4] != want[4]:
+            return f"B={B} V={V}: RNG states differ"
+    return None
+
+
 def run_bigk(BL, steps):
     """top_k 250 and 256 logprob alternatives at V=151936: 38 chunks x 256 candidates per row."""
     V, seed = 151936, 11
@@ -710,6 +750,8 @@ def main():
         elif kind == "unfilt":
             rows = [int(v) for v in f[2].split(",")] if len(f) > 2 else None
             results.append(("unfiltered rows at V=151936", run_unfiltered(BL, int(f[1]), rows)))
+        elif kind == "noalloc":
+            results.append(("allocation-free step", run_noalloc(BL)))
         elif kind == "bigk":
             results.append(("large top-k / n_probs", run_bigk(BL, int(f[1]))))
         elif kind == "w3":

@@ -213,6 +213,13 @@ enum hipMemcpyKind { hipMemcpyHostToDevice, hipMemcpyDeviceToHost, hipMemcpyDevi
 #define hipStreamNonBlocking 1
 inline const char *hipGetErrorString(hipError_t) { return "simt"; }
 inline hipError_t hipSetDevice(int) { return hipSuccess; }
+/* a __device__ variable is a host variable: its "device address" is its address */
+#define __align__(n) __attribute__((aligned(n)))
+#define HIP_SYMBOL(x) (&(x))
+inline hipError_t hipGetSymbolAddress(void **p, const void *sym) {
+  *p = const_cast<void *>(sym);
+  return hipSuccess;
+}
 inline hipError_t hipStreamBeginCapture(hipStream_t, int) { return hipErrorNotSupported; }
 inline hipError_t hipStreamEndCapture(hipStream_t, hipGraph_t *) { return hipErrorNotSupported; }
 inline hipError_t hipGraphInstantiate(hipGraphExec_t *, hipGraph_t, void *, void *, size_t) { return hipErrorNotSupported; }

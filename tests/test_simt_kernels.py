@@ -103,6 +103,14 @@ def test_grammar_masks_and_tokens(simt_lib):
     assert out.count("ok   grammar case") == 7
 
 
+def test_allocation_free_step(simt_lib):
+    """bl_sample_rows_noalloc (slot state and workspace carved from its fixed array), twice in a row with
+    the second call smaller, equals bl_sample_step over fresh slots with the same parameters and RNG states:
+    tokens, logprobs, alternatives and advanced states."""
+    out = _run(simt_lib, ["noalloc"], {"SIMT_ORDER": "rand"})
+    assert "ok   allocation-free step" in out
+
+
 def test_small_cases_address_sanitizer():
     _build("asan")
     pre = []
