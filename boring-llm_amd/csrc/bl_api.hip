@@ -232,6 +232,7 @@ static bool dev_layout(bl_dev &d, size_t S, size_t R, int vocab, Take take) {
                   take(d.cand_i, R * d.nc * BL_KSEL_MAX) && take(grec, R * 2 * G * 32) && take(d.full_v, R * d.nb * BL_EB) &&
                   take(d.full_i, R * d.nb * BL_EB) && take(d.full_cnt, R * d.nb) && take(d.full_s, R * d.nb) &&
                   take(d.sortk, R * 2 * V) && take(d.gsum, R * G) && take(d.crit, R * BL_CRIT_MAX) && take(d.ncrit, R) &&
+                  take(d.mkeys, R * BL_KSEL_MAX) && take(d.mstat, R) && take(d.rmax, R) && take(d.rarg, R) &&
                   take(brec, R * d.nb * 16) && take(d.bcrit, R * d.nb) && take(d.gram, S) &&
                   take(d.gmask, R * 2 * ((V + 63) / 64)) && take(d.gstat, R) && take(d.gamb, R) &&
                   take(d.gm_max, R * d.gm_blocks) && take(d.gm_arg, R * d.gm_blocks) && take(d.gm_eq, R * d.gm_blocks);

@@ -147,6 +147,10 @@ struct bl_dev {
   double *gsum;     /* [rows][V/64 + 64] */
   bl_crit *crit;    /* [rows][BL_CRIT_MAX] the normaliser's critical groups, in order of arrival */
   int32_t *ncrit;   /* [rows] critical groups found (entries past BL_CRIT_MAX are not stored) */
+  uint64_t *mkeys;  /* [rows][KSEL_MAX] the row's top-K keys, merged by the exponent pass */
+  int32_t *mstat;   /* [rows] 1: mkeys holds the merge; 0: the selection merges the chunk lists itself */
+  float *rmax;      /* [rows] the row maximum and its first index, reduced by the exponent pass */
+  int32_t *rarg;
   void *brec;       /* [rows][nb] bl_grec1 per BL_EB terms: the block's binade and composed automaton, or
                        BL_E_NONE when it holds a critical group or two binades */
   uint32_t *bcrit;  /* [rows][nb] the block's critical groups (bit i: group 16 b + i) */
@@ -174,6 +178,7 @@ struct bl_rows {
   int16_t slot_inline[BL_ROWS_INLINE];
   const int32_t *rng_skip; /* [B] draws consumed before this row's draw (speculative rows), or null */
   int32_t commit;          /* append the chosen token to the slot history */
+  int32_t merged;          /* the exponent pass ran: it left each row's maximum and merged top-K keys */
   int32_t *tok;            /* [B] */
   float *lp;               /* [B] */
   int32_t *top_ids;        /* [B][top_stride] */

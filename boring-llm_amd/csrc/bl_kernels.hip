@@ -48,6 +48,21 @@ __device__ __forceinline__ void argmax_merge(float &m, int &mi, float m2, int mi
   }
 }
 
+/* keys of a[0..n) (LDS) greater than k, U reads in flight at a time */
+template <int U = 8>
+__device__ __forceinline__ int count_gt(const uint64_t *a, int n, uint64_t k) {
+  int r = 0, j = 0;
+  for (; j + U <= n; j += U) {
+    uint64_t x[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) x[u] = a[j + u];
+#pragma unroll
+    for (int u = 0; u < U; u++) r += x[u] > k ? 1 : 0;
+  }
+  for (; j < n; j++) r += a[j] > k ? 1 : 0;
+  return r;
+}
+
 template <int NT>
 __device__ __forceinline__ void block_argmax(float &m, int &mi, float *sm, int *si) {
   int t = threadIdx.x, lane = t & 63, w = t >> 6;
@@ -484,11 +499,7 @@ __device__ __forceinline__ void rowpass_body(const bl_dev &d, const float *__res
       /* rank by counting; the K largest go out in order */
       for (int q = t; q < nk; q += BL_RP_THREADS) {
         const uint64_t kk = tkeys[q];
-        int rr = 0, j = 0;
-        for (; j + 4 <= nk; j += 4)
-          rr += (tkeys[j] > kk ? 1 : 0) + (tkeys[j + 1] > kk ? 1 : 0) + (tkeys[j + 2] > kk ? 1 : 0) +
-                (tkeys[j + 3] > kk ? 1 : 0);
-        for (; j < nk; j++) rr += tkeys[j] > kk ? 1 : 0;
+        const int rr = count_gt(tkeys, nk, kk);
         if (rr < K) {
           d.cand_v[cbase + rr] = ckey_v(kk);
           d.cand_i[cbase + rr] = ckey_i(kk);
@@ -633,12 +644,115 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass_spec(bl_dev d, con
  * The critical list is appended with one device-scope atomic per critical group (a few per row); no
  * workgroup waits for another: the selection kernel, a later launch, reads the list.
  */
+#define BL_MU_MAX 512 /* the exponent pass's merge: first keys of the chunk lists held in LDS */
+#define BL_MSURV 1024 /* the exponent pass's merge: survivors of the cut held in LDS */
+#define BL_MREG 8     /* the exponent pass's merge: list entries per thread loaded at once */
+
+/*
+ * The exponent pass's last workgroup of each row, beside the row's exponent blocks: the row maximum and its
+ * first index (d.rmax, d.rarg) from the chunk statistics, and the row's top K keys in (value desc, index asc)
+ * order (top_k_select, src/sampling.br:280-296) merged from the row pass's chunk lists into
+ * d.mkeys[row][0..K) (0 past the valid keys). The cut is the selection's merge's: the K-th largest of the
+ * lists' first L = ceil(K/nc) keys is at most the row's K-th key, so the row's top K are among the keys at
+ * or above it, which are ranked by counting (keys are distinct: they carry the index). d.mstat[row] = 1 once
+ * done; 0 when the first keys or the survivors exceed this workgroup's LDS, and the selection then merges the
+ * lists itself.
+ */
+template <int NT>
+__device__ __forceinline__ void exp_merge_role(const bl_dev &d, const bl_rows &rows, int row) {
+  const int t = threadIdx.x, lane = t & 63, nc = d.nc;
+  __shared__ uint64_t m_u[BL_MU_MAX];
+  __shared__ uint64_t m_sv[BL_MSURV];
+  __shared__ uint64_t m_tau;
+  __shared__ int m_n;
+  const int K = d.slots[bl_row_slot(rows, row)].k_sel;
+  if (t < 64) {
+    float M = BL_NEG_INF;
+    int Mi = 0x7fffffff;
+    for (int k = lane; k < nc; k += 64) argmax_merge(M, Mi, d.c_max[(int64_t)row * nc + k], d.c_arg[(int64_t)row * nc + k]);
+    bl_wargmax(M, Mi, lane);
+    if (t == 0) {
+      d.rmax[row] = M;
+      d.rarg[row] = Mi;
+    }
+  }
+  const int L = K > 0 ? (K + nc - 1) / nc : 0, nu = nc * L, total = nc * K;
+  if (K <= 0 || nu > BL_MU_MAX) {
+    if (t == 0) d.mstat[row] = K <= 0 ? 1 : 0;
+    return;
+  }
+  auto gkey = [&](int c, int q) -> uint64_t {
+    const int64_t o = ((int64_t)row * nc + c) * BL_KSEL_MAX + q;
+    const int32_t id = d.cand_i[o];
+    const float v = d.cand_v[o]; /* loaded with the id, not after it */
+    return id >= 0 ? ckey(v, id) : 0ull;
+  };
+  if (t == 0) {
+    m_tau = 1ull; /* every valid key, when fewer than K exist */
+    m_n = 0;
+  }
+  /* every list entry up to BL_MREG * NT of them in registers, all loads in flight at once; the lists' first
+   * L keys among them go to LDS */
+  constexpr int PU = BL_MREG;
+  uint64_t kr[PU];
+#pragma unroll
+  for (int u = 0; u < PU; u++) {
+    const int i = t + u * NT;
+    const int c = i / K;
+    kr[u] = i < total ? gkey(c, i - c * K) : 0ull;
+  }
+  if (total <= PU * NT) {
+#pragma unroll
+    for (int u = 0; u < PU; u++) {
+      const int i = t + u * NT;
+      const int c = i / K, q = i - c * K;
+      if (i < total && q < L) m_u[c * L + q] = kr[u];
+    }
+  } else {
+    for (int i = t; i < nu; i += NT) m_u[i] = gkey(i / L, i - (i / L) * L);
+  }
+  __syncthreads();
+  for (int i = t; i < nu; i += NT) {
+    const uint64_t k = m_u[i];
+    if (k && count_gt<4>(m_u, nu, k) == K - 1) m_tau = k;
+  }
+  __syncthreads();
+  const uint64_t tau = m_tau;
+  auto keep = [&](uint64_t k) {
+    if (k >= tau) {
+      const int p = atomicAdd(&m_n, 1);
+      if (p < BL_MSURV) m_sv[p] = k;
+    }
+  };
+#pragma unroll
+  for (int u = 0; u < PU; u++) keep(kr[u]);
+  for (int i = PU * NT + t; i < total; i += NT) keep(gkey(i / K, i - (i / K) * K));
+  __syncthreads();
+  const int C = m_n;
+  if (C > BL_MSURV) {
+    if (t == 0) d.mstat[row] = 0;
+    return;
+  }
+  uint64_t *out = d.mkeys + (int64_t)row * BL_KSEL_MAX;
+  for (int i = t; i < C; i += NT) {
+    const uint64_t k = m_sv[i];
+    const int r = count_gt<4>(m_sv, C, k);
+    if (r < K) out[r] = k;
+  }
+  for (int q = C + t; q < K; q += NT) out[q] = 0ull;
+  if (t == 0) d.mstat[row] = 1;
+}
+
 template <bool SPEC>
 __device__ __forceinline__ void exppass_body(const bl_dev &d, const float *__restrict__ logits, int64_t ld,
                                              const bl_rows &rows) {
   const int V = d.vocab, nc = d.nc;
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int b = blockIdx.x, row = blockIdx.y;
+  if (b == d.nb) {
+    exp_merge_role<BL_RP_THREADS>(d, rows, row);
+    return;
+  }
   const int slot = bl_row_slot(rows, row);
   const bl_slot_dev &sp = slot_of(d, slot);
   const int mode = sp.mode;
@@ -668,10 +782,18 @@ __device__ __forceinline__ void exppass_body(const bl_dev &d, const float *__res
 #pragma unroll
     for (int k = 0; k < 4; k++) x[k] = j0 + k < cnt ? src[k] : BL_NEG_INF;
   }
-  /* the row maximum and its first index, by every wavefront from the chunk statistics */
+  /* the row maximum and its first index, by every wavefront from the chunk statistics; lane k also keeps
+   * chunk k's maximum and sub-block sums (the first 64 chunks), loaded with them for the prefix below */
   float M = BL_NEG_INF;
   int Mi = 0x7fffffff;
-  for (int k = lane; k < nc; k += 64) argmax_merge(M, Mi, d.c_max[(int64_t)row * nc + k], d.c_arg[(int64_t)row * nc + k]);
+  float cm0 = BL_NEG_INF;
+  float4 cb0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (lane < nc) {
+    cm0 = d.c_max[(int64_t)row * nc + lane];
+    cb0 = *reinterpret_cast<const float4 *>(d.c_bsum + ((int64_t)row * nc + lane) * BL_SUBS);
+    argmax_merge(M, Mi, cm0, d.c_arg[(int64_t)row * nc + lane]);
+  }
+  for (int k = lane + 64; k < nc; k += 64) argmax_merge(M, Mi, d.c_max[(int64_t)row * nc + k], d.c_arg[(int64_t)row * nc + k]);
   /* model tail and server stages, as the row pass applied them */
   *reinterpret_cast<float4 *>(vals + j0) = make_float4(x[0], x[1], x[2], x[3]);
   apply_stages<SPEC>(d, sp, rows, row, slot, i0, cnt, vals, st_sup, st_done);
@@ -692,8 +814,8 @@ __device__ __forceinline__ void exppass_body(const bl_dev &d, const float *__res
     const int nsub = i0 / BL_EB;
     double part = 0.0;
     for (int k = lane; k * BL_SUBS < nsub; k += 64) {
-      const float cm = d.c_max[(int64_t)row * nc + k];
-      const float4 cb = *reinterpret_cast<const float4 *>(d.c_bsum + ((int64_t)row * nc + k) * BL_SUBS);
+      const float cm = k < 64 ? cm0 : d.c_max[(int64_t)row * nc + k];
+      const float4 cb = k < 64 ? cb0 : *reinterpret_cast<const float4 *>(d.c_bsum + ((int64_t)row * nc + k) * BL_SUBS);
       if (cm > BL_NEG_INF) {
         const int lim = nsub - k * BL_SUBS;
         const double cs = (double)cb.x + (lim > 1 ? (double)cb.y : 0.0) + (lim > 2 ? (double)cb.z : 0.0) +
@@ -1109,9 +1231,11 @@ struct sel_shared {
   uint64_t mtau;                       /* the merge's lower bound on the K-th key */
   int mcnt;                            /* the merge's survivors */
   uint64_t etab[BL_EXP2_N];            /* expf's 2^(i/32) table (a global table read is a dependent load) */
+  double ltab[32];                     /* logf's (1/c, log c) table */
 };
-/* expf through the selection's LDS copy of the table */
+/* expf and logf through the selection's LDS copies of their tables */
 #define SEL_EXPF(x) bl_expf_tab((x), [&](uint32_t i_) { return sh.etab[i_]; })
+#define SEL_LOGF(x) bl_logf_tab((x), [&](int j_) { return sh.ltab[j_]; })
 
 /* sample_candidates_with_probs (src/sampling.br:490-607) for T > 0: the stages without a device path, and
  * a min_keep that reaches past the materialised list, leave the row unsupported */
@@ -1747,11 +1871,11 @@ __device__ __forceinline__ void norm_prep(const bl_dev &d, int row, float M, sel
   const int ncrit = have ? ncrit_all : 0;
   /* 2. the slot of each critical group's entry (its rank among the entries' groups) */
   if (have) {
-    if (t < ncrit) {
-      const int g = nm.eg[t];
+    if (w == 0) { /* lane j holds entry j's group; the others are broadcast from their lanes */
+      const int g = lane < ncrit ? nm.eg[lane] : 0x7fffffff;
       int p = 0;
-      for (int j = 0; j < ncrit; j++) p += nm.eg[j] < g ? 1 : 0;
-      nm.epos[p] = t;
+      for (int j = 0; j < ncrit; j++) p += (int)bl_bcast((uint32_t)g, j) < g ? 1 : 0;
+      if (lane < ncrit) nm.epos[p] = lane;
     }
     __syncthreads();
   }
@@ -1768,10 +1892,12 @@ __device__ __forceinline__ void norm_prep(const bl_dev &d, int row, float M, sel
     int st = 0, Er = BL_E_NONE;
     bl_inc acc = bl_inc_ident();
     if (lo < hi) {
-      const int gb0 = min((lo + 15) & ~15, hi), gb1 = max(hi & ~15, gb0);
-      const int npre = gb0 - lo, nblk = (gb1 - gb0) >> 4, nit = npre + nblk + (hi - gb1);
-      /* a group of a critical group's block from that entry; others (the row's trailing partial block) from
-       * the exponent pass's records */
+      const int gb0 = min((lo + 15) & ~15, hi);
+      /* whole blocks from their summaries, the row's short last block included (its summary covers its groups) */
+      const int gb1 = (hi == G && (hi & 15) && gb0 <= (hi & ~15)) ? hi : max(hi & ~15, gb0);
+      const int npre = gb0 - lo, nblk = (gb1 - gb0 + 15) >> 4, nit = npre + nblk + (hi - gb1);
+      /* a group of a critical group's block from that entry; others (a short last block that a critical group
+       * cuts) from the exponent pass's records */
       auto grp = [&](int g) -> bl_grec1 {
         const int bg = g >> 4;
         if (it > 0 && (nm.crit[it - 1] >> 4) == bg) return edge(it - 1, g);
@@ -2094,10 +2220,7 @@ __device__ __forceinline__ void sel_merge(const bl_dev &d, int row, int K, sel_s
     __syncthreads();
     for (int i = t; i < nu; i += NT) {
       const uint64_t k = ua[i];
-      if (!k) continue;
-      int r = 0;
-      for (int j = 0; j < nu; j++) r += ua[j] > k ? 1 : 0;
-      if (r == K - 1) sh.mtau = k;
+      if (k && count_gt(ua, nu, k) == K - 1) sh.mtau = k;
     }
     __syncthreads();
     const uint64_t tau = sh.mtau;
@@ -2164,10 +2287,7 @@ __device__ __forceinline__ void sel_merge(const bl_dev &d, int row, int K, sel_s
   const int C = min(sh.mcnt, BL_LDS_SORT);
   for (int i = t; i < C; i += NT) {
     const uint64_t k = surv[i];
-    int r = 0, j = 0;
-    for (; j + 4 <= C; j += 4)
-      r += (surv[j] > k ? 1 : 0) + (surv[j + 1] > k ? 1 : 0) + (surv[j + 2] > k ? 1 : 0) + (surv[j + 3] > k ? 1 : 0);
-    for (; j < C; j++) r += surv[j] > k ? 1 : 0;
+    const int r = count_gt(surv, C, k);
     if (r < K) sh.mkeys[r] = k;
   }
   for (int q = C + t; q < K; q += NT) sh.mkeys[q] = 0ull;
@@ -2179,11 +2299,19 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
   const int V = d.vocab, nc = d.nc;
   const int row = blockIdx.x, t = threadIdx.x, w = t >> 6, lane = t & 63;
   __shared__ sel_shared sh;
-  /* loads that need only the row index go out first; wavefront 0 reduces the row maximum and its first
-   * index from the chunk statistics */
+  /* loads that need only the row index go out first: the exponent pass's row maximum and merged top-K keys
+   * (thread t keeps the t-th); without that pass, wavefront 0 reduces the maximum from the chunk statistics */
+  const bool pre = rows.merged != 0;
   float M = BL_NEG_INF;
   int Mi = 0x7fffffff;
-  if (w == 0) {
+  int mst = 0;
+  uint64_t mk_pre = 0ull;
+  if (pre) {
+    M = d.rmax[row];
+    Mi = d.rarg[row];
+    mst = d.mstat[row];
+    if (t < BL_KSEL_MAX) mk_pre = d.mkeys[(int64_t)row * BL_KSEL_MAX + t];
+  } else if (w == 0) {
     for (int k = lane; k < nc; k += 64) argmax_merge(M, Mi, d.c_max[(int64_t)row * nc + k], d.c_arg[(int64_t)row * nc + k]);
     bl_wargmax(M, Mi, lane);
     if (lane == 0) {
@@ -2194,6 +2322,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
   uint32_t m_pre = 0u; /* the normaliser's first block flags and summaries (used by logprob rows) */
   bl_grec1 br_pre{};
   const int n_ent = d.ncrit[row]; /* the normaliser's critical-group entries */
+
   if (t < d.nb) {
     m_pre = d.bcrit[(int64_t)row * d.nb + t];
     br_pre = reinterpret_cast<const bl_grec1 *>(d.brec)[(int64_t)row * d.nb + t];
@@ -2212,13 +2341,17 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
   const int n_eog = d.n_eog;
   if (t < n_eog && t < BL_EOG_LDS) sh.eog[t] = d.eog[t];
   if (t < BL_EXP2_N) sh.etab[t] = bl_exp2_tab[t];
+  if (t >= 64 && t < 96) sh.ltab[t - 64] = bl_log_tab[t - 64];
   __syncthreads();
-  M = sh.red_m[0];
-  Mi = sh.red_i[0];
+  if (!pre) {
+    M = sh.red_m[0];
+    Mi = sh.red_i[0];
+  }
   if (Mi == 0x7fffffff) Mi = 0;
   /* the row's top K keys: thread t keeps the t-th (used when K > t) */
-  if (K > 0) sel_merge(d, row, K, sh);
-  const uint64_t mk = t < K ? sh.mkeys[t] : 0ull;
+  const bool merged = pre && mst;
+  if (K > 0 && !merged) sel_merge(d, row, K, sh);
+  const uint64_t mk = t < K ? (merged ? mk_pre : sh.mkeys[t]) : 0ull;
 
   int status = 0;
   uint64_t rng = sp.rng;
@@ -2289,12 +2422,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
       /* rank by counting (keys are distinct: they carry the index) */
       for (int i = t; i < nf; i += BL_SEL_THREADS) {
         const uint64_t k = sh.c.tmp[i];
-        int r = 0, j = 0;
-        for (; j + 4 <= nf; j += 4)
-          r += (sh.c.tmp[j] > k ? 1 : 0) + (sh.c.tmp[j + 1] > k ? 1 : 0) + (sh.c.tmp[j + 2] > k ? 1 : 0) +
-               (sh.c.tmp[j + 3] > k ? 1 : 0);
-        for (; j < nf; j++) r += sh.c.tmp[j] > k ? 1 : 0;
-        keys[r] = k;
+        keys[count_gt(sh.c.tmp, nf, k)] = k;
       }
     } else if (nf <= BL_LDS_SORT) {
       int P = 1;
@@ -2619,7 +2747,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
   }
 
   /* outputs, logprobs (src/server.br:1027-1035): alternatives = the first n_probs of the merged list */
-  const float lse = lp_row ? bl_logf(S_norm) : 0.0f; /* sum_exp.ln(), glibc's logf (src/sampling.br:265) */
+  const float lse = lp_row ? SEL_LOGF(S_norm) : 0.0f; /* sum_exp.ln(), glibc's logf (src/sampling.br:265) */
   if (lp_row) {
     const int n = sp.n_probs < rows.top_stride ? sp.n_probs : rows.top_stride;
     if (t < n) {
@@ -2681,8 +2809,10 @@ __global__ void bl_k_synth(float *out, int64_t ld, int cfg, int64_t seed, int64_
 
 /* ------------------------------------------------------------------ host-side launchers */
 /* ev: optional 4 events recorded before/after the three kernels (kernel timing for the benchmark) */
-void bl_launch_step(const bl_dev &d, const float *logits, int64_t ld, const bl_rows &rows, int B, bool need_pass2,
+void bl_launch_step(const bl_dev &d, const float *logits, int64_t ld, const bl_rows &rows_in, int B, bool need_pass2,
                     bool need_gram, hipStream_t s, hipEvent_t *ev) {
+  bl_rows rows = rows_in;
+  rows.merged = need_pass2 ? 1 : 0;
   dim3 g1(d.nc, B);
   if (ev) (void)hipEventRecord(ev[0], s);
   if (rows.delta)
@@ -2693,9 +2823,9 @@ void bl_launch_step(const bl_dev &d, const float *logits, int64_t ld, const bl_r
   if (need_gram) hipLaunchKernelGGL(bl_k_gmask, dim3(d.gm_blocks, B), dim3(BL_GM_THREADS), 0, s, d, logits, ld, rows, 1);
   if (need_pass2) {
     if (rows.delta)
-      hipLaunchKernelGGL(bl_k_exppass_spec, dim3(d.nb, B), dim3(BL_RP_THREADS), 0, s, d, logits, ld, rows);
+      hipLaunchKernelGGL(bl_k_exppass_spec, dim3(d.nb + 1, B), dim3(BL_RP_THREADS), 0, s, d, logits, ld, rows);
     else
-      hipLaunchKernelGGL(bl_k_exppass, dim3(d.nb, B), dim3(BL_RP_THREADS), 0, s, d, logits, ld, rows);
+      hipLaunchKernelGGL(bl_k_exppass, dim3(d.nb + 1, B), dim3(BL_RP_THREADS), 0, s, d, logits, ld, rows);
   }
   if (ev) (void)hipEventRecord(ev[2], s);
   hipLaunchKernelGGL(bl_k_select, dim3(B), dim3(BL_SEL_THREADS), 0, s, d, logits, ld, rows);

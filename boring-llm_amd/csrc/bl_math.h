@@ -118,15 +118,26 @@ BL_FN float bl_expf(float x) {
  * (1/c, log c) from the table, log1p by a cubic in double, one rounding to float at the end.
  * Equal to host glibc logf on every positive float (CPU, tests/cpu/check_exact.cpp samples it) and on
  * all 2^32 bit patterns on the device (tests/golden/math_digest.bin). */
-BL_FN float bl_logf(float x) {
-  const double invc[16] = {0x1.661ec79f8f3bep+0, 0x1.571ed4aaf883dp+0, 0x1.49539f0f010bp+0,  0x1.3c995b0b80385p+0,
-                           0x1.30d190c8864a5p+0, 0x1.25e227b0b8eap+0,  0x1.1bb4a4a1a343fp+0, 0x1.12358f08ae5bap+0,
-                           0x1.0953f419900a7p+0, 0x1p+0,               0x1.e608cfd9a47acp-1, 0x1.ca4b31f026aap-1,
-                           0x1.b2036576afce6p-1, 0x1.9c2d163a1aa2dp-1, 0x1.886e6037841edp-1, 0x1.767dcf5534862p-1};
-  const double logc[16] = {-0x1.57bf7808caadep-2, -0x1.2bef0a7c06ddbp-2, -0x1.01eae7f513a67p-2, -0x1.b31d8a68224e9p-3,
-                           -0x1.6574f0ac07758p-3, -0x1.1aa2bc79c81p-3,   -0x1.a4e76ce8c0e5ep-4, -0x1.1973c5a611cccp-4,
-                           -0x1.252f438e10c1ep-5, 0x0p+0,                0x1.aa5aa5df25984p-5,  0x1.c5e53aa362eb4p-4,
-                           0x1.526e57720db08p-3,  0x1.bc2860d22477p-3,   0x1.1058bc8a07ee1p-2,  0x1.4043057b6ee09p-2};
+/* (1/c, log c) of the 16 subintervals, interleaved */
+#if defined(__HIP_DEVICE_COMPILE__)
+__constant__
+#else
+static
+#endif
+const double bl_log_tab[32] = {
+    0x1.661ec79f8f3bep+0, -0x1.57bf7808caadep-2, 0x1.571ed4aaf883dp+0, -0x1.2bef0a7c06ddbp-2,
+    0x1.49539f0f010bp+0, -0x1.01eae7f513a67p-2, 0x1.3c995b0b80385p+0, -0x1.b31d8a68224e9p-3,
+    0x1.30d190c8864a5p+0, -0x1.6574f0ac07758p-3, 0x1.25e227b0b8eap+0, -0x1.1aa2bc79c81p-3,
+    0x1.1bb4a4a1a343fp+0, -0x1.a4e76ce8c0e5ep-4, 0x1.12358f08ae5bap+0, -0x1.1973c5a611cccp-4,
+    0x1.0953f419900a7p+0, -0x1.252f438e10c1ep-5, 0x1p+0, 0x0p+0,
+    0x1.e608cfd9a47acp-1, 0x1.aa5aa5df25984p-5, 0x1.ca4b31f026aap-1, 0x1.c5e53aa362eb4p-4,
+    0x1.b2036576afce6p-1, 0x1.526e57720db08p-3, 0x1.9c2d163a1aa2dp-1, 0x1.bc2860d22477p-3,
+    0x1.886e6037841edp-1, 0x1.1058bc8a07ee1p-2, 0x1.767dcf5534862p-1, 0x1.4043057b6ee09p-2};
+
+/* logf with the (1/c, log c) table read through tab(j), j = 2 i and 2 i + 1 (a kernel may stage the table
+ * in LDS) */
+template <class Tab>
+BL_FN float bl_logf_tab(float x, Tab tab) {
   const double LN2 = 0x1.62e42fefa39efp-1, A0 = -0x1.00ea348b88334p-2, A1 = 0x1.5575b0be00b6ap-2,
                A2 = -0x1.ffffef20a4123p-2;
   uint32_t ix = bl_f2u(x);
@@ -143,13 +154,17 @@ BL_FN float bl_logf(float x) {
   const int k = (int32_t)tmp >> 23;
   const uint32_t iz = ix - (tmp & 0xff800000u);
   const double z = (double)bl_u2f(iz);
-  const double r = z * invc[i] - 1.0;
-  const double y0 = logc[i] + (double)k * LN2;
+  const double r = z * tab(2 * i) - 1.0;
+  const double y0 = tab(2 * i + 1) + (double)k * LN2;
   const double r2 = r * r;
   double y = A1 * r + A2;
   y = A0 * r2 + y;
   y = y * r2 + (y0 + r);
   return (float)y;
+}
+
+BL_FN float bl_logf(float x) {
+  return bl_logf_tab(x, [](int j) { return bl_log_tab[j]; });
 }
 
 /* ---------------- expm1f / tanhf (float arithmetic) ---------------- */
