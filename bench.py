@@ -4,14 +4,19 @@ Workload: B=8 slots, V=151936, per-row temperature {0
 {0,20,64} x top_p {1.0,0.9}, frequency 0.5 / presence 0.3 over 4096 Zipf(1.1) reply ids, 300 logit_bias
 ids in [-100,100], n_probs=10 logprobs, logits ~N(0,4^2). A step is one decode-loop sampling block for
 the 8 rows (transform, rank, exact draw, logprobs, history commit) through the C ABI. Inputs are
-resident in HBM: a pool of 64 steps of logits (311 MB, more than the 256 MB Infinity Cache) is
-generated on the device beforehand and the steps cycle through it.
+resident in HBM: the logits of up to 512 distinct workload steps (at least 64 of them, 311 MB, more than
+the 256 MB Infinity Cache) are generated on the device beforehand; step t reads those of step t mod P.
 
-Prints one JSON line. `value` is steps/s of back-to-back HIP-graph replays; p50 is one replay + sync.
-The roofline object reports the dominant kernel's algorithmic HBM bytes (the 4*B*V logits it must read)
-over its event-timed average duration against 8 TB/s. The CPU baseline times the oracle (the
-reference's algorithms restated in C++: per-stage row copies, insertion top-k, heap sort, hash maps,
-sequential sums) on one host core over a bounded sample of the same workload.
+Prints one JSON line. `value` is steps/s of back-to-back direct launches of the step, each writing its
+tokens and logprobs to its own row of a device log; after the timed region the logged warmup and timed
+steps (up to --check-steps of them) are compared with the oracle's stream of the same workload, and a
+mismatch fails the run. p50 is one step + stream synchronisation (direct launches, and HIP-graph replays).
+`roofline` is the step's: the 4*B*V logits a step must read over the summed durations of its three kernels,
+each timed by the start and end events of an extended launch (the kernel's own execution); a second entry
+does the same for the row pass, the kernel that reads the logits. `traffic` is FETCH_SIZE + WRITE_SIZE per
+launch from the committed counter summary. The CPU baseline times the oracle (the reference's algorithms
+restated in C++: per-stage row copies, insertion top-k, heap sort, hash maps, sequential sums) on one host
+core over a bounded sample of the same workload.
 """
 import argparse
 import json
@@ -26,7 +31,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "boring-llm_amd"))
 
 METRIC = "sampling steps/s + p50 µs/step at B=8,V=151936; HBM GB/s vs peak"
-V, B, SEED, POOL, TOPN = 151936, 8, 2, 64, 10
+V, B, SEED, POOL_MAX, TOPN = 151936, 8, 2, 512, 10
 HBM_PEAK_GBS = 8000.0
 
 
@@ -252,7 +257,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-graph", action="store_true", help="direct launches (hardware-counter runs)")
+    ap.add_argument("--no-graph", action="store_true", help="skip the HIP-graph latency leg (hardware-counter runs)")
+    ap.add_argument("--check-steps", type=int, default=256,
+                    help="leading steps of the logged stream compared with the oracle after the timed region")
     ap.add_argument("--copy-calib", action="store_true",
                     help="run only a plain 256 MiB device-to-device copy (calibrates FETCH_SIZE/WRITE_SIZE)")
     ap.add_argument("--workload", type=int, default=2,
@@ -285,89 +292,93 @@ def main():
     ctx = BL.Context(V, B, B)
     setup_slots(BL, ctx)
     ctx.bind_rows(list(range(B)))
-    pool = torch.empty((POOL, B, V), dtype=torch.float32, device=dev)
-    for p in range(POOL):
+    W, K = args.warmup, args.steps
+    n_stream = W + K  # the warmup and timed steps: their tokens and logprobs are logged
+    # step t reads the logits of workload step t % P (P distinct steps, 64 of them already larger than the
+    # 256 MB Infinity Cache); the checked steps are all distinct, so their stream is the oracle's
+    P = max(64, min(n_stream, POOL_MAX))
+    pool = torch.empty((P, B, V), dtype=torch.float32, device=dev)
+    for p in range(P):
         ctx.synth_logits(pool[p].data_ptr(), V, 2, SEED, p, B, V)
+    log_tok = torch.full((n_stream, B), -2, dtype=torch.int32, device=dev)
+    log_lp = torch.zeros((n_stream, B), dtype=torch.float32, device=dev)
     d_tok = torch.zeros(B, dtype=torch.int32, device=dev)
     d_lp = torch.zeros(B, dtype=torch.float32, device=dev)
     d_ti = torch.zeros(B * TOPN, dtype=torch.int32, device=dev)
     d_tl = torch.zeros(B * TOPN, dtype=torch.float32, device=dev)
     torch.cuda.synchronize()
 
-    def launch(p):
-        ctx.sample_step_async(B, pool[p].data_ptr(), V, d_tok.data_ptr(), d_lp.data_ptr(), d_ti.data_ptr(),
-                              d_tl.data_ptr(), TOPN)
+    def launch(i, tok, lp):
+        ctx.sample_step_async(B, pool[i % P].data_ptr(), V, tok, lp, d_ti.data_ptr(), d_tl.data_ptr(), TOPN)
 
-    # one HIP graph per pool entry, captured by the library on its own stream (bl_step_graph_create): no
-    # allocation and no host synchronisation inside a step
-    graphs = []
-    if not args.no_graph:
-        graphs = [ctx.step_graph(B, pool[p].data_ptr(), V, d_tok.data_ptr(), d_lp.data_ptr(), d_ti.data_ptr(),
-                                 d_tl.data_ptr(), TOPN) for p in range(POOL)]
-    use_graph = bool(graphs)
+    def logged(i):
+        launch(i, log_tok[i].data_ptr(), log_lp[i].data_ptr())
 
-    def step(i):
-        if use_graph:
-            ctx.graph_launch(graphs[i % POOL])
-        else:
-            launch(i % POOL)
-
-    for i in range(args.warmup):
-        step(i)
+    for i in range(W):
+        logged(i)
     ctx.sync()
-
-    # throughput: K back-to-back steps
+    # throughput: K back-to-back steps (direct launches; each step's outputs go to its own log row)
     t0 = time.perf_counter()
-    for i in range(args.steps):
-        step(args.warmup + i)
+    for i in range(W, W + K):
+        logged(i)
     ctx.sync()
     elapsed = time.perf_counter() - t0
+    checked = check_tokens(log_tok.cpu().numpy(), log_lp.cpu().numpy(), min(n_stream, args.check_steps, P))
 
-    # latency: one step + stream synchronisation
-    lat = []
-    base = args.warmup + args.steps
-    for i in range(min(args.steps, 1000)):
-        a = time.perf_counter()
-        step(base + i)
-        ctx.sync()
-        lat.append(time.perf_counter() - a)
-    p50_graph = 1e6 * float(np.median(lat))
-    # the same single-step latency with the step's kernels launched directly (no graph)
+    # latency: one step + stream synchronisation, continuing the stream
+    nxt = n_stream
     lat_d = []
-    for i in range(min(args.steps, 1000)):
+    for i in range(min(K, 1000)):
         a = time.perf_counter()
-        launch((base + i) % POOL)
+        launch(nxt, d_tok.data_ptr(), d_lp.data_ptr())
         ctx.sync()
         lat_d.append(time.perf_counter() - a)
+        nxt += 1
     p50_direct = 1e6 * float(np.median(lat_d))
-    p50_us = min(p50_graph, p50_direct) if use_graph else p50_direct
+    # the same with the step captured in a HIP graph (bl_step_graph_create: no allocation, no host work)
+    p50_graph = None
+    if not args.no_graph:
+        graphs = [ctx.step_graph(B, pool[(nxt + g) % P].data_ptr(), V, d_tok.data_ptr(), d_lp.data_ptr(),
+                                 d_ti.data_ptr(), d_tl.data_ptr(), TOPN) for g in range(16)]
+        lat_g = []
+        for i in range(min(K, 500)):
+            a = time.perf_counter()
+            ctx.graph_launch(graphs[i % 16])
+            ctx.sync()
+            lat_g.append(time.perf_counter() - a)
+        for g in graphs:
+            BL.Context.graph_destroy(g)
+        p50_graph = 1e6 * float(np.median(lat_g))
+        nxt += len(lat_g)
+    p50_us = min(p50_direct, p50_graph) if p50_graph is not None else p50_direct
 
-    # per-kernel durations (events around each kernel on the launch stream)
+    # each kernel's own duration (start and end events of an extended launch, on the launch stream)
     ctx.set_timing(True)
-    n_t = min(args.steps, 400)
+    n_t = min(K, 400)
     for i in range(n_t):
-        launch((base + i) % POOL)
+        launch(nxt + i, d_tok.data_ptr(), d_lp.data_ptr())
     kms, nsteps = ctx.get_timing()
     ctx.set_timing(False)
     ctx.sync()
-    for g in graphs:
-        BL.Context.graph_destroy(g)
 
     names = ["bl_k_rowpass", "bl_k_exppass", "bl_k_select"]
-    dom = int(np.argmax(kms))
-    alg_bytes = 4.0 * B * V  # logits each step must read (the path's algorithmic traffic)
-    achieved = alg_bytes / (kms[dom] * 1e-3) / 1e9
+    kus = {names[k]: 1e3 * kms[k] for k in range(3)}
+    step_us = sum(kus.values())
+    alg_bytes = 4.0 * B * V  # the logits a step must read (the path's algorithmic traffic)
     traffic = measured_traffic()
+    step_traffic = sum(traffic.values()) if traffic else None
+    achieved = alg_bytes / (step_us * 1e-6) / 1e9
+    k1 = kus["bl_k_rowpass"]
     out = {
         "metric": METRIC,
-        "value": args.steps / elapsed,
+        "value": K / elapsed,
         "unit": "steps/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": 1e3 * elapsed / args.steps,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": 1e3 * elapsed / K,
         "p50_us_per_step": p50_us,
-        "p50_us_by_launch": {"graph_replay": p50_graph if use_graph else None, "direct_launches": p50_direct},
+        "p50_us_by_launch": {"direct_launches": p50_direct, "graph_replay": p50_graph},
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -375,21 +386,51 @@ def main():
         "data": "synthetic (seeded integer-hash logits, Zipf histories, bias lists; BASELINE configs[1])",
         "config": {"workload": "B=8 slots, V=151936, per-row T/top_k/top_p table, freq 0.5 / presence 0.3 over "
                                "4096 Zipf(1.1) ids, 300 bias ids in [-100,100], n_probs 10",
-                   "batch": B, "vocab": V, "hip_graph": use_graph, "logits_pool_MB": POOL * B * V * 4 / 1e6},
-        "kernels_us": {names[k]: 1e3 * kms[k] for k in range(3)},
-        "roofline": {"bound": "hbm", "kernel": names[dom], "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": traffic.get(names[dom]) if traffic else None,
-                     "algorithmic_bytes_per_launch": alg_bytes},
+                   "batch": B, "vocab": V, "launch": "direct", "logits_pool_MB": P * B * V * 4 / 1e6},
+        "kernels_us": kus,
+        "kernels_timed_steps": nsteps,
+        "step_kernels_us": step_us,
+        # the step: the logits it must read over its three kernels' summed durations
+        "roofline": {"bound": "hbm", "kernel": "step: bl_k_rowpass + bl_k_exppass + bl_k_select",
+                     "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": step_traffic, "algorithmic_bytes_per_launch": alg_bytes},
+        # the kernel that reads the logits first (the row pass)
+        "roofline_logits_kernel": {"bound": "hbm", "kernel": "bl_k_rowpass", "achieved": alg_bytes / (k1 * 1e-6) / 1e9,
+                                   "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                   "frac": alg_bytes / (k1 * 1e-6) / 1e9 / HBM_PEAK_GBS,
+                                   "traffic": traffic.get("bl_k_rowpass") if traffic else None,
+                                   "algorithmic_bytes_per_launch": alg_bytes},
         "traffic_bytes_per_launch": traffic,
-        # each kernel's measured HBM bytes (counters) over its event-timed duration
-        "kernel_hbm_GBs": ({names[k]: traffic[names[k]] / (kms[k] * 1e-3) / 1e9 for k in range(3)}
-                           if traffic else None),
-        "hbm_GBs_step": alg_bytes / (1e-3 * sum(kms)) / 1e9,
+        "traffic_vs_algorithmic": step_traffic / alg_bytes if traffic else None,
+        "tokens_checked": checked,
     }
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(out))
+    if not checked["tokens_match"] or not checked["logprobs_within_tolerance"]:
+        print(f"bench.py: the timed steps differ from the oracle's stream: {checked}", file=sys.stderr)
+        sys.exit(1)
+
+
+def check_tokens(tok, lp, n):
+    """The first n logged steps against the oracle's stream of the workload (tokens bit-exact, logprobs within
+    the 1e-5 relative tolerance of the north star)."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import ctypes
+    import _oracle as O
+    wt = np.zeros(n * B, np.int32)
+    wl = np.zeros(n * B, np.float32)
+    wi = np.zeros(n * B * TOPN, np.int32)
+    wp = np.zeros(n * B * TOPN, np.float32)
+    assert O.lib().orc_run_c2(SEED, n, B, O.ip(wt), O.fp(wl), O.ip(wi), O.fp(wp), ctypes.byref(ctypes.c_double())) == 0
+    got_t = tok[:n].reshape(-1)
+    got_l = lp[:n].reshape(-1).astype(np.float64)
+    bad = np.nonzero(got_t != wt)[0]
+    rel = np.abs(got_l - wl) / np.maximum(np.maximum(np.abs(got_l), np.abs(wl)), 1e-30)
+    return {"steps": int(n), "rows": B, "first_step": 0, "tokens_match": bool(len(bad) == 0),
+            "first_mismatch": None if len(bad) == 0 else [int(bad[0] // B), int(bad[0] % B)],
+            "logprob_max_rel_err": float(rel.max()) if n else 0.0,
+            "logprobs_within_tolerance": bool((rel <= 1e-5).all())}
 
 
 if __name__ == "__main__":

@@ -76,7 +76,7 @@ struct bl_ctx {
   int bound_B = 0;
   std::vector<void *> allocs;
   bool timing = false;
-  hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};
+  hipEvent_t ev[6] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr}; /* kernel timing: start, end of each */
   double kernel_ms[3] = {0.0, 0.0, 0.0};
   int64_t timed_steps = 0;
   /* grammar: host copies of the vocabulary and of each slot's reply, compiled grammars by text */
@@ -925,18 +925,19 @@ int bl_sample_step_async(bl_ctx *c, int B, const float *d_logits, int64_t ld, in
   hipEvent_t *ev = nullptr;
   if (c->timing) {
     if (!c->ev[0])
-      for (int k = 0; k < 4; k++) HIPCHK(hipEventCreate(&c->ev[k]));
+      for (int k = 0; k < 6; k++) HIPCHK(hipEventCreate(&c->ev[k]));
     ev = c->ev;
   }
-  bl_launch_step(c->d, d_logits, ld, rows, B, needs_pass2(c, c->h_bound, B), needs_gram(c, c->h_bound, B), c->stream,
-                 ev);
+  const bool pass2 = needs_pass2(c, c->h_bound, B);
+  bl_launch_step(c->d, d_logits, ld, rows, B, pass2, needs_gram(c, c->h_bound, B), c->stream, ev);
   HIPCHK(hipGetLastError());
   if (ev) {
-    /* per-kernel durations of this step, accumulated (the caller asked for timing: synchronous) */
-    HIPCHK(hipEventSynchronize(ev[3]));
+    /* each kernel's own duration in this step, accumulated (the caller asked for timing: synchronous) */
+    HIPCHK(hipEventSynchronize(ev[5]));
     for (int k = 0; k < 3; k++) {
+      if (k == 1 && !pass2) continue;
       float ms = 0.0f;
-      HIPCHK(hipEventElapsedTime(&ms, ev[k], ev[k + 1]));
+      HIPCHK(hipEventElapsedTime(&ms, ev[2 * k], ev[2 * k + 1]));
       c->kernel_ms[k] += ms;
     }
     c->timed_steps += 1;

@@ -20,6 +20,7 @@
  * No MFMA: the work is bandwidth- and latency-bound scanning, selection and integer arithmetic.
  */
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <stdint.h>
 
 #include <type_traits>
@@ -2808,28 +2809,35 @@ __global__ void bl_k_synth(float *out, int64_t ld, int cfg, int64_t seed, int64_
 }
 
 /* ------------------------------------------------------------------ host-side launchers */
-/* ev: optional 4 events recorded before/after the three kernels (kernel timing for the benchmark) */
+/* one kernel of the step; with a pair of timing events, an extended launch that records the kernel's own
+ * start and end (its execution alone, as a profiler's kernel trace reports it) */
+template <typename F, typename... Args>
+static void step_launch(F k, dim3 g, dim3 b, hipStream_t s, hipEvent_t *ev, Args... args) {
+  if (ev)
+    hipExtLaunchKernelGGL(k, g, b, 0, s, ev[0], ev[1], 0, args...);
+  else
+    hipLaunchKernelGGL(k, g, b, 0, s, args...);
+}
+
+/* ev: optional 6 events, the start and end of the row pass, the exponent pass and the selection kernel
+ * (kernel timing for the benchmark) */
 void bl_launch_step(const bl_dev &d, const float *logits, int64_t ld, const bl_rows &rows_in, int B, bool need_pass2,
                     bool need_gram, hipStream_t s, hipEvent_t *ev) {
   bl_rows rows = rows_in;
   rows.merged = need_pass2 ? 1 : 0;
-  dim3 g1(d.nc, B);
-  if (ev) (void)hipEventRecord(ev[0], s);
+  const dim3 g1(d.nc, B), g2(d.nb + 1, B), t1(BL_RP_THREADS);
   if (rows.delta)
-    hipLaunchKernelGGL(bl_k_rowpass_spec, g1, dim3(BL_RP_THREADS), 0, s, d, logits, ld, rows);
+    step_launch(bl_k_rowpass_spec, g1, t1, s, ev, d, logits, ld, rows);
   else
-    hipLaunchKernelGGL(bl_k_rowpass, g1, dim3(BL_RP_THREADS), 0, s, d, logits, ld, rows);
-  if (ev) (void)hipEventRecord(ev[1], s);
+    step_launch(bl_k_rowpass, g1, t1, s, ev, d, logits, ld, rows);
   if (need_gram) hipLaunchKernelGGL(bl_k_gmask, dim3(d.gm_blocks, B), dim3(BL_GM_THREADS), 0, s, d, logits, ld, rows, 1);
   if (need_pass2) {
     if (rows.delta)
-      hipLaunchKernelGGL(bl_k_exppass_spec, dim3(d.nb + 1, B), dim3(BL_RP_THREADS), 0, s, d, logits, ld, rows);
+      step_launch(bl_k_exppass_spec, g2, t1, s, ev ? ev + 2 : nullptr, d, logits, ld, rows);
     else
-      hipLaunchKernelGGL(bl_k_exppass, dim3(d.nb + 1, B), dim3(BL_RP_THREADS), 0, s, d, logits, ld, rows);
+      step_launch(bl_k_exppass, g2, t1, s, ev ? ev + 2 : nullptr, d, logits, ld, rows);
   }
-  if (ev) (void)hipEventRecord(ev[2], s);
-  hipLaunchKernelGGL(bl_k_select, dim3(B), dim3(BL_SEL_THREADS), 0, s, d, logits, ld, rows);
-  if (ev) (void)hipEventRecord(ev[3], s);
+  step_launch(bl_k_select, dim3(B), dim3(BL_SEL_THREADS), s, ev ? ev + 4 : nullptr, d, logits, ld, rows);
 }
 
 /* the allow-mask of one slot's current position, without a step (bl_grammar_mask); rows.slot[0] is

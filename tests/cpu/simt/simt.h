@@ -281,3 +281,6 @@ inline hipError_t hipEventElapsedTime(float *ms, hipEvent_t, hipEvent_t) {
 
 #define hipLaunchKernelGGL(kernel, grid, block, shmem, stream, ...) \
   simt::launch(dim3(grid), dim3(block), [&]() { kernel(__VA_ARGS__); })
+/* a launch with start and stop events: the emulator times nothing */
+#define hipExtLaunchKernelGGL(kernel, grid, block, shmem, stream, e0, e1, flags, ...) \
+  simt::launch(dim3(grid), dim3(block), [&]() { kernel(__VA_ARGS__); })
