@@ -31,6 +31,16 @@ def test_library_exports_every_declared_symbol():
     assert set(BL.EXPORTS) <= declared()
 
 
+def test_integration_extern_block_names_every_export():
+    """INTEGRATION.md's Rust `extern "C"` block declares every function of include/*.h, and nothing else."""
+    text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    start = text.index('extern "C" {')
+    block = text[start:text.index("\n}\n", start)]
+    named = set(re.findall(r"pub fn (bl_\w+)\s*\(", block))
+    assert declared() - named == set(), sorted(declared() - named)
+    assert named - declared() == set(), sorted(named - declared())
+
+
 def test_params_layout_matches_header():
     # bl_params is 28 4-byte fields in the header's order
     assert ctypes.sizeof(BL.Params) == 28 * 4
