@@ -228,7 +228,7 @@ static bool dev_layout(bl_dev &d, size_t S, size_t R, int vocab, Take take) {
   char *grec = nullptr, *brec = nullptr;
   const bool ok = take(d.slots, S) && take(d.rec, S * d.nb * BL_EB) && take(d.rcnt, S * d.nb) && take(d.ridx, S * V) &&
                   take(d.ring, S * BL_WCAP) && take(d.eog, 1024) && take(d.c_max, R * d.nc) && take(d.c_arg, R * d.nc) &&
-                  take(d.c_bsum, R * d.nc * BL_SUBS) && take(d.cand_v, R * d.nc * BL_KSEL_MAX) &&
+                  take(d.c_bsum, R * d.nc * BL_SUBS) && take(d.c_tns, R * d.nc * BL_TNS_W) && take(d.cand_v, R * d.nc * BL_KSEL_MAX) &&
                   take(d.cand_i, R * d.nc * BL_KSEL_MAX) && take(grec, R * 2 * G * 32) && take(d.full_v, R * d.nb * BL_EB) &&
                   take(d.full_i, R * d.nb * BL_EB) && take(d.full_cnt, R * d.nb) && take(d.full_s, R * d.nb) &&
                   take(d.sortk, R * 2 * V) && take(d.gsum, R * G) && take(d.crit, R * BL_CRIT_MAX) && take(d.ncrit, R) &&
@@ -431,8 +431,10 @@ static int configure(int V, const bl_params *p, bl_slot_dev &s) {
   if (mode & BL_M_TOPK) k = p->top_k;
   if ((mode & BL_M_LOGPROBS) && p->n_probs > k) k = p->n_probs;
   s.k_sel = k;
+  /* top-n-sigma filters the candidates of a sampled row (src/sampling.br:752-753); mirostat replaces that chain */
+  if (p->temperature > 0.0f && p->top_n_sigma > 0.0f && !(mode & BL_M_MIRO)) mode |= BL_M_TNS;
+  s.mode = mode;
   /* stages without a device path yet */
-  if (p->temperature > 0.0f && p->top_n_sigma > 0.0f) return fail(BL_EUNSUPPORTED, "top_n_sigma is not supported on the device");
   if (p->dry_multiplier != 0.0f && p->dry_base >= 1.0f && p->dry_penalty_last_n != 0)
     return fail(BL_EUNSUPPORTED, "DRY is not supported on the device");
   if (p->temperature > 0.0f && p->dynatemp_range > 0.0f && p->dynatemp_exponent != 1.0f)
@@ -726,6 +728,9 @@ static int status_error(int st) {
   if (st & BL_SE_UNSUPPORTED) return fail(BL_EUNSUPPORTED, "a sampler stage outside the device path was reached");
   if (st & BL_SE_TIE)
     return fail(BL_ETIE, "the draw landed on equal logits past the device's heap-order simulation");
+  if (st & BL_SE_SIGMA)
+    return fail(BL_ETIE, "top_n_sigma: the standard deviation lies within the reference's float64 rounding error of a "
+                         "float32 rounding boundary");
   if (st & BL_SE_CAND_FULL) return fail(BL_EDEVICE, "candidate buffer overflow");
   if (st & BL_SE_EMPTY) return fail(BL_EEMPTY, "sample_candidates: empty or mismatched candidates");
   if (st & BL_SE_GDEAD) return fail(BL_EGRAMMAR_DEAD, "the reply no longer matches the grammar");

@@ -130,6 +130,73 @@ BL_SD bool bl_group_critical(float ga, float gb, int E, double floor) {
          bl_binade_of(lb > floor ? lb : floor) != E || bl_binade_of((double)gb * hi) != E;
 }
 
+/* ---- top-n-sigma's statistics (src/sampling.br:376-400): sums of float32 values in float64 ---- */
+/* a + b = s + e exactly (Knuth's two-sum; no contraction, no reassociation) */
+BL_SD void bl_two_sum(double a, double b, double &s, double &e) {
+  s = a + b;
+  const double bb = s - a;
+  e = (a - (s - bb)) + (b - bb);
+}
+/* a double-double: hi + lo, |lo| <= half an ulp of hi */
+struct bl_dd {
+  double hi, lo;
+};
+BL_SD bl_dd bl_dd_add(bl_dd x, bl_dd y) {
+  double s, e, h, l;
+  bl_two_sum(x.hi, y.hi, s, e);
+  e += x.lo + y.lo;
+  bl_two_sum(s, e, h, l);
+  return bl_dd{h, l};
+}
+BL_SD bl_dd bl_dd_add_d(bl_dd x, double v) { return bl_dd_add(x, bl_dd{v, 0.0}); }
+
+/* [lo, hi] -> an interval that also holds every rounding of a value in it, and the rounding of this
+ * computation's own operations (4 ulps relative, plus the smallest normal) */
+BL_SD void bl_widen(double &lo, double &hi) {
+  const double u4 = 0x1p-51, tiny = 0x1p-1022;
+  lo = lo - (lo < 0.0 ? -lo : lo) * u4 - tiny;
+  hi = hi + (hi < 0.0 ? -hi : hi) * u4 + tiny;
+}
+
+/*
+ * The float32 sigma that top_n_sigma_logits computes (src/sampling.br:376-400) from the row's statistics:
+ * the count n of values above -1e29, the sums S of the values and Q of their squares (double-doubles, within
+ * 2^-100 relative of the exact sums) and bounds Es, Eq on the rounding error of the reference's sequential
+ * float64 sums (each addition errs by at most half an ulp of its partial sum). The reference's later float64
+ * operations (sum / n, mean * mean, sum_sq / n, their difference, the square root) each round once; the
+ * interval of their possible results is carried through them, and the square root goes to float32 by a
+ * monotone rounding. Returns 1 with that sigma, 0 when the reference's variance is not positive (no filter),
+ * and -1 when the interval holds zero or a float32 rounding boundary (undecided).
+ */
+BL_SD int bl_tns_sigma(double n, bl_dd S, bl_dd Q, double Es, double Eq, float &sigma) {
+  double s_lo = (S.hi + S.lo) - Es, s_hi = (S.hi + S.lo) + Es;
+  bl_widen(s_lo, s_hi);
+  double m_lo = s_lo / n, m_hi = s_hi / n;
+  bl_widen(m_lo, m_hi);
+  double mm_lo, mm_hi;
+  if (m_lo <= 0.0 && m_hi >= 0.0) {
+    mm_lo = 0.0;
+    mm_hi = (-m_lo > m_hi ? m_lo * m_lo : m_hi * m_hi);
+  } else {
+    const double a = m_lo < 0.0 ? -m_hi : m_lo, b = m_lo < 0.0 ? -m_lo : m_hi; /* 0 < a <= b */
+    mm_lo = a * a;
+    mm_hi = b * b;
+  }
+  bl_widen(mm_lo, mm_hi);
+  double q_lo = ((Q.hi + Q.lo) - Eq) / n, q_hi = ((Q.hi + Q.lo) + Eq) / n;
+  bl_widen(q_lo, q_hi);
+  double v_lo = q_lo - mm_hi, v_hi = q_hi - mm_lo;
+  bl_widen(v_lo, v_hi);
+  if (v_hi <= 0.0) return 0;
+  if (v_lo <= 0.0) return -1;
+  double r_lo = sqrt(v_lo), r_hi = sqrt(v_hi);
+  bl_widen(r_lo, r_hi);
+  const float f_lo = (float)r_lo, f_hi = (float)r_hi;
+  if (f_lo != f_hi) return -1;
+  sigma = f_lo;
+  return 1;
+}
+
 #if defined(__HIPCC__)
 /* ---- wave primitives (wavefront of 64) ---- */
 __device__ __forceinline__ bl_inc bl_shfl_up(bl_inc v, int k) {

@@ -40,6 +40,7 @@
 #define BL_RANK_MAX 1024    /* full-vocabulary candidate lists up to this size are sorted by counting */
 #define BL_NBUCKET 8192     /* value buckets of the sort of longer lists (more than BL_LDS_SORT) */
 #define BL_EOG_LDS 64       /* end-of-generation ids the selection keeps in LDS */
+#define BL_TNS_W 6          /* doubles of top-n-sigma statistics per chunk */
 
 /* record flags (bl_rec.wf above BL_WF_SHIFT) */
 #define BL_TF_BIAS 1u
@@ -54,6 +55,7 @@
 #define BL_M_GRAMMAR 16
 #define BL_M_PSP 32 /* logprobs as post-sampling probabilities (src/server.br:1015-1025) */
 #define BL_M_MIRO 64 /* the draw is mirostat v2's */
+#define BL_M_TNS 128 /* top-n-sigma filters the ranked candidates (src/sampling.br:376-407) */
 
 /* grammar mask kernel: tokens per workgroup */
 #define BL_GM_THREADS 256
@@ -71,6 +73,7 @@
 #define BL_SE_GDEAD 16
 #define BL_SE_GREJECT 32
 #define BL_SE_GAMBIG 64
+#define BL_SE_SIGMA 128 /* top-n-sigma's sigma undecided (at a float32 rounding boundary) */
 
 /* one modified token's server-stage inputs in one slot (src/server.br:940-944, src/sampling.br:65-107,
  * :175-188) */
@@ -136,6 +139,8 @@ struct bl_dev {
   float *c_max;     /* [rows][nc] */
   int32_t *c_arg;   /* [rows][nc] */
   float *c_bsum;    /* [rows][nc][BL_SUBS] approximate sums of exp(x - c_max) over each BL_EB positions */
+  double *c_tns;    /* [rows][nc][BL_TNS_W] top-n-sigma's chunk statistics: sum and sum of squares as
+                       double-doubles, sum of magnitudes, count */
   float *cand_v;    /* [rows][nc][KSEL_MAX] */
   int32_t *cand_i;
   void *grec;       /* [rows][2 * (V/64 + 64)] bl_grec: index-order records, then sorted-list records */

@@ -439,6 +439,53 @@ __device__ __forceinline__ void rowpass_body(const bl_dev &d, const float *__res
       d.c_max[o] = cm;
       d.c_arg[o] = ci == 0x7fffffff ? i0 : i0 + ci;
     }
+    if (sp.mode & BL_M_TNS) {
+      /* top-n-sigma's statistics over the chunk's values above -1e29 (src/sampling.br:383-393): the sums of
+       * x and x^2 (a float32 square is exact in float64) as double-doubles, the sum of |x| and the count */
+      bl_dd ts{0.0, 0.0}, tq{0.0, 0.0};
+      double ta = 0.0, tn = 0.0;
+#pragma unroll
+      for (int k = 0; k < 4 * NV; k++)
+        if (x[k] > -1.0e29f) {
+          const double v = (double)x[k];
+          ts = bl_dd_add_d(ts, v);
+          tq = bl_dd_add_d(tq, v * v);
+          ta += v < 0.0 ? -v : v;
+          tn += 1.0;
+        }
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) {
+        ts = bl_dd_add(ts, bl_dd{__shfl_xor(ts.hi, off, 64), __shfl_xor(ts.lo, off, 64)});
+        tq = bl_dd_add(tq, bl_dd{__shfl_xor(tq.hi, off, 64), __shfl_xor(tq.lo, off, 64)});
+        ta += __shfl_xor(ta, off, 64);
+        tn += __shfl_xor(tn, off, 64);
+      }
+      __shared__ double tns_w[BL_RP_THREADS / 64][BL_TNS_W];
+      if (lane == 0) {
+        tns_w[w][0] = ts.hi;
+        tns_w[w][1] = ts.lo;
+        tns_w[w][2] = tq.hi;
+        tns_w[w][3] = tq.lo;
+        tns_w[w][4] = ta;
+        tns_w[w][5] = tn;
+      }
+      __syncthreads();
+      if (t == 0) {
+        for (int q = 1; q < BL_RP_THREADS / 64; q++) {
+          ts = bl_dd_add(ts, bl_dd{tns_w[q][0], tns_w[q][1]});
+          tq = bl_dd_add(tq, bl_dd{tns_w[q][2], tns_w[q][3]});
+          ta += tns_w[q][4];
+          tn += tns_w[q][5];
+        }
+        double *out = d.c_tns + o * BL_TNS_W;
+        out[0] = ts.hi;
+        out[1] = ts.lo;
+        out[2] = tq.hi;
+        out[3] = tq.lo;
+        out[4] = ta;
+        out[5] = tn;
+      }
+    }
   }
 
   /* chunk top-K by (value desc, index asc) over values > -1e30 (src/sampling.br:280-296). Order keys
@@ -1233,6 +1280,8 @@ struct sel_shared {
   int mcnt;                            /* the merge's survivors */
   uint64_t etab[BL_EXP2_N];            /* expf's 2^(i/32) table (a global table read is a dependent load) */
   double ltab[32];                     /* logf's (1/c, log c) table */
+  float tns_thr;                       /* top-n-sigma's threshold */
+  int tns_st;                          /* its sigma undecided */
 };
 /* expf and logf through the selection's LDS copies of their tables */
 #define SEL_EXPF(x) bl_expf_tab((x), [&](uint32_t i_) { return sh.etab[i_]; })
@@ -2361,13 +2410,58 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
   float tokv = M;
   const bool gram = (mode & BL_M_GRAMMAR) != 0;
   const bool sampled = !gram && T > 0.0f;
+  /* top-n-sigma (src/sampling.br:376-407): the threshold max - n * sigma, by wavefront 0 from the row pass's
+   * chunk statistics; candidates below it leave the ranked list (the reference sets them to -1e30, which
+   * ranks them after every other value and gives them no weight) */
+  float tns_thr = BL_NEG_INF;
+  if (sampled && (mode & BL_M_TNS)) {
+    if (w == 0) {
+      bl_dd S{0.0, 0.0}, Q{0.0, 0.0};
+      double n = 0.0, es = 0.0, eq = 0.0, off_s = 0.0, off_q = 0.0;
+      for (int c0 = 0; c0 < nc; c0 += 64) {
+        const int c = c0 + lane;
+        double p[BL_TNS_W];
+#pragma unroll
+        for (int k = 0; k < BL_TNS_W; k++) p[k] = c < nc ? d.c_tns[((int64_t)row * nc + c) * BL_TNS_W + k] : 0.0;
+        const double cs = p[0] + p[1], cq = p[2] + p[3];
+        /* the reference's additions over chunk c err by at most half an ulp of each partial sum, and a partial
+         * sum there is at most |the earlier chunks' sum| + the chunk's sum of magnitudes (approximate prefixes:
+         * only the bound reads them) */
+        const double ps = off_s + bl_wave_excl_scan_d(cs, lane), pq = off_q + bl_wave_excl_scan_d(cq, lane);
+        es += bl_wave_sum_d(p[5] * ((ps < 0.0 ? -ps : ps) + p[4]));
+        eq += bl_wave_sum_d(p[5] * (pq + cq));
+        off_s += bl_wave_sum_d(cs);
+        off_q += bl_wave_sum_d(cq);
+        bl_dd sd{p[0], p[1]}, qd{p[2], p[3]};
+        double nn = p[5];
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+          sd = bl_dd_add(sd, bl_dd{__shfl_xor(sd.hi, off, 64), __shfl_xor(sd.lo, off, 64)});
+          qd = bl_dd_add(qd, bl_dd{__shfl_xor(qd.hi, off, 64), __shfl_xor(qd.lo, off, 64)});
+          nn += __shfl_xor(nn, off, 64);
+        }
+        S = bl_dd_add(S, sd);
+        Q = bl_dd_add(Q, qd);
+        n += nn;
+      }
+      float sigma = 0.0f;
+      const int r = n > 1.0 ? bl_tns_sigma(n, S, Q, es * 0x1p-53 * 1.001, eq * 0x1p-53 * 1.001, sigma) : 0;
+      if (lane == 0) {
+        sh.tns_thr = r == 1 ? M - sp.top_n_sigma * sigma : BL_NEG_INF;
+        sh.tns_st = r < 0 ? 1 : 0;
+      }
+    }
+    __syncthreads();
+    tns_thr = sh.tns_thr;
+    if (sh.tns_st) status |= BL_SE_SIGMA;
+  }
   /* the ranked candidate list of a sampled row */
   uint64_t *keys = sh.c.keys;
   int64_t n_list = 0, n_logical = 0;
   if (sampled && (mode & BL_M_TOPK)) {
     /* top_k_select list: kk = min(top_k, V) <= K entries, unfilled slots are (-1e30, 0) */
     const int kk = sp.top_k < V ? sp.top_k : V;
-    if (t < kk) keys[t] = mk;
+    if (t < kk) keys[t] = (mk && ckey_v(mk) >= tns_thr) ? mk : 0ull; /* top-n-sigma: unfilled past its threshold */
     n_list = n_logical = kk;
   } else if (sampled) {
     /* full-vocabulary rank (src/sampling.br:301-365): the exponent blocks' candidates (block b's at
@@ -2417,27 +2511,40 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
       }
     };
     int nl = nf;
+    /* top-n-sigma's survivors (key 0 for the others, which rank last) */
+    auto tns_key = [&](float v, int32_t id) { return v >= tns_thr ? ckey(v, id) : 0ull; };
+    auto tns_count = [&]() {
+      int c = 0;
+      for (int i = t; i < nf; i += BL_SEL_THREADS) c += sh.c.tmp[i] != 0ull ? 1 : 0;
+      return (int)block_sum_d<BL_SEL_THREADS>((double)c, sh.c.gsum);
+    };
     if (nf <= BL_RANK_MAX) {
-      each_cand([&](int i, float v, int32_t id) { sh.c.tmp[i] = ckey(v, id); });
+      each_cand([&](int i, float v, int32_t id) { sh.c.tmp[i] = tns_key(v, id); });
       __syncthreads();
+      if (mode & BL_M_TNS) nl = tns_count();
       /* rank by counting (keys are distinct: they carry the index) */
       for (int i = t; i < nf; i += BL_SEL_THREADS) {
         const uint64_t k = sh.c.tmp[i];
-        keys[count_gt(sh.c.tmp, nf, k)] = k;
+        if (k) keys[count_gt(sh.c.tmp, nf, k)] = k;
       }
     } else if (nf <= BL_LDS_SORT) {
       int P = 1;
       while (P < nf) P <<= 1;
       for (int i = nf + t; i < P; i += BL_SEL_THREADS) keys[i] = 0ull;
-      each_cand([&](int i, float v, int32_t id) { keys[i] = ckey(v, id); });
+      each_cand([&](int i, float v, int32_t id) { keys[i] = tns_key(v, id); });
       __syncthreads();
+      if (mode & BL_M_TNS) {
+        int c = 0;
+        for (int i = t; i < nf; i += BL_SEL_THREADS) c += keys[i] != 0ull ? 1 : 0;
+        nl = (int)block_sum_d<BL_SEL_THREADS>((double)c, sh.c.gsum);
+      }
       bitonic_desc(keys, P);
     } else {
       /* a large list: the candidates the draw can still see (below), bucketed by value (larger values in
        * lower buckets, equal values in one bucket), scattered by bucket, then ranked by counting within
        * each bucket, one LDS tile of the bucketed list at a time */
       const float T = sp.temperature;
-      float thr = M - bl_cand_span(sp); /* the exponent pass's candidates */
+      float thr = fmaxf(M - bl_cand_span(sp), tns_thr); /* the exponent pass's candidates, top-n-sigma's survivors */
       if (!filt) {
         /* the draw adds exp((v - M) / T) in descending order. With u = 2^-24 and m <= V terms, the float
          * running sum past every term >= 2^(k-24) is at least (1 - g) (S - V 2^(k-24)), g = m u / (1 - m u)

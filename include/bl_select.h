@@ -31,13 +31,15 @@ enum {
   BL_EGRAMMAR_DEAD = -5,   /* "the reply no longer matches the grammar" (src/server.br:320) */
   BL_EGRAMMAR_REJECT = -6, /* "the grammar rejected every vocabulary token" (src/server.br:361) */
   BL_EGRAMMAR_AMBIG = -7,  /* "grammar is left-recursive or too ambiguous to match" (src/grammar.br:354) */
-  BL_EUNSUPPORTED = -8,    /* a sampler stage this library does not run on the device yet: top_n_sigma,
-                              DRY, a dynatemp exponent other than 1 (rejected by bl_slot_reset); XTC, mirostat
+  BL_EUNSUPPORTED = -8,    /* a sampler stage this library does not run on the device yet: DRY, a dynatemp
+                              exponent other than 1, mirostat v1 (rejected by bl_slot_reset); XTC, mirostat
                               or a grammar on speculative rows, or more than 32 drafts with history-dependent
                               penalties; typical_p over a full-vocabulary list above 512 candidates */
   BL_ETIE = -9,            /* a draw on equal logits whose heap order is past the device simulation (more than
-                              8192 values at or above the tied one), equal allowed maxima of a grammar row, or
-                              post-sampling alternatives of a full-vocabulary rank that meet equal values */
+                              8192 values at or above the tied one), equal allowed maxima of a grammar row,
+                              post-sampling alternatives of a full-vocabulary rank that meet equal values, or a
+                              top_n_sigma whose float32 sigma the reference's float64 rounding error leaves
+                              undecided (the sigma within ~1e-11 relative of a float32 rounding boundary) */
   BL_ESCHEMA = -10         /* a JSON schema that does not parse (src/json.br json_parse messages) or that
                               json_schema_to_gbnf rejects (src/schema_grammar.br messages) */
 };
@@ -48,7 +50,8 @@ typedef struct {
   float temperature;       /* <= 0: greedy */
   float dynatemp_range;
   float dynatemp_exponent;
-  float top_n_sigma;       /* <= 0: off */
+  float top_n_sigma;       /* <= 0: off; with temperature > 0, keep values >= max - n * sigma (population sigma
+                              of the values above -1e29, src/sampling.br:376-407) */
   int32_t top_k;           /* <= 0 or >= vocab: full-vocabulary rank */
   float typical_p;
   float top_p;

@@ -104,6 +104,11 @@ void orc_finish_logits(const float *logits, int64_t n, float logit_mul, float ca
   Row r = finish_logits(Row(logits, logits + n), logit_mul, cap);
   memcpy(out, r.data(), n * sizeof(float));
 }
+/* top_n_sigma_logits' threshold (1) or 0 when the row is kept whole */
+int orc_top_n_sigma_threshold(const float *logits, int64_t n, float sig, float *threshold) {
+  return top_n_sigma_threshold(Row(logits, logits + n), n, sig, *threshold) ? 1 : 0;
+}
+
 void orc_top_n_sigma(const float *logits, int64_t n, float sig, float *out) {
   Row r = top_n_sigma_logits(Row(logits, logits + n), n, sig);
   memcpy(out, r.data(), n * sizeof(float));

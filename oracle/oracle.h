@@ -96,6 +96,7 @@ float token_logprob(const Row &logits, int64_t vocab, int32_t token);
 void top_k_select(const Row &logits, int64_t vocab, int64_t k, Row &top_val, Ids &top_idx);
 void all_candidates_sorted(const Row &logits, int64_t vocab, Row &values, Ids &ids);
 void rank_candidates(const Row &logits, int64_t vocab, int64_t top_k, Row &values, Ids &ids);
+bool top_n_sigma_threshold(const Row &logits, int64_t vocab, float n, float &threshold);
 Row top_n_sigma_logits(const Row &logits, int64_t vocab, float n);
 void typical_filter(const Row &probs, const Row &logits, const Ids &ids, float typical_p, int64_t min_keep,
                     Row &kept_probs, Row &kept_logits, Ids &kept_ids);

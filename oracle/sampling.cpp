@@ -321,9 +321,9 @@ void rank_candidates(const Row &logits, int64_t vocab, int64_t top_k, Row &value
   else all_candidates_sorted(logits, vocab, values, ids);
 }
 
-/* :376-407 (statistics in float64) */
-Row top_n_sigma_logits(const Row &logits, int64_t vocab, float n) {
-  if (n <= 0.0f || vocab <= 1) return logits;
+/* :376-407 (statistics in float64); the threshold maximum - n * sigma, or false when the row is kept whole */
+bool top_n_sigma_threshold(const Row &logits, int64_t vocab, float n, float &threshold) {
+  if (n <= 0.0f || vocab <= 1) return false;
   float maximum = -1.0e30f;
   double sum = 0.0, sum_sq = 0.0;
   int64_t count = 0;
@@ -331,21 +331,31 @@ Row top_n_sigma_logits(const Row &logits, int64_t vocab, float n) {
     float value = logits[i];
     if (value > -1.0e29f) {
       if (value > maximum) maximum = value;
+#if ORC_MUTANT == 5 /* planted mistake (tests only): the value sum in float32 */
+      sum = (double)((float)sum + value);
+#else
       sum += (double)value;
+#endif
       double vd = (double)value;
       double sq = vd * vd;
       sum_sq += sq;
       count += 1;
     }
   }
-  if (count <= 1) return logits;
+  if (count <= 1) return false;
   double mean = sum / (double)count;
   double msq = mean * mean;
   double variance = sum_sq / (double)count - msq;
-  if (variance <= 0.0) return logits;
+  if (variance <= 0.0) return false;
   float sigma = (float)sqrt(variance);
   float ns = n * sigma;
-  float threshold = maximum - ns;
+  threshold = maximum - ns;
+  return true;
+}
+
+Row top_n_sigma_logits(const Row &logits, int64_t vocab, float n) {
+  float threshold;
+  if (!top_n_sigma_threshold(logits, vocab, n, threshold)) return logits;
   Row filtered(vocab, -1.0e30f);
   for (int64_t i = 0; i < vocab; i++)
     if (logits[i] >= threshold) filtered[i] = logits[i];

@@ -33,6 +33,10 @@ CASES = [
     dict(temperature=0.9, top_k=50, typical_p=0.6, logprobs=1, n_probs=5, post_sampling_probs=1),
     dict(temperature=1.1, top_k=120, typical_p=0.9, min_keep=4, top_p=0.95, min_p=0.02, xtc_probability=0.4,
          xtc_threshold=0.1, dynatemp_range=0.3),
+    # top-n-sigma (src/sampling.br:376-407) before a full-vocabulary rank and before top-k
+    dict(temperature=0.9, top_k=0, top_n_sigma=1.5, logprobs=1, n_probs=4),
+    dict(temperature=1.0, top_k=40, top_n_sigma=0.8, top_p=0.9, repeat_penalty=1.2, repeat_last_n=16),
+    dict(temperature=1.2, top_k=0, top_n_sigma=3.0, min_p=0.02, frequency_penalty=0.3, presence_penalty=0.2),
 ]
 SMALL_V = 5003
 EOS, EOGS = 7, [11, 13]

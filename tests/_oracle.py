@@ -80,6 +80,7 @@ def _configure(L):
         L.orc_top_k_select.argtypes = [f32p, i64, i64, f32p, i32p]
         L.orc_all_candidates_sorted.argtypes = [f32p, i64, f32p, i32p]
         L.orc_top_n_sigma.argtypes = [f32p, i64, C.c_float, f32p]
+        L.orc_top_n_sigma_threshold.argtypes = [f32p, i64, C.c_float, f32p]
         L.orc_sample_candidates.restype = C.c_int32
         L.orc_sample_candidates.argtypes = [u64p, f32p, i32p, i64, C.c_float, C.c_float, C.c_float, C.c_float,
                                             C.c_float, C.c_float, C.c_float, C.c_float, i64, f32p, i32p, i64,

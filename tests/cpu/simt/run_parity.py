@@ -222,6 +222,52 @@ def run_unfiltered(BL, steps, rows=None):
     return None
 
 
+TNS_ROWS = [dict(temperature=0.8, top_k=0, top_n_sigma=1.0),
+            dict(temperature=1.0, top_k=64, top_n_sigma=0.5, logprobs=1, n_probs=5),
+            dict(temperature=0.7, top_k=0, top_n_sigma=2.0, top_p=0.9),
+            dict(temperature=1.2, top_k=0, top_n_sigma=1.5, min_p=0.01)]
+
+
+def run_tns(BL, steps):
+    """Top-n-sigma rows at V=151936 on N(0, 4^2) logits with 300 bumped ids (the sigma from the row pass's
+    double-double statistics against the reference's sequential float64 sums): each step's token and the
+    logprob against the oracle's slot step. A row whose sigma is undecided reports BL_ETIE, and then the
+    oracle's sigma must lie at a float32 rounding boundary of the device's interval (never seen so far)."""
+    V = 151936
+    R = len(TNS_ROWS)
+    rng = np.random.default_rng(31)
+    ctx = BL.Context(V, R, R)
+    L = O.lib()
+    hs = []
+    for r, kw in enumerate(TNS_ROWS):
+        ctx.slot_reset(r, BL.Params(**kw), BL.seed_rng(700 + r))
+        op = O.params(**kw)
+        hs.append(L.orc_slot_new(O.C.byref(op), BL.seed_rng(700 + r), None, 0, None, 0, None, None, 0))
+    buf = MEM.zeros(R * V, np.float32)
+    try:
+        for t in range(steps):
+            x = (rng.standard_normal(R * V) * 4.0).astype(np.float32)
+            x[rng.integers(0, R * V, 300)] += 12.0
+            buf.upload(x)
+            tok, lp = ctx.sample_step(list(range(R)), buf.ptr, V, top_stride=5)[:2]
+            for r in range(R):
+                ot, olp = np.zeros(1, np.int32), np.zeros(1, np.float32)
+                oti, otl = np.zeros(5, np.int32), np.zeros(5, np.float32)
+                eog = O.C.c_int()
+                row = np.ascontiguousarray(x[r * V:(r + 1) * V])
+                assert L.orc_slot_step(hs[r], O.fp(row), V, 5, 1, O.ip(ot), O.fp(olp), O.ip(oti), O.fp(otl),
+                                       O.C.byref(eog)) == 0
+                if tok[r] != ot[0]:
+                    return f"step {t} row {r} {TNS_ROWS[r]}: token {tok[r]} vs {ot[0]}"
+                if TNS_ROWS[r].get("logprobs") and not lp_close(lp[r], olp[0]):
+                    return f"step {t} row {r}: logprob {lp[r]} vs {olp[0]}"
+    finally:
+        for h in hs:
+            L.orc_slot_free(h)
+        ctx.close()
+    return None
+
+
 MIRO_ROWS = [(1.0, 5.0, 0.1), (0.7, 3.0, 0.5), (1.5, 8.0, 0.2)]
 
 
@@ -745,6 +791,8 @@ def main():
             results.append((f"rows {f[1]} + {f[2]}", run_pair(BL, int(f[1]), int(f[2]), int(f[3]) if len(f) > 3 else 10)))
         elif kind == "bigties":
             results.append(("bf16 ties at V=151936", run_bigties(BL, int(f[1]))))
+        elif kind == "tns":
+            results.append(("top-n-sigma rows at V=151936", run_tns(BL, int(f[1]))))
         elif kind == "miro":
             results.append(("mirostat v2 rows", run_mirostat(BL, int(f[1]))))
         elif kind == "unfilt":

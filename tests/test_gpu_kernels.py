@@ -30,6 +30,12 @@ def device_memory():
     RP.MEM = old
 
 
+def test_top_n_sigma_full_size():
+    print("top-n-sigma rows, V=151936: 20 steps", flush=True)
+    err = RP.run_tns(BL, 20)
+    assert err is None, err
+
+
 def test_large_top_k_and_alternatives():
     print("top_k 250, n_probs 256, V=151936: 20 steps", flush=True)
     err = RP.run_bigk(BL, 20)

@@ -8,8 +8,12 @@ that each check fails against an oracle with a planted mistake (oracle/Makefile 
   the rank-order sums of sample_candidates_with_probs (src/sampling.br:506-598): sum_exp, the top-p running
       probability, the min-p cut, the tempered sum and the draw's running sum, the same way, with the RNG
       draw from the xorshift closed form.
+  top_n_sigma_logits (src/sampling.br:376-407): the count, sum and sum of squares of the values above -1e29
+      as sequential float64 sums (np.cumsum over float64), then mean, variance, the square root rounded to
+      float32 and the threshold max - n * sigma in float32.
 The planted mistakes: ties sent to the right child in the sift (1), a pairwise normaliser sum (2), the
-softmax sum in reverse rank order (3), the tempered sum as two halves (4).
+softmax sum in reverse rank order (3), the tempered sum as two halves (4), top-n-sigma's value sum in
+float32 (5).
 """
 import ctypes
 from fractions import Fraction
@@ -209,3 +213,53 @@ def test_rank_order_sums_are_sequential_glibc_sums():
 @pytest.mark.parametrize("k", [3, 4])
 def test_rank_order_check_fails_on_planted_mistake(k):
     assert trace_mismatches(O.mutant(k), ranked_cases()) > 0
+
+
+# ---------------------------------------------------------------- top-n-sigma statistics
+
+def tns_rows():
+    rng = np.random.default_rng(41)
+    rows = []
+    for k in range(60):
+        n = int(rng.integers(2, 3000)) if k % 3 else 151936
+        x = (rng.standard_normal(n) * float(rng.uniform(0.5, 8.0)) + float(rng.uniform(-3, 3))).astype(F)
+        x[rng.integers(0, n, max(1, n // 500))] = F(-1e30)  # excluded from the statistics
+        rows.append((x, float(rng.choice([0.5, 1.0, 1.7, 3.0]))))
+    return rows
+
+
+def tns_threshold(x, n):
+    """max - n * sigma, or None when the row is kept whole"""
+    v = x[x > F(-1e29)].astype(np.float64)
+    cnt = len(v)
+    if n <= 0.0 or cnt <= 1:
+        return None
+    s = np.cumsum(v)[-1]
+    q = np.cumsum(v * v)[-1]
+    mean = s / cnt
+    var = q / cnt - mean * mean
+    if var <= 0.0:
+        return None
+    sigma = F(np.sqrt(var))
+    return F(x[x > F(-1e29)].max() - F(F(n) * sigma))
+
+
+def tns_mismatches(L, rows):
+    bad = 0
+    for x, n in rows:
+        want = tns_threshold(x, n)
+        thr = ctypes.c_float()
+        kept = L.orc_top_n_sigma_threshold(O.fp(x), len(x), n, ctypes.byref(thr))
+        bad += (want is None) != (kept == 0) or (want is not None and thr.value != want)
+        o = np.zeros_like(x)
+        L.orc_top_n_sigma(O.fp(x), len(x), n, O.fp(o))
+        bad += not np.array_equal(o, x if want is None else np.where(x >= want, x, F(-1e30)).astype(F))
+    return bad
+
+
+def test_top_n_sigma_is_the_sequential_float64_statistics():
+    assert tns_mismatches(O.lib(), tns_rows()) == 0
+
+
+def test_top_n_sigma_check_fails_on_planted_mistake():
+    assert tns_mismatches(O.mutant(5), tns_rows()) > 0

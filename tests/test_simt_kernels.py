@@ -103,6 +103,14 @@ def test_grammar_masks_and_tokens(simt_lib):
     assert out.count("ok   grammar case") == 7
 
 
+def test_top_n_sigma(simt_lib):
+    """Top-n-sigma rows (src/sampling.br:376-407): small cases 21-23 (full-vocabulary and top-k ranks) and
+    full-size rows at V=151936, the sigma from the row pass's statistics against the oracle's sequential
+    float64 sums."""
+    out = _run(simt_lib, ["small:21-23:12", "tns:2"], {"SIMT_ORDER": "rand"})
+    assert out.count("ok   small case") == 3 and "ok   top-n-sigma rows at V=151936" in out
+
+
 def test_allocation_free_step(simt_lib):
     """bl_sample_rows_noalloc (slot state and workspace carved from its fixed array), twice in a row with
     the second call smaller, equals bl_sample_step over fresh slots with the same parameters and RNG states:
