@@ -227,7 +227,7 @@ static bool dev_layout(bl_dev &d, size_t S, size_t R, int vocab, Take take) {
   d.n_eog = 0;
   char *grec = nullptr, *brec = nullptr;
   const bool ok = take(d.slots, S) && take(d.rec, S * d.nb * BL_EB) && take(d.rcnt, S * d.nb) && take(d.ridx, S * V) &&
-                  take(d.ring, S * BL_WCAP) && take(d.eog, 1024) && take(d.c_max, R * d.nc) && take(d.c_arg, R * d.nc) &&
+                  take(d.ring, S * BL_WCAP) && take(d.eog, 1024) && take(d.eff, R * V) && take(d.c_max, R * d.nc) && take(d.c_arg, R * d.nc) &&
                   take(d.c_bsum, R * d.nc * BL_SUBS) && take(d.c_tns, R * d.nc * BL_TNS_W) && take(d.cand_v, R * d.nc * BL_KSEL_MAX) &&
                   take(d.cand_i, R * d.nc * BL_KSEL_MAX) && take(grec, R * 2 * G * 32) && take(d.full_v, R * d.nb * BL_EB) &&
                   take(d.full_i, R * d.nb * BL_EB) && take(d.full_cnt, R * d.nb) && take(d.full_s, R * d.nb) &&

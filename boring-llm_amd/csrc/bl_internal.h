@@ -136,6 +136,7 @@ struct bl_dev {
   int32_t *eog;      /* [n_eog] end-of-generation ids */
   int32_t n_eog;
   /* workspace for up to max_rows rows */
+  float *eff;       /* [rows][V] the values after the model tail and the server stages, rows with a tail only */
   float *c_max;     /* [rows][nc] */
   int32_t *c_arg;   /* [rows][nc] */
   float *c_bsum;    /* [rows][nc][BL_SUBS] approximate sums of exp(x - c_max) over each BL_EB positions */
@@ -197,6 +198,11 @@ struct bl_rows {
 #if defined(__HIPCC__)
 __device__ __forceinline__ int bl_row_slot(const bl_rows &r, int row) {
   return row < BL_ROWS_INLINE ? (int)r.slot_inline[row] : r.slot[row];
+}
+
+/* the model tail (src/model.br:973-984) changes the row: logit_mul != 1 or a final soft-cap */
+__device__ __forceinline__ bool bl_tail_on(const bl_slot_dev &sp) {
+  return sp.logit_mul != 1.0f || sp.final_softcap > 0.0f;
 }
 
 /* XTC runs (src/sampling.br:552-572): it draws its chance whenever the candidates reach two */

@@ -391,6 +391,19 @@ __device__ __forceinline__ void rowpass_body(const bl_dev &d, const float *__res
       x[4 * j + 2] = v.z;
       x[4 * j + 3] = v.w;
     }
+    /* a row with a model tail leaves its values for the exponent pass */
+    if (bl_tail_on(sp)) {
+      float *dst = d.eff + (int64_t)row * V + i0;
+      if (cnt == BL_CH && (((uintptr_t)dst) & 15) == 0) {
+#pragma unroll
+        for (int j = 0; j < NV; j++)
+          reinterpret_cast<float4 *>(dst)[j * BL_RP_THREADS + t] = make_float4(x[4 * j], x[4 * j + 1], x[4 * j + 2], x[4 * j + 3]);
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4 * NV; k++)
+          if (pos_of(k) < cnt) dst[pos_of(k)] = x[k];
+      }
+    }
   }
   /* max and first argmax; then, for logprob rows, approximate sums of exp(x - chunk max) over each BL_EB
    * positions, from which the exponent pass predicts the binades of the normaliser's running sum
@@ -692,12 +705,15 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass_spec(bl_dev d, con
  * The critical list is appended with one device-scope atomic per critical group (a few per row); no
  * workgroup waits for another: the selection kernel, a later launch, reads the list.
  */
-#define BL_MU_MAX 512 /* the exponent pass's merge: first keys of the chunk lists held in LDS */
-#define BL_MSURV 1024 /* the exponent pass's merge: survivors of the cut held in LDS */
+#define BL_MU_MAX 256 /* the exponent pass's merge: first keys of the chunk lists held in LDS */
+#define BL_MSURV 512  /* the exponent pass's merge: survivors of the cut held in LDS */
+/* the exponent pass's LDS shared by its two roles: a block's values, or the merge's keys */
+#define BL_K2_LDS_U64 (BL_MU_MAX + BL_MSURV)
+static_assert(BL_K2_LDS_U64 * 8 >= BL_EB * 4, "a block's values fit the shared area");
 #define BL_MREG 8     /* the exponent pass's merge: list entries per thread loaded at once */
 
 /*
- * The exponent pass's last workgroup of each row, beside the row's exponent blocks: the row maximum and its
+ * The exponent pass's first workgroup of each row, beside the row's exponent blocks: the row maximum and its
  * first index (d.rmax, d.rarg) from the chunk statistics, and the row's top K keys in (value desc, index asc)
  * order (top_k_select, src/sampling.br:280-296) merged from the row pass's chunk lists into
  * d.mkeys[row][0..K) (0 past the valid keys). The cut is the selection's merge's: the K-th largest of the
@@ -707,10 +723,9 @@ __global__ __launch_bounds__(BL_RP_THREADS) void bl_k_rowpass_spec(bl_dev d, con
  * lists itself.
  */
 template <int NT>
-__device__ __forceinline__ void exp_merge_role(const bl_dev &d, const bl_rows &rows, int row) {
+__device__ __forceinline__ void exp_merge_role(const bl_dev &d, const bl_rows &rows, int row, uint64_t *lds) {
   const int t = threadIdx.x, lane = t & 63, nc = d.nc;
-  __shared__ uint64_t m_u[BL_MU_MAX];
-  __shared__ uint64_t m_sv[BL_MSURV];
+  uint64_t *const m_u = lds, *const m_sv = lds + BL_MU_MAX;
   __shared__ uint64_t m_tau;
   __shared__ int m_n;
   const int K = d.slots[bl_row_slot(rows, row)].k_sel;
@@ -774,7 +789,16 @@ __device__ __forceinline__ void exp_merge_role(const bl_dev &d, const bl_rows &r
   };
 #pragma unroll
   for (int u = 0; u < PU; u++) keep(kr[u]);
-  for (int i = PU * NT + t; i < total; i += NT) keep(gkey(i / K, i - (i / K) * K));
+  for (int i0 = PU * NT; i0 < total; i0 += PU * NT) { /* longer lists: the next PU keys per thread at once */
+#pragma unroll
+    for (int u = 0; u < PU; u++) {
+      const int i = i0 + t + u * NT;
+      const int c = i / K;
+      kr[u] = i < total ? gkey(c, i - c * K) : 0ull;
+    }
+#pragma unroll
+    for (int u = 0; u < PU; u++) keep(kr[u]);
+  }
   __syncthreads();
   const int C = m_n;
   if (C > BL_MSURV) {
@@ -796,9 +820,11 @@ __device__ __forceinline__ void exppass_body(const bl_dev &d, const float *__res
                                              const bl_rows &rows) {
   const int V = d.vocab, nc = d.nc;
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-  const int b = blockIdx.x, row = blockIdx.y;
-  if (b == d.nb) {
-    exp_merge_role<BL_RP_THREADS>(d, rows, row);
+  /* workgroup 0 of each row merges (dispatched first: it takes longer than a block), 1 + b computes block b */
+  const int b = (int)blockIdx.x - 1, row = blockIdx.y;
+  __shared__ uint64_t k2_lds[BL_K2_LDS_U64];
+  if (b < 0) {
+    exp_merge_role<BL_RP_THREADS>(d, rows, row, k2_lds);
     return;
   }
   const int slot = bl_row_slot(rows, row);
@@ -806,7 +832,7 @@ __device__ __forceinline__ void exppass_body(const bl_dev &d, const float *__res
   const int mode = sp.mode;
   if (!(mode & (BL_M_LOGPROBS | BL_M_FULL))) return;
   __shared__ uint64_t s_tab[BL_EXP2_N]; /* expf's 2^(i/32) table */
-  __shared__ float vals[BL_EB];
+  float *const vals = reinterpret_cast<float *>(k2_lds); /* [BL_EB] */
   __shared__ uint32_t st_sup[BL_EB / 32], st_done[SPEC ? BL_EB / 32 : 1];
   __shared__ double wtot[BL_RP_THREADS / 64];
   __shared__ uint32_t bs_crit[BL_RP_THREADS / 64];
@@ -819,7 +845,10 @@ __device__ __forceinline__ void exppass_body(const bl_dev &d, const float *__res
   const int cnt = min(BL_EB, V - i0);
   const int j0 = 4 * t;
   float x[4];
-  const float *src = logits + (int64_t)row * ld + i0 + j0;
+  /* a row with a model tail reads the values the row pass left (the tail's tanhf is not worth computing twice);
+   * the others re-read their logits and apply the sparse stages again */
+  const bool from_eff = bl_tail_on(sp);
+  const float *src = from_eff ? d.eff + (int64_t)row * V + i0 + j0 : logits + (int64_t)row * ld + i0 + j0;
   if (j0 + 4 <= cnt && (((uintptr_t)src) & 15) == 0) {
     const float4 v = *reinterpret_cast<const float4 *>(src);
     x[0] = v.x;
@@ -843,9 +872,9 @@ __device__ __forceinline__ void exppass_body(const bl_dev &d, const float *__res
   }
   for (int k = lane + 64; k < nc; k += 64) argmax_merge(M, Mi, d.c_max[(int64_t)row * nc + k], d.c_arg[(int64_t)row * nc + k]);
   /* model tail and server stages, as the row pass applied them */
-  *reinterpret_cast<float4 *>(vals + j0) = make_float4(x[0], x[1], x[2], x[3]);
-  apply_stages<SPEC>(d, sp, rows, row, slot, i0, cnt, vals, st_sup, st_done);
-  {
+  if (!from_eff) {
+    *reinterpret_cast<float4 *>(vals + j0) = make_float4(x[0], x[1], x[2], x[3]);
+    apply_stages<SPEC>(d, sp, rows, row, slot, i0, cnt, vals, st_sup, st_done);
     const float4 v = *reinterpret_cast<const float4 *>(vals + j0);
     x[0] = v.x;
     x[1] = v.y;

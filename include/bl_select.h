@@ -169,7 +169,7 @@ int bl_sample_step_async(bl_ctx *ctx, int B, const float *d_logits, int64_t ld, 
  * end-of-generation ids; rng_states (host) are advanced in place and the outputs are bl_sample_step's. The
  * slot state and step workspace live in one fixed device array of BL_NOALLOC_BYTES, which each device that
  * runs the call holds until the process ends; no device memory is allocated or freed. Limits: B up to
- * BL_NOALLOC_ROWS, and the workspace (about 44 bytes per row and vocabulary entry, e.g. B = 8 at V = 151936)
+ * BL_NOALLOC_ROWS, and the workspace (about 48.5 bytes per row and vocabulary entry, e.g. B = 8 at V = 151936)
  * within the array, else BL_EPARAM. Work is ordered on `stream` (a hipStream_t; NULL: the null stream) and
  * the call returns when results are in host memory. Calls that overlap on one device (threads or streams)
  * race on the array. */
