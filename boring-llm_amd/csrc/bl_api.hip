@@ -420,16 +420,17 @@ static int configure(int V, const bl_params *p, bl_slot_dev &s) {
     return fail(BL_EPARAM, "`mirostat` must be 0, 1, or 2 with non-negative tau and eta");
   if (p->mirostat != 0 && p->post_sampling_probs && p->logprobs)
     return fail(BL_EPARAM, "post_sampling_probs require the standard unconstrained sampling chain");
-  if (p->mirostat == 1) return fail(BL_EUNSUPPORTED, "mirostat v1 is not supported on the device");
   s.mirostat = p->mirostat;
   s.mirostat_tau = p->mirostat_tau;
   s.mirostat_eta = p->mirostat_eta;
   s.mu = 2.0f * p->mirostat_tau;
-  if (p->mirostat == 2 && p->temperature > 0.0f) mode = (mode & ~(BL_M_TOPK | BL_M_FULL)) | BL_M_FULL | BL_M_MIRO;
+  if (p->mirostat != 0 && p->temperature > 0.0f) mode = (mode & ~(BL_M_TOPK | BL_M_FULL)) | BL_M_FULL | BL_M_MIRO;
   s.mode = mode;
   int k = 0;
   if (mode & BL_M_TOPK) k = p->top_k;
   if ((mode & BL_M_LOGPROBS) && p->n_probs > k) k = p->n_probs;
+  /* mirostat v1 fits the first min(V, 100) ranked probabilities: the merged top-K list supplies them */
+  if ((mode & BL_M_MIRO) && p->mirostat == 1 && k < (V < 100 ? V : 100)) k = V < 100 ? V : 100;
   s.k_sel = k;
   /* top-n-sigma filters the candidates of a sampled row (src/sampling.br:752-753); mirostat replaces that chain */
   if (p->temperature > 0.0f && p->top_n_sigma > 0.0f && !(mode & BL_M_MIRO)) mode |= BL_M_TNS;
@@ -437,8 +438,6 @@ static int configure(int V, const bl_params *p, bl_slot_dev &s) {
   /* stages without a device path yet */
   if (p->dry_multiplier != 0.0f && p->dry_base >= 1.0f && p->dry_penalty_last_n != 0)
     return fail(BL_EUNSUPPORTED, "DRY is not supported on the device");
-  if (p->temperature > 0.0f && p->dynatemp_range > 0.0f && p->dynatemp_exponent != 1.0f)
-    return fail(BL_EUNSUPPORTED, "dynamic temperature with an exponent other than 1 is not supported on the device");
   if (k > BL_KSEL_MAX)
     return fail(BL_EUNSUPPORTED, "top_k/n_probs of %d exceeds the device selection limit", k);
   if (p->repeat_last_n > BL_WCAP) return fail(BL_EUNSUPPORTED, "repeat_last_n above %d", BL_WCAP);
@@ -1129,7 +1128,7 @@ int bl_workload_drafts(int64_t seed, int64_t step, int seq, const int32_t *argma
 }
 
 int bl_math_digest(bl_ctx *c, int fn, uint32_t first_block, int n_blocks, uint64_t *out) {
-  if (!c || fn < 0 || fn > 2 || n_blocks <= 0 || (uint64_t)first_block + n_blocks > 4096 || !out)
+  if (!c || fn < 0 || fn > 5 || n_blocks <= 0 || (uint64_t)first_block + n_blocks > 4096 || !out)
     return fail(BL_EPARAM, "bl_math_digest: invalid arguments");
   hipSetDevice(c->device);
   unsigned long long *d = nullptr;

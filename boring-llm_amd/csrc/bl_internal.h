@@ -121,7 +121,7 @@ struct bl_slot_dev {
   /* grammar (src/server.br:309-362): position of the reply in the slot's automaton */
   bl_gram_pos gpos;
   int32_t g_on, pad2;
-  /* mirostat v2 (src/sampling.br:663-674): tau, eta and the running mu */
+  /* mirostat v1 / v2 (src/sampling.br:663-700): the version, tau, eta and the running mu */
   int32_t mirostat;
   float mirostat_tau, mirostat_eta, mu;
 };

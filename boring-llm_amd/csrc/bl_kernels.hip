@@ -1408,8 +1408,8 @@ __device__ __forceinline__ sel_draw ranked_serial(const bl_slot_dev &sp, int n, 
     }
   }
   const int n_eff = (int)(cut < n ? cut : n);
-  /* dynamic_temperature (src/sampling.br:467-488), exponent 1 (powf(x, 1) = x): the entropy of the
-   * renormalised probabilities over [first, cut) against that of a uniform choice */
+  /* dynamic_temperature (src/sampling.br:467-488): the entropy of the renormalised probabilities over
+   * [first, cut) against that of a uniform choice, raised to the exponent */
   float Teff = sp.temperature;
   if (sp.dynatemp_range > 0.0f && cut - first > 1) {
     if (cut > n) {
@@ -1423,7 +1423,7 @@ __device__ __forceinline__ sel_draw ranked_serial(const bl_slot_dev &sp, int n, 
         if (q > 0.0f) ent -= q * bl_logf(q);
       }
       const float maxe = bl_logf((float)(cut - first));
-      const float ne = ent / maxe;
+      const float ne = bl_powf(ent / maxe, sp.dynatemp_exponent);
       const float T = sp.temperature, rg = sp.dynatemp_range;
       const float tmin = T > rg ? T - rg : 0.0f, tmax = T + rg;
       Teff = tmin + (tmax - tmin) * ne;
@@ -1666,8 +1666,8 @@ __device__ __forceinline__ sel_draw sample_ranked_long(const bl_slot_dev &sp, Va
   const int64_t m = n_eff - first;
   const float vf = val(first);
   auto valF = [&](int64_t j) { return val(first + j); };
-  /* dynamic_temperature (src/sampling.br:467-488), exponent 1: the surviving probabilities' sum, then
-   * the entropy of the renormalised ones (entropy -= q ln q adds the non-negative -(q ln q)) */
+  /* dynamic_temperature (src/sampling.br:467-488): the surviving probabilities' sum, then the entropy of
+   * the renormalised ones (entropy -= q ln q adds the non-negative -(q ln q)), raised to the exponent */
   float Teff = T;
   if (sp.dynatemp_range > 0.0f && cutoff - first > 1) {
     if (cutoff > n_list) { /* the entropy would need candidates past the materialised list */
@@ -1696,7 +1696,7 @@ __device__ __forceinline__ sel_draw sample_ranked_long(const bl_slot_dev &sp, Va
     const float ent = sh.fres[3];
     __syncthreads();
     const float maxe = bl_logf((float)(cutoff - first));
-    const float ne = ent / maxe;
+    const float ne = bl_powf(ent / maxe, sp.dynatemp_exponent);
     const float rg = sp.dynatemp_range;
     const float tmin = T > rg ? T - rg : 0.0f, tmax = T + rg;
     Teff = tmin + (tmax - tmin) * ne;
@@ -1747,15 +1747,17 @@ __device__ __forceinline__ sel_draw sample_ranked_long(const bl_slot_dev &sp, Va
 }
 
 /*
- * sample_mirostat_v2 (src/sampling.br:663-674, draw_mirostat_prefix :643-659) over the full-vocabulary
- * list, by the block: scaled values v/T, the softmax of exp(v/T - v0/T) over every candidate (the terms
- * past the list are below half an ulp of the sum), the prefix whose surprise -ln p / ln 2 stays within
- * mu, the softmax and draw over that prefix, and mu - eta (surprise - tau) for the slot (sh.fres[6]).
+ * sample_mirostat_v2 (src/sampling.br:663-674, draw_mirostat_prefix :643-659) and sample_mirostat_v1
+ * (:676-700) over the full-vocabulary list, by the block: scaled values v/T, the softmax of exp(v/T - v0/T)
+ * over every candidate (the terms past the list are below half an ulp of the sum), the prefix (v2: while
+ * the surprise -ln p / ln 2 stays within mu; v1: the length predicted by a Zipf fit), the softmax and draw
+ * over that prefix, and mu - eta (surprise - tau) for the slot (sh.fres[6]). `mk` is this thread's key of
+ * the row's merged top-K list (v1 reads the first min(V, 100)).
  */
 template <class ValF>
 __device__ __forceinline__ sel_draw sample_mirostat(const bl_slot_dev &sp, ValF val, int64_t n_list, int64_t n_logical,
-                                    uint64_t &rng, int rng_skip, bl_grec *recs, double *gsum, float *tbuf,
-                                    sel_shared &sh, int &status) {
+                                    uint64_t mk, uint64_t &rng, int rng_skip, bl_grec *recs, double *gsum,
+                                    float *tbuf, sel_shared &sh, int &status) {
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   const float T = sp.temperature;
   const float s0 = val(0) / T;
@@ -1766,6 +1768,9 @@ __device__ __forceinline__ sel_draw sample_mirostat(const bl_slot_dev &sp, ValF 
   out.first = 0;
   out.cut = 0;
   out.S = 0.0f;
+  const bool v1 = sp.mirostat == 1;
+  const int m1 = n_logical < 100 ? (int)n_logical : 100; /* v1's fitted ranks */
+  if (v1 && t < m1) sh.ser_v[t] = ckey_v(mk);             /* short-list LDS: unused by these rows */
   /* softmax_prefix over the whole rank */
   block_records(n_list, val, termE, recs, gsum, tbuf);
   if (w == 0) {
@@ -1779,15 +1784,61 @@ __device__ __forceinline__ sel_draw sample_mirostat(const bl_slot_dev &sp, ValF 
   __syncthreads();
   const float total = sh.fres[0];
   const float ln2 = bl_logf(2.0f), mu = sp.mu;
-  /* the cutoff: the first candidate whose surprise exceeds mu */
-  for (int64_t j = t; j < n_list; j += BL_SEL_THREADS) {
-    const float p = tbuf[j] / total;
-    if (!((-bl_logf(p)) / ln2 <= mu)) atomicMin(&sh.ires[1], (int)j);
+  bool past;   /* the prefix runs past the list */
+  int64_t cut; /* the prefix within the list */
+  if (v1) {
+    /* the fit (src/sampling.br:683-699): lane l of wavefront 0 forms pairs l and l + 64 of
+     * t_i = ln((i + 2) / (i + 1)), b_i = ln(p_i / p_(i+1)); every lane then adds t_i b_i and t_i^2 in order */
+    if (w == 0) {
+      float a[2], q[2];
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        const int i = lane + 64 * h;
+        a[h] = q[h] = 0.0f;
+        if (i < m1 - 1) {
+          const float ti = SEL_LOGF((float)(i + 2) / (float)(i + 1));
+          const float pi = termE(sh.ser_v[i]) / total, pn = termE(sh.ser_v[i + 1]) / total;
+          const float bi = SEL_LOGF(pi / pn);
+          a[h] = ti * bi;
+          q[h] = ti * ti;
+        }
+      }
+      float sa = 0.0f, sq = 0.0f;
+#pragma unroll
+      for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int l = 0; l < 64; l++)
+          if (64 * h + l < m1 - 1) {
+            sa += bl_u2f((uint32_t)__builtin_amdgcn_readlane((int)bl_f2u(a[h]), l));
+            sq += bl_u2f((uint32_t)__builtin_amdgcn_readlane((int)bl_f2u(q[h]), l));
+          }
+      if (lane == 0) {
+        const float s_hat = sa / sq;
+        const float eps = s_hat - 1.0f;
+        const float num = eps * bl_powf(2.0f, mu);
+        const float den = 1.0f - bl_powf((float)n_logical, -eps);
+        const float est = bl_powf(num / den, 1.0f / s_hat);
+        /* `as int`: truncation, saturating, NaN to 0; then clamped to [1, V] */
+        int64_t e = est != est ? 0 : est >= 0x1p63f ? INT64_MAX : est <= -0x1p63f ? INT64_MIN : (int64_t)est;
+        if (e < 1) e = 1;
+        if (e > n_logical) e = n_logical;
+        sh.ires[1] = (int)e;
+      }
+    }
+    __syncthreads();
+    past = sh.ires[1] > n_list;
+    cut = past ? n_list : sh.ires[1];
+  } else {
+    /* the cutoff: the first candidate whose surprise exceeds mu */
+    for (int64_t j = t; j < n_list; j += BL_SEL_THREADS) {
+      const float p = tbuf[j] / total;
+      if (!((-bl_logf(p)) / ln2 <= mu)) atomicMin(&sh.ires[1], (int)j);
+    }
+    __syncthreads();
+    past = sh.ires[1] == 0x7fffffff && n_list < n_logical;
+    cut = sh.ires[1] == 0x7fffffff ? n_list : sh.ires[1];
+    if (cut == 0) cut = 1;
   }
-  __syncthreads();
-  const bool past = sh.ires[1] == 0x7fffffff && n_list < n_logical; /* the prefix runs past the list */
-  int64_t cut = sh.ires[1] == 0x7fffffff ? n_list : sh.ires[1];
-  if (cut == 0) cut = 1;
   __syncthreads();
   /* softmax_prefix over the cut, then the draw (draw_mirostat_prefix) */
   block_records(cut, val, termE, recs, gsum, tbuf);
@@ -2812,7 +2863,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
         gsum = d.gsum + (int64_t)row * (V / 64 + 64);
       }
       float *tbuf = reinterpret_cast<float *>(d.sortk + (int64_t)row * 2 * V); /* free once the list is sorted */
-      dr = miro ? sample_mirostat(sp, val, n_list, n_logical, rng, skip, recs, gsum, tbuf, sh, status)
+      dr = miro ? sample_mirostat(sp, val, n_list, n_logical, mk, rng, skip, recs, gsum, tbuf, sh, status)
                 : sample_ranked_long(sp, val, n_list, n_logical, keep, rng, skip, recs, gsum, tbuf, sh, status);
       pos = dr.pos;
       dterm = tbuf;
@@ -2994,6 +3045,10 @@ void bl_launch_synth(float *out, int64_t ld, int cfg, int64_t seed, int64_t step
 
 /* ------------------------------------------------------------------ math self-test */
 /* Digest of f over input bit patterns [b*2^20, (b+1)*2^20): sum of splitmix(u << 32 | bits(f(u))). */
+/* exponent of the two-argument powf family: a multiple of 1/512 in [-8, 8] hashed from the input */
+__device__ inline float bl_digest_pow_y(uint32_t u) {
+  return (float)((int)((bl_splitmix(u) >> 40) % 8193u) - 4096) * 0x1p-9f;
+}
 __global__ void bl_k_math_digest(int fn, uint32_t first_block, unsigned long long *out) {
   const uint32_t blk = first_block + blockIdx.y;
   const uint32_t base = blk << 20;
@@ -3001,7 +3056,13 @@ __global__ void bl_k_math_digest(int fn, uint32_t first_block, unsigned long lon
   for (int k = 0; k < 16; k++) {
     uint32_t u = base + (uint32_t)(blockIdx.x * 4096 + k * 256 + threadIdx.x);
     float x = bl_u2f(u);
-    float y = fn == 0 ? bl_expf(x) : fn == 1 ? bl_tanhf(x) : bl_logf(x);
+    float y;
+    if (fn == 0) y = bl_expf(x);
+    else if (fn == 1) y = bl_tanhf(x);
+    else if (fn == 2) y = bl_logf(x);
+    else if (fn == 3) y = bl_powf(x, 0.7f);
+    else if (fn == 4) y = bl_powf(2.0f, x);
+    else y = bl_powf(x, bl_digest_pow_y(u));
     uint32_t yb = y != y ? 0x7fc00000u : bl_f2u(y); /* NaN payloads are not part of the path */
     h += bl_splitmix(((uint64_t)u << 32) | yb);
   }

@@ -167,6 +167,113 @@ BL_FN float bl_logf(float x) {
   return bl_logf_tab(x, [](int j) { return bl_log_tab[j]; });
 }
 
+/* ---------------- powf ---------------- */
+/* ARM optimized-routines powf (as in glibc >= 2.28): log2(x) in double from the (1/c, log2 c) table of the
+ * same 16 subintervals as logf's (log2 c = log c / ln 2 rounded) and a degree-5 polynomial, y log2(x) in
+ * double, then 2^(y log2 x) by expf's 2^(i/32) table and cubic; special cases (zero, infinity, NaN and
+ * signalling NaN, negative x with integer y, subnormal x, overflow and underflow in round-to-nearest) as
+ * the published code handles them. As for expf, the multiply-adds are fused the way the glibc x86-64
+ * build for FMA-capable hosts fuses them. Equal to host glibc powf on all 2^32 inputs of powf(x, 0.7),
+ * powf(2, x) and powf(x, y(x)) with y a multiple of 1/512 in [-8, 8] (tests/golden/math_digest.bin, on
+ * the device) and on 4 million random and structured pairs (tests/cpu/check_exact.cpp). */
+#if defined(__HIP_DEVICE_COMPILE__)
+__constant__
+#else
+static
+#endif
+const double bl_log2_tab[32] = {
+    0x1.661ec79f8f3bep+0, -0x1.efec65b963019p-2, 0x1.571ed4aaf883dp+0, -0x1.b0b6832d4fca4p-2,
+    0x1.49539f0f010bp+0, -0x1.7418b0a1fb77bp-2, 0x1.3c995b0b80385p+0, -0x1.39de91a6dcf7cp-2,
+    0x1.30d190c8864a5p+0, -0x1.01d9bf3f2b631p-2, 0x1.25e227b0b8eap+0, -0x1.97c1d1b3b7af1p-3,
+    0x1.1bb4a4a1a343fp+0, -0x1.2f9e393af3c9fp-3, 0x1.12358f08ae5bap+0, -0x1.960cbbf788d5bp-4,
+    0x1.0953f419900a7p+0, -0x1.a6f9db6475fcep-5, 0x1p+0, 0x0p+0,
+    0x1.e608cfd9a47acp-1, 0x1.338ca9f24f53ep-4, 0x1.ca4b31f026aap-1, 0x1.476a9543891bbp-3,
+    0x1.b2036576afce6p-1, 0x1.e840b4ac4e4d2p-3, 0x1.9c2d163a1aa2dp-1, 0x1.40645f0c6651cp-2,
+    0x1.886e6037841edp-1, 0x1.88e9c2c1b9ff8p-2, 0x1.767dcf5534862p-1, 0x1.ce0a44eb17bcdp-2};
+
+/* y is an integer: 0 no, 1 odd, 2 even */
+BL_FN int bl_pow_checkint(uint32_t iy) {
+  const int e = (int)(iy >> 23 & 0xff);
+  if (e < 0x7f) return 0;
+  if (e > 0x7f + 23) return 2;
+  if (iy & ((1u << (0x7f + 23 - e)) - 1u)) return 0;
+  if (iy & (1u << (0x7f + 23 - e))) return 1;
+  return 2;
+}
+BL_FN bool bl_pow_zeroinfnan(uint32_t ix) { return 2u * ix - 1u >= 2u * 0x7f800000u - 1u; }
+BL_FN bool bl_pow_snan(uint32_t ix) { return 2u * (ix ^ 0x00400000u) > 2u * 0x7fc00000u; }
+
+BL_FN float bl_powf(float x, float y) {
+  const double A0 = 0x1.27616c9496e0bp-2, A1 = -0x1.71969a075c67ap-2, A2 = 0x1.ec70a6ca7baddp-2,
+               A3 = -0x1.7154748bef6c8p-1, A4 = 0x1.71547652ab82bp0;
+  const double C0 = 0x1.c6af84b912394p-5, C1 = 0x1.ebfce50fac4f3p-3, C2 = 0x1.62e42ff0c52d6p-1;
+  const double SHIFT = 0x1.8p+52 / BL_EXP2_N;
+  uint64_t sign_bias = 0;
+  uint32_t ix = bl_f2u(x);
+  const uint32_t iy = bl_f2u(y);
+  if (ix - 0x00800000u >= 0x7f800000u - 0x00800000u || bl_pow_zeroinfnan(iy)) {
+    if (bl_pow_zeroinfnan(iy)) {
+      if (2u * iy == 0u) return bl_pow_snan(ix) ? x + y : 1.0f;
+      if (ix == 0x3f800000u) return bl_pow_snan(iy) ? x + y : 1.0f;
+      if (2u * ix > 2u * 0x7f800000u || 2u * iy > 2u * 0x7f800000u) return x + y;
+      if (2u * ix == 2u * 0x3f800000u) return 1.0f;
+      if ((2u * ix < 2u * 0x3f800000u) == !(iy & 0x80000000u)) return 0.0f;
+      return y * y;
+    }
+    if (bl_pow_zeroinfnan(ix)) {
+      float x2 = x * x;
+      if ((ix & 0x80000000u) && bl_pow_checkint(iy) == 1) x2 = -x2;
+      return (iy & 0x80000000u) ? 1.0f / x2 : x2;
+    }
+    if (ix & 0x80000000u) { /* negative x: y must be an integer */
+      const int yint = bl_pow_checkint(iy);
+      if (yint == 0) return bl_u2f(0x7fc00000u);
+      if (yint == 1) sign_bias = 1ull << (BL_EXP2_BITS + 11);
+      ix &= 0x7fffffffu;
+    }
+    if (ix < 0x00800000u) { /* subnormal x: normalise */
+      ix = bl_f2u(bl_u2f(ix) * 0x1p23f);
+      ix &= 0x7fffffffu;
+      ix -= 23u << 23;
+    }
+  }
+  /* log2(x) */
+  const uint32_t tmp = ix - 0x3f330000u;
+  const int i = (int)((tmp >> 19) % 16u);
+  const uint32_t top = tmp & 0xff800000u;
+  const uint32_t iz = ix - top;
+  const int k = (int32_t)top >> 23;
+  const double z = (double)bl_u2f(iz);
+  const double r = BL_FMA(z, bl_log2_tab[2 * i], -1.0);
+  const double y0 = bl_log2_tab[2 * i + 1] + (double)k;
+  const double r2 = r * r;
+  double p = BL_FMA(A0, r, A1);
+  const double q0 = BL_FMA(A2, r, A3);
+  const double r4 = r2 * r2;
+  double q = BL_FMA(A4, r, y0);
+  q = BL_FMA(q0, r2, q);
+  p = BL_FMA(p, r4, q);
+  const double ylogx = (double)y * p;
+  if ((bl_d2u(ylogx) >> 47 & 0xffff) >= bl_d2u(126.0) >> 47) {
+    if (ylogx > 0x1.fffffffd1d571p+6) return sign_bias ? bl_u2f(0xff800000u) : bl_u2f(0x7f800000u);
+    if (ylogx <= -150.0) return sign_bias ? -0.0f : 0.0f;
+  }
+  /* 2^ylogx */
+  double kd = ylogx + SHIFT;
+  const uint64_t ki = bl_d2u(kd);
+  kd -= SHIFT;
+  const double rr = ylogx - kd;
+  uint64_t t = bl_exp2_tab[ki % BL_EXP2_N];
+  t += (ki + sign_bias) << (52 - BL_EXP2_BITS);
+  const double s = bl_u2d(t);
+  const double zz = BL_FMA(C0, rr, C1);
+  const double rr2 = rr * rr;
+  double yy = BL_FMA(C2, rr, 1.0);
+  yy = BL_FMA(zz, rr2, yy);
+  yy = yy * s;
+  return (float)yy;
+}
+
 /* ---------------- expm1f / tanhf (float arithmetic) ---------------- */
 BL_FN float bl_expm1f(float x) {
   const float huge = 1.0e+30f, tiny = 1.0e-30f, one = 1.0f, o_threshold = 8.8721679688e+01f,

@@ -31,10 +31,11 @@ enum {
   BL_EGRAMMAR_DEAD = -5,   /* "the reply no longer matches the grammar" (src/server.br:320) */
   BL_EGRAMMAR_REJECT = -6, /* "the grammar rejected every vocabulary token" (src/server.br:361) */
   BL_EGRAMMAR_AMBIG = -7,  /* "grammar is left-recursive or too ambiguous to match" (src/grammar.br:354) */
-  BL_EUNSUPPORTED = -8,    /* a sampler stage this library does not run on the device yet: DRY, a dynatemp
-                              exponent other than 1, mirostat v1 (rejected by bl_slot_reset); XTC, mirostat
-                              or a grammar on speculative rows, or more than 32 drafts with history-dependent
-                              penalties; typical_p over a full-vocabulary list above 512 candidates */
+  BL_EUNSUPPORTED = -8,    /* a sampler stage this library does not run on the device yet: DRY (rejected by
+                              bl_slot_reset); XTC, mirostat or a grammar on speculative rows, or more than 32
+                              drafts with history-dependent penalties; typical_p over a full-vocabulary list
+                              above 512 candidates; a mirostat draw that falls through to a prefix end past
+                              the candidates within 17.6 T of the maximum */
   BL_ETIE = -9,            /* a draw on equal logits whose heap order is past the device simulation (more than
                               8192 values at or above the tied one), equal allowed maxima of a grammar row,
                               post-sampling alternatives of a full-vocabulary rank that meet equal values, or a
@@ -75,8 +76,8 @@ typedef struct {
   int32_t ignore_eos;
   float final_softcap;     /* model tail (src/model.br:973-984): 0 = off */
   float logit_mul;         /* model tail: 1 = off */
-  int32_t mirostat;        /* server extras (src/server.br:684-686): 0 off, 2 = sample_mirostat_v2
-                              (src/sampling.br:663-674) on the device; 1 (needs powf) is BL_EUNSUPPORTED */
+  int32_t mirostat;        /* server extras (src/server.br:684-686): 0 off, 1 = sample_mirostat_v1
+                              (src/sampling.br:676-700), 2 = sample_mirostat_v2 (:663-674) */
   float mirostat_tau;      /* target surprise; the slot's mu starts at 2 tau (src/server.br:936) */
   float mirostat_eta;
 } bl_params;
@@ -226,8 +227,9 @@ int bl_workload_bias(int cfg, int64_t seed, int row, int n, int vocab, float lo,
 int bl_workload_c3_vocab(int64_t seed, int vocab, uint8_t *blob, size_t blob_cap, uint32_t *offsets, int32_t *eos_id);
 int bl_workload_drafts(int64_t seed, int64_t step, int seq, const int32_t *argmax, int k, int vocab, int32_t *out);
 
-/* Self-test (no reference counterpart): digests of the device expf (fn 0) / tanhf (fn 1) / logf (fn 2) over
- * input bit-pattern blocks [b*2^20, (b+1)*2^20), b = first_block .. first_block+n_blocks-1; each digest
+/* Self-test (no reference counterpart): digests of the device expf (fn 0) / tanhf (fn 1) / logf (fn 2) /
+ * powf(x, 0.7f) (fn 3) / powf(2, x) (fn 4) / powf(x, y(u)) (fn 5, y(u) = ((splitmix64(u) >> 40) % 8193 - 4096)
+ * / 512) over input bit-pattern blocks [b*2^20, (b+1)*2^20), b = first_block .. first_block+n_blocks-1; each digest
  * is the wrapping sum of splitmix64(u << 32 | bits(f(u))) with NaN results canonicalised to 0x7fc00000.
  * Compared with host-glibc fixtures. */
 int bl_math_digest(bl_ctx *ctx, int fn, uint32_t first_block, int n_blocks, uint64_t *out);

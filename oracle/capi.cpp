@@ -206,6 +206,9 @@ int32_t orc_mirostat(int version, uint64_t *rng, const float *logits, int64_t n,
   *mu = r.mu;
   return r.token;
 }
+int64_t orc_mirostat_v1_cutoff(const float *logits, int64_t n, float t, float mu, float *s_hat) {
+  return mirostat_v1_cutoff_of(Row(logits, logits + n), n, t, mu, *s_hat);
+}
 int32_t orc_adaptive_p(uint64_t *rng, const float *logits, int64_t n, float target, float decay, float *ws, float *tw) {
   AdaptiveResult r = sample_adaptive_p(Rng{*rng}, Row(logits, logits + n), n, target, decay, *ws, *tw);
   *rng = r.rng.state;

@@ -137,6 +137,8 @@ MirostatResult sample_mirostat_v2(Rng rng, const Row &logits, int64_t vocab, flo
                                   float mu);
 MirostatResult sample_mirostat_v1(Rng rng, const Row &logits, int64_t vocab, float temperature, float tau, float eta,
                                   float mu);
+/* the prefix length sample_mirostat_v1 draws from (temperature > 0), and the fitted exponent s_hat */
+int64_t mirostat_v1_cutoff_of(const Row &logits, int64_t vocab, float temperature, float mu, float &s_hat);
 struct AdaptiveResult {
   int32_t token;
   Rng rng;

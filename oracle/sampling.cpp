@@ -638,17 +638,14 @@ MirostatResult sample_mirostat_v2(Rng rng, const Row &logits, int64_t vocab, flo
   return draw_mirostat_prefix(rng, values, ids, cutoff, tau, eta, mu);
 }
 
-/* :676-700 */
-MirostatResult sample_mirostat_v1(Rng rng, const Row &logits, int64_t vocab, float temperature, float tau, float eta,
-                                  float mu) {
-  if (temperature <= 0.0f) return MirostatResult{sample_greedy(logits, vocab), rng, mu};
-  Row values;
-  Ids ids;
-  temperature_ranked(logits, vocab, temperature, values, ids);
-  float total;
-  Row probs = softmax_prefix(values, vocab, total);
+/* :683-699: the Zipf exponent s_hat fitted to the first min(vocab, 100) ranked probabilities, and the
+ * prefix length it predicts for the target surprise mu */
+static int64_t mirostat_v1_cutoff(const Row &probs, int64_t vocab, float mu, float &s_hat_out) {
   int64_t m = vocab < 100 ? vocab : 100;
   float sum_ti_bi = 0.0f, sum_ti_sq = 0.0f;
+#if ORC_MUTANT == 6 /* planted mistake (tests only): the fit's last pair dropped */
+  m -= 1;
+#endif
   for (int64_t i = 0; i < m - 1; i++) {
     float t_i = logf((float)(i + 2) / (float)(i + 1));
     float b_i = logf(probs[i] / probs[i + 1]);
@@ -666,6 +663,30 @@ MirostatResult sample_mirostat_v1(Rng rng, const Row &logits, int64_t vocab, flo
   int64_t estimate = est != est ? 0 : (est >= 9.2e18f ? INT64_MAX : (est <= -9.2e18f ? INT64_MIN : (int64_t)est));
   int64_t cutoff = estimate > 1 ? estimate : 1;
   if (cutoff > vocab) cutoff = vocab;
+  s_hat_out = s_hat;
+  return cutoff;
+}
+
+/* :676-700 */
+int64_t mirostat_v1_cutoff_of(const Row &logits, int64_t vocab, float temperature, float mu, float &s_hat) {
+  Row values;
+  Ids ids;
+  temperature_ranked(logits, vocab, temperature, values, ids);
+  float total;
+  Row probs = softmax_prefix(values, vocab, total);
+  return mirostat_v1_cutoff(probs, vocab, mu, s_hat);
+}
+
+MirostatResult sample_mirostat_v1(Rng rng, const Row &logits, int64_t vocab, float temperature, float tau, float eta,
+                                  float mu) {
+  if (temperature <= 0.0f) return MirostatResult{sample_greedy(logits, vocab), rng, mu};
+  Row values;
+  Ids ids;
+  temperature_ranked(logits, vocab, temperature, values, ids);
+  float total;
+  Row probs = softmax_prefix(values, vocab, total);
+  float s_hat;
+  const int64_t cutoff = mirostat_v1_cutoff(probs, vocab, mu, s_hat);
   return draw_mirostat_prefix(rng, values, ids, cutoff, tau, eta, mu);
 }
 

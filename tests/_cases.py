@@ -37,6 +37,10 @@ CASES = [
     dict(temperature=0.9, top_k=0, top_n_sigma=1.5, logprobs=1, n_probs=4),
     dict(temperature=1.0, top_k=40, top_n_sigma=0.8, top_p=0.9, repeat_penalty=1.2, repeat_last_n=16),
     dict(temperature=1.2, top_k=0, top_n_sigma=3.0, min_p=0.02, frequency_penalty=0.3, presence_penalty=0.2),
+    # dynamic temperature with exponents other than 1 (glibc powf of the normalised entropy)
+    dict(temperature=1.0, top_k=0, min_p=0.05, dynatemp_range=0.8, dynatemp_exponent=0.5),
+    dict(temperature=0.9, top_k=30, dynatemp_range=0.5, dynatemp_exponent=2.3, logprobs=1, n_probs=4,
+         post_sampling_probs=1),
 ]
 SMALL_V = 5003
 EOS, EOGS = 7, [11, 13]

@@ -113,5 +113,26 @@ int main() {
     if (bl_f2u(bl_u64_to_f32(v)) != bl_f2u((float)v)) mc++;
   }
   printf("u64->f32 mismatches %ld\n", mc);
-  return (bad || me || mt || ml || mc) ? 1 : 0;
+  // 4) glibc-identical powf: random bit patterns of x and y, and x in [1, 101) with y in [-100, 100)
+  long mp = 0, np_ = 0;
+  for (int i = 0; i < 4000000; i++) {
+    const uint64_t a = rng(), b = rng();
+    float x = bl_u2f((uint32_t)a), y = bl_u2f((uint32_t)(b >> 32));
+    if (i % 3 == 0) {
+      x = 1.0f + (float)(a % 100000) / 1000.0f;
+      y = ((float)((b >> 20) % 20000) - 10000.0f) / 100.0f;
+    } else if (i % 3 == 1) {
+      x = bl_u2f((uint32_t)a & 0x3fffffffu); /* (0, 2) and subnormals */
+      y = (float)((int)(b % 41) - 20) * 0.5f; /* integers and halves, with negative x below */
+      if (b & (1ull << 40)) x = -x;
+    }
+    const float pa = bl_powf(x, y), pb = powf(x, y);
+    np_++;
+    if (!(pa != pa && pb != pb) && bl_f2u(pa) != bl_f2u(pb)) {
+      if (mp < 5) printf("powf mismatch x=%a y=%a mine=%a glibc=%a\n", x, y, pa, pb);
+      mp++;
+    }
+  }
+  printf("powf mismatches %ld of %ld\n", mp, np_);
+  return (bad || me || mt || ml || mc || mp) ? 1 : 0;
 }

@@ -271,31 +271,42 @@ def run_tns(BL, steps):
 MIRO_ROWS = [(1.0, 5.0, 0.1), (0.7, 3.0, 0.5), (1.5, 8.0, 0.2)]
 
 
-def run_mirostat(BL, steps):
-    """Mirostat v2 rows (temperature, tau, eta) on the small vocabulary's logits (planted ties: the heap's
-    order) against the oracle's sample_mirostat_v2, the running mu carried by both; the final RNG states."""
+def miro_logits(rng, V):
+    """N(0, 2.5^2) logits with 30 bumped ids and 5 planted equal values (the small cases' shape at any V)."""
+    if V == SMALL_V:
+        return small_case_logits(rng)
+    x = (rng.standard_normal(V) * 2.5).astype(np.float32)
+    x[rng.integers(0, V, 30)] += 6.0
+    x[rng.integers(0, V, 5)] = x[int(rng.integers(0, V))]
+    return x
+
+
+def run_mirostat(BL, steps, version=2, V=SMALL_V):
+    """Mirostat rows (temperature, tau, eta) of one version on logits with planted ties (the heap's order)
+    against the oracle's sample_mirostat_v1 / v2, the running mu carried by both; the final RNG states."""
     L = O.lib()
     L.orc_mirostat.restype = O.C.c_int32
     L.orc_mirostat.argtypes = [O.C.c_int, O.C.POINTER(O.C.c_uint64), O.C.POINTER(O.C.c_float), O.C.c_int64,
                                O.C.c_float, O.C.c_float, O.C.c_float, O.C.POINTER(O.C.c_float)]
     R = len(MIRO_ROWS)
-    ctx = BL.Context(SMALL_V, R, R)
-    rng = np.random.default_rng(77)
+    ctx = BL.Context(V, R, R)
+    rng = np.random.default_rng(77 + version)
     states, mus = [], []
     for r, (T, tau, eta) in enumerate(MIRO_ROWS):
-        ctx.slot_reset(r, BL.Params(temperature=T, mirostat=2, mirostat_tau=tau, mirostat_eta=eta), BL.seed_rng(300 + r))
+        ctx.slot_reset(r, BL.Params(temperature=T, mirostat=version, mirostat_tau=tau, mirostat_eta=eta),
+                       BL.seed_rng(300 + r))
         states.append(O.C.c_uint64(BL.seed_rng(300 + r)))
         mus.append(O.C.c_float(2.0 * tau))
-    buf = MEM.zeros(R * SMALL_V, np.float32)
+    buf = MEM.zeros(R * V, np.float32)
     try:
         for t in range(steps):
-            xs = [small_case_logits(rng) for _ in range(R)]
+            xs = [miro_logits(rng, V) for _ in range(R)]
             buf.upload(np.concatenate(xs))
-            tok = ctx.sample_step(list(range(R)), buf.ptr, SMALL_V)[0]
+            tok = ctx.sample_step(list(range(R)), buf.ptr, V)[0]
             for r, (T, tau, eta) in enumerate(MIRO_ROWS):
                 x = np.ascontiguousarray(xs[r])
-                ot = L.orc_mirostat(2, O.C.byref(states[r]), x.ctypes.data_as(O.C.POINTER(O.C.c_float)), SMALL_V, T,
-                                    tau, eta, O.C.byref(mus[r]))
+                ot = L.orc_mirostat(version, O.C.byref(states[r]), x.ctypes.data_as(O.C.POINTER(O.C.c_float)), V,
+                                    T, tau, eta, O.C.byref(mus[r]))
                 if tok[r] != ot:
                     return f"step {t} row {r}: token {tok[r]} vs {ot} (mu {mus[r].value})"
         for r in range(R):
@@ -795,6 +806,9 @@ def main():
             results.append(("top-n-sigma rows at V=151936", run_tns(BL, int(f[1]))))
         elif kind == "miro":
             results.append(("mirostat v2 rows", run_mirostat(BL, int(f[1]))))
+        elif kind == "miro1":  # miro1:steps[:V]
+            V = int(f[2]) if len(f) > 2 else SMALL_V
+            results.append((f"mirostat v1 rows at V={V}", run_mirostat(BL, int(f[1]), 1, V)))
         elif kind == "unfilt":
             rows = [int(v) for v in f[2].split(",")] if len(f) > 2 else None
             results.append(("unfiltered rows at V=151936", run_unfiltered(BL, int(f[1]), rows)))

@@ -89,6 +89,14 @@ def test_mirostat_v2_rows():
     assert err is None, err
 
 
+def test_mirostat_v1_rows():
+    print("three mirostat v1 rows, V=5003: 40 steps; V=151936: 12 steps", flush=True)
+    err = RP.run_mirostat(BL, 40, 1)
+    assert err is None, err
+    err = RP.run_mirostat(BL, 12, 1, 151936)
+    assert err is None, err
+
+
 def test_async_step_equals_sync():
     print("bound rows, asynchronous step: 4 steps", flush=True)
     err = RP.run_async(BL, 4)

@@ -11,9 +11,12 @@ that each check fails against an oracle with a planted mistake (oracle/Makefile 
   top_n_sigma_logits (src/sampling.br:376-407): the count, sum and sum of squares of the values above -1e29
       as sequential float64 sums (np.cumsum over float64), then mean, variance, the square root rounded to
       float32 and the threshold max - n * sigma in float32.
+  sample_mirostat_v1's fit (src/sampling.br:683-699): the sequential float32 loop over the first 100 ranked
+      probabilities with glibc's logf and powf through ctypes, and on exact Zipf probabilities the fitted
+      exponent and the closed-form cutoff.
 The planted mistakes: ties sent to the right child in the sift (1), a pairwise normaliser sum (2), the
 softmax sum in reverse rank order (3), the tempered sum as two halves (4), top-n-sigma's value sum in
-float32 (5).
+float32 (5), the mirostat v1 fit's last pair dropped (6).
 """
 import ctypes
 from fractions import Fraction
@@ -263,3 +266,101 @@ def test_top_n_sigma_is_the_sequential_float64_statistics():
 
 def test_top_n_sigma_check_fails_on_planted_mistake():
     assert tns_mismatches(O.mutant(5), tns_rows()) > 0
+
+
+# ---------------------------------------------------------------- mirostat v1's Zipf fit
+
+_m.powf.restype = ctypes.c_float
+_m.powf.argtypes = [ctypes.c_float, ctypes.c_float]
+
+
+def miro_v1_cutoff(x, T, mu):
+    """(cutoff, s_hat) of sample_mirostat_v1 (src/sampling.br:676-699) from numpy's sort and glibc's expf,
+    logf and powf: the ranked values divided by T, their softmax with a sequential float32 sum, the fit
+    over the first min(V, 100), the estimate cast as Rust `as int` does (saturating, NaN to 0), clamped."""
+    V = len(x)
+    v = (np.sort(np.asarray(x, F))[::-1] / F(T)).astype(F)
+    terms = gexpf(v - v[0])
+    probs = (terms / seq_sum(terms)).astype(F)
+    sa, sb = F(0.0), F(0.0)
+    with np.errstate(all="ignore"):
+        for i in range(min(V, 100) - 1):
+            t_i = F(_m.logf(F(F(i + 2) / F(i + 1))))
+            b_i = F(_m.logf(F(probs[i] / probs[i + 1])))
+            sa = F(sa + F(t_i * b_i))
+            sb = F(sb + F(t_i * t_i))
+        s_hat = F(sa / sb)
+        eps = F(s_hat - F(1.0))
+        num = F(eps * F(_m.powf(2.0, mu)))
+        den = F(F(1.0) - F(_m.powf(F(V), -eps)))
+        est = F(_m.powf(F(num / den), F(F(1.0) / s_hat)))
+    if est != est:
+        e = 0
+    elif est >= F(2.0 ** 63):
+        e = 2 ** 63 - 1
+    elif est <= F(-2.0 ** 63):
+        e = -2 ** 63
+    else:
+        e = int(est)
+    return min(max(e, 1), V), s_hat
+
+
+def miro_rows():
+    rng = np.random.default_rng(53)
+    rows = []
+    for k in range(40):
+        V = int(rng.choice([3, 50, 101, 1000, 5003, 40000]))
+        if k % 4 == 0:  # Zipf: p_i proportional to (i + 1)^-s, shuffled
+            s = float(rng.uniform(1.05, 2.5))
+            x = (-s * np.log(np.arange(1, V + 1))).astype(F)
+            rng.shuffle(x)
+            T = 1.0
+        elif k % 4 == 1:  # wide spread: tail probabilities underflow to zero (NaN fit, cutoff 1)
+            x = (rng.standard_normal(V) * 60.0).astype(F)
+            T = float(rng.choice([0.5, 1.0]))
+        else:
+            x = (rng.standard_normal(V) * float(rng.uniform(0.5, 4.0))).astype(F)
+            x[rng.integers(0, V, max(1, V // 50))] = x[int(rng.integers(0, V))]  # equal values
+            T = float(rng.choice([0.5, 0.9, 1.0, 1.7]))
+        rows.append((x, T, float(rng.choice([3.0, 6.0, 10.0, 16.0]))))
+    return rows
+
+
+def miro_mismatches(L, rows):
+    L.orc_mirostat_v1_cutoff.restype = ctypes.c_int64
+    L.orc_mirostat_v1_cutoff.argtypes = [O.f32p, ctypes.c_int64, ctypes.c_float, ctypes.c_float,
+                                         ctypes.POINTER(ctypes.c_float)]
+    bad = 0
+    for x, T, mu in rows:
+        want, ws = miro_v1_cutoff(x, T, mu)
+        s = ctypes.c_float()
+        got = L.orc_mirostat_v1_cutoff(O.fp(x), len(x), T, mu, ctypes.byref(s))
+        bad += got != want or not (np.float32(s.value).view(np.uint32) == ws.view(np.uint32) or (ws != ws and s.value != s.value))
+    return bad
+
+
+def test_mirostat_v1_fit_is_the_sequential_float32_loop():
+    assert miro_mismatches(O.lib(), miro_rows()) == 0
+
+
+def test_mirostat_v1_fit_recovers_a_zipf_exponent():
+    """On exact Zipf probabilities the fit returns the exponent s and the cutoff follows the closed form
+    ((s - 1) 2^mu / (1 - V^(1 - s)))^(1/s) (float64, here)."""
+    L = O.lib()
+    L.orc_mirostat_v1_cutoff.restype = ctypes.c_int64
+    L.orc_mirostat_v1_cutoff.argtypes = [O.f32p, ctypes.c_int64, ctypes.c_float, ctypes.c_float,
+                                         ctypes.POINTER(ctypes.c_float)]
+    rng = np.random.default_rng(5)
+    for s, V, mu in ((1.1, 5003, 10.0), (1.5, 40000, 6.0), (2.0, 1000, 10.0), (1.3, 151936, 8.0)):
+        x = (-s * np.log(np.arange(1, V + 1))).astype(F)
+        rng.shuffle(x)
+        sh = ctypes.c_float()
+        got = L.orc_mirostat_v1_cutoff(O.fp(x), V, 1.0, mu, ctypes.byref(sh))
+        assert abs(sh.value - s) < 2e-3 * s, (s, sh.value)
+        est = ((s - 1) * 2.0 ** mu / (1 - V ** (1 - s))) ** (1 / s)
+        want = min(max(int(est), 1), V)
+        assert abs(got - want) <= max(2, 0.02 * want), (s, V, mu, got, want)
+
+
+def test_mirostat_v1_check_fails_on_planted_mistake():
+    assert miro_mismatches(O.mutant(6), miro_rows()) > 0

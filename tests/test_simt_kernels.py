@@ -70,6 +70,13 @@ def test_mirostat_v2(simt_lib):
     assert "ok   mirostat v2 rows" in out
 
 
+def test_mirostat_v1(simt_lib):
+    """Mirostat v1 rows: the Zipf fit over the merged top-100 keys and its glibc powf estimate, the draw over
+    the predicted prefix and the running mu, against the oracle's sample_mirostat_v1 (V=5003 and 20000)."""
+    out = _run(simt_lib, ["miro1:10", "miro1:4:20000"], {"SIMT_ORDER": "rand"})
+    assert "ok   mirostat v1 rows at V=5003" in out and "ok   mirostat v1 rows at V=20000" in out
+
+
 def test_unfiltered_candidate_cut(simt_lib):
     """Full-vocabulary rows without top-p or min-p at V=151936: the candidates cut at half an ulp of the
     draw's running sum (six rows, 12 steps; the bfloat16 row's draws on equal values include one whose heap
@@ -109,6 +116,13 @@ def test_top_n_sigma(simt_lib):
     float64 sums."""
     out = _run(simt_lib, ["small:21-23:12", "tns:2"], {"SIMT_ORDER": "rand"})
     assert out.count("ok   small case") == 3 and "ok   top-n-sigma rows at V=151936" in out
+
+
+def test_dynatemp_exponents(simt_lib):
+    """Dynamic temperature with exponents 0.5 and 2.3 (small cases 24-25: a full-vocabulary min-p row and a
+    top-k row with post-sampling probabilities), the normalised entropy raised by the device's glibc powf."""
+    out = _run(simt_lib, ["small:24-25:12"], {"SIMT_ORDER": "rand"})
+    assert out.count("ok   small case") == 2
 
 
 def test_allocation_free_step(simt_lib):
