@@ -51,6 +51,7 @@ EXPORTS = [
     "bl_workload_drafts", "bl_set_timing", "bl_get_timing", "bl_set_vocab", "bl_slot_grammar", "bl_grammar_mask",
     "bl_workload_c3_vocab", "bl_step_graph_create", "bl_step_graph_launch", "bl_step_graph_destroy",
     "bl_stream_sync", "bl_json_schema_to_gbnf", "bl_slot_schema", "bl_slot_status", "bl_sample_rows_noalloc",
+    "bl_resolve_seed", "bl_seed_rng",
 ]
 NOALLOC_BYTES = 64 << 20
 NOALLOC_ROWS = 16
@@ -92,6 +93,10 @@ def lib():
         L.bl_synth_logits.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_int, C.c_int64, C.c_int64, C.c_int,
                                       C.c_int]
         L.bl_math_digest.argtypes = [C.c_void_p, C.c_int, C.c_uint32, C.c_int, u64p]
+        L.bl_resolve_seed.restype = C.c_int64
+        L.bl_resolve_seed.argtypes = [C.c_int64, C.c_uint64, C.c_int64]
+        L.bl_seed_rng.restype = C.c_uint64
+        L.bl_seed_rng.argtypes = [C.c_int64]
         L.bl_set_timing.argtypes = [C.c_void_p, C.c_int]
         L.bl_get_timing.argtypes = [C.c_void_p, C.POINTER(C.c_double), C.POINTER(C.c_int64)]
         L.bl_workload_ids.argtypes = [C.c_int, C.c_int, C.c_int64, C.c_int, C.c_int, C.c_int, i32p]
@@ -316,9 +321,14 @@ def workload_c3_vocab(seed, vocab):
 
 
 def seed_rng(seed):
-    """seed_rng of src/sampling.br:35-40 (the initial xorshift state for a request seed)."""
-    K = 88172645463325252
-    return K if seed == 0 else (seed & 0xFFFFFFFFFFFFFFFF) ^ K
+    """seed_rng of src/sampling.br:35-40 (the initial xorshift state for a request seed), bl_seed_rng."""
+    return int(lib().bl_seed_rng(seed))
+
+
+def resolve_seed(requested, entropy, request_counter):
+    """resolve_seed of src/sampling.br:21-33 (a negative request seed chosen from entropy and the request
+    counter), bl_resolve_seed."""
+    return int(lib().bl_resolve_seed(requested, entropy & 0xFFFFFFFFFFFFFFFF, request_counter))
 
 
 def json_schema_to_gbnf(schema):

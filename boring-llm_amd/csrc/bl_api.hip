@@ -245,6 +245,22 @@ extern "C" {
 
 const char *bl_last_error(void) { return g_err.c_str(); }
 
+int64_t bl_resolve_seed(int64_t requested, uint64_t entropy, int64_t request_counter) {
+  if (requested >= 0) return requested;
+  const uint64_t c = (uint64_t)request_counter;
+  uint64_t x = entropy ^ (c << 32) ^ c;
+  x ^= x << 13;
+  x ^= x >> 7;
+  x ^= x << 17;
+  const int64_t chosen = (int64_t)(x & 0x7fffffffull);
+  return chosen ? chosen : 1;
+}
+
+uint64_t bl_seed_rng(int64_t seed) {
+  const uint64_t fold = 88172645463325252ull; /* keeps the state off xorshift's fixed point 0 */
+  return seed == 0 ? fold : ((uint64_t)seed ^ fold);
+}
+
 void bl_params_default(bl_params *p) {
   memset(p, 0, sizeof *p);
   p->temperature = 0.0f;

@@ -96,6 +96,15 @@ int bl_set_stream(bl_ctx *ctx, void *stream);
 /* End-of-generation registry: src/sampling.br:200-237 (set_eog_tokens / is_eog_token). */
 int bl_set_eog(bl_ctx *ctx, int32_t eos_id, const int32_t *eog_ids, int n_eog);
 
+/* Request seeds (host arithmetic, no device work; callable without a GPU):
+ * bl_resolve_seed replaces resolve_seed (src/sampling.br:21-33): a non-negative request seed is kept; a
+ * negative one is chosen from `entropy` (the caller's wall-clock bits) and the server's request counter by
+ * one xorshift round, masked to 31 bits, 0 mapped to 1.
+ * bl_seed_rng replaces seed_rng (:35-40): the initial xorshift state of a seed, the value bl_slot_reset
+ * takes as rng_state. */
+int64_t bl_resolve_seed(int64_t requested, uint64_t entropy, int64_t request_counter);
+uint64_t bl_seed_rng(int64_t seed);
+
 /* A new request on `slot`: seed_rng (src/sampling.br:35-40) is the caller's rng_state; history =
  * prompt + reply tokens (repeat penalty / DRY, src/sampling.br:65-85), reply = reply tokens
  * (frequency / presence, :91-107), logit_bias as parallel arrays (src/server.br:150-185, :940). */

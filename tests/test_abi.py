@@ -50,9 +50,38 @@ def test_params_layout_matches_header():
 
 
 def test_seed_fold():
-    # seed_rng (src/sampling.br:35-40)
+    # seed_rng (src/sampling.br:35-40), through the library's host entry point
     assert BL.seed_rng(0) == 88172645463325252
     assert BL.seed_rng(5) == 5 ^ 88172645463325252
+    assert BL.seed_rng(-3) == ((-3) & (2 ** 64 - 1)) ^ 88172645463325252
+
+
+def test_resolve_seed_equals_the_oracle():
+    """bl_resolve_seed against the oracle's resolve_seed (src/sampling.br:21-33) on random requests, and the
+    xorshift round written out with Python integers."""
+    import numpy as np
+    import _oracle as O
+    L = O.lib()
+    L.orc_resolve_seed.restype = ctypes.c_int64
+    L.orc_resolve_seed.argtypes = [ctypes.c_int64, ctypes.c_uint64, ctypes.c_int64]
+    M = 2 ** 64 - 1
+    rng = np.random.default_rng(3)
+    for k in range(2000):
+        req = int(rng.integers(-5, 5)) if k % 2 else -1
+        ent = int(rng.integers(0, 2 ** 63)) * 2 + (k & 1)
+        cnt = int(rng.integers(0, 2 ** 40)) if k % 3 else k
+        got = BL.resolve_seed(req, ent, cnt)
+        assert got == L.orc_resolve_seed(req, ent, cnt)
+        if req < 0:
+            x = ent ^ ((cnt << 32) & M) ^ cnt
+            x ^= (x << 13) & M
+            x ^= x >> 7
+            x ^= (x << 17) & M
+            assert got == ((x & 0x7FFFFFFF) or 1)
+        else:
+            assert got == req
+    # the mixed value 0 maps to 1
+    assert BL.resolve_seed(-1, 0, 0) == 1
 
 
 def test_workload_generators_are_deterministic():
