@@ -51,7 +51,7 @@ EXPORTS = [
     "bl_workload_drafts", "bl_set_timing", "bl_get_timing", "bl_set_vocab", "bl_slot_grammar", "bl_grammar_mask",
     "bl_workload_c3_vocab", "bl_step_graph_create", "bl_step_graph_launch", "bl_step_graph_destroy",
     "bl_stream_sync", "bl_json_schema_to_gbnf", "bl_slot_schema", "bl_slot_status", "bl_sample_rows_noalloc",
-    "bl_resolve_seed", "bl_seed_rng",
+    "bl_resolve_seed", "bl_seed_rng", "bl_slot_dry_breakers",
 ]
 NOALLOC_BYTES = 64 << 20
 NOALLOC_ROWS = 16
@@ -77,6 +77,7 @@ def lib():
         L.bl_set_eog.argtypes = [C.c_void_p, C.c_int32, i32p, C.c_int]
         L.bl_slot_reset.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_uint64, i32p, C.c_int, i32p, C.c_int,
                                     i32p, f32p, C.c_int]
+        L.bl_slot_dry_breakers.argtypes = [C.c_void_p, C.c_int, i32p, i32p, C.c_int]
         L.bl_slot_rng.argtypes = [C.c_void_p, C.c_int, u64p]
         L.bl_slot_status.argtypes = [C.c_void_p, C.c_int]
         L.bl_slot_commit.argtypes = [C.c_void_p, C.c_int, i32p, C.c_int]
@@ -171,6 +172,13 @@ class Context:
         bi, nb = _arr(C.c_int32, bias.keys())
         bv, _ = _arr(C.c_float, bias.values())
         _check(lib().bl_slot_reset(self.h, slot, C.byref(params), C.c_uint64(rng_state), h, nh, r, nr, bi, bv, nb))
+
+    def slot_dry_breakers(self, slot, breakers):
+        """The request's tokenised DRY sequence breakers, in order (bl_slot_dry_breakers)."""
+        flat = [t for b in breakers for t in b]
+        a, _ = _arr(C.c_int32, flat)
+        ln, n = _arr(C.c_int32, [len(b) for b in breakers])
+        _check(lib().bl_slot_dry_breakers(self.h, slot, a, ln, n))
 
     def slot_rng(self, slot):
         s = C.c_uint64()

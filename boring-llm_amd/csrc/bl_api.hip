@@ -27,6 +27,7 @@ void bl_launch_step(const bl_dev &d, const float *logits, int64_t ld, const bl_r
 void bl_launch_gmask(const bl_dev &d, const bl_rows &rows, hipStream_t s);
 void bl_launch_synth(float *out, int64_t ld, int cfg, int64_t seed, int64_t step, int rows, int V, hipStream_t s);
 void bl_launch_math_digest(int fn, uint32_t first_block, int n_blocks, unsigned long long *out, hipStream_t s);
+void bl_launch_dry_prime(const bl_dev &d, int slot, hipStream_t s);
 
 static thread_local std::string g_err;
 
@@ -92,6 +93,7 @@ struct bl_ctx {
   };
   std::unordered_map<std::string, gram_entry *> grammars;
   std::vector<char> stepped; /* the slot took part in a step since its reset */
+  std::vector<void *> dry_mem; /* [slots] the slot's DRY breakers on the device (bl_slot_dry_breakers) */
   std::vector<int32_t> eog_ids; /* host copy of the end-of-generation registry */
 };
 
@@ -111,6 +113,7 @@ __device__ void commit_one(const bl_dev &d, bl_slot_dev &sp, int slot, int32_t t
   bool is_eog = false;
   for (int k = 0; k < d.n_eog; k++) is_eog |= d.eog[k] == tok;
   sp.n_tokens += 1;
+  bl_dry_push(d, sp, slot, tok);
   if (sp.rep_on) {
     int rl = sp.repeat_last_n;
     if (rl > 0) {
@@ -227,7 +230,8 @@ static bool dev_layout(bl_dev &d, size_t S, size_t R, int vocab, Take take) {
   d.n_eog = 0;
   char *grec = nullptr, *brec = nullptr;
   const bool ok = take(d.slots, S) && take(d.rec, S * d.nb * BL_EB) && take(d.rcnt, S * d.nb) && take(d.ridx, S * V) &&
-                  take(d.ring, S * BL_WCAP) && take(d.eog, 1024) && take(d.eff, R * V) && take(d.c_max, R * d.nc) && take(d.c_arg, R * d.nc) &&
+                  take(d.ring, S * BL_WCAP) && take(d.dring, S * BL_DRY_WCAP) && take(d.dlist, S * BL_DRY_WCAP) &&
+                  take(d.eog, 1024) && take(d.eff, R * V) && take(d.c_max, R * d.nc) && take(d.c_arg, R * d.nc) &&
                   take(d.c_bsum, R * d.nc * BL_SUBS) && take(d.c_tns, R * d.nc * BL_TNS_W) && take(d.cand_v, R * d.nc * BL_KSEL_MAX) &&
                   take(d.cand_i, R * d.nc * BL_KSEL_MAX) && take(grec, R * 2 * G * 32) && take(d.full_v, R * d.nb * BL_EB) &&
                   take(d.full_i, R * d.nb * BL_EB) && take(d.full_cnt, R * d.nb) && take(d.full_s, R * d.nb) &&
@@ -356,6 +360,7 @@ int bl_create(int device, int max_slots, int max_rows, int vocab, bl_ctx **out) 
   c->slot_ready.assign(max_slots, false);
   c->reply.assign(max_slots, {});
   c->stepped.assign(max_slots, 0);
+  c->dry_mem.assign(max_slots, nullptr);
   *out = c;
   return BL_OK;
 }
@@ -371,6 +376,8 @@ void bl_destroy(bl_ctx *c) {
   }
   if (c->d_vblob) hipFree(c->d_vblob);
   if (c->d_voff) hipFree(c->d_voff);
+  for (void *p : c->dry_mem)
+    if (p) hipFree(p);
   void *hp[] = {c->h_slot, c->h_bound, c->h_skip, c->h_tok, c->h_status, c->h_lp, c->h_top_ids, c->h_top_lp, c->h_acc, c->h_out};
   for (void *p : hp)
     if (p) hipHostFree(p);
@@ -451,9 +458,24 @@ static int configure(int V, const bl_params *p, bl_slot_dev &s) {
   /* top-n-sigma filters the candidates of a sampled row (src/sampling.br:752-753); mirostat replaces that chain */
   if (p->temperature > 0.0f && p->top_n_sigma > 0.0f && !(mode & BL_M_MIRO)) mode |= BL_M_TNS;
   s.mode = mode;
-  /* stages without a device path yet */
-  if (p->dry_multiplier != 0.0f && p->dry_base >= 1.0f && p->dry_penalty_last_n != 0)
-    return fail(BL_EUNSUPPORTED, "DRY is not supported on the device");
+  /* DRY (src/sampling.br:114-171): off at multiplier 0, base below 1 or a window of 0; a negative window
+   * leaves the logits unchanged as well */
+  s.dry_on = (p->dry_multiplier != 0.0f && p->dry_base >= 1.0f && p->dry_penalty_last_n > 0) ? 1 : 0;
+  s.dry_mult = p->dry_multiplier;
+  s.dry_base = p->dry_base;
+  s.dry_allowed = p->dry_allowed_length;
+  s.dry_n = p->dry_penalty_last_n;
+  s.dry_maxexp = 0x7fffffff;
+  if (s.dry_on) {
+    if (p->dry_penalty_last_n > BL_DRY_WCAP)
+      return fail(BL_EUNSUPPORTED, "dry_penalty_last_n above %d", BL_DRY_WCAP);
+    if (p->dry_allowed_length < 0) return fail(BL_EUNSUPPORTED, "a negative dry_allowed_length");
+    /* llama.cpp's overflow guard, `(88.7228391 / base.ln()) as int` (truncating, saturating) */
+    if (p->dry_base > 1.000001f) {
+      const float q = 88.7228391f / bl_logf(p->dry_base);
+      s.dry_maxexp = q >= 2147483647.0f ? 0x7fffffff : (int)q;
+    }
+  }
   if (k > BL_KSEL_MAX)
     return fail(BL_EUNSUPPORTED, "top_k/n_probs of %d exceeds the device selection limit", k);
   if (p->repeat_last_n > BL_WCAP) return fail(BL_EUNSUPPORTED, "repeat_last_n above %d", BL_WCAP);
@@ -506,6 +528,20 @@ int bl_slot_reset(bl_ctx *c, int slot, const bl_params *p, uint64_t rng_state, c
       s.win_head = 0;
     }
   }
+  /* DRY's window: the last dry_penalty_last_n history tokens, each with a record; the breakers are set by
+   * bl_slot_dry_breakers (none until then) */
+  std::vector<int32_t> dwin;
+  if (s.dry_on) {
+    const int w = n_hist < s.dry_n ? n_hist : s.dry_n;
+    dwin.assign(history + (n_hist - w), history + n_hist);
+    for (int32_t id : dwin) rec_of(id);
+    s.dh_len = w;
+    s.dh_head = 0;
+  }
+  s.dry_cnt = 0;
+  s.n_bsingle = s.n_bmulti = 0;
+  s.bsingle = nullptr;
+  s.bmulti = nullptr;
   s.rng = rng_state;
   s.n_tokens = n_hist;
   s.n_reply = n_reply;
@@ -518,9 +554,81 @@ int bl_slot_reset(bl_ctx *c, int slot, const bl_params *p, uint64_t rng_state, c
   HIPCHK(hipMemcpy(c->d.rcnt + (size_t)slot * NB, rcnt.data(), NB * sizeof(int32_t), hipMemcpyHostToDevice));
   HIPCHK(hipMemcpy(c->d.ridx + (size_t)slot * V, ridx.data(), (size_t)V * sizeof(int16_t), hipMemcpyHostToDevice));
   HIPCHK(hipMemcpy(c->d.ring + (size_t)slot * BL_WCAP, ring.data(), BL_WCAP * 4, hipMemcpyHostToDevice));
+  if (!dwin.empty())
+    HIPCHK(hipMemcpy(c->d.dring + (size_t)slot * BL_DRY_WCAP, dwin.data(), dwin.size() * 4, hipMemcpyHostToDevice));
   HIPCHK(hipMemcpy(c->d.slots + slot, &s, sizeof s, hipMemcpyHostToDevice));
+  if (c->dry_mem[slot]) {
+    HIPCHK(hipFree(c->dry_mem[slot]));
+    c->dry_mem[slot] = nullptr;
+  }
+  if (s.dry_on) {
+    bl_launch_dry_prime(c->d, slot, c->stream);
+    HIPCHK(hipGetLastError());
+    HIPCHK(hipStreamSynchronize(c->stream));
+  }
   c->host_slots[slot] = s;
   c->slot_ready[slot] = true;
+  return BL_OK;
+}
+
+int bl_slot_dry_breakers(bl_ctx *c, int slot, const int32_t *tokens, const int32_t *lens, int n) {
+  if (!c || slot < 0 || slot >= c->d.max_slots || n < 0 || (n > 0 && (!tokens || !lens)))
+    return fail(BL_EPARAM, "bl_slot_dry_breakers: invalid arguments");
+  if (!c->slot_ready[slot]) return fail(BL_EPARAM, "slot %d is not set up", slot);
+  const int V = c->d.vocab;
+  /* singles: first occurrence, with the count of longer breakers before it; longer ones in list order */
+  std::unordered_map<int32_t, int32_t> first;
+  std::vector<int32_t> multi;
+  int nm = 0;
+  size_t at = 0;
+  for (int i = 0; i < n; i++) {
+    const int L = lens[i];
+    if (L < 0) return fail(BL_EPARAM, "bl_slot_dry_breakers: negative length");
+    for (int q = 0; q < L; q++)
+      if (tokens[at + q] < 0 || tokens[at + q] >= V)
+        return fail(BL_EPARAM, "DRY breaker token %d is outside the vocabulary", tokens[at + q]);
+    if (L == 1) {
+      first.emplace(tokens[at], nm);
+    } else if (L > 1) {
+      if (L > BL_DRY_MLEN || nm >= BL_DRY_MMAX)
+        return fail(BL_EUNSUPPORTED, "DRY breakers: at most %d of 2 to %d tokens", BL_DRY_MMAX, BL_DRY_MLEN);
+      multi.push_back(L);
+      for (int q = 0; q < BL_DRY_MLEN; q++) multi.push_back(q < L ? tokens[at + q] : -1);
+      nm++;
+    }
+    at += (size_t)L;
+  }
+  std::vector<uint64_t> single;
+  single.reserve(first.size());
+  for (auto &kv : first) single.push_back((uint64_t)(uint32_t)kv.first << 32 | (uint32_t)kv.second);
+  std::sort(single.begin(), single.end());
+  hipSetDevice(c->device);
+  HIPCHK(hipStreamSynchronize(c->stream));
+  if (c->dry_mem[slot]) HIPCHK(hipFree(c->dry_mem[slot]));
+  c->dry_mem[slot] = nullptr;
+  const size_t sb = single.size() * 8, mb = multi.size() * 4;
+  if (sb + mb) {
+    HIPCHK(hipMalloc(&c->dry_mem[slot], sb + mb + 16));
+    if (sb) HIPCHK(hipMemcpy(c->dry_mem[slot], single.data(), sb, hipMemcpyHostToDevice));
+    if (mb) HIPCHK(hipMemcpy((char *)c->dry_mem[slot] + sb, multi.data(), mb, hipMemcpyHostToDevice));
+  }
+  /* the device slot has advanced since its reset: only the breaker fields change */
+  bl_slot_dev s;
+  HIPCHK(hipMemcpy(&s, c->d.slots + slot, sizeof s, hipMemcpyDeviceToHost));
+  s.n_bsingle = (int32_t)single.size();
+  s.n_bmulti = nm;
+  s.bsingle = sb ? (const uint64_t *)c->dry_mem[slot] : nullptr;
+  s.bmulti = mb ? (const int32_t *)((char *)c->dry_mem[slot] + sb) : nullptr;
+  HIPCHK(hipMemcpy(c->d.slots + slot, &s, sizeof s, hipMemcpyHostToDevice));
+  c->host_slots[slot].n_bsingle = s.n_bsingle;
+  c->host_slots[slot].n_bmulti = s.n_bmulti;
+  c->host_slots[slot].bsingle = s.bsingle;
+  c->host_slots[slot].bmulti = s.bmulti;
+  if (s.dry_on) {
+    bl_launch_dry_prime(c->d, slot, c->stream);
+    HIPCHK(hipGetLastError());
+    HIPCHK(hipStreamSynchronize(c->stream));
+  }
   return BL_OK;
 }
 
@@ -550,6 +658,10 @@ int bl_slot_commit(bl_ctx *c, int slot, const int32_t *toks, int n) {
   HIPCHK(hipMemcpyAsync(c->d_commit_toks, toks, n * sizeof(int32_t), hipMemcpyHostToDevice, c->stream));
   hipLaunchKernelGGL(bl_k_commit, dim3(1), dim3(64), 0, c->stream, c->d, slot, c->d_commit_toks, n, 0);
   HIPCHK(hipGetLastError());
+  if (c->host_slots[slot].dry_on) {
+    bl_launch_dry_prime(c->d, slot, c->stream);
+    HIPCHK(hipGetLastError());
+  }
   HIPCHK(hipStreamSynchronize(c->stream));
   return BL_OK;
 }
@@ -1047,6 +1159,8 @@ int bl_spec_verify(bl_ctx *c, const int32_t *slots, int B, int k, const float *d
       return fail(BL_EUNSUPPORTED, "speculative rows with XTC are not supported on the device");
     if (k > 0 && (s.mode & BL_M_MIRO))
       return fail(BL_EUNSUPPORTED, "speculative rows with mirostat are not supported on the device");
+    /* row i's DRY window would hold drafts[0..i) */
+    if (k > 0 && s.dry_on) return fail(BL_EUNSUPPORTED, "speculative rows with DRY are not supported on the device");
     /* with dynatemp_range >= temperature the effective temperature can reach 0, and such a row makes no draw
      * (src/sampling.br:576-582): the rows after it would start one draw early in the RNG chain */
     if (k > 0 && s.temperature > 0.0f && s.dynatemp_range > 0.0f && s.dynatemp_range >= s.temperature)

@@ -44,8 +44,13 @@
 
 /* record flags (bl_rec.wf above BL_WF_SHIFT) */
 #define BL_TF_BIAS 1u
+#define BL_TF_DRY 2u        /* the token carries this step's DRY penalty; its exponent above BL_DRY_ESHIFT */
 #define BL_WF_SHIFT 16
 #define BL_WF_WMASK 0xFFFFu /* repeat-window count (at most BL_WCAP) */
+#define BL_DRY_ESHIFT 18    /* DRY exponent (at most BL_DRY_WCAP) in the record's top 14 bits */
+#define BL_DRY_WCAP 2048    /* DRY window (dry_penalty_last_n) capacity */
+#define BL_DRY_MMAX 512     /* DRY sequence breakers of two or more tokens per slot */
+#define BL_DRY_MLEN 24      /* tokens of one such breaker */
 
 /* row modes */
 #define BL_M_GREEDY 1
@@ -124,6 +129,15 @@ struct bl_slot_dev {
   /* mirostat v1 / v2 (src/sampling.br:663-700): the version, tau, eta and the running mu */
   int32_t mirostat;
   float mirostat_tau, mirostat_eta, mu;
+  /* DRY (src/sampling.br:114-171): parameters, the cap on the exponent, the last dry_n history tokens (ring
+   * dh_len / dh_head in bl_dev.dring), the tokens flagged by the last update (bl_dev.dlist), and the sequence
+   * breakers: single tokens sorted as (token << 32 | segment), where segment = the longer breakers listed
+   * before the token's first single occurrence; longer breakers as [length, tokens...] rows in list order */
+  int32_t dry_on, dry_allowed, dry_n, dry_maxexp;
+  float dry_mult, dry_base;
+  int32_t dh_len, dh_head, dry_cnt, n_bsingle, n_bmulti, pad3;
+  const uint64_t *bsingle;
+  const int32_t *bmulti; /* [n_bmulti][BL_DRY_MLEN + 1] */
 };
 
 struct bl_dev {
@@ -133,6 +147,8 @@ struct bl_dev {
   int32_t *rcnt;     /* [slots][nb] */
   int16_t *ridx;     /* [slots][V] */
   int32_t *ring;     /* [slots][WCAP] */
+  int32_t *dring;    /* [slots][DRY_WCAP] DRY's history window */
+  int32_t *dlist;    /* [slots][DRY_WCAP] tokens carrying a DRY penalty */
   int32_t *eog;      /* [n_eog] end-of-generation ids */
   int32_t n_eog;
   /* workspace for up to max_rows rows */
@@ -248,6 +264,21 @@ __device__ inline bl_rec *bl_rec_get(const bl_dev &d, int slot, int32_t tok) {
     base[i] = bl_rec{tok, 0.0f, 0, 0u};
   }
   return base + i;
+}
+
+/* the DRY window's tokens.push (src/server.br:1004); one thread. Every window token keeps a record, where
+ * the update sets its penalty. */
+__device__ inline void bl_dry_push(const bl_dev &d, bl_slot_dev &sp, int slot, int32_t tok) {
+  if (!sp.dry_on) return;
+  int32_t *ring = d.dring + (int64_t)slot * BL_DRY_WCAP;
+  if (sp.dh_len == sp.dry_n) {
+    ring[sp.dh_head] = tok;
+    sp.dh_head = (sp.dh_head + 1) % sp.dry_n;
+  } else {
+    ring[(sp.dh_head + sp.dh_len) % sp.dry_n] = tok;
+    sp.dh_len += 1;
+  }
+  bl_rec_get(d, slot, tok);
 }
 
 /* appends token `tok`'s bytes to the slot's grammar position (reply_tokens.push of a non-EOG token,

@@ -180,6 +180,15 @@ __device__ __forceinline__ float stage_counts(const bl_slot_dev &sp, float v, in
   if (wc > 0) v = v > 0.0f ? v / sp.repeat_penalty : v * sp.repeat_penalty;
   return v;
 }
+/* then DRY's penalty of a token the last update flagged: multiplier * base^exponent (src/sampling.br:163-170) */
+__device__ __forceinline__ float stage_dry(const bl_slot_dev &sp, float v, uint32_t wf) {
+  if ((wf >> BL_WF_SHIFT) & BL_TF_DRY) {
+    const float pw = bl_powf(sp.dry_base, (float)(int)(wf >> BL_DRY_ESHIFT));
+    const float tt = sp.dry_mult * pw;
+    v = v - tt;
+  }
+  return v;
+}
 
 /*
  * The decode loop's per-token stages (src/server.br:940-944: logit_bias, ignore_eos suppression,
@@ -262,7 +271,7 @@ __device__ void apply_stages(const bl_dev &d, const bl_slot_dev &sp, const bl_ro
     }
     float v = vals[p];
     if (!((sup[p >> 5] >> (p & 31)) & 1u) && ((r.wf >> BL_WF_SHIFT) & BL_TF_BIAS)) v = v + r.bias;
-    vals[p] = stage_counts(sp, v, cc, wc);
+    vals[p] = stage_dry(sp, stage_counts(sp, v, cc, wc), r.wf);
     }
   }
   if (SPEC && nd > 0) {
@@ -303,12 +312,14 @@ __device__ __forceinline__ float bl_row_value(const bl_dev &d, const bl_slot_dev
   if (sup) x = -1000000000.0f;
   const bool fp = sp.fp_on && sp.n_reply > 0, rp = sp.rep_on && sp.n_tokens > 0;
   int cc = 0, wc = 0;
+  uint32_t wf = 0u;
   const int ri = d.ridx[(int64_t)slot * d.vocab + tok];
   if (ri >= 0) {
     const bl_rec r = d.rec[((int64_t)slot * d.nb + tok / BL_EB) * BL_EB + ri];
     if (!sup && ((r.wf >> BL_WF_SHIFT) & BL_TF_BIAS)) x = x + r.bias;
     cc = fp ? r.cnt : 0;
     wc = rp ? (int)(r.wf & BL_WF_WMASK) : 0;
+    wf = r.wf;
   }
   if (rows.delta) {
     const int nd = rows.delta_n[row];
@@ -319,7 +330,7 @@ __device__ __forceinline__ float bl_row_value(const bl_dev &d, const bl_slot_dev
         if (sp.rep_on) wc += dl[e].dwcnt;
       }
   }
-  return stage_counts(sp, x, cc, wc);
+  return stage_dry(sp, stage_counts(sp, x, cc, wc), wf);
 }
 
 /* ------------------------------------------------------------------ K1: row pass */
@@ -2424,6 +2435,126 @@ __device__ __forceinline__ void sel_merge(const bl_dev &d, int row, int K, sel_s
   __syncthreads();
 }
 
+/* ------------------------------------------------------------------ DRY's penalty map */
+/* the segment of single-token breaker `tok` (the longer breakers listed before its first occurrence), or -1 */
+__device__ __forceinline__ int dry_single_seg(const bl_slot_dev &sp, int32_t tok) {
+  int lo = 0, hi = sp.n_bsingle;
+  const uint64_t want = (uint64_t)(uint32_t)tok << 32;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (sp.bsingle[mid] < want) lo = mid + 1;
+    else hi = mid;
+  }
+  return lo < sp.n_bsingle && (sp.bsingle[lo] >> 32) == (uint64_t)(uint32_t)tok ? (int)(uint32_t)sp.bsingle[lo] : -1;
+}
+
+#define BL_DRY_LDS (BL_DRY_WCAP * 4 + BL_DRY_WCAP * 8 + (2 * BL_DRY_MMAX + 16) * 4)
+/*
+ * apply_dry_penalty's map (src/sampling.br:114-171) for the slot's next step, from its last dh_len history
+ * tokens, by one workgroup with `lds` (BL_DRY_LDS bytes) as scratch:
+ *   1. the previous update's flags are cleared;
+ *   2. the suffix start (:121-134): each breaker, in list order, moves the start past its last occurrence
+ *      at or after the start. A single token's step is a maximum, so the singles between two longer breakers
+ *      reduce to one maximum per segment; a longer breaker's step needs its last occurrence;
+ *   3. per candidate position, the match between the tokens before it and the context tail (:143-151);
+ *      positions matching at least allowed_length tokens give (token + 1, length) keys, sorted in descending
+ *      order, so that a token's first key holds its maximum repeat;
+ *   4. each such token that is not a single-token breaker gets the flag and the exponent
+ *      min(maximum repeat - allowed_length, cap) in its record (:157-170), and joins the flagged list.
+ * The slot's state is read after the caller's barrier.
+ */
+__device__ __forceinline__ void dry_update(const bl_dev &d, bl_slot_dev &sp, int slot, unsigned char *lds) {
+  const int t = threadIdx.x, NT = (int)blockDim.x;
+  int32_t *lw = reinterpret_cast<int32_t *>(lds);
+  uint64_t *lk = reinterpret_cast<uint64_t *>(lds + BL_DRY_WCAP * 4);
+  int32_t *lseg = reinterpret_cast<int32_t *>(lds + BL_DRY_WCAP * 12); /* [BL_DRY_MMAX + 1] */
+  int32_t *lam = lseg + BL_DRY_MMAX + 1;                           /* [BL_DRY_MMAX] */
+  int32_t *lsc = lam + BL_DRY_MMAX;                                /* start, flagged count */
+  int32_t *dl = d.dlist + (int64_t)slot * BL_DRY_WCAP;
+  auto rec_of = [&](int32_t tok) -> bl_rec * {
+    const int ri = d.ridx[(int64_t)slot * d.vocab + tok];
+    return ri >= 0 ? d.rec + ((int64_t)slot * d.nb + tok / BL_EB) * BL_EB + ri : nullptr;
+  };
+  const uint32_t keep = (1u << (BL_WF_SHIFT + 1)) - 1u; /* window count and the bias flag */
+  const int n_old = sp.dry_cnt, W = sp.dh_len, A = sp.dry_allowed, nm = sp.n_bmulti;
+  for (int i = t; i < n_old; i += NT) {
+    bl_rec *r = rec_of(dl[i]);
+    if (r) r->wf &= keep;
+  }
+  const int32_t *ring = d.dring + (int64_t)slot * BL_DRY_WCAP;
+  for (int p = t; p < W; p += NT) lw[p] = ring[(sp.dh_head + p) % sp.dry_n];
+  for (int m = t; m <= nm; m += NT) lseg[m] = 0;
+  for (int m = t; m < nm; m += NT) lam[m] = -1;
+  if (t == 0) {
+    lsc[0] = 0;
+    lsc[1] = 0;
+  }
+  __syncthreads();
+  if (W > A) { /* window <= allowed_length: no penalty (:120) */
+    for (int p = t; p < W; p += NT) {
+      const int sg = dry_single_seg(sp, lw[p]);
+      if (sg >= 0) atomicMax(&lseg[sg], p + 1);
+    }
+    for (int idx = t; idx < nm * W; idx += NT) {
+      const int m = idx / W, p = idx - m * W;
+      const int32_t *b = sp.bmulti + (int64_t)m * (BL_DRY_MLEN + 1);
+      const int L = b[0];
+      if (p + L <= W) {
+        bool eq = true;
+        for (int q = 0; q < L && eq; q++) eq = lw[p + q] == b[1 + q];
+        if (eq) atomicMax(&lam[m], p);
+      }
+    }
+    __syncthreads();
+    if (t == 0) {
+      int s = 0;
+      for (int m = 0; m < nm; m++) {
+        s = max(s, lseg[m]);
+        if (lam[m] >= s) s = lam[m] + sp.bmulti[(int64_t)m * (BL_DRY_MLEN + 1)];
+      }
+      lsc[0] = max(s, lseg[nm]);
+    }
+    __syncthreads();
+    const int s = lsc[0], suffix = W - s;
+    if (suffix >= A) {
+      int P = 64;
+      while (P < W) P <<= 1;
+      for (int c = t; c < P; c += NT) {
+        uint64_t key = 0ull;
+        if (c > s && c < W) {
+          int r = 0;
+          while (r < suffix && c - r - 1 >= s && lw[c - r - 1] == lw[W - r - 1]) r++;
+          if (r >= A) key = ((uint64_t)((uint32_t)lw[c] + 1u) << 16) | (uint64_t)r;
+        }
+        lk[c] = key;
+      }
+      __syncthreads();
+      bitonic_desc(lk, P);
+      for (int i = t; i < P; i += NT) {
+        const uint64_t k = lk[i];
+        if (!k || (i > 0 && (lk[i - 1] >> 16) == (k >> 16))) continue;
+        const int32_t tok = (int32_t)((k >> 16) - 1u);
+        if (dry_single_seg(sp, tok) >= 0) continue; /* a one-token breaker is exempt */
+        int e = (int)(k & 0xFFFFu) - A;
+        if (e > sp.dry_maxexp) e = sp.dry_maxexp;
+        bl_rec *r = rec_of(tok);
+        if (r) {
+          r->wf = (r->wf & keep) | (BL_TF_DRY << BL_WF_SHIFT) | ((uint32_t)e << BL_DRY_ESHIFT);
+          dl[atomicAdd(&lsc[1], 1)] = tok;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (t == 0) sp.dry_cnt = lsc[1];
+}
+
+/* the penalty map of one slot from its window (after bl_slot_reset, bl_slot_dry_breakers and bl_slot_commit) */
+__global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_dry_prime(bl_dev d, int slot) {
+  __shared__ __align__(16) unsigned char lds[BL_DRY_LDS];
+  dry_update(d, d.slots[slot], slot, lds);
+}
+
 __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const float *__restrict__ logits, int64_t ld,
                                                               bl_rows rows) {
   const int V = d.vocab, nc = d.nc;
@@ -2978,10 +3109,21 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
         if (fp_on) bl_rec_get(d, slot, tok)->cnt += 1;
         if (g_on) grammar_commit(d, sp, d.gram[slot], tok);
       }
+      bl_dry_push(d, sp, slot, tok);
       sp.rng = rng;
       if (mode & BL_M_MIRO) sp.mu = sh.fres[6];
+      sh.ires[7] = 1;
+    } else {
+      sh.ires[7] = 0;
     }
     if (status) sp.err |= status;
+  }
+  if (sp.dry_on) { /* the next step's DRY penalties, from the window with this step's token */
+    __syncthreads();
+    const bool pushed = sh.ires[7] != 0;
+    __syncthreads();
+    static_assert(sizeof(sel_shared) >= BL_DRY_LDS, "DRY scratch");
+    if (pushed) dry_update(d, sp, slot, reinterpret_cast<unsigned char *>(&sh));
   }
 }
 
@@ -3036,6 +3178,10 @@ void bl_launch_gmask(const bl_dev &d, const bl_rows &rows, hipStream_t s) {
   hipLaunchKernelGGL(bl_k_gclear, dim3(1), dim3(64), 0, s, d);
   hipLaunchKernelGGL(bl_k_gmask, dim3(d.gm_blocks, 1), dim3(BL_GM_THREADS), 0, s, d, (const float *)nullptr, (int64_t)0,
                      rows, 0);
+}
+
+void bl_launch_dry_prime(const bl_dev &d, int slot, hipStream_t s) {
+  hipLaunchKernelGGL(bl_k_dry_prime, dim3(1), dim3(BL_SEL_THREADS), 0, s, d, slot);
 }
 
 void bl_launch_synth(float *out, int64_t ld, int cfg, int64_t seed, int64_t step, int rows, int V, hipStream_t s) {

@@ -31,8 +31,9 @@ enum {
   BL_EGRAMMAR_DEAD = -5,   /* "the reply no longer matches the grammar" (src/server.br:320) */
   BL_EGRAMMAR_REJECT = -6, /* "the grammar rejected every vocabulary token" (src/server.br:361) */
   BL_EGRAMMAR_AMBIG = -7,  /* "grammar is left-recursive or too ambiguous to match" (src/grammar.br:354) */
-  BL_EUNSUPPORTED = -8,    /* a sampler stage this library does not run on the device yet: DRY (rejected by
-                              bl_slot_reset); XTC, mirostat or a grammar on speculative rows, or more than 32
+  BL_EUNSUPPORTED = -8,    /* a sampler stage this library does not run on the device yet: DRY windows above
+                              2048 tokens or a negative dry_allowed_length (rejected by bl_slot_reset); XTC,
+                              mirostat, DRY or a grammar on speculative rows, or more than 32
                               drafts with history-dependent penalties; typical_p over a full-vocabulary list
                               above 512 candidates; a mirostat draw that falls through to a prefix end past
                               the candidates within 17.6 T of the maximum */
@@ -110,6 +111,13 @@ uint64_t bl_seed_rng(int64_t seed);
  * (frequency / presence, :91-107), logit_bias as parallel arrays (src/server.br:150-185, :940). */
 int bl_slot_reset(bl_ctx *ctx, int slot, const bl_params *p, uint64_t rng_state, const int32_t *history, int n_hist,
                   const int32_t *reply, int n_reply, const int32_t *bias_ids, const float *bias_vals, int n_bias);
+
+/* The request's DRY sequence breakers, already tokenised (request_dry_breakers, src/server.br:187-232):
+ * n breakers of lens[i] tokens each, concatenated in `tokens`, in the request's order (the order decides where
+ * the repeated suffix may start, src/sampling.br:121-134). bl_slot_reset clears them; call this after it and
+ * before the slot's first step. One-token breakers are unlimited; at most 512 longer ones of up to 24 tokens
+ * (BL_EUNSUPPORTED past that). */
+int bl_slot_dry_breakers(bl_ctx *ctx, int slot, const int32_t *tokens, const int32_t *lens, int n);
 /* The slot's current xorshift64 state (Rng.state, src/sampling.br:18-19). */
 int bl_slot_rng(bl_ctx *ctx, int slot, uint64_t *state);
 /* Append tokens chosen elsewhere to the slot history (tokens.push / reply_tokens.push,

@@ -349,7 +349,21 @@ orc_slot *orc_slot_new(const orc_params *cp, uint64_t rng_state, const int32_t *
   return h;
 }
 void orc_slot_free(orc_slot *h) { delete h; }
+/* the request's tokenised DRY breakers (flat + lens, in order) */
+void orc_slot_set_breakers(orc_slot *h, const int32_t *flat, const int32_t *lens, int64_t nb) {
+  h->s.params.dry_breakers.clear();
+  int64_t at = 0;
+  for (int64_t i = 0; i < nb; i++) {
+    h->s.params.dry_breakers.push_back(Ids(flat + at, flat + at + lens[i]));
+    at += lens[i];
+  }
+}
 uint64_t orc_slot_rng(orc_slot *h) { return h->s.rng.state; }
+/* a token chosen outside the sampler: tokens.push, and reply_tokens.push unless end-of-generation */
+void orc_slot_push(orc_slot *h, int32_t tok, int32_t eos_id) {
+  h->s.tokens.push_back(tok);
+  if (!is_eog_token(tok, eos_id)) h->s.reply.push_back(tok);
+}
 int orc_slot_set_grammar(orc_slot *h, const char *gbnf, const uint8_t *blob, const uint32_t *offsets, int64_t n_tokens,
                          int32_t eos_id) {
   try {

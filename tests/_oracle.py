@@ -121,6 +121,8 @@ def _configure(L):
         L.orc_slot_new.restype = C.c_void_p
         L.orc_slot_new.argtypes = [C.POINTER(OrcParams), C.c_uint64, i32p, i64, i32p, i64, i32p, f32p, i64]
         L.orc_slot_free.argtypes = [C.c_void_p]
+        L.orc_slot_set_breakers.argtypes = [C.c_void_p, i32p, i32p, i64]
+        L.orc_slot_push.argtypes = [C.c_void_p, C.c_int32, C.c_int32]
         L.orc_slot_rng.restype = C.c_uint64
         L.orc_slot_rng.argtypes = [C.c_void_p]
         L.orc_slot_set_grammar.argtypes = [C.c_void_p, C.c_char_p, C.c_char_p, u32p, i64, C.c_int32]

@@ -125,6 +125,107 @@ def run_small(BL, case, steps, coarse=False, ramp=False, quant=None):
     return None
 
 
+DRY_CASES = [
+    # (params, breakers over the alphabet's indices: 0-19 form the phrases, 20-23 are sparse inserts)
+    (dict(temperature=0.0, dry_multiplier=0.8, dry_base=1.75, dry_allowed_length=2, dry_penalty_last_n=64,
+          logprobs=1, n_probs=5), [[20], [21, 22], [4]]),
+    (dict(temperature=0.9, top_k=0, min_p=0.05, dry_multiplier=1.5, dry_base=2.0, dry_allowed_length=1,
+          dry_penalty_last_n=200, repeat_penalty=1.2, repeat_last_n=32, frequency_penalty=0.3), []),
+    (dict(temperature=0.7, top_k=40, dry_multiplier=0.5, dry_base=1.1, dry_allowed_length=3,
+          dry_penalty_last_n=2048, ignore_eos=1, logprobs=1, n_probs=3), [[21], [22, 23], [20], [23, 20, 21]]),
+    (dict(temperature=1.0, top_k=10, dry_multiplier=3.0, dry_base=1.0000005, dry_allowed_length=0,
+          dry_penalty_last_n=16), [[0]]),
+    (dict(temperature=0.0, dry_multiplier=1e-30, dry_base=10.0, dry_allowed_length=0, dry_penalty_last_n=300,
+          logprobs=1, n_probs=2), [[20, 21]]),
+    # a two-token breaker inside a long repeat: the suffix starts after it
+    (dict(temperature=0.0, dry_multiplier=1e-3, dry_base=1.05, dry_allowed_length=2, dry_penalty_last_n=300,
+          logprobs=1, n_probs=8), [[20, 21]]),
+    (dict(temperature=0.0, dry_multiplier=1e-3, dry_base=1.05, dry_allowed_length=2, dry_penalty_last_n=300,
+          logprobs=1, n_probs=8), [[20], [20, 21]]),
+    # phrases holding the pair 20, 21: listing the pair before or after the single 20 moves the start by one
+    # token (cases 7 and 8)
+    (dict(temperature=0.0, dry_multiplier=0.05, dry_base=1.5, dry_allowed_length=0, dry_penalty_last_n=300,
+          logprobs=1, n_probs=8), [[20, 21], [20]]),
+    (dict(temperature=0.0, dry_multiplier=0.05, dry_base=1.5, dry_allowed_length=0, dry_penalty_last_n=300,
+          logprobs=1, n_probs=8), [[20], [20, 21]]),
+]
+
+
+def dry_inputs(case):
+    """A history of 400 tokens of repeated phrases over alphabet tokens 0-19 (so that suffixes recur), with
+    sparse inserts of tokens 20-23 (the breakers' material); the logits favour the phrase tokens, so that the
+    reply keeps repeating. Returns (rng, alphabet, history, reply)."""
+    rng = np.random.default_rng(900 + case)
+    alpha = [int(x) for x in rng.choice(np.arange(20, SMALL_V), 24, replace=False)]
+    phrases = [[alpha[int(i)] for i in rng.integers(0, 20, int(rng.integers(3, 9)))] for _ in range(6)]
+    hist = []
+    while len(hist) < 400:
+        hist += phrases[int(rng.integers(0, 6))]
+        if rng.random() < 0.12:
+            hist += [alpha[20 + int(rng.integers(0, 4))] for _ in range(int(rng.integers(1, 3)))]
+    if case == 4:  # a long exact repeat: maximum repeats past the exponent cap (38 for base 10)
+        hist = (phrases[0] * 80)[:300]
+    if case in (5, 6):  # a phrase repeated, the breaker pair 20, 21 three phrases from the end
+        ph = alpha[:7]
+        hist = ph * 37 + [alpha[20], alpha[21]] + ph * 3
+    if case in (7, 8):
+        hist = [alpha[0], alpha[20], alpha[21], alpha[1], alpha[2], alpha[3]] * 50
+    return rng, alpha, hist[:400], hist[-30:]
+
+
+def run_dry(BL, case, steps):
+    """DRY rows (src/sampling.br:114-171) against the oracle's decode step: the penalty map recomputed on the
+    device after every commit (and after an explicit bl_slot_commit at step steps // 2), breakers in list
+    order (single and multi-token), the exponent cap, logprobs of the penalised logits."""
+    kw, br_idx = DRY_CASES[case]
+    rng, alpha, hist, reply = dry_inputs(case)
+    breakers = [[alpha[i] for i in b] for b in br_idx]
+    ctx = BL.Context(SMALL_V, 2, 2)
+    ctx.set_eog(EOS, EOGS)
+    ctx.slot_reset(1, BL.Params(**kw), BL.seed_rng(950 + case), history=hist, reply=reply)
+    ctx.slot_dry_breakers(1, breakers)
+    op = O.params(**kw)
+    L = O.lib()
+    L.orc_set_eog_tokens(O.ip(O.i32([EOS] + EOGS)), 1 + len(EOGS), -1)
+    hh, rr = O.i32(hist), O.i32(reply)
+    h = L.orc_slot_new(O.C.byref(op), BL.seed_rng(950 + case), O.ip(hh), len(hist), O.ip(rr), len(reply),
+                       O.ip(O.i32([0])), O.fp(O.f32([0.0])), 0)
+    flat = O.i32([t for b in breakers for t in b] or [0])
+    L.orc_slot_set_breakers(h, O.ip(flat), O.ip(O.i32([len(b) for b in breakers] or [0])), len(breakers))
+    wants = 1 if kw.get("logprobs") else 0
+    n_probs = kw.get("n_probs", 0)
+    buf = MEM.zeros(SMALL_V, np.float32)
+    try:
+        for t in range(steps):
+            if t == steps // 2:
+                extra = alpha[t % 24]
+                ctx.commit(1, [extra])
+                L.orc_slot_push(h, extra, EOS)
+            x = (rng.standard_normal(SMALL_V) * 2.0).astype(np.float32)
+            x[alpha[:20]] += np.float32(7.0)
+            buf.upload(x)
+            tok, lp, ti, tl = ctx.sample_step([1], buf.ptr, SMALL_V, top_stride=max(n_probs, 1))
+            ot, olp = np.zeros(1, np.int32), np.zeros(1, np.float32)
+            oti, otl = np.full(max(n_probs, 1), -1, np.int32), np.zeros(max(n_probs, 1), np.float32)
+            eog = O.C.c_int()
+            assert L.orc_slot_step(h, O.fp(x), SMALL_V, wants, 1, O.ip(ot), O.fp(olp), O.ip(oti), O.fp(otl),
+                                   O.C.byref(eog)) == 0
+            if tok[0] != ot[0]:
+                return f"step {t}: token {tok[0]} vs {ot[0]}"
+            if wants and not eog.value:
+                if not lp_close(lp[0], olp[0]):
+                    return f"step {t}: logprob {lp[0]} vs {olp[0]}"
+                if ti[0][:n_probs] != list(oti[:n_probs]) or not all(lp_close(tl[0][q], otl[q]) for q in range(n_probs)):
+                    return f"step {t}: alternatives differ"
+        if ctx.slot_rng(1) != L.orc_slot_rng(h):
+            return "final RNG state differs"
+    finally:
+        L.orc_slot_free(h)
+        L.orc_set_eog_tokens(O.ip(O.i32([0])), 0, -1)
+        ctx.close()
+    return None
+
+
 def run_bigties(BL, steps):
     """Two full-vocabulary rows (T 1.0 with min-p 0.05; T 0.7 with top-p 0.95 and min-p 0.02) at V=151936 on
     N(0, 3^2) logits rounded to bfloat16 (several tokens share each bfloat16 value within 4 of the maximum,
@@ -806,6 +907,9 @@ def main():
             results.append(("top-n-sigma rows at V=151936", run_tns(BL, int(f[1]))))
         elif kind == "miro":
             results.append(("mirostat v2 rows", run_mirostat(BL, int(f[1]))))
+        elif kind == "dry":  # dry:cases[:steps]
+            for c in parse_range(f[1]):
+                results.append((f"DRY case {c}", run_dry(BL, c, int(f[2]) if len(f) > 2 else 20)))
         elif kind == "miro1":  # miro1:steps[:V]
             V = int(f[2]) if len(f) > 2 else SMALL_V
             results.append((f"mirostat v1 rows at V={V}", run_mirostat(BL, int(f[1]), 1, V)))

@@ -89,6 +89,13 @@ def test_mirostat_v2_rows():
     assert err is None, err
 
 
+@pytest.mark.parametrize("case", range(len(RP.DRY_CASES)))
+def test_dry_rows(case):
+    print(f"DRY case {case}: {RP.DRY_CASES[case]}: 40 steps", flush=True)
+    err = RP.run_dry(BL, case, 40)
+    assert err is None, err
+
+
 def test_mirostat_v1_rows():
     print("three mirostat v1 rows, V=5003: 40 steps; V=151936: 12 steps", flush=True)
     err = RP.run_mirostat(BL, 40, 1)

@@ -125,6 +125,14 @@ def test_dynatemp_exponents(simt_lib):
     assert out.count("ok   small case") == 2
 
 
+def test_dry(simt_lib):
+    """DRY rows (src/sampling.br:114-171): the device's penalty map, recomputed after every commit and after an
+    explicit bl_slot_commit, against the oracle's decode step: one- and two-token breakers in both list orders,
+    the exponent cap, a base within 1e-6 of 1, logprobs of the penalised logits (nine cases)."""
+    out = _run(simt_lib, ["dry:0-8:10"], {"SIMT_ORDER": "rand"})
+    assert out.count("ok   DRY case") == 9
+
+
 def test_allocation_free_step(simt_lib):
     """bl_sample_rows_noalloc (slot state and workspace carved from its fixed array), twice in a row with
     the second call smaller, equals bl_sample_step over fresh slots with the same parameters and RNG states:
@@ -141,7 +149,7 @@ def test_small_cases_address_sanitizer():
         assert os.path.isabs(p) and os.path.exists(p), f"{rt} not found"
         pre.append(p)
     env = {"LD_PRELOAD": " ".join(pre), "ASAN_OPTIONS": "detect_leaks=0", "UBSAN_OPTIONS": "print_stacktrace=1"}
-    out = _run(os.path.join(SIMT, "_build", "libbl_simt_asan.so"), ["small:0-20:3", "coarse:1,5:3", "ramp:8:2", "grammar:0-6:20", "q4:2,9:4"], env)
+    out = _run(os.path.join(SIMT, "_build", "libbl_simt_asan.so"), ["small:0-20:3", "coarse:1,5:3", "ramp:8:2", "grammar:0-6:20", "q4:2,9:4", "dry:0-8:3"], env)
     assert "ERROR: AddressSanitizer" not in out and "runtime error" not in out
 
 
