@@ -740,13 +740,13 @@ int bl_slot_grammar(bl_ctx *c, int slot, const char *gbnf, size_t len) {
   bl_slot_dev s = c->host_slots[slot];
   if (!gbnf || len == 0) {
     s.g_on = 0;
-    s.mode &= ~BL_M_GRAMMAR;
+    s.mode &= ~(BL_M_GRAMMAR | BL_M_GFULL);
   } else {
     if (c->voff.empty()) return fail(BL_EPARAM, "bl_slot_grammar: the vocabulary pieces are not set (bl_set_vocab)");
     if (s.mirostat != 0)
       return fail(BL_EPARAM, "stateful adaptive sampling cannot be combined with constrained decoding");
-    if (s.temperature > 0.0f)
-      return fail(BL_EUNSUPPORTED, "grammar-constrained sampling with temperature > 0 is not supported on the device");
+    if (s.temperature > 0.0f && s.top_n_sigma > 0.0f)
+      return fail(BL_EUNSUPPORTED, "grammar-constrained sampling with top_n_sigma is not supported on the device");
     bl_ctx::gram_entry *e = nullptr;
     int rc = grammar_tables(c, std::string(gbnf, len), &e);
     if (rc) return rc;
@@ -759,6 +759,12 @@ int bl_slot_grammar(bl_ctx *c, int slot, const char *gbnf, size_t len) {
     s.gpos = pos;
     s.g_on = 1;
     s.mode |= BL_M_GRAMMAR;
+    /* a sampled top-k row widens k 4-fold while no allowed token ranks within it: the merged list keeps the
+     * first BL_KSEL_MAX ranks for those levels */
+    if (s.temperature > 0.0f && (s.mode & BL_M_TOPK)) {
+      s.k_sel = BL_KSEL_MAX < c->d.vocab ? BL_KSEL_MAX : c->d.vocab;
+      s.mode |= BL_M_GFULL;
+    }
     hipSetDevice(c->device);
     HIPCHK(hipStreamSynchronize(c->stream));
     HIPCHK(hipMemcpy(c->d.gram + slot, &e->dev, sizeof(bl_gram_view), hipMemcpyHostToDevice));
@@ -846,7 +852,7 @@ static void mark_stepped(bl_ctx *c, const int32_t *slots, int B) {
 static bool needs_pass2(bl_ctx *c, const int32_t *slots, int B) {
   for (int i = 0; i < B; i++) {
     const bl_slot_dev &s = c->host_slots[slots[i]];
-    if (s.mode & (BL_M_LOGPROBS | BL_M_FULL)) return true;
+    if (s.mode & (BL_M_LOGPROBS | BL_M_FULL | BL_M_GFULL)) return true;
   }
   return false;
 }
@@ -1011,7 +1017,7 @@ int bl_sample_rows_noalloc(int device, void *stream, const bl_params *params, ui
   rows.top_ids = d_out + 3 * B;
   rows.top_lp = reinterpret_cast<float *>(d_out + 3 * B + B * tsa);
   bool pass2 = false;
-  for (int i = 0; i < B; i++) pass2 |= (hs[i].mode & (BL_M_LOGPROBS | BL_M_FULL)) != 0;
+  for (int i = 0; i < B; i++) pass2 |= (hs[i].mode & (BL_M_LOGPROBS | BL_M_FULL | BL_M_GFULL)) != 0;
   bl_launch_step(d, d_logits, ld, rows, B, pass2, false, st, nullptr);
   HIPCHK(hipGetLastError());
   int32_t status[BL_NOALLOC_ROWS];

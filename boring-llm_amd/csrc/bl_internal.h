@@ -61,6 +61,8 @@
 #define BL_M_PSP 32 /* logprobs as post-sampling probabilities (src/server.br:1015-1025) */
 #define BL_M_MIRO 64 /* the draw is mirostat v2's */
 #define BL_M_TNS 128 /* top-n-sigma filters the ranked candidates (src/sampling.br:376-407) */
+#define BL_M_GFULL 256 /* a sampled top-k grammar row: the exponent pass also lists its allowed candidates, for
+                          the widening level that ranks the whole vocabulary */
 
 /* grammar mask kernel: tokens per workgroup */
 #define BL_GM_THREADS 256

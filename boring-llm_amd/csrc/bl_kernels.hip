@@ -841,7 +841,7 @@ __device__ __forceinline__ void exppass_body(const bl_dev &d, const float *__res
   const int slot = bl_row_slot(rows, row);
   const bl_slot_dev &sp = slot_of(d, slot);
   const int mode = sp.mode;
-  if (!(mode & (BL_M_LOGPROBS | BL_M_FULL))) return;
+  if (!(mode & (BL_M_LOGPROBS | BL_M_FULL | BL_M_GFULL))) return;
   __shared__ uint64_t s_tab[BL_EXP2_N]; /* expf's 2^(i/32) table */
   float *const vals = reinterpret_cast<float *>(k2_lds); /* [BL_EB] */
   __shared__ uint32_t st_sup[BL_EB / 32], st_done[SPEC ? BL_EB / 32 : 1];
@@ -1042,17 +1042,38 @@ __device__ __forceinline__ void exppass_body(const bl_dev &d, const float *__res
       }
     }
   }
-  if (mode & BL_M_FULL) {
+  if (mode & (BL_M_FULL | BL_M_GFULL)) {
     /* candidates of a full-vocabulary rank (within bl_cand_span of the maximum). The block writes them
      * in index order to its own BL_EB-entry region, and their count: no counter is shared between
-     * workgroups */
+     * workgroups. A sampled full-vocabulary grammar row ranks its allowed tokens only (src/server.br:334-357):
+     * the mask filters them, and the span counts from the allowed maximum (the grammar pass's block maxima);
+     * a sampled top-k grammar row lists every candidate, for its widening levels */
     __shared__ int f_w[BL_RP_THREADS / 64];
     const float T = sp.temperature;
     const bool filt = bl_probs_on(sp);
-    const float thr = M - bl_cand_span(sp);
+    const bool gsel = (mode & BL_M_GRAMMAR) && (mode & BL_M_FULL) && T > 0.0f;
+    float Mc = M;
+    uint32_t amask = 0xFu; /* this thread's four tokens: allowed */
+    if (gsel) {
+      __shared__ float g_m[BL_RP_THREADS / 64];
+      float gm = BL_NEG_INF;
+      for (int k = t; k < d.gm_blocks; k += BL_RP_THREADS) gm = fmaxf(gm, d.gm_max[(int64_t)row * d.gm_blocks + k]);
+      int gi = 0;
+      bl_wargmax(gm, gi, lane);
+      if (lane == 0) g_m[w] = gm;
+      __syncthreads();
+      Mc = g_m[0];
+#pragma unroll
+      for (int q = 1; q < BL_RP_THREADS / 64; q++) Mc = fmaxf(Mc, g_m[q]);
+      const int64_t words = 2 * (((int64_t)V + 63) / 64);
+      const int tk = i0 + j0;
+      amask = tk < V ? (d.gmask[(int64_t)row * words + (tk >> 6) * 2 + ((tk >> 5) & 1)] >> (tk & 31)) & 0xFu : 0u;
+    }
+    const float thr = Mc - bl_cand_span(sp);
+    auto keep_k = [&](int k) { return j0 + k < cnt && x[k] >= thr && ((amask >> k) & 1u); };
     int mine = 0;
 #pragma unroll
-    for (int k = 0; k < 4; k++) mine += (j0 + k < cnt && x[k] >= thr) ? 1 : 0;
+    for (int k = 0; k < 4; k++) mine += keep_k(k) ? 1 : 0;
     const int incl = bl_wscan_add(mine, lane);
     if (lane == 63) f_w[w] = incl;
     __syncthreads();
@@ -1065,7 +1086,7 @@ __device__ __forceinline__ void exppass_body(const bl_dev &d, const float *__res
     const int64_t ro = ((int64_t)row * d.nb + b) * BL_EB;
 #pragma unroll
     for (int k = 0; k < 4; k++)
-      if (j0 + k < cnt && x[k] >= thr) {
+      if (keep_k(k)) {
         d.full_v[ro + pos] = x[k];
         d.full_i[ro + pos] = i0 + j0 + k;
         pos++;
@@ -1078,7 +1099,7 @@ __device__ __forceinline__ void exppass_body(const bl_dev &d, const float *__res
       float ps = 0.0f;
 #pragma unroll
       for (int k = 0; k < 4; k++)
-        if (j0 + k < cnt && x[k] >= thr) ps += __expf((x[k] - M) * rT);
+        if (keep_k(k)) ps += __expf((x[k] - Mc) * rT);
       const double ws = bl_wave_sum_d((double)ps);
       __shared__ double f_s[BL_RP_THREADS / 64];
       if (lane == 0) f_s[w] = ws;
@@ -2620,7 +2641,11 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
   int32_t tok = Mi;
   float tokv = M;
   const bool gram = (mode & BL_M_GRAMMAR) != 0;
-  const bool sampled = !gram && T > 0.0f;
+  /* a grammar row with T > 0 samples from its allowed candidates (src/server.br:323-362) unless its frontier
+   * is dead, ambiguous or forces the end of sequence (then the grammar block below decides) */
+  const int gst0 = gram ? d.gstat[row] : 0;
+  const bool sampled =
+      T > 0.0f && (!gram || (!(gst0 & (BL_GR_FAMBIG | BL_GR_DEAD | BL_GR_FORCED)) && d.gamb[row] == 0));
   /* top-n-sigma (src/sampling.br:376-407): the threshold max - n * sigma, by wavefront 0 from the row pass's
    * chunk statistics; candidates below it leave the ranked list (the reference sets them to -1e30, which
    * ranks them after every other value and gives them no weight) */
@@ -2669,15 +2694,69 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
   /* the ranked candidate list of a sampled row */
   uint64_t *keys = sh.c.keys;
   int64_t n_list = 0, n_logical = 0;
-  if (sampled && (mode & BL_M_TOPK)) {
+  const int64_t gwords = 2 * (((int64_t)V + 63) / 64);
+  const uint32_t *gmk = d.gmask + (int64_t)row * gwords;
+  auto g_allowed = [&](int32_t id) { return ((gmk[(id >> 6) * 2 + ((id >> 5) & 1)] >> (id & 31)) & 1u) != 0u; };
+  float Mc = M; /* the top of the ranked list: the row maximum, or a grammar row's allowed maximum */
+  bool gfull = false; /* a top-k grammar row's widening went past the merged list */
+  int gk = 0;         /* its next level */
+  if (sampled && gram && (mode & BL_M_TOPK)) {
+    /* sample_grammar_token's levels (src/server.br:323-362): the allowed entries of top_k_select(k) in rank
+     * order, k widened 4-fold while none is allowed. The merged list holds the first K ranks; a level past
+     * it is left unsupported */
+    const int32_t my_id = mk ? ckey_i(mk) : 0; /* an unfilled entry reads (-1e30, 0), as in top_k_select */
+    const bool a_me = t < K && g_allowed(my_id);
+    int kk = sp.top_k < V ? sp.top_k : V;
+    for (;;) {
+      if (kk > K || kk >= V) { /* past the merged list: the levels continue on the sorted full list below */
+        gfull = true;
+        gk = kk;
+        break;
+      }
+      const int f = a_me && t < kk ? 1 : 0;
+      const int incl = bl_wscan_add(f, lane);
+      if (lane == 63) sh.red_i[w] = incl;
+      __syncthreads();
+      int before = incl - f, tot = 0;
+      for (int q = 0; q < SEL_NW; q++) {
+        if (q < w) before += sh.red_i[q];
+        tot += sh.red_i[q];
+      }
+      __syncthreads();
+      if (tot > 0) {
+        if (f) keys[before] = mk;
+        n_list = n_logical = tot;
+        break;
+      }
+      kk = kk * 4 < V ? kk * 4 : V;
+    }
+  } else if (sampled && (mode & BL_M_TOPK)) {
     /* top_k_select list: kk = min(top_k, V) <= K entries, unfilled slots are (-1e30, 0) */
     const int kk = sp.top_k < V ? sp.top_k : V;
     if (t < kk) keys[t] = (mk && ckey_v(mk) >= tns_thr) ? mk : 0ull; /* top-n-sigma: unfilled past its threshold */
     n_list = n_logical = kk;
-  } else if (sampled) {
+  }
+  if (sampled && (gfull || !(mode & BL_M_TOPK))) {
     /* full-vocabulary rank (src/sampling.br:301-365): the exponent blocks' candidates (block b's at
-     * [b*BL_EB, b*BL_EB + count)), concatenated by the prefix sum of the counts, then sorted */
+     * [b*BL_EB, b*BL_EB + count)), concatenated by the prefix sum of the counts, then sorted. A grammar
+     * row's candidates are its allowed tokens near the allowed maximum, and its list counts every allowed
+     * token */
     const int NB = d.nb;
+    if (gram && !(mode & BL_M_TOPK)) {
+      float gm = BL_NEG_INF;
+      int ga = 0;
+      for (int k = t; k < d.gm_blocks; k += BL_SEL_THREADS) gm = fmaxf(gm, d.gm_max[(int64_t)row * d.gm_blocks + k]);
+      double na = 0.0;
+      for (int64_t q = t; q < gwords; q += BL_SEL_THREADS) na += (double)__popc(gmk[q]);
+      bl_wargmax(gm, ga, lane);
+      if (lane == 0) sh.red_m[w] = gm;
+      na = block_sum_d<BL_SEL_THREADS>(na, sh.c.gsum); /* synchronises */
+      Mc = sh.red_m[0];
+      for (int q = 1; q < SEL_NW; q++) Mc = fmaxf(Mc, sh.red_m[q]);
+      __syncthreads();
+      if (na < 1.0) status |= BL_SE_GREJECT;
+      n_logical = (int64_t)na;
+    }
     const float *fv = d.full_v + (int64_t)row * NB * BL_EB;
     const int32_t *fi = d.full_i + (int64_t)row * NB * BL_EB;
     int *boff = reinterpret_cast<int *>(&sh.n); /* [NB + 1]; the normaliser's LDS is free until norm_prep */
@@ -2755,8 +2834,8 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
        * lower buckets, equal values in one bucket), scattered by bucket, then ranked by counting within
        * each bucket, one LDS tile of the bucketed list at a time */
       const float T = sp.temperature;
-      float thr = fmaxf(M - bl_cand_span(sp), tns_thr); /* the exponent pass's candidates, top-n-sigma's survivors */
-      if (!filt) {
+      float thr = fmaxf(Mc - bl_cand_span(sp), tns_thr); /* the exponent pass's candidates, top-n-sigma's survivors */
+      if (!filt && !(gram && (mode & BL_M_TOPK))) { /* a top-k grammar row draws from a subset: no cut */
         /* the draw adds exp((v - M) / T) in descending order. With u = 2^-24 and m <= V terms, the float
          * running sum past every term >= 2^(k-24) is at least (1 - g) (S - V 2^(k-24)), g = m u / (1 - m u)
          * (recursive summation bound), S the exact sum; that is >= 2^k when S >= 2^k (1 / (1 - g) + V u).
@@ -2770,16 +2849,16 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
         const double s_lo = s_ap * 0.999 / need;
         if (mu < 0.5 && s_lo > 0.0) {
           const int k = (int)((bl_d2u(s_lo) >> 52) & 0x7ff) - 1023; /* floor(log2 s_lo), s_lo normal */
-          const float cut = M + T * ((float)((double)(k - 24) * 0.6931471805599453) - 1.0e-3f);
+          const float cut = Mc + T * ((float)((double)(k - 24) * 0.6931471805599453) - 1.0e-3f);
           thr = fmaxf(thr, cut);
         }
       }
       uint64_t *A = d.sortk + (int64_t)row * (2 * (int64_t)V), *Bk = A + V;
       uint32_t *cnt = reinterpret_cast<uint32_t *>(sh.c.keys); /* BL_NBUCKET counters; the list is in memory */
-      const float span = M - thr;
+      const float span = Mc - thr;
       const float scale = span > 0.0f ? (float)BL_NBUCKET / span : 0.0f;
       auto bucket = [&](float v) -> int {
-        const float q = (M - v) * scale;
+        const float q = (Mc - v) * scale;
         return q >= 0.0f ? (q < (float)(BL_NBUCKET - 1) ? (int)q : BL_NBUCKET - 1) : 0;
       };
       for (int b = t; b < BL_NBUCKET; b += BL_SEL_THREADS) cnt[b] = 0u;
@@ -2895,9 +2974,63 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
       nl = nk;
     }
     n_list = nl;
-    n_logical = V;
+    if (!gram) n_logical = V;
   }
   __syncthreads();
+  bool glevel_v = gram && !(mode & BL_M_TOPK); /* the list ranks the whole vocabulary (heap order of ties) */
+  if (sampled && gram && gfull && !status) {
+    /* the widening levels past the merged list, on the sorted candidates (every value within the span of
+     * the row maximum): level k's entries are the allowed ones among the first k. A level past the list's
+     * end would need tokens beyond the span: unsupported, as is the whole-vocabulary level when an allowed
+     * token lies beyond the span */
+    double na = 0.0;
+    for (int64_t q = t; q < gwords; q += BL_SEL_THREADS) na += (double)__popc(gmk[q]);
+    na = block_sum_d<BL_SEL_THREADS>(na, sh.c.gsum);
+    int kk = gk;
+    for (;;) {
+      const bool vlevel = kk >= V;
+      if (!vlevel && kk > n_list) {
+        status |= BL_SE_UNSUPPORTED;
+        break;
+      }
+      const int64_t lim = vlevel ? n_list : kk;
+      double c = 0.0;
+      for (int64_t j = t; j < lim; j += BL_SEL_THREADS) c += g_allowed(keys[j] ? ckey_i(keys[j]) : 0) ? 1.0 : 0.0;
+      c = block_sum_d<BL_SEL_THREADS>(c, sh.c.gsum);
+      if (c > 0.0) {
+        if (vlevel && c != na) {
+          status |= BL_SE_UNSUPPORTED;
+          break;
+        }
+        glevel_v = vlevel;
+        /* stable compaction of the level's allowed entries to the list's front, a tile at a time */
+        int64_t off = 0;
+        for (int64_t base = 0; base < lim; base += BL_SEL_THREADS) {
+          const int64_t j = base + t;
+          const uint64_t k = j < lim ? keys[j] : 0ull;
+          const int f = j < lim && g_allowed(k ? ckey_i(k) : 0) ? 1 : 0;
+          const int incl = bl_wscan_add(f, lane);
+          if (lane == 63) sh.red_i[w] = incl;
+          __syncthreads();
+          int before = incl - f, tot = 0;
+          for (int q = 0; q < SEL_NW; q++) {
+            if (q < w) before += sh.red_i[q];
+            tot += sh.red_i[q];
+          }
+          if (f) keys[off + before] = k;
+          off += tot;
+          __syncthreads();
+        }
+        n_list = n_logical = (int64_t)c;
+        break;
+      }
+      if (vlevel) {
+        status |= na < 1.0 ? BL_SE_GREJECT : BL_SE_UNSUPPORTED;
+        break;
+      }
+      kk = kk * 4 < V ? kk * 4 : V;
+    }
+  }
   auto val = [&](int64_t j) -> float { return keys[j] ? ckey_v(keys[j]) : -1.0e30f; };
   int64_t keep = 1;
   const bool miro = sampled && (mode & BL_M_MIRO) != 0;
@@ -2923,7 +3056,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
   /* a draw position -> its list position */
   auto lpos = [&](int64_t j) -> int64_t { return typ ? (int64_t)sh.ser_o[j] : j; };
 
-  if (gram) {
+  if (gram && !sampled) {
     /* sample_grammar_token, greedy (src/server.br:308-361): the frontier's status, then the first
      * allowed candidate in rank order = the allowed maximum; the lowest index among equal allowed
      * maxima is top_k_select's order but not the heap rank's, so a tie is reported */
@@ -3007,11 +3140,12 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
       tokv = kp ? ckey_v(kp) : bl_row_value(d, sp, rows, row, slot, logits, ld, tok);
       /* the heap rank orders equal values its own way (src/sampling.br:310-364): a draw on a tie takes
        * the heap's token (or reports the tie when the simulation does not fit) */
-      if (mode & BL_M_FULL) {
+      if ((mode & BL_M_FULL) || glevel_v) {
         const float vp = val(pos);
         if ((pos > 0 && val(pos - 1) == vp) || (pos + 1 < n_list && val(pos + 1) == vp)) {
-          const int hid = heap_tie_id([&](int64_t j) { return keys[j]; }, keys == sh.c.keys, n_list, pos, V,
-                                      d.full_i + (int64_t)row * d.nb * BL_EB, sh);
+          /* a grammar row's list is the heap order of the whole row restricted to its allowed tokens */
+          const int hid = gram ? -1 : heap_tie_id([&](int64_t j) { return keys[j]; }, keys == sh.c.keys, n_list, pos, V,
+                                                  d.full_i + (int64_t)row * d.nb * BL_EB, sh);
           if (hid >= 0) tok = hid;
           else status |= BL_SE_TIE;
         }
@@ -3028,7 +3162,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
   int psp_n = 0;
   float psp_tok = 0.0f;
   if (psp_row) {
-    if (sampled) {
+    if (sampled && !gram) {
       if (!status) {
         const int64_t avail = (int64_t)dr.cut - dr.first;
         psp_n = (int)(avail < n_alt ? avail : n_alt);

@@ -138,10 +138,14 @@ int bl_set_vocab(bl_ctx *ctx, const uint8_t *blob, const uint32_t *offsets, int 
 /* Attach a GBNF grammar to a slot set up by bl_slot_reset, before its first step (the request's
  * `grammar` field; parse_gbnf src/grammar.br:309-323). The slot's steps then follow
  * sample_grammar_token (src/server.br:308-361): forced EOS when the reply is complete and cannot
- * continue, otherwise the first allowed candidate in rank order (greedy: temperature <= 0 only on the
- * device). gbnf = NULL detaches. Errors: BL_EGRAMMAR (parse, with the reference's message),
- * BL_EGRAMMAR_AMBIG, BL_EUNSUPPORTED (temperature > 0, or a grammar whose reachable automaton exceeds
- * 65536 states: a recursive one). */
+ * continue, otherwise the allowed candidates in rank order: the first (temperature <= 0), or a draw of
+ * sample_candidates over them (temperature > 0: the allowed entries of top_k_select(k), k widened 4-fold
+ * while none is allowed; of the whole ranking without top_k). gbnf = NULL detaches. Errors: BL_EGRAMMAR
+ * (parse, with the reference's message), BL_EGRAMMAR_AMBIG, BL_EUNSUPPORTED (top_n_sigma with
+ * temperature > 0, or a grammar whose reachable automaton exceeds 65536 states: a recursive one). A
+ * sampled step returns BL_EUNSUPPORTED when the widening reaches a level whose ranks go past the values
+ * within the candidate span of the row maximum, and BL_ETIE when a whole-vocabulary draw lands on equal
+ * allowed values. */
 int bl_slot_grammar(bl_ctx *ctx, int slot, const char *gbnf, size_t len);
 
 /* JSON Schema -> GBNF (json_schema_to_gbnf, src/schema_grammar.br:313-337, over the schema text parsed as

@@ -761,6 +761,7 @@ GRAMMAR_CASES = [
     None,  # the workload-3 schema grammar (tests/golden/c3_schema.gbnf)
     'root ::= [^\\x00-\\x7f]{1,6} ("." [^\\x00-\\x7f])* ";"\n',
     'root ::= ("\\u00e9\\u20ac" | "\\U0001F600" | "a")+ "."\n',
+    'root ::= "x" [0-9]+ ";"\n',  # few allowed tokens: sampled top-k rows widen past the merged list
 ]
 
 
@@ -784,8 +785,29 @@ def grammar_vocab(rng, n_extra):
     return b"".join(pieces), off, len(pieces) - 1
 
 
-def run_grammar_case(BL, case, steps):
-    """Masks and greedy tokens of a small grammar against the oracle's slot on random rows."""
+# sampled grammar rows (src/server.br:323-362): (grammar case, parameters, logit sigma)
+GRAMMAR_SAMPLED = [
+    (0, dict(temperature=0.8, top_k=40), 3.0),
+    (3, dict(temperature=0.8, top_k=40, top_p=0.9, logprobs=1, n_probs=4), 3.0),
+    (4, dict(temperature=1.0, top_k=0, min_p=0.05), 3.0),
+    (2, dict(temperature=0.7, top_k=0, repeat_penalty=1.2, repeat_last_n=16, logprobs=1, n_probs=3,
+             post_sampling_probs=1), 3.0),
+    (6, dict(temperature=1.2, top_k=200, xtc_probability=0.5, xtc_threshold=0.1), 3.0),
+    (1, dict(temperature=0.9, top_k=5), 3.0),
+    # widening past the merged top-256 list (levels 640 and the whole vocabulary)
+    (7, dict(temperature=0.9, top_k=40), 3.0),
+    (7, dict(temperature=0.8, top_k=10, logprobs=1, n_probs=2), 2.0),
+    # full-vocabulary rows whose allowed maximum lies far below the row maximum
+    (4, dict(temperature=1.0, top_k=0), 12.0),
+    (7, dict(temperature=0.8, top_k=0, top_p=0.95), 12.0),
+]
+
+
+def run_grammar_case(BL, case, steps, kw=None, sigma=3.0):
+    """Masks and tokens of a small grammar against the oracle's slot on random rows: greedy, or sampled with
+    the parameters `kw` (the RNG carried across the replies that end or die); logits N(0, sigma^2)."""
+    kw = kw or {}
+    seed = 77 if kw else 1
     rng = np.random.default_rng(500 + case)
     blob, off, eos = grammar_vocab(rng, 700)
     V = len(off) - 1
@@ -795,16 +817,24 @@ def run_grammar_case(BL, case, steps):
             gbnf = f.read()
     L = O.lib()
     L.orc_set_eog_tokens(O.ip(O.i32([0])), 0, -1)
-    op = O.params()
-    h = L.orc_slot_new(O.C.byref(op), 1, None, 0, None, 0, None, None, 0)
+    op = O.params(**kw)
+    rs = BL.seed_rng(seed) if kw else 1
+    h = L.orc_slot_new(O.C.byref(op), rs, None, 0, None, 0, None, None, 0)
     oo = np.array(off, np.uint32)
     assert L.orc_slot_set_grammar(h, gbnf.encode(), blob, oo.ctypes.data_as(O.C.POINTER(O.C.c_uint32)), V,
                                   eos) == 0, O.last_error()
     ctx = BL.Context(V, 1, 1)
     ctx.set_eog(eos, [])
     ctx.set_vocab(blob, off)
-    ctx.slot_reset(0, BL.Params(), 1)
+    ctx.slot_reset(0, BL.Params(**kw), rs)
     ctx.slot_grammar(0, gbnf)
+    wants = 1 if kw.get("logprobs") else 0
+    n_probs = kw.get("n_probs", 0)
+
+    def restart():
+        L.orc_slot_restart(h)
+        ctx.slot_reset(0, BL.Params(**kw), ctx.slot_rng(0))
+        ctx.slot_grammar(0, gbnf)
     words = (V + 31) // 32
     mask, want = MEM.zeros(words, np.uint32), np.zeros(words, np.uint32)
     buf = MEM.zeros(V, np.float32)
@@ -819,9 +849,7 @@ def run_grammar_case(BL, case, steps):
                     return f"step {t}: device '{e}', oracle mask status {ok}"
                 # both find the reply dead (a piece can be allowed and the re-decoded reply still fail,
                 # src/server.br:311-318): start a new reply
-                L.orc_slot_restart(h)
-                ctx.slot_reset(0, BL.Params(), 1)
-                ctx.slot_grammar(0, gbnf)
+                restart()
                 continue
             if ok != 1:
                 return f"step {t}: the oracle's reply is dead ({ok}) but the device's is not"
@@ -829,13 +857,15 @@ def run_grammar_case(BL, case, steps):
             if not np.array_equal(got, want) or bool(of.value) != forced:
                 bad = np.nonzero(got != want)[0]
                 return f"step {t}: mask differs in {len(bad)} words (first {bad[:4]}), forced {forced} vs {of.value}"
-            x = (rng.standard_normal(V) * 3.0).astype(np.float32)
+            x = (rng.standard_normal(V) * sigma).astype(np.float32)
             buf.upload(x)
-            ot = np.zeros(1, np.int32)
+            ot, olp = np.zeros(1, np.int32), np.zeros(1, np.float32)
+            oti, otl = np.full(max(n_probs, 1), -1, np.int32), np.zeros(max(n_probs, 1), np.float32)
             eg = O.C.c_int()
-            orc = L.orc_slot_step(h, O.fp(x), V, 0, 1, O.ip(ot), None, None, None, O.C.byref(eg))
+            orc = L.orc_slot_step(h, O.fp(x), V, wants, 1, O.ip(ot), O.fp(olp), O.ip(oti), O.fp(otl), O.C.byref(eg))
             try:
-                tok = ctx.sample_step([0], buf.ptr, V)[0][0]
+                tok, lp, ti, tl = ctx.sample_step([0], buf.ptr, V, top_stride=max(n_probs, 1))
+                tok = tok[0]
             except BL.BLError as e:
                 # the reference's errors (dead reply, every token rejected) must be the same errors
                 if orc == 0 or O.last_error() not in str(e):
@@ -845,10 +875,15 @@ def run_grammar_case(BL, case, steps):
                 return f"step {t}: oracle error '{O.last_error()}', device token {tok}"
             if tok != ot[0]:
                 return f"step {t}: token {tok} vs {ot[0]}"
+            if wants and not eg.value:
+                if not lp_close(lp[0], olp[0]):
+                    return f"step {t}: logprob {lp[0]} vs {olp[0]}"
+                if ti[0][:n_probs] != list(oti[:n_probs]) or not all(lp_close(tl[0][q], otl[q]) for q in range(n_probs)):
+                    return f"step {t}: alternatives differ"
+            if kw and ctx.slot_rng(0) != L.orc_slot_rng(h):
+                return f"step {t}: RNG state differs"
             if tok == eos:
-                L.orc_slot_restart(h)
-                ctx.slot_reset(0, BL.Params(), 1)
-                ctx.slot_grammar(0, gbnf)
+                restart()
     finally:
         L.orc_slot_free(h)
         ctx.close()
@@ -927,6 +962,11 @@ def main():
                       '"count":{"type":"integer"},"tags":{"type":"array","items":{"type":"string"}}},'
                       '"required":["name","count","tags"]}')
             results.append(("workload 3 via the schema entry point", run_w3(BL, int(f[1]), schema=schema)))
+        elif kind == "gsamp":  # sampled grammar rows: gsamp:indices[:steps]
+            for c in parse_range(f[1]):
+                gc, gkw, gsig = GRAMMAR_SAMPLED[c]
+                results.append((f"sampled grammar {c}",
+                                 run_grammar_case(BL, gc, int(f[2]) if len(f) > 2 else 30, gkw, gsig)))
         elif kind == "grammar":
             for c in parse_range(f[1]):
                 results.append((f"grammar case {c}", run_grammar_case(BL, c, int(f[2]) if len(f) > 2 else 30)))

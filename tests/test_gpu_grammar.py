@@ -84,6 +84,14 @@ def test_grammar_cases(case):
     assert err is None, err
 
 
+@pytest.mark.parametrize("case", range(len(RP.GRAMMAR_SAMPLED)))
+def test_sampled_grammar_cases(case):
+    gc, kw, sigma = RP.GRAMMAR_SAMPLED[case]
+    say(f"sampled grammar case {case}: grammar {gc}, {kw}, logits N(0, {sigma}^2)")
+    err = RP.run_grammar_case(BL, gc, 120, kw, sigma)
+    assert err is None, err
+
+
 def test_grammar_errors():
     say("grammar errors")
     blob, off, eos = RP.grammar_vocab(np.random.default_rng(1), 50)
@@ -105,6 +113,8 @@ def test_grammar_errors():
         ctx.slot_grammar(0, 'root ::= a\na ::= a "x" | "y"\n')
     assert e.value.code == BL.BL_EGRAMMAR_AMBIG
     ctx.slot_reset(1, BL.Params(temperature=0.8), 1)
+    ctx.slot_grammar(1, 'root ::= "a"\n')  # sampled grammar rows have a device path
+    ctx.slot_reset(1, BL.Params(temperature=0.8, top_n_sigma=1.0), 1)
     with pytest.raises(BL.BLError) as e:
         ctx.slot_grammar(1, 'root ::= "a"\n')
     assert e.value.code == BL.BL_EUNSUPPORTED

@@ -103,11 +103,12 @@ def test_spec_verify_with_penalties(simt_lib):
 
 def test_grammar_masks_and_tokens(simt_lib):
     """The grammar path (GBNF automaton tables, per-token mask walk, masked greedy, on-device commit of
-    the reply position) against the oracle's whole-reply re-decode: workload 3 and seven adversarial
-    byte-level vocabularies."""
-    out = _run(simt_lib, ["w3:3", "w3schema:3", "grammar:0-6:40"], {"SIMT_ORDER": "rand"})
+    the reply position) against the oracle's whole-reply re-decode: workload 3 and eight adversarial
+    byte-level vocabularies; sampled grammar rows (top-k widening within and past the merged list,
+    full-vocabulary rows whose allowed maximum lies far below the row maximum)."""
+    out = _run(simt_lib, ["w3:3", "w3schema:3", "grammar:0-7:40", "gsamp:0-9:30"], {"SIMT_ORDER": "rand"})
     assert "ok   workload 3\n" in out and "ok   workload 3 via the schema entry point" in out
-    assert out.count("ok   grammar case") == 7
+    assert out.count("ok   grammar case") == 8 and out.count("ok   sampled grammar") == 10
 
 
 def test_top_n_sigma(simt_lib):
