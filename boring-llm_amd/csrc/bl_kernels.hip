@@ -1374,11 +1374,19 @@ __device__ __forceinline__ void ranked_terms(const bl_slot_dev &sp, ValF val, in
   }
 }
 
-/* ... then the reference's sequential float32 loops over those terms, by one thread: softmax sum, top-p
- * prefix, min-p cut, XTC, tempered sum and the draw (src/sampling.br:505-607); *rng_out = the state after
- * the draw */
+/* lane k's float as a wavefront-uniform value */
+__device__ __forceinline__ float sel_rl(float x, int k) {
+  return bl_u2f((uint32_t)__builtin_amdgcn_readlane((int)bl_f2u(x), k));
+}
+
+/* ... then the reference's sequential float32 loops over those terms, by one wavefront: softmax sum, top-p
+ * prefix, min-p cut, XTC, tempered sum and the draw (src/sampling.br:505-607). Each loop's per-term work
+ * (a division, a logarithm, a comparison) runs in the lanes, 64 terms at a time; the running sums add the
+ * lanes' values in list order, every lane computing the same sum, so they are the reference's float32
+ * sums. *rng_out = the state after the draw (written by lane 0) */
 __device__ __forceinline__ sel_draw ranked_serial(const bl_slot_dev &sp, int n, int64_t n_logical, int64_t keep, uint64_t rng,
                                  int rng_skip, bool pre, sel_shared &sh, uint64_t *rng_out) {
+  const int lane = threadIdx.x & 63;
   const float *ser_e = sh.ser_e, *ser_v = sh.ser_v;
   float *ser_r = sh.ser_r;
   const bool xtc = bl_xtc_on(sp);
@@ -1386,18 +1394,33 @@ __device__ __forceinline__ sel_draw ranked_serial(const bl_slot_dev &sp, int n, 
   int64_t cut = n_logical;
   bool unsup = false;
   float sum_exp = 0.0f;
+  /* term j of a batch: lane j - b0 */
+  auto at = [&](const float *arr, int j) { return j < n ? arr[j] : 0.0f; };
   if (filt) {
     /* `pre`: ser_e already holds the probabilities (after the typical filter), divided here by 1 */
-    if (pre) sum_exp = 1.0f;
-    else
-      for (int j = 0; j < n; j++) sum_exp += ser_e[j];
+    if (pre) {
+      sum_exp = 1.0f;
+    } else {
+      for (int b0 = 0; b0 < n; b0 += 64) {
+        const float e = at(ser_e, b0 + lane);
+        const int m = n - b0 < 64 ? n - b0 : 64;
+        for (int k = 0; k < m; k++) sum_exp += sel_rl(e, k);
+      }
+    }
     if (sp.top_p < 1.0f) {
       float cum = 0.0f;
-      for (int j = 0; j < n; j++) {
-        cum += ser_e[j] / sum_exp;
-        if (j >= keep - 1 && cum >= sp.top_p) {
-          cut = j + 1;
-          break;
+      bool done = false;
+      for (int b0 = 0; b0 < n && !done; b0 += 64) {
+        const float pj = at(ser_e, b0 + lane) / sum_exp;
+        const int m = n - b0 < 64 ? n - b0 : 64;
+        for (int k = 0; k < m; k++) {
+          cum += sel_rl(pj, k);
+          const int j = b0 + k;
+          if (j >= keep - 1 && cum >= sp.top_p) {
+            cut = j + 1;
+            done = true;
+            break;
+          }
         }
       }
     }
@@ -1406,11 +1429,12 @@ __device__ __forceinline__ sel_draw ranked_serial(const bl_slot_dev &sp, int n, 
       const float threshold = p0 * sp.min_p;
       const int64_t lim = cut < n ? cut : n;
       int64_t first_small = -1;
-      for (int64_t j = keep; j < lim; j++)
-        if (ser_e[j] / sum_exp < threshold) {
-          first_small = j;
-          break;
-        }
+      for (int64_t b0 = keep; b0 < lim && first_small < 0; b0 += 64) {
+        const int64_t j = b0 + lane;
+        const bool small = j < lim && ser_e[j] / sum_exp < threshold;
+        const unsigned long long bm = __ballot(small);
+        if (bm) first_small = b0 + __ffsll((long long)bm) - 1;
+      }
       if (first_small < 0) {
         if (lim < cut) {
           /* the next, unmaterialised candidate is below 2^-25 of the top one */
@@ -1431,11 +1455,27 @@ __device__ __forceinline__ sel_draw ranked_serial(const bl_slot_dev &sp, int n, 
     if (chance <= sp.xtc_probability) {
       /* the sum of the probabilities before the cut, then the last of the leading run at or above the
        * threshold (candidates past the materialised list are below it, by the candidate span) */
-      const int64_t lim = cut < n ? cut : n;
+      const int lim = (int)(cut < n ? cut : n);
       float xs = 0.0f;
-      for (int64_t i = 0; i < lim; i++) xs += ser_e[i] / sum_exp;
+      for (int b0 = 0; b0 < lim; b0 += 64) {
+        const float pj = (b0 + lane < lim ? ser_e[b0 + lane] : 0.0f) / sum_exp;
+        const int m = lim - b0 < 64 ? lim - b0 : 64;
+        for (int k = 0; k < m; k++) xs += sel_rl(pj, k);
+      }
       int64_t pos_last = 0;
-      for (int64_t i = 0; i < lim && (ser_e[i] / sum_exp) / xs >= sp.xtc_threshold; i++) pos_last = i;
+      bool ended = false;
+      for (int b0 = 0; b0 < lim && !ended; b0 += 64) {
+        const int j = b0 + lane;
+        const bool stop = j < lim && !((ser_e[j] / sum_exp) / xs >= sp.xtc_threshold);
+        const unsigned long long bm = __ballot(stop);
+        if (bm) {
+          const int f = b0 + __ffsll((long long)bm) - 1;
+          if (f > 0) pos_last = f - 1;
+          ended = true;
+        } else {
+          pos_last = (b0 + 64 < lim ? b0 + 64 : lim) - 1;
+        }
+      }
       if (pos_last > 0 && cut - pos_last >= keep) first = (int)pos_last;
     }
   }
@@ -1448,11 +1488,19 @@ __device__ __forceinline__ sel_draw ranked_serial(const bl_slot_dev &sp, int n, 
       unsup = true; /* the entropy would need candidates past the materialised list */
     } else {
       float ss = 0.0f;
-      for (int i = first; i < n_eff; i++) ss += ser_e[i] / sum_exp;
+      for (int b0 = first; b0 < n_eff; b0 += 64) {
+        const float pj = (b0 + lane < n_eff ? ser_e[b0 + lane] : 0.0f) / sum_exp;
+        const int m = n_eff - b0 < 64 ? n_eff - b0 : 64;
+        for (int k = 0; k < m; k++) ss += sel_rl(pj, k);
+      }
       float ent = 0.0f;
-      for (int i = first; i < n_eff; i++) {
-        const float q = (ser_e[i] / sum_exp) / ss;
-        if (q > 0.0f) ent -= q * bl_logf(q);
+      for (int b0 = first; b0 < n_eff; b0 += 64) {
+        const float q = ((b0 + lane < n_eff ? ser_e[b0 + lane] : 0.0f) / sum_exp) / ss;
+        const float tq = q > 0.0f ? q * bl_logf(q) : 0.0f;
+        const int m = n_eff - b0 < 64 ? n_eff - b0 : 64;
+        for (int k = 0; k < m; k++) {
+          if (sel_rl(q, k) > 0.0f) ent -= sel_rl(tq, k);
+        }
       }
       const float maxe = bl_logf((float)(cut - first));
       const float ne = bl_powf(ent / maxe, sp.dynatemp_exponent);
@@ -1464,8 +1512,10 @@ __device__ __forceinline__ sel_draw ranked_serial(const bl_slot_dev &sp, int n, 
   sel_draw r;
   if (!(Teff > 0.0f)) {
     /* no draw: the first candidate, probability 1 (src/sampling.br:581-582) */
-    ser_r[first] = 1.0f;
-    *rng_out = st;
+    if (lane == 0) {
+      ser_r[first] = 1.0f;
+      *rng_out = st;
+    }
     r.pos = unsup ? -2 : first;
     r.first = first;
     r.cut = first + 1;
@@ -1475,25 +1525,33 @@ __device__ __forceinline__ sel_draw ranked_serial(const bl_slot_dev &sp, int n, 
   if (first > 0 || Teff != sp.temperature) {
     /* the draw's terms from the first candidate at the effective temperature */
     const float vf = ser_v[first];
-    for (int j = first; j < n_eff; j++) {
+    for (int j = first + lane; j < n_eff; j += 64) {
       const float dd = ser_v[j] - vf;
       const float q = dd / Teff;
       ser_r[j] = SEL_EXPF(q);
     }
   }
   float S = 0.0f;
-  for (int j = first; j < n_eff; j++) S += ser_r[j];
+  for (int b0 = first; b0 < n_eff; b0 += 64) {
+    const float e = b0 + lane < n_eff ? ser_r[b0 + lane] : 0.0f;
+    const int m = n_eff - b0 < 64 ? n_eff - b0 : 64;
+    for (int k = 0; k < m; k++) S += sel_rl(e, k);
+  }
   const float target = bl_rng_f32(&st) * S;
   float run = 0.0f;
   int64_t f = -1;
-  for (int j = first; j < n_eff; j++) {
-    run += ser_r[j];
-    if (run >= target) {
-      f = j;
-      break;
+  for (int b0 = first; b0 < n_eff && f < 0; b0 += 64) {
+    const float e = b0 + lane < n_eff ? ser_r[b0 + lane] : 0.0f;
+    const int m = n_eff - b0 < 64 ? n_eff - b0 : 64;
+    for (int k = 0; k < m; k++) {
+      run += sel_rl(e, k);
+      if (run >= target) {
+        f = b0 + k;
+        break;
+      }
     }
   }
-  *rng_out = st;
+  if (lane == 0) *rng_out = st;
   r.pos = unsup ? -2 : (int)(f >= 0 ? f : cut - 1);
   r.first = first;
   r.cut = (int)cut;
@@ -3097,8 +3155,10 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
   __syncthreads();
   if (lp_row && w == 0)
     norm_chain(d, row, sh, [&](int64_t j) { return SEL_EXPF(bl_row_value(d, sp, rows, row, slot, logits, ld, (int32_t)j) - M); });
-  if (sampled && !status && short_list && w == 1 && lane == 0)
-    sh.draw = ranked_serial(sp, n_draw, nlog_draw, keep, rng, skip, typ, sh, &sh.rng_out);
+  if (sampled && !status && short_list && w == 1) {
+    const sel_draw r = ranked_serial(sp, n_draw, nlog_draw, keep, rng, skip, typ, sh, &sh.rng_out);
+    if (lane == 0) sh.draw = r;
+  }
   __syncthreads();
   const float S_norm = sh.n.S; /* the normaliser's LDS is scratch from here on (heap ties) */
   sel_draw dr;
