@@ -51,7 +51,7 @@ EXPORTS = [
     "bl_workload_drafts", "bl_set_timing", "bl_get_timing", "bl_set_vocab", "bl_slot_grammar", "bl_grammar_mask",
     "bl_workload_c3_vocab", "bl_step_graph_create", "bl_step_graph_launch", "bl_step_graph_destroy",
     "bl_stream_sync", "bl_json_schema_to_gbnf", "bl_slot_schema", "bl_slot_status", "bl_sample_rows_noalloc",
-    "bl_resolve_seed", "bl_seed_rng", "bl_slot_dry_breakers",
+    "bl_resolve_seed", "bl_seed_rng", "bl_slot_dry_breakers", "bl_slot_json_object",
 ]
 NOALLOC_BYTES = 64 << 20
 NOALLOC_ROWS = 16
@@ -78,6 +78,7 @@ def lib():
         L.bl_slot_reset.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_uint64, i32p, C.c_int, i32p, C.c_int,
                                     i32p, f32p, C.c_int]
         L.bl_slot_dry_breakers.argtypes = [C.c_void_p, C.c_int, i32p, i32p, C.c_int]
+        L.bl_slot_json_object.argtypes = [C.c_void_p, C.c_int, C.c_int]
         L.bl_slot_rng.argtypes = [C.c_void_p, C.c_int, u64p]
         L.bl_slot_status.argtypes = [C.c_void_p, C.c_int]
         L.bl_slot_commit.argtypes = [C.c_void_p, C.c_int, i32p, C.c_int]
@@ -179,6 +180,10 @@ class Context:
         a, _ = _arr(C.c_int32, flat)
         ln, n = _arr(C.c_int32, [len(b) for b in breakers])
         _check(lib().bl_slot_dry_breakers(self.h, slot, a, ln, n))
+
+    def slot_json_object(self, slot, on=True):
+        """response_format json_object on the slot (bl_slot_json_object)."""
+        _check(lib().bl_slot_json_object(self.h, slot, 1 if on else 0))
 
     def slot_rng(self, slot):
         s = C.c_uint64()

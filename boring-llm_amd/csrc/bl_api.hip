@@ -133,7 +133,7 @@ __device__ void commit_one(const bl_dev &d, bl_slot_dev &sp, int slot, int32_t t
   if (!is_eog) {
     sp.n_reply += 1;
     if (sp.fp_on) bl_rec_get(d, slot, tok)->cnt += 1;
-    if (sp.g_on) grammar_commit(d, sp, d.gram[slot], tok);
+    if (sp.g_on) grammar_commit(d, sp, d.gram[slot], tok, slot);
   }
 }
 
@@ -237,7 +237,7 @@ static bool dev_layout(bl_dev &d, size_t S, size_t R, int vocab, Take take) {
                   take(d.full_i, R * d.nb * BL_EB) && take(d.full_cnt, R * d.nb) && take(d.full_s, R * d.nb) &&
                   take(d.sortk, R * 2 * V) && take(d.gsum, R * G) && take(d.crit, R * BL_CRIT_MAX) && take(d.ncrit, R) &&
                   take(d.mkeys, R * BL_KSEL_MAX) && take(d.mstat, R) && take(d.rmax, R) && take(d.rarg, R) &&
-                  take(brec, R * d.nb * 16) && take(d.bcrit, R * d.nb) && take(d.gram, S) &&
+                  take(brec, R * d.nb * 16) && take(d.bcrit, R * d.nb) && take(d.gram, S) && take(d.jstack, S * BL_JSON_DEPTH) &&
                   take(d.gmask, R * 2 * ((V + 63) / 64)) && take(d.gstat, R) && take(d.gamb, R) &&
                   take(d.gm_max, R * d.gm_blocks) && take(d.gm_arg, R * d.gm_blocks) && take(d.gm_eq, R * d.gm_blocks);
   d.grec = grec;
@@ -738,6 +738,7 @@ int bl_slot_grammar(bl_ctx *c, int slot, const char *gbnf, size_t len) {
     return fail(BL_EPARAM, "bl_slot_grammar: slot %d is not set up", slot);
   if (c->stepped[slot]) return fail(BL_EPARAM, "bl_slot_grammar: attach the grammar before the slot's first step");
   bl_slot_dev s = c->host_slots[slot];
+  s.g_kind = 0;
   if (!gbnf || len == 0) {
     s.g_on = 0;
     s.mode &= ~(BL_M_GRAMMAR | BL_M_GFULL);
@@ -768,6 +769,48 @@ int bl_slot_grammar(bl_ctx *c, int slot, const char *gbnf, size_t len) {
     hipSetDevice(c->device);
     HIPCHK(hipStreamSynchronize(c->stream));
     HIPCHK(hipMemcpy(c->d.gram + slot, &e->dev, sizeof(bl_gram_view), hipMemcpyHostToDevice));
+  }
+  hipSetDevice(c->device);
+  HIPCHK(hipStreamSynchronize(c->stream));
+  HIPCHK(hipMemcpy(c->d.slots + slot, &s, sizeof s, hipMemcpyHostToDevice));
+  c->host_slots[slot] = s;
+  return BL_OK;
+}
+
+int bl_slot_json_object(bl_ctx *c, int slot, int on) {
+  if (!c || slot < 0 || slot >= c->d.max_slots || !c->slot_ready[slot])
+    return fail(BL_EPARAM, "bl_slot_json_object: slot %d is not set up", slot);
+  if (c->stepped[slot]) return fail(BL_EPARAM, "bl_slot_json_object: constrain the slot before its first step");
+  bl_slot_dev s = c->host_slots[slot];
+  if (!on) {
+    s.g_on = 0;
+    s.g_kind = 0;
+    s.mode &= ~(BL_M_GRAMMAR | BL_M_GFULL);
+  } else {
+    if (c->voff.empty()) return fail(BL_EPARAM, "bl_slot_json_object: the vocabulary pieces are not set (bl_set_vocab)");
+    if (s.mirostat != 0)
+      return fail(BL_EPARAM, "stateful adaptive sampling cannot be combined with constrained decoding");
+    if (s.temperature > 0.0f && s.top_n_sigma > 0.0f)
+      return fail(BL_EUNSUPPORTED, "JSON-object sampling with top_n_sigma is not supported on the device");
+    /* the classifier's position after the reply (the reference re-decodes it every step) */
+    std::vector<uint8_t> stack(BL_JSON_DEPTH, 0);
+    bl_json_pos p;
+    bl_js_start(p, stack.data());
+    for (int32_t id : c->reply[slot]) {
+      const uint8_t *b = c->vblob.data() + c->voff[id];
+      bl_js_commit(p, stack.data(), [&](int i) { return (uint32_t)b[i]; }, (int)(c->voff[id + 1] - c->voff[id]));
+    }
+    s.jpos = p;
+    s.g_on = 1;
+    s.g_kind = 1;
+    s.mode |= BL_M_GRAMMAR;
+    if (s.temperature > 0.0f && (s.mode & BL_M_TOPK)) {
+      s.k_sel = BL_KSEL_MAX < c->d.vocab ? BL_KSEL_MAX : c->d.vocab;
+      s.mode |= BL_M_GFULL;
+    }
+    hipSetDevice(c->device);
+    HIPCHK(hipStreamSynchronize(c->stream));
+    HIPCHK(hipMemcpy(c->d.jstack + (size_t)slot * BL_JSON_DEPTH, stack.data(), BL_JSON_DEPTH, hipMemcpyHostToDevice));
   }
   hipSetDevice(c->device);
   HIPCHK(hipStreamSynchronize(c->stream));
@@ -821,6 +864,7 @@ int bl_grammar_mask(bl_ctx *c, int slot, uint32_t *d_mask_out, int32_t *forced_e
   HIPCHK(hipMemcpyAsync(&st[1], c->d.gamb, 4, hipMemcpyDeviceToHost, c->stream));
   HIPCHK(hipStreamSynchronize(c->stream));
   if (forced_eos) *forced_eos = (st[0] & BL_GR_FORCED) ? 1 : 0;
+  if (st[1] & 2) return fail(BL_EUNSUPPORTED, "a JSON reply nested past the device's stack capacity");
   if ((st[0] & BL_GR_FAMBIG) || st[1]) return fail(BL_EGRAMMAR_AMBIG, "grammar is left-recursive or too ambiguous to match");
   if (st[0] & BL_GR_DEAD) return fail(BL_EGRAMMAR_DEAD, "the reply no longer matches the grammar");
   return BL_OK;
@@ -869,6 +913,7 @@ static int status_error(int st) {
   if (st & BL_SE_GDEAD) return fail(BL_EGRAMMAR_DEAD, "the reply no longer matches the grammar");
   if (st & BL_SE_GAMBIG) return fail(BL_EGRAMMAR_AMBIG, "grammar is left-recursive or too ambiguous to match");
   if (st & BL_SE_GREJECT) return fail(BL_EGRAMMAR_REJECT, "the grammar rejected every vocabulary token");
+  if (st & BL_SE_JREJECT) return fail(BL_EGRAMMAR_REJECT, "JSON response grammar rejected every vocabulary token");
   return BL_OK;
 }
 

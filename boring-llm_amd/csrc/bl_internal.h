@@ -23,6 +23,7 @@
 
 #include "bl_exact.h"
 #include "bl_gwalk.h"
+#include "bl_jwalk.h"
 
 #define BL_CH 4096          /* vocabulary chunk per workgroup in the row passes */
 #define BL_RP_THREADS 256   /* row-pass workgroup */
@@ -81,6 +82,7 @@
 #define BL_SE_GREJECT 32
 #define BL_SE_GAMBIG 64
 #define BL_SE_SIGMA 128 /* top-n-sigma's sigma undecided (at a float32 rounding boundary) */
+#define BL_SE_JREJECT 256 /* a JSON-object slot: every vocabulary token rejected (src/server.br:302) */
 
 /* one modified token's server-stage inputs in one slot (src/server.br:940-944, src/sampling.br:65-107,
  * :175-188) */
@@ -125,9 +127,12 @@ struct bl_slot_dev {
   /* state */
   uint64_t rng;
   int32_t n_tokens, n_reply, win_len, win_head, err, pad;
-  /* grammar (src/server.br:309-362): position of the reply in the slot's automaton */
+  /* grammar (src/server.br:309-362): position of the reply in the slot's automaton; or, with g_kind 1,
+   * response_format json_object (src/server.br:261-304): the JSON classifier's position (stack in
+   * bl_dev.jstack) */
   bl_gram_pos gpos;
-  int32_t g_on, pad2;
+  int32_t g_on, g_kind;
+  bl_json_pos jpos;
   /* mirostat v1 / v2 (src/sampling.br:663-700): the version, tau, eta and the running mu */
   int32_t mirostat;
   float mirostat_tau, mirostat_eta, mu;
@@ -181,6 +186,7 @@ struct bl_dev {
   int32_t nb;       /* ceil(V / BL_EB) */
   /* grammar-constrained sampling */
   bl_gram_view *gram; /* [slots] the slot's compiled grammar (device pointers) */
+  uint8_t *jstack;    /* [slots][BL_JSON_DEPTH] JSON-object slots' container stacks */
   const uint8_t *vblob;   /* vocabulary piece bytes */
   const uint32_t *voff;   /* [V+1] byte offsets of each token's piece */
   int32_t eos_id;
@@ -284,11 +290,14 @@ __device__ inline void bl_dry_push(const bl_dev &d, bl_slot_dev &sp, int slot, i
 }
 
 /* appends token `tok`'s bytes to the slot's grammar position (reply_tokens.push of a non-EOG token,
- * src/server.br:1037); one thread */
-__device__ inline void grammar_commit(const bl_dev &d, bl_slot_dev &sp, const bl_gram_view &g, int32_t tok) {
+ * src/server.br:1037), or to its JSON classifier's; one thread */
+__device__ inline void grammar_commit(const bl_dev &d, bl_slot_dev &sp, const bl_gram_view &g, int32_t tok, int slot) {
   const uint32_t o0 = d.voff[tok], o1 = d.voff[tok + 1];
   const uint8_t *b = d.vblob + o0;
-  bl_gw_commit(g, sp.gpos, [&](int i) { return (uint32_t)b[i]; }, (int)(o1 - o0));
+  if (sp.g_kind == 1)
+    bl_js_commit(sp.jpos, d.jstack + (int64_t)slot * BL_JSON_DEPTH, [&](int i) { return (uint32_t)b[i]; }, (int)(o1 - o0));
+  else
+    bl_gw_commit(g, sp.gpos, [&](int i) { return (uint32_t)b[i]; }, (int)(o1 - o0));
 }
 #endif
 

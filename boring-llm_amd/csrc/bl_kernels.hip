@@ -1069,7 +1069,8 @@ __device__ __forceinline__ void exppass_body(const bl_dev &d, const float *__res
       const int tk = i0 + j0;
       amask = tk < V ? (d.gmask[(int64_t)row * words + (tk >> 6) * 2 + ((tk >> 5) & 1)] >> (tk & 31)) & 0xFu : 0u;
     }
-    const float thr = Mc - bl_cand_span(sp);
+    /* a top-k grammar row's widening levels read the first ranks of the whole row: four spans deep */
+    const float thr = Mc - ((mode & BL_M_FULL) ? 1.0f : 4.0f) * bl_cand_span(sp);
     auto keep_k = [&](int k) { return j0 + k < cnt && x[k] >= thr && ((amask >> k) & 1u); };
     int mine = 0;
 #pragma unroll
@@ -1145,10 +1146,28 @@ __global__ __launch_bounds__(BL_GM_THREADS) void bl_k_gmask(bl_dev d, const floa
   __shared__ int red_n[BL_GM_THREADS / 64];
   const bl_gram_view g = d.gram[slot];
   const bl_gram_pos pos = sp.gpos;
-  const int32_t front = bl_gw_frontier(g, pos);
+  const bool js = sp.g_kind == 1;
+  const bl_json_pos jp = sp.jpos;
+  const uint8_t *jst = d.jstack + (int64_t)slot * BL_JSON_DEPTH;
+  const int32_t front = js ? 0 : bl_gw_frontier(g, pos);
   const int64_t tok = (int64_t)blockIdx.x * BL_GM_THREADS + t;
   bool allowed = false, ambig = false;
-  if (front >= 0 && tok < V) {
+  if (js && tok < V) {
+    /* json_object_decoded_candidate_allowed (src/json.br:420-426): an end-of-generation token only when the
+     * reply is a complete object, where the step forces it (src/server.br:266-269); any other token when
+     * the reply with its piece stays viable */
+    bool eog = false;
+    for (int k = 0; k < d.n_eog; k++) eog |= d.eog[k] == (int32_t)tok;
+    if (!eog) {
+      const uint32_t o0 = d.voff[tok], o1 = d.voff[tok + 1];
+      const uint8_t *b = d.vblob + o0;
+      bool over = false;
+      allowed = bl_js_walk(jp, jst, [&](int i) { return (uint32_t)b[i]; }, (int)(o1 - o0), &over);
+      ambig = over;
+    } else {
+      allowed = !sp.ignore_eos && bl_js_complete(jp, jp.depth > 0 ? (int)jst[jp.depth - 1] : -1);
+    }
+  } else if (front >= 0 && tok < V) {
     bool eog = false;
     for (int k = 0; k < d.n_eog; k++) eog |= d.eog[k] == (int32_t)tok;
     if (eog) {
@@ -1170,9 +1189,15 @@ __global__ __launch_bounds__(BL_GM_THREADS) void bl_k_gmask(bl_dev d, const floa
       d.gmask[(int64_t)row * words + wi] = (uint32_t)bm;
       d.gmask[(int64_t)row * words + wi + 1] = (uint32_t)(bm >> 32);
     }
-    if (am) atomicOr(&d.gamb[row], 1);
+    if (am) atomicOr(&d.gamb[row], js ? 2 : 1); /* 2: a JSON walk outgrew its stack overlay */
   }
-  if (blockIdx.x == 0 && t == 0) {
+  if (js && blockIdx.x == 0 && t == 0) {
+    /* should_stop (src/server.br:266-269); a slot stack past its capacity leaves the row undecided */
+    const int top = jp.depth > 0 ? (int)jst[jp.depth - 1] : -1;
+    d.gstat[row] = bl_js_complete(jp, top) && !sp.ignore_eos ? BL_GR_FORCED : 0;
+    if (jp.dead == 2) atomicOr(&d.gamb[row], 2);
+  }
+  if (!js && blockIdx.x == 0 && t == 0) {
     int st = 0;
     if (front == BL_GT_AMBIG) st |= BL_GR_FAMBIG;
     else if (front < 0) st |= BL_GR_DEAD;
@@ -2812,7 +2837,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
       Mc = sh.red_m[0];
       for (int q = 1; q < SEL_NW; q++) Mc = fmaxf(Mc, sh.red_m[q]);
       __syncthreads();
-      if (na < 1.0) status |= BL_SE_GREJECT;
+      if (na < 1.0) status |= sp.g_kind == 1 ? BL_SE_JREJECT : BL_SE_GREJECT;
       n_logical = (int64_t)na;
     }
     const float *fv = d.full_v + (int64_t)row * NB * BL_EB;
@@ -2892,7 +2917,8 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
        * lower buckets, equal values in one bucket), scattered by bucket, then ranked by counting within
        * each bucket, one LDS tile of the bucketed list at a time */
       const float T = sp.temperature;
-      float thr = fmaxf(Mc - bl_cand_span(sp), tns_thr); /* the exponent pass's candidates, top-n-sigma's survivors */
+      /* the exponent pass's candidates (four spans deep for a top-k grammar row), top-n-sigma's survivors */
+      float thr = fmaxf(Mc - (gram && (mode & BL_M_TOPK) ? 4.0f : 1.0f) * bl_cand_span(sp), tns_thr);
       if (!filt && !(gram && (mode & BL_M_TOPK))) { /* a top-k grammar row draws from a subset: no cut */
         /* the draw adds exp((v - M) / T) in descending order. With u = 2^-24 and m <= V terms, the float
          * running sum past every term >= 2^(k-24) is at least (1 - g) (S - V 2^(k-24)), g = m u / (1 - m u)
@@ -3045,7 +3071,11 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
     for (int64_t q = t; q < gwords; q += BL_SEL_THREADS) na += (double)__popc(gmk[q]);
     na = block_sum_d<BL_SEL_THREADS>(na, sh.c.gsum);
     int kk = gk;
-    for (;;) {
+    if (na < 1.0) { /* no level holds an allowed token: the widening ends in the rejection */
+      status |= sp.g_kind == 1 ? BL_SE_JREJECT : BL_SE_GREJECT;
+      kk = -1;
+    }
+    for (; kk >= 0;) {
       const bool vlevel = kk >= V;
       if (!vlevel && kk > n_list) {
         status |= BL_SE_UNSUPPORTED;
@@ -3083,7 +3113,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
         break;
       }
       if (vlevel) {
-        status |= na < 1.0 ? BL_SE_GREJECT : BL_SE_UNSUPPORTED;
+        status |= BL_SE_UNSUPPORTED;
         break;
       }
       kk = kk * 4 < V ? kk * 4 : V;
@@ -3127,7 +3157,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
       tok = d.eos_id;
       tokv = bl_row_value(d, sp, rows, row, slot, logits, ld, tok);
     } else if (d.gamb[row]) {
-      status |= BL_SE_GAMBIG;
+      status |= d.gamb[row] & 2 ? BL_SE_UNSUPPORTED : BL_SE_GAMBIG;
     } else {
       float gm = BL_NEG_INF;
       int gi = 0x7fffffff;
@@ -3140,7 +3170,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
           if (d.gm_arg[go + k] != 0x7fffffff && d.gm_max[go + k] == gm) n_eq += (double)d.gm_eq[go + k];
       n_eq = block_sum_d<BL_SEL_THREADS>(n_eq, sh.c.gsum);
       if (gi == 0x7fffffff) {
-        status |= BL_SE_GREJECT;
+        status |= sp.g_kind == 1 ? BL_SE_JREJECT : BL_SE_GREJECT;
       } else {
         tok = gi;
         tokv = gm;
@@ -3301,7 +3331,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
       if (!is_eog) {
         sp.n_reply = n_reply0 + 1;
         if (fp_on) bl_rec_get(d, slot, tok)->cnt += 1;
-        if (g_on) grammar_commit(d, sp, d.gram[slot], tok);
+        if (g_on) grammar_commit(d, sp, d.gram[slot], tok, slot);
       }
       bl_dry_push(d, sp, slot, tok);
       sp.rng = rng;

@@ -148,6 +148,16 @@ int bl_set_vocab(bl_ctx *ctx, const uint8_t *blob, const uint32_t *offsets, int 
  * allowed values. */
 int bl_slot_grammar(bl_ctx *ctx, int slot, const char *gbnf, size_t len);
 
+/* `response_format: {type: json_object}` on a slot set up by bl_slot_reset, before its first step (on = 0
+ * lifts it): the steps follow sample_json_token (src/server.br:261-304) with the classifier
+ * json_object_prefix_state (src/json.br:394-426): end of sequence once the reply is a complete object,
+ * otherwise the candidates whose piece keeps the reply a viable object prefix, in rank order (greedy or
+ * sampled, with the K×4 widening of bl_slot_grammar). Needs bl_set_vocab. Errors: BL_EPARAM (mirostat),
+ * BL_EUNSUPPORTED (top_n_sigma with temperature > 0). A step returns BL_EGRAMMAR_REJECT ("JSON response
+ * grammar rejected every vocabulary token") when no token is allowed, and BL_EUNSUPPORTED past 1024 nested
+ * containers or for a token that opens more than 32. */
+int bl_slot_json_object(bl_ctx *ctx, int slot, int on);
+
 /* JSON Schema -> GBNF (json_schema_to_gbnf, src/schema_grammar.br:313-337, over the schema text parsed as
  * src/json.br's json_parse does; the text must be UTF-8). Writes the NUL-terminated grammar into `out`
  * (`cap` bytes) and its length into *out_len (either may be NULL: out = NULL only reports the length).

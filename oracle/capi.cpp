@@ -403,11 +403,26 @@ int orc_slot_step(orc_slot *h, const float *logits, int64_t V, int wants_logprob
   }
 }
 /* grammar allow-mask of the current reply; returns 1 ok, 0 dead state, -1 error */
+/* response_format json_object on the slot (src/server.br:726), with the vocabulary pieces */
+void orc_slot_set_json_object(orc_slot *h, const uint8_t *blob, const uint32_t *offsets, int64_t n_tokens,
+                              int32_t eos_id) {
+  h->s.json_object = true;
+  h->vocab.blob.assign(blob, blob + offsets[n_tokens]);
+  h->vocab.offsets.assign(offsets, offsets + n_tokens + 1);
+  h->vocab.eos_id = eos_id;
+  h->has_vocab = true;
+}
+/* the classifiers over code points (src/json.br:227, :394) */
+int orc_json_prefix_state(const uint32_t *cps, int64_t n, int object) {
+  std::vector<uint32_t> cs(cps, cps + n);
+  return object ? json_object_prefix_state(cs) : json_prefix_state(cs);
+}
 int orc_slot_grammar_mask(orc_slot *h, int64_t V, uint32_t *mask, int *forced_eos, int fast) {
   try {
     std::vector<uint32_t> m;
     bool forced = false;
-    bool ok = grammar_mask(h->s, h->vocab, V, m, forced, fast != 0);
+    bool ok = h->s.json_object ? json_object_mask(h->s, h->vocab, V, m, forced)
+                               : grammar_mask(h->s, h->vocab, V, m, forced, fast != 0);
     memcpy(mask, m.data(), m.size() * sizeof(uint32_t));
     *forced_eos = forced ? 1 : 0;
     return ok ? 1 : 0;

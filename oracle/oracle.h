@@ -14,7 +14,8 @@
  *   src/schema_grammar.br  JSON Schema -> GBNF (+ src/json.br json_parse, src/jinja.br jv_to_json)
  *   src/speculative.br     n-gram drafting
  *   src/server.br          decode-step stage order (:939-1036), grammar-constrained sampling
- *                          (:309-362), speculative verification (:1173-1216)
+ *                          (:309-362), response_format json_object (:261-304, with src/json.br:227-426),
+ *                          speculative verification (:1173-1216)
  *   src/model.br:973-984   final logit soft-capping
  *
  * Arithmetic follows the reference's lowering: Boring float32 -> Rust f32 -> IEEE binary32 with
@@ -47,8 +48,13 @@
  *                                 the candidate's piece, the piece is bytes_to_str of the carry form, and the
  *                                 carry form equals the literal whole-reply re-decode (test_oracle_grammar.py)
  *   speculative verification      sequential decoding of the same rows (CHANGELOG.md:92's invariant)
+ *   top-n-sigma statistics        numpy's sequential float64 sums, bit for bit (test_oracle_pinning.py)
+ *   mirostat v1 fit               a float32 loop over glibc logf/powf, and a Zipf closed form
+ *   JSON prefix classifier        the reference's known answers (test/test_json.br:67-99) and the prefixes of
+ *                                 documents Python's json module writes (test_oracle_json.py)
  * Every check above fails against a build with a planted mistake where one is listed in oracle/Makefile
- * (`mutants`: sift tie direction, pairwise normaliser, reversed softmax sum, split tempered sum).
+ * (`mutants`: sift tie direction, pairwise normaliser, reversed softmax sum, split tempered sum, top-n-sigma
+ * float32 sum, mirostat v1 fit without its last pair, a leading zero followed by digits).
  * Assumed, not pinned: that the external `boring` compiler lowers float32 exp/ln/tanh/powf to Rust f32 and
  * so to glibc (it is not vendored); the oracle and the device follow glibc 2.35 exactly.
  */
@@ -261,6 +267,7 @@ struct Slot {
   Params params;
   std::unique_ptr<Grammar> grammar;
   std::unique_ptr<Matcher> matcher;
+  bool json_object = false; /* response_format json_object (src/server.br:726, :985) */
 };
 
 struct StepOut {
@@ -276,6 +283,12 @@ struct StepOut {
  * error paths. `wants_logprobs` follows :943 (logprobs requested). `vocab` may be null when no
  * grammar is set. `fast_grammar` selects the carry-based piece computation (identical results to
  * re-decoding the whole reply, proven by the tests) instead of the literal per-candidate re-decode. */
+/* ---------------- json.br prefix classifier, sample_json_token (json_prefix.cpp) ---------------- */
+int json_prefix_state(const std::vector<uint32_t> &cs);
+int json_object_prefix_state(const std::vector<uint32_t> &cs);
+bool json_object_mask(const Slot &slot, const Vocab &v, int64_t V, std::vector<uint32_t> &mask, bool &forced_eos);
+int32_t sample_json_token(Slot &slot, const Vocab &v, const Row &logits, int64_t vocab);
+
 StepOut decode_step(Slot &slot, const float *logits, int64_t V, const Vocab *vocab, bool wants_logprobs,
                     bool fast_grammar);
 

@@ -195,6 +195,9 @@ StepOut decode_step(Slot &slot, const float *logits, int64_t V, const Vocab *voc
   if (slot.grammar) {
     if (!vocab) throw std::runtime_error("grammar sampling needs a vocabulary");
     out.token = sample_grammar_token(slot, *vocab, penalized, V, fast_grammar);
+  } else if (slot.json_object) {
+    if (!vocab) throw std::runtime_error("JSON-object sampling needs a vocabulary");
+    out.token = sample_json_token(slot, *vocab, penalized, V);
   } else {
     SampleResult r = sample_with_probs(slot.rng, penalized, V, p, slot.tokens);
     slot.rng = r.rng;

@@ -890,6 +890,117 @@ def run_grammar_case(BL, case, steps, kw=None, sigma=3.0):
     return None
 
 
+JSON_CASES = [
+    # response_format json_object (src/server.br:261-304): (parameters, logit sigma)
+    (dict(temperature=0.0), 3.0),
+    (dict(temperature=0.8, top_k=40), 3.0),
+    (dict(temperature=1.0, top_k=0, min_p=0.02, logprobs=1, n_probs=3), 4.0),
+    (dict(temperature=0.7, top_k=10, repeat_penalty=1.3, repeat_last_n=8, ignore_eos=1), 3.0),
+]
+
+
+def json_vocab(rng, n_extra):
+    """Byte tokens plus pieces of JSON syntax, literals, numbers and multi-byte characters (some cut inside a
+    UTF-8 sequence), and an end-of-sequence token."""
+    pieces = [bytes([b]) for b in range(256)]
+    chars = ["{", "}", "[", "]", ":", ",", '"', "\\", " ", "\n", "t", "r", "u", "e", "f", "a", "l", "s", "n",
+             "0", "1", "9", "-", ".", "E", "+", "é", "€", "\U0001F600", "x", "k"]
+    for _ in range(n_extra):
+        k = int(rng.integers(1, 6))
+        s = "".join(chars[int(i)] for i in rng.integers(0, len(chars), k)).encode()
+        if rng.random() < 0.2:
+            cut = int(rng.integers(0, len(s) + 1))
+            s = s[cut:] if rng.random() < 0.5 else s[:cut]
+        if not s:
+            s = bytes([int(rng.integers(0, 256))])
+        pieces.append(s)
+    for w in (b'{"', b'":', b'",', b'"}', b"true", b"null", b"false", b"12", b"-0.5", b"1e+3", b"[]", b"{}", b"  "):
+        pieces.append(w)
+    pieces.append(b"<|eos|>")
+    off = [0]
+    for pc in pieces:
+        off.append(off[-1] + len(pc))
+    return b"".join(pieces), off, len(pieces) - 1
+
+
+def run_json_case(BL, case, steps):
+    """Masks and tokens of a response_format json_object slot against the oracle's sample_json_token: the
+    classifier over the re-decoded reply, forced end of sequence on a complete object, rank-order widening,
+    the sampling chain over the allowed candidates; a new reply after each end of sequence."""
+    kw, sigma = JSON_CASES[case]
+    rng = np.random.default_rng(800 + case)
+    blob, off, eos = json_vocab(rng, 900)
+    V = len(off) - 1
+    L = O.lib()
+    L.orc_set_eog_tokens(O.ip(O.i32([0])), 0, -1)
+    L.orc_slot_set_json_object.argtypes = [O.C.c_void_p, O.C.c_char_p, O.C.POINTER(O.C.c_uint32), O.C.c_int64,
+                                           O.C.c_int32]
+    op = O.params(**kw)
+    rs = BL.seed_rng(60 + case)
+    h = L.orc_slot_new(O.C.byref(op), rs, None, 0, None, 0, None, None, 0)
+    oo = np.array(off, np.uint32)
+    L.orc_slot_set_json_object(h, blob, oo.ctypes.data_as(O.C.POINTER(O.C.c_uint32)), V, eos)
+    ctx = BL.Context(V, 1, 1)
+    ctx.set_eog(eos, [])
+    ctx.set_vocab(blob, off)
+    ctx.slot_reset(0, BL.Params(**kw), rs)
+    ctx.slot_json_object(0)
+    wants = 1 if kw.get("logprobs") else 0
+    n_probs = kw.get("n_probs", 0)
+
+    def restart():
+        L.orc_slot_restart(h)
+        ctx.slot_reset(0, BL.Params(**kw), ctx.slot_rng(0))
+        ctx.slot_json_object(0)
+    words = (V + 31) // 32
+    mask, want = MEM.zeros(words, np.uint32), np.zeros(words, np.uint32)
+    buf = MEM.zeros(V, np.float32)
+    # closing pieces favoured, so that replies complete (and the end of sequence is forced) now and then
+    closing = np.array([b"}" in blob[off[i]:off[i + 1]] or b'"' in blob[off[i]:off[i + 1]] for i in range(V)])
+    ends = 0
+    try:
+        for t in range(steps):
+            of = O.C.c_int()
+            L.orc_slot_grammar_mask(h, V, want.ctypes.data_as(O.C.POINTER(O.C.c_uint32)), O.C.byref(of), 1)
+            forced = ctx.grammar_mask(0, mask.ptr)
+            got = mask.host()
+            if not np.array_equal(got, want) or bool(of.value) != forced:
+                bad = np.nonzero(got != want)[0]
+                return f"step {t}: mask differs in {len(bad)} words (first {bad[:4]}), forced {forced} vs {of.value}"
+            x = (rng.standard_normal(V) * sigma).astype(np.float32)
+            x[closing] += np.float32(3.0 * sigma)
+            buf.upload(x)
+            ot, olp = np.zeros(1, np.int32), np.zeros(1, np.float32)
+            oti, otl = np.full(max(n_probs, 1), -1, np.int32), np.zeros(max(n_probs, 1), np.float32)
+            eg = O.C.c_int()
+            orc = L.orc_slot_step(h, O.fp(x), V, wants, 1, O.ip(ot), O.fp(olp), O.ip(oti), O.fp(otl), O.C.byref(eg))
+            try:
+                tok, lp, ti, tl = ctx.sample_step([0], buf.ptr, V, top_stride=max(n_probs, 1))
+                tok = tok[0]
+            except BL.BLError as e:
+                if orc == 0 or O.last_error() not in str(e):
+                    return f"step {t}: device error '{e}', oracle {'token ' + str(ot[0]) if orc == 0 else O.last_error()}"
+                return None
+            if orc != 0:
+                return f"step {t}: oracle error '{O.last_error()}', device token {tok}"
+            if tok != ot[0]:
+                return f"step {t}: token {tok} vs {ot[0]}"
+            if wants and not eg.value:
+                if not lp_close(lp[0], olp[0]):
+                    return f"step {t}: logprob {lp[0]} vs {olp[0]}"
+                if ti[0][:n_probs] != list(oti[:n_probs]) or not all(lp_close(tl[0][q], otl[q]) for q in range(n_probs)):
+                    return f"step {t}: alternatives differ"
+            if ctx.slot_rng(0) != L.orc_slot_rng(h):
+                return f"step {t}: RNG state differs"
+            if tok == eos:
+                ends += 1
+                restart()
+    finally:
+        L.orc_slot_free(h)
+        ctx.close()
+    return None
+
+
 def parse_range(s):
     out = []
     for part in s.split(","):
@@ -967,6 +1078,9 @@ def main():
                 gc, gkw, gsig = GRAMMAR_SAMPLED[c]
                 results.append((f"sampled grammar {c}",
                                  run_grammar_case(BL, gc, int(f[2]) if len(f) > 2 else 30, gkw, gsig)))
+        elif kind == "json":  # json:cases[:steps]
+            for c in parse_range(f[1]):
+                results.append((f"JSON-object case {c}", run_json_case(BL, c, int(f[2]) if len(f) > 2 else 40)))
         elif kind == "grammar":
             for c in parse_range(f[1]):
                 results.append((f"grammar case {c}", run_grammar_case(BL, c, int(f[2]) if len(f) > 2 else 30)))

@@ -92,6 +92,33 @@ def test_sampled_grammar_cases(case):
     assert err is None, err
 
 
+@pytest.mark.parametrize("case", range(len(RP.JSON_CASES)))
+def test_json_object_cases(case):
+    say(f"JSON-object case {case}: {RP.JSON_CASES[case]}")
+    err = RP.run_json_case(BL, case, 150)
+    assert err is None, err
+
+
+def test_json_object_errors():
+    say("JSON-object errors")
+    blob, off, eos = RP.json_vocab(np.random.default_rng(2), 20)
+    V = len(off) - 1
+    ctx = BL.Context(V, 1, 1)
+    ctx.set_eog(eos, [])
+    ctx.set_vocab(blob, off)
+    ctx.slot_reset(0, BL.Params(temperature=1.0, mirostat=2), 1)
+    with pytest.raises(BL.BLError) as e:
+        ctx.slot_json_object(0)
+    assert e.value.code == BL.BL_EPARAM and "cannot be combined with constrained decoding" in str(e.value)
+    ctx.slot_reset(0, BL.Params(temperature=0.0), 1)
+    ctx.slot_json_object(0)
+    x = np.zeros(V, np.float32)
+    x[[i for i in range(V) if blob[off[i]:off[i + 1]] == b"{"]] = 5.0
+    buf = torch.from_numpy(x).to("cuda:0")
+    assert blob[off[ctx.sample_step([0], buf.data_ptr(), V)[0][0]]:][:1] == b"{"
+    ctx.close()
+
+
 def test_grammar_errors():
     say("grammar errors")
     blob, off, eos = RP.grammar_vocab(np.random.default_rng(1), 50)

@@ -105,10 +105,13 @@ def test_grammar_masks_and_tokens(simt_lib):
     """The grammar path (GBNF automaton tables, per-token mask walk, masked greedy, on-device commit of
     the reply position) against the oracle's whole-reply re-decode: workload 3 and eight adversarial
     byte-level vocabularies; sampled grammar rows (top-k widening within and past the merged list,
-    full-vocabulary rows whose allowed maximum lies far below the row maximum)."""
-    out = _run(simt_lib, ["w3:3", "w3schema:3", "grammar:0-7:40", "gsamp:0-9:30"], {"SIMT_ORDER": "rand"})
+    full-vocabulary rows whose allowed maximum lies far below the row maximum); response_format json_object
+    slots (the JSON prefix classifier per candidate, forced end of sequence on complete objects)."""
+    out = _run(simt_lib, ["w3:3", "w3schema:3", "grammar:0-7:40", "gsamp:0-9:30", "json:0-3:60"],
+               {"SIMT_ORDER": "rand"})
     assert "ok   workload 3\n" in out and "ok   workload 3 via the schema entry point" in out
     assert out.count("ok   grammar case") == 8 and out.count("ok   sampled grammar") == 10
+    assert out.count("ok   JSON-object case") == 4
 
 
 def test_top_n_sigma(simt_lib):
