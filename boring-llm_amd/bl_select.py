@@ -35,6 +35,7 @@ class Params(C.Structure):
         ("logprobs", C.c_int32), ("n_probs", C.c_int32), ("post_sampling_probs", C.c_int32),
         ("ignore_eos", C.c_int32), ("final_softcap", C.c_float), ("logit_mul", C.c_float),
         ("mirostat", C.c_int32), ("mirostat_tau", C.c_float), ("mirostat_eta", C.c_float),
+        ("adaptive_target", C.c_float), ("adaptive_decay", C.c_float),
     ]
 
     def __init__(self, **kw):

@@ -283,6 +283,8 @@ void bl_params_default(bl_params *p) {
   p->min_keep = 0;
   p->repeat_penalty = 1.0f;
   p->repeat_last_n = 64;
+  p->adaptive_target = -1.0f;
+  p->adaptive_decay = 0.9f;
   p->dry_multiplier = 0.0f;
   p->dry_base = 1.75f;
   p->dry_allowed_length = 2;
@@ -448,6 +450,17 @@ static int configure(int V, const bl_params *p, bl_slot_dev &s) {
   s.mirostat_eta = p->mirostat_eta;
   s.mu = 2.0f * p->mirostat_tau;
   if (p->mirostat != 0 && p->temperature > 0.0f) mode = (mode & ~(BL_M_TOPK | BL_M_FULL)) | BL_M_FULL | BL_M_MIRO;
+  /* adaptive-p takes the step before mirostat and the chain (src/server.br:953-963), at any temperature */
+  if (p->adaptive_target >= 0.0f) {
+    if (p->post_sampling_probs && p->logprobs)
+      return fail(BL_EPARAM, "post_sampling_probs require the standard unconstrained sampling chain");
+    mode = (mode & BL_M_LOGPROBS) | BL_M_ADAPT;
+    s.adapt_target = p->adaptive_target;
+    s.adapt_decay = p->adaptive_decay;
+    const float one_minus = 1.0f - p->adaptive_decay;
+    s.adapt_ws = p->adaptive_target / one_minus;
+    s.adapt_tw = 1.0f / one_minus;
+  }
   s.mode = mode;
   int k = 0;
   if (mode & BL_M_TOPK) k = p->top_k;
@@ -456,7 +469,7 @@ static int configure(int V, const bl_params *p, bl_slot_dev &s) {
   if ((mode & BL_M_MIRO) && p->mirostat == 1 && k < (V < 100 ? V : 100)) k = V < 100 ? V : 100;
   s.k_sel = k;
   /* top-n-sigma filters the candidates of a sampled row (src/sampling.br:752-753); mirostat replaces that chain */
-  if (p->temperature > 0.0f && p->top_n_sigma > 0.0f && !(mode & BL_M_MIRO)) mode |= BL_M_TNS;
+  if (p->temperature > 0.0f && p->top_n_sigma > 0.0f && !(mode & (BL_M_MIRO | BL_M_ADAPT))) mode |= BL_M_TNS;
   s.mode = mode;
   /* DRY (src/sampling.br:114-171): off at multiplier 0, base below 1 or a window of 0; a negative window
    * leaves the logits unchanged as well */
@@ -744,7 +757,7 @@ int bl_slot_grammar(bl_ctx *c, int slot, const char *gbnf, size_t len) {
     s.mode &= ~(BL_M_GRAMMAR | BL_M_GFULL);
   } else {
     if (c->voff.empty()) return fail(BL_EPARAM, "bl_slot_grammar: the vocabulary pieces are not set (bl_set_vocab)");
-    if (s.mirostat != 0)
+    if (s.mirostat != 0 || (s.mode & BL_M_ADAPT))
       return fail(BL_EPARAM, "stateful adaptive sampling cannot be combined with constrained decoding");
     if (s.temperature > 0.0f && s.top_n_sigma > 0.0f)
       return fail(BL_EUNSUPPORTED, "grammar-constrained sampling with top_n_sigma is not supported on the device");
@@ -788,7 +801,7 @@ int bl_slot_json_object(bl_ctx *c, int slot, int on) {
     s.mode &= ~(BL_M_GRAMMAR | BL_M_GFULL);
   } else {
     if (c->voff.empty()) return fail(BL_EPARAM, "bl_slot_json_object: the vocabulary pieces are not set (bl_set_vocab)");
-    if (s.mirostat != 0)
+    if (s.mirostat != 0 || (s.mode & BL_M_ADAPT))
       return fail(BL_EPARAM, "stateful adaptive sampling cannot be combined with constrained decoding");
     if (s.temperature > 0.0f && s.top_n_sigma > 0.0f)
       return fail(BL_EUNSUPPORTED, "JSON-object sampling with top_n_sigma is not supported on the device");
@@ -896,7 +909,7 @@ static void mark_stepped(bl_ctx *c, const int32_t *slots, int B) {
 static bool needs_pass2(bl_ctx *c, const int32_t *slots, int B) {
   for (int i = 0; i < B; i++) {
     const bl_slot_dev &s = c->host_slots[slots[i]];
-    if (s.mode & (BL_M_LOGPROBS | BL_M_FULL | BL_M_GFULL)) return true;
+    if (s.mode & (BL_M_LOGPROBS | BL_M_FULL | BL_M_GFULL | BL_M_ADAPT)) return true;
   }
   return false;
 }
@@ -1062,7 +1075,7 @@ int bl_sample_rows_noalloc(int device, void *stream, const bl_params *params, ui
   rows.top_ids = d_out + 3 * B;
   rows.top_lp = reinterpret_cast<float *>(d_out + 3 * B + B * tsa);
   bool pass2 = false;
-  for (int i = 0; i < B; i++) pass2 |= (hs[i].mode & (BL_M_LOGPROBS | BL_M_FULL | BL_M_GFULL)) != 0;
+  for (int i = 0; i < B; i++) pass2 |= (hs[i].mode & (BL_M_LOGPROBS | BL_M_FULL | BL_M_GFULL | BL_M_ADAPT)) != 0;
   bl_launch_step(d, d_logits, ld, rows, B, pass2, false, st, nullptr);
   HIPCHK(hipGetLastError());
   int32_t status[BL_NOALLOC_ROWS];
@@ -1208,8 +1221,8 @@ int bl_spec_verify(bl_ctx *c, const int32_t *slots, int B, int k, const float *d
     /* each row's draw starts at its position in the RNG chain; an XTC chance draw would shift the rest */
     if (k > 0 && s.temperature > 0.0f && s.xtc_probability > 0.0f && s.xtc_threshold <= 0.5f)
       return fail(BL_EUNSUPPORTED, "speculative rows with XTC are not supported on the device");
-    if (k > 0 && (s.mode & BL_M_MIRO))
-      return fail(BL_EUNSUPPORTED, "speculative rows with mirostat are not supported on the device");
+    if (k > 0 && (s.mode & (BL_M_MIRO | BL_M_ADAPT)))
+      return fail(BL_EUNSUPPORTED, "speculative rows with mirostat or adaptive-p are not supported on the device");
     /* row i's DRY window would hold drafts[0..i) */
     if (k > 0 && s.dry_on) return fail(BL_EUNSUPPORTED, "speculative rows with DRY are not supported on the device");
     /* with dynatemp_range >= temperature the effective temperature can reach 0, and such a row makes no draw

@@ -62,6 +62,7 @@
 #define BL_M_PSP 32 /* logprobs as post-sampling probabilities (src/server.br:1015-1025) */
 #define BL_M_MIRO 64 /* the draw is mirostat v2's */
 #define BL_M_TNS 128 /* top-n-sigma filters the ranked candidates (src/sampling.br:376-407) */
+#define BL_M_ADAPT 512 /* adaptive-p replaces the chain (src/sampling.br:705-740); the row's normaliser is formed */
 #define BL_M_GFULL 256 /* a sampled top-k grammar row: the exponent pass also lists its allowed candidates, for
                           the widening level that ranks the whole vocabulary */
 
@@ -140,6 +141,8 @@ struct bl_slot_dev {
    * dh_len / dh_head in bl_dev.dring), the tokens flagged by the last update (bl_dev.dlist), and the sequence
    * breakers: single tokens sorted as (token << 32 | segment), where segment = the longer breakers listed
    * before the token's first single occurrence; longer breakers as [length, tokens...] rows in list order */
+  /* adaptive-p: target, decay and the running weighted sum and total weight (src/server.br:937-938) */
+  float adapt_target, adapt_decay, adapt_ws, adapt_tw;
   int32_t dry_on, dry_allowed, dry_n, dry_maxexp;
   float dry_mult, dry_base;
   int32_t dh_len, dh_head, dry_cnt, n_bsingle, n_bmulti, pad3;

@@ -440,7 +440,7 @@ __device__ __forceinline__ void rowpass_body(const bl_dev &d, const float *__res
 #pragma unroll
     for (int k = 1; k < BL_RP_THREADS / 64; k++) argmax_merge(cm, ci, red_m[k], red_i[k]);
     const int64_t o = (int64_t)row * nc + c;
-    if (sp.mode & BL_M_LOGPROBS) {
+    if (sp.mode & (BL_M_LOGPROBS | BL_M_ADAPT)) {
       float *red_s = xs; /* [BL_SUBS][BL_RP_THREADS]; the value area is free until the key list */
 #pragma unroll
       for (int j = 0; j < NV; j++) {
@@ -841,7 +841,7 @@ __device__ __forceinline__ void exppass_body(const bl_dev &d, const float *__res
   const int slot = bl_row_slot(rows, row);
   const bl_slot_dev &sp = slot_of(d, slot);
   const int mode = sp.mode;
-  if (!(mode & (BL_M_LOGPROBS | BL_M_FULL | BL_M_GFULL))) return;
+  if (!(mode & (BL_M_LOGPROBS | BL_M_FULL | BL_M_GFULL | BL_M_ADAPT))) return;
   __shared__ uint64_t s_tab[BL_EXP2_N]; /* expf's 2^(i/32) table */
   float *const vals = reinterpret_cast<float *>(k2_lds); /* [BL_EB] */
   __shared__ uint32_t st_sup[BL_EB / 32], st_done[SPEC ? BL_EB / 32 : 1];
@@ -894,7 +894,7 @@ __device__ __forceinline__ void exppass_body(const bl_dev &d, const float *__res
   }
   bl_wargmax(M, Mi, lane);
 
-  if (mode & BL_M_LOGPROBS) {
+  if (mode & (BL_M_LOGPROBS | BL_M_ADAPT)) {
     /* lane k: chunk k's sub-blocks before this block, scaled by the hardware exponential (a prediction:
      * its error, ~1e-7 relative, is far inside the 2^-20 margin of the critical-group test, and a wrong
      * binade is caught on the exact state) */
@@ -2539,6 +2539,97 @@ __device__ __forceinline__ void sel_merge(const bl_dev &d, int row, int K, sel_s
   __syncthreads();
 }
 
+/* ------------------------------------------------------------------ adaptive-p */
+/*
+ * sample_adaptive_p (src/sampling.br:705-740) by the block, after the row's normaliser (M, lse): the
+ * adapted target 2 target - average (clamped to [0, 1]); each value's probability exp(x - M - lse) and its
+ * transform 5 - 10 d^2 / (1 + d), d = |p - target'| / 0.3 (values <= -1e29 kept), over the row in
+ * chunks through the server stages; the transform's maximum and its sum of exp(t - tmax) in index order
+ * (exact: the group records and the walk of the sequential float32 sums); then the draw's running sum of
+ * exp(t - tmax - ln sum) in index order up to the uniform draw. Returns the token; ws / tw = the slot's
+ * next weighted sum and total weight.
+ */
+__device__ __forceinline__ int32_t sample_adaptive(const bl_dev &d, const bl_slot_dev &sp, const bl_rows &rows, int row,
+                                                int slot, const float *__restrict__ logits, int64_t ld, float M,
+                                                float lse, uint64_t &rng, sel_shared &sh, float &ws, float &tw) {
+  const int V = d.vocab, t = threadIdx.x, w = t >> 6, lane = t & 63;
+  float *tbuf = reinterpret_cast<float *>(d.sortk + (int64_t)row * 2 * V); /* terms [V] */
+  float *tv = tbuf + 2 * (int64_t)V;                                      /* transformed values [V] */
+  bl_grec *recs = reinterpret_cast<bl_grec *>(d.grec) + (int64_t)row * 2 * (V / 64 + 64) + (V / 64 + 64);
+  double *gsum = d.gsum + (int64_t)row * (V / 64 + 64);
+  const float avg = sp.adapt_tw == 0.0f ? sp.adapt_target : sp.adapt_ws / sp.adapt_tw;
+  float at = 2.0f * sp.adapt_target - avg;
+  if (at < 0.0f) at = 0.0f;
+  if (at > 1.0f) at = 1.0f;
+  float *vals = reinterpret_cast<float *>(sh.c.keys); /* [BL_CH] */
+  uint32_t *sup = reinterpret_cast<uint32_t *>(sh.c.tmp), *done = sup + BL_CH / 32;
+  static_assert(BL_CH * 4 <= sizeof(sh.c.keys) && (BL_CH / 32 + 1) * 4 <= sizeof(sh.c.tmp), "adaptive-p scratch");
+  float tm = BL_NEG_INF;
+  for (int i0 = 0; i0 < V; i0 += BL_CH) {
+    const int cnt = V - i0 < BL_CH ? V - i0 : BL_CH;
+    for (int p = t; p < cnt; p += BL_SEL_THREADS) vals[p] = logits[(int64_t)row * ld + i0 + p];
+    apply_stages<false>(d, sp, rows, row, slot, i0, cnt, vals, sup, done);
+    for (int p = t; p < cnt; p += BL_SEL_THREADS) {
+      const float x = vals[p];
+      float tt = x;
+      if (!(x <= -1.0e29f)) {
+        const float a = x - M;
+        const float pr = SEL_EXPF(a - lse);
+        const float dist = fabsf(pr - at) / 0.3f;
+        float num = 10.0f * dist;
+        num = num * dist;
+        tt = 5.0f - num / (1.0f + dist);
+      }
+      tv[i0 + p] = tt;
+      tm = fmaxf(tm, tt);
+    }
+    __syncthreads();
+  }
+  int ti = 0;
+  bl_wargmax(tm, ti, lane);
+  if (lane == 0) sh.red_m[w] = tm;
+  __syncthreads();
+  float tmax = sh.red_m[0];
+  for (int q = 1; q < SEL_NW; q++) tmax = fmaxf(tmax, sh.red_m[q]);
+  __syncthreads();
+  auto tval = [&](int64_t j) { return tv[j]; };
+  auto termS = [&](int64_t j) { return tbuf[j]; };
+  /* logprob_normalizer(transformed) (src/sampling.br:725): sum of exp(t - tmax), index order */
+  block_records(V, tval, [&](float v) { return SEL_EXPF(v - tmax); }, recs, gsum, tbuf);
+  if (w == 0) {
+    float S;
+    bl_seq_walk(V, termS, [&](int64_t g) { return recs[g]; }, false, 0.0f, 0, S, lane);
+    if (lane == 0) sh.fres[4] = S;
+  }
+  __syncthreads();
+  const float tsum = SEL_LOGF(sh.fres[4]);
+  __syncthreads();
+  /* the draw (:726-736): the first index whose running sum of exp(t - tmax - tsum) reaches it */
+  uint64_t st = rng;
+  const float draw = bl_rng_f32(&st);
+  block_records(V, tval, [&](float v) {
+    const float a = v - tmax;
+    return SEL_EXPF(a - tsum);
+  }, recs, gsum, tbuf);
+  if (w == 0) {
+    float S;
+    const int f = bl_seq_walk(V, termS, [&](int64_t g) { return recs[g]; }, true, draw, 0, S, lane);
+    if (lane == 0) sh.ires[5] = f >= 0 ? f : V - 1;
+  }
+  __syncthreads();
+  const int32_t sel = sh.ires[5];
+  __syncthreads();
+  rng = st;
+  /* the chosen token's original probability, then the running sums (:737-740) */
+  const float xs = bl_row_value(d, sp, rows, row, slot, logits, ld, sel);
+  const float a = xs - M;
+  const float psel = SEL_EXPF(a - lse);
+  const float wsd = sp.adapt_decay * sp.adapt_ws, twd = sp.adapt_decay * sp.adapt_tw;
+  ws = psel + wsd;
+  tw = 1.0f + twd;
+  return sel;
+}
+
 /* ------------------------------------------------------------------ DRY's penalty map */
 /* the segment of single-token breaker `tok` (the longer breakers listed before its first occurrence), or -1 */
 __device__ __forceinline__ int dry_single_seg(const bl_slot_dev &sp, int32_t tok) {
@@ -2697,6 +2788,8 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
   const int mode = sp.mode, K = sp.k_sel;
   const float T = sp.temperature;
   const bool lp_row = (mode & BL_M_LOGPROBS) && rows.lp;
+  const bool adapt = (mode & BL_M_ADAPT) != 0;
+  const bool norm_row = lp_row || adapt; /* the row's normaliser is formed */
   /* slot state the commit updates */
   const int rl = sp.repeat_last_n, win_len = sp.win_len, win_head = sp.win_head;
   const int n_tokens0 = sp.n_tokens, n_reply0 = sp.n_reply;
@@ -2727,8 +2820,8 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
   /* a grammar row with T > 0 samples from its allowed candidates (src/server.br:323-362) unless its frontier
    * is dead, ambiguous or forces the end of sequence (then the grammar block below decides) */
   const int gst0 = gram ? d.gstat[row] : 0;
-  const bool sampled =
-      T > 0.0f && (!gram || (!(gst0 & (BL_GR_FAMBIG | BL_GR_DEAD | BL_GR_FORCED)) && d.gamb[row] == 0));
+  const bool sampled = !(mode & BL_M_ADAPT) && T > 0.0f &&
+                       (!gram || (!(gst0 & (BL_GR_FAMBIG | BL_GR_DEAD | BL_GR_FORCED)) && d.gamb[row] == 0));
   /* top-n-sigma (src/sampling.br:376-407): the threshold max - n * sigma, by wavefront 0 from the row pass's
    * chunk statistics; candidates below it leave the ranked list (the reference sets them to -1e30, which
    * ranks them after every other value and gives them no weight) */
@@ -3181,9 +3274,9 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
 
   /* the normaliser, prepared by every wavefront; then wavefront 0 chains it while wavefront 1 runs the
    * short list's sequential loops */
-  if (lp_row) norm_prep(d, row, M, sh, m_pre, br_pre, n_ent);
+  if (norm_row) norm_prep(d, row, M, sh, m_pre, br_pre, n_ent);
   __syncthreads();
-  if (lp_row && w == 0)
+  if (norm_row && w == 0)
     norm_chain(d, row, sh, [&](int64_t j) { return SEL_EXPF(bl_row_value(d, sp, rows, row, slot, logits, ld, (int32_t)j) - M); });
   if (sampled && !status && short_list && w == 1) {
     const sel_draw r = ranked_serial(sp, n_draw, nlog_draw, keep, rng, skip, typ, sh, &sh.rng_out);
@@ -3191,6 +3284,13 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
   }
   __syncthreads();
   const float S_norm = sh.n.S; /* the normaliser's LDS is scratch from here on (heap ties) */
+  float ad_ws = 0.0f, ad_tw = 0.0f; /* adaptive-p's next running sums */
+  if (adapt && !status) {
+    __syncthreads();
+    const float lse1 = SEL_LOGF(S_norm);
+    tok = sample_adaptive(d, sp, rows, row, slot, logits, ld, M, lse1, rng, sh, ad_ws, ad_tw);
+    tokv = bl_row_value(d, sp, rows, row, slot, logits, ld, tok);
+  }
   sel_draw dr;
   dr.pos = -1;
   dr.first = dr.cut = 0;
@@ -3336,6 +3436,10 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
       bl_dry_push(d, sp, slot, tok);
       sp.rng = rng;
       if (mode & BL_M_MIRO) sp.mu = sh.fres[6];
+      if (adapt) {
+        sp.adapt_ws = ad_ws;
+        sp.adapt_tw = ad_tw;
+      }
       sh.ires[7] = 1;
     } else {
       sh.ires[7] = 0;

@@ -33,7 +33,7 @@ enum {
   BL_EGRAMMAR_AMBIG = -7,  /* "grammar is left-recursive or too ambiguous to match" (src/grammar.br:354) */
   BL_EUNSUPPORTED = -8,    /* a sampler stage this library does not run on the device yet: DRY windows above
                               2048 tokens or a negative dry_allowed_length (rejected by bl_slot_reset); XTC,
-                              mirostat, DRY or a grammar on speculative rows, or more than 32
+                              mirostat, adaptive-p, DRY or a grammar on speculative rows, or more than 32
                               drafts with history-dependent penalties; typical_p over a full-vocabulary list
                               above 512 candidates; a mirostat draw that falls through to a prefix end past
                               the candidates within 17.6 T of the maximum */
@@ -81,6 +81,9 @@ typedef struct {
                               (src/sampling.br:676-700), 2 = sample_mirostat_v2 (:663-674) */
   float mirostat_tau;      /* target surprise; the slot's mu starts at 2 tau (src/server.br:936) */
   float mirostat_eta;
+  float adaptive_target;   /* adaptive-p (src/sampling.br:705-740, src/server.br:953-963): on when >= 0 (it then
+                              replaces the sampler chain, at any temperature); default -1 */
+  float adaptive_decay;    /* the running average's decay; default 0.9 */
 } bl_params;
 
 void bl_params_default(bl_params *p);

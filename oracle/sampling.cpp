@@ -707,7 +707,11 @@ AdaptiveResult sample_adaptive_p(Rng rng, const Row &logits, int64_t vocab, floa
     if (logits[i] <= -1.0e29f) {
       transformed[i] = logits[i];
     } else {
+#if ORC_MUTANT == 8 /* planted mistake (tests only): the distance scaled by 0.25 */
+      float distance = fabsf(probability - adapted_target) / 0.25f;
+#else
       float distance = fabsf(probability - adapted_target) / 0.3f;
+#endif
       float num = 10.0f * distance;
       num = num * distance;
       transformed[i] = 5.0f - num / (1.0f + distance);

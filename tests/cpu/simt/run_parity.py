@@ -418,6 +418,48 @@ def run_mirostat(BL, steps, version=2, V=SMALL_V):
     return None
 
 
+ADAPT_ROWS = [(0.3, 0.9, 1.0), (0.05, 0.5, 0.0), (0.8, 0.99, 0.7), (0.0, 0.0, 1.2)]  # target, decay, temperature
+
+
+def run_adaptive(BL, steps, V=SMALL_V):
+    """Adaptive-p rows (target, decay, temperature: the sampler ignores it) on logits with planted ties and
+    excluded (-1e30) values against the oracle's sample_adaptive_p, the running weighted sum and total weight
+    carried by both; the final RNG states."""
+    L = O.lib()
+    L.orc_adaptive_p.restype = O.C.c_int32
+    L.orc_adaptive_p.argtypes = [O.C.POINTER(O.C.c_uint64), O.C.POINTER(O.C.c_float), O.C.c_int64, O.C.c_float,
+                                 O.C.c_float, O.C.POINTER(O.C.c_float), O.C.POINTER(O.C.c_float)]
+    R = len(ADAPT_ROWS)
+    ctx = BL.Context(V, R, R)
+    rng = np.random.default_rng(91)
+    states, wss, tws = [], [], []
+    for r, (tg, dc, T) in enumerate(ADAPT_ROWS):
+        ctx.slot_reset(r, BL.Params(temperature=T, adaptive_target=tg, adaptive_decay=dc), BL.seed_rng(400 + r))
+        states.append(O.C.c_uint64(BL.seed_rng(400 + r)))
+        one = np.float32(1.0) - np.float32(dc)
+        wss.append(O.C.c_float(np.float32(tg) / one))
+        tws.append(O.C.c_float(np.float32(1.0) / one))
+    buf = MEM.zeros(R * V, np.float32)
+    try:
+        for t in range(steps):
+            xs = [miro_logits(rng, V) for _ in range(R)]
+            xs[t % R][rng.integers(0, V, 20)] = np.float32(-1e30)
+            buf.upload(np.concatenate(xs))
+            tok = ctx.sample_step(list(range(R)), buf.ptr, V)[0]
+            for r, (tg, dc, T) in enumerate(ADAPT_ROWS):
+                x = np.ascontiguousarray(xs[r])
+                ot = L.orc_adaptive_p(O.C.byref(states[r]), x.ctypes.data_as(O.C.POINTER(O.C.c_float)), V, tg, dc,
+                                      O.C.byref(wss[r]), O.C.byref(tws[r]))
+                if tok[r] != ot:
+                    return f"step {t} row {r}: token {tok[r]} vs {ot}"
+        for r in range(R):
+            if ctx.slot_rng(r) != states[r].value:
+                return f"row {r}: final RNG state differs"
+    finally:
+        ctx.close()
+    return None
+
+
 def run_pair(BL, ca, cb, steps):
     """Two small cases stepped together in one call (rows 0 and 1 of an odd-length vocabulary: row 1 starts
     at a 4-byte but not 16-byte aligned address)."""
@@ -1056,6 +1098,9 @@ def main():
         elif kind == "dry":  # dry:cases[:steps]
             for c in parse_range(f[1]):
                 results.append((f"DRY case {c}", run_dry(BL, c, int(f[2]) if len(f) > 2 else 20)))
+        elif kind == "adapt":  # adapt:steps[:V]
+            V = int(f[2]) if len(f) > 2 else SMALL_V
+            results.append((f"adaptive-p rows at V={V}", run_adaptive(BL, int(f[1]), V)))
         elif kind == "miro1":  # miro1:steps[:V]
             V = int(f[2]) if len(f) > 2 else SMALL_V
             results.append((f"mirostat v1 rows at V={V}", run_mirostat(BL, int(f[1]), 1, V)))

@@ -42,11 +42,12 @@ def test_integration_extern_block_names_every_export():
 
 
 def test_params_layout_matches_header():
-    # bl_params is 28 4-byte fields in the header's order
-    assert ctypes.sizeof(BL.Params) == 28 * 4
+    # bl_params is 30 4-byte fields in the header's order
+    assert ctypes.sizeof(BL.Params) == 30 * 4
     p = BL.Params()
     assert p.temperature == 0.0 and p.top_p == 1.0 and p.repeat_last_n == 64 and p.dynatemp_exponent == 1.0
     assert p.mirostat == 0 and p.mirostat_tau == 5.0 and abs(p.mirostat_eta - 0.1) < 1e-7
+    assert p.adaptive_target == -1.0 and abs(p.adaptive_decay - 0.9) < 1e-7
 
 
 def test_seed_fold():

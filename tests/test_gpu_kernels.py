@@ -96,6 +96,14 @@ def test_dry_rows(case):
     assert err is None, err
 
 
+def test_adaptive_p_rows():
+    print("four adaptive-p rows, V=5003: 40 steps; V=151936: 10 steps", flush=True)
+    err = RP.run_adaptive(BL, 40)
+    assert err is None, err
+    err = RP.run_adaptive(BL, 10, 151936)
+    assert err is None, err
+
+
 def test_mirostat_v1_rows():
     print("three mirostat v1 rows, V=5003: 40 steps; V=151936: 12 steps", flush=True)
     err = RP.run_mirostat(BL, 40, 1)

@@ -242,6 +242,10 @@ def test_errors_are_reported(cuda):
     ctx.slot_reset(0, BL.Params(temperature=1.0, dynatemp_range=0.5, dynatemp_exponent=2.0), 1)  # device path
     ctx.slot_reset(0, BL.Params(temperature=1.0, mirostat=1), 1)  # device path
     ctx.slot_reset(0, BL.Params(temperature=1.0, dry_multiplier=0.8), 1)  # device path
+    ctx.slot_reset(0, BL.Params(temperature=1.0, adaptive_target=0.3), 1)  # device path
+    with pytest.raises(BL.BLError) as e:
+        ctx.slot_reset(0, BL.Params(temperature=1.0, adaptive_target=0.3, logprobs=1, post_sampling_probs=1), 1)
+    assert e.value.code == BL.BL_EPARAM
     with pytest.raises(BL.BLError) as e:
         ctx.slot_reset(0, BL.Params(temperature=1.0, dry_multiplier=0.8, dry_penalty_last_n=4096), 1)
     assert e.value.code == BL.BL_EUNSUPPORTED

@@ -14,9 +14,12 @@ that each check fails against an oracle with a planted mistake (oracle/Makefile 
   sample_mirostat_v1's fit (src/sampling.br:683-699): the sequential float32 loop over the first 100 ranked
       probabilities with glibc's logf and powf through ctypes, and on exact Zipf probabilities the fitted
       exponent and the closed-form cutoff.
+  sample_adaptive_p (src/sampling.br:705-740): the row's normaliser, the transformed values, their
+      normaliser and the draw's running sum in index order, with numpy sequential sums and glibc's expf/logf.
 The planted mistakes: ties sent to the right child in the sift (1), a pairwise normaliser sum (2), the
 softmax sum in reverse rank order (3), the tempered sum as two halves (4), top-n-sigma's value sum in
-float32 (5), the mirostat v1 fit's last pair dropped (6).
+float32 (5), the mirostat v1 fit's last pair dropped (6), adaptive-p's distance scaled by 0.25 (8); the
+JSON classifier's mistake (7) is caught in test_oracle_json.py.
 """
 import ctypes
 from fractions import Fraction
@@ -364,3 +367,63 @@ def test_mirostat_v1_fit_recovers_a_zipf_exponent():
 
 def test_mirostat_v1_check_fails_on_planted_mistake():
     assert miro_mismatches(O.mutant(6), miro_rows()) > 0
+
+
+# ---------------------------------------------------------------- adaptive-p
+
+def adaptive_trace(state, x, target, decay, ws, tw):
+    """sample_adaptive_p (src/sampling.br:705-740) from numpy's sequential float32 sums and glibc's expf/logf:
+    the normaliser of the row, the transformed values, their normaliser, the draw's running sum in index
+    order (the RNG's first draw from its closed form); returns (token, state, weighted sum, total weight)."""
+    x = np.asarray(x, F)
+    M = x.max()
+    lse = F(_m.logf(seq_sum(gexpf(x - M))))
+    p = gexpf((x - M) - lse)
+    avg = target if tw == F(0.0) else F(ws / tw)
+    at = F(F(2.0) * target - avg)
+    at = min(max(at, F(0.0)), F(1.0))
+    dist = (np.abs(p - at) / F(0.3)).astype(F)
+    num = ((F(10.0) * dist).astype(F) * dist).astype(F)
+    t = np.where(x <= F(-1e29), x, (F(5.0) - (num / (F(1.0) + dist)).astype(F)).astype(F)).astype(F)
+    tmax = t.max()
+    tsum = F(_m.logf(seq_sum(gexpf(t - tmax))))
+    s1 = xorshift(state)
+    draw = F(F(u64_to_f32(s1)) / F(2.0 ** 64))
+    run = np.cumsum(gexpf((t - tmax) - tsum), dtype=F)
+    hit = np.nonzero(run >= draw)[0]
+    sel = int(hit[0]) if len(hit) else len(x) - 1
+    return sel, s1, F(p[sel] + F(decay * ws)), F(F(1.0) + F(decay * tw))
+
+
+def adaptive_rows():
+    rng = np.random.default_rng(29)
+    rows = []
+    for k in range(24):
+        V = int(rng.choice([3, 40, 777, 3000]))
+        x = (rng.standard_normal(V) * float(rng.uniform(0.5, 5.0))).astype(F)
+        if k % 5 == 0:
+            x[rng.integers(0, V, max(1, V // 30))] = F(-1e30)  # excluded from the transform
+        target, decay = F(rng.choice([0.05, 0.3, 0.6, 0.95])), F(rng.choice([0.0, 0.5, 0.9, 0.99]))
+        ws, tw = (F(0.0), F(0.0)) if k % 7 == 0 else (F(target / F(F(1.0) - decay)), F(F(1.0) / F(F(1.0) - decay)))
+        rows.append((int(rng.integers(1, 2 ** 63)), x, target, decay, ws, tw))
+    return rows
+
+
+def adaptive_mismatches(L):
+    bad = 0
+    for state, x, target, decay, ws, tw in adaptive_rows():
+        want = adaptive_trace(state, x, target, decay, ws, tw)
+        s = ctypes.c_uint64(state)
+        w, tt = ctypes.c_float(ws), ctypes.c_float(tw)
+        tok = L.orc_adaptive_p(ctypes.byref(s), O.fp(x), len(x), float(target), float(decay), ctypes.byref(w),
+                               ctypes.byref(tt))
+        bad += (tok, s.value) != want[:2] or F(w.value) != want[2] or F(tt.value) != want[3]
+    return bad
+
+
+def test_adaptive_p_is_the_sequential_loop():
+    assert adaptive_mismatches(O.lib()) == 0
+
+
+def test_adaptive_p_check_fails_on_planted_mistake():
+    assert adaptive_mismatches(O.mutant(8)) > 0

@@ -70,6 +70,14 @@ def test_mirostat_v2(simt_lib):
     assert "ok   mirostat v2 rows" in out
 
 
+def test_adaptive_p(simt_lib):
+    """Adaptive-p rows (src/sampling.br:705-740): the row's normaliser, the transformed values through the
+    server stages, their index-order sums and the draw, the running weighted sum carried across steps, against
+    the oracle's sample_adaptive_p (V=5003 and 20000)."""
+    out = _run(simt_lib, ["adapt:8", "adapt:3:20000"], {"SIMT_ORDER": "rand"})
+    assert "ok   adaptive-p rows at V=5003" in out and "ok   adaptive-p rows at V=20000" in out
+
+
 def test_mirostat_v1(simt_lib):
     """Mirostat v1 rows: the Zipf fit over the merged top-100 keys and its glibc powf estimate, the draw over
     the predicted prefix and the running mu, against the oracle's sample_mirostat_v1 (V=5003 and 20000)."""
