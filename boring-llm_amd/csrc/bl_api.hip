@@ -71,7 +71,9 @@ struct bl_ctx {
   int32_t *d_out = nullptr, *h_out = nullptr;
   int32_t *d_commit_toks = nullptr;
   int32_t *d_mslot = nullptr; /* row table of bl_grammar_mask */
-  int32_t *d_bslot = nullptr, *d_acc = nullptr, *h_acc = nullptr; /* speculative verification: slots, accepted */
+  /* speculative verification's inputs (row slots, RNG skips, drafts, sequence slots) and outputs (tokens,
+   * statuses, accepted lengths), each packed in one block per side: one copy each way */
+  int32_t *d_spec_in = nullptr, *h_spec_in = nullptr, *d_spec_out = nullptr, *h_spec_out = nullptr;
   bl_sdelta *d_delta = nullptr; /* speculative rows' count corrections [rows][BL_SPEC_DCAP] */
   int32_t *d_delta_n = nullptr;
   int bound_B = 0;
@@ -326,11 +328,11 @@ int bl_create(int device, int max_slots, int max_rows, int vocab, bl_ctx **out) 
   ALLOC(c->d_top_lp, R * 256);
   ALLOC(c->d_commit_toks, 4096);
   ALLOC(c->d_mslot, 1);
-  ALLOC(c->d_bslot, R);
-  ALLOC(c->d_acc, R);
   ALLOC(c->d_out, R * (3 + 2 * 256));
   ALLOC(c->d_delta, R * BL_SPEC_DCAP);
   ALLOC(c->d_delta_n, R);
+  ALLOC(c->d_spec_in, 3 * (size_t)R + 4096);
+  ALLOC(c->d_spec_out, 3 * (size_t)R);
 #undef ALLOC
   /* slot records and grammar views start zeroed: a slot is only stepped or committed after bl_slot_reset, and
    * nothing reads uninitialised state even when a caller breaks that rule */
@@ -348,7 +350,8 @@ int bl_create(int device, int max_slots, int max_rows, int vocab, bl_ctx **out) 
       hipHostMalloc((void **)&c->h_lp, R * sizeof(float)) != hipSuccess ||
       hipHostMalloc((void **)&c->h_top_ids, R * 256 * sizeof(int32_t)) != hipSuccess ||
       hipHostMalloc((void **)&c->h_top_lp, R * 256 * sizeof(float)) != hipSuccess ||
-      hipHostMalloc((void **)&c->h_acc, R * sizeof(int32_t)) != hipSuccess ||
+      hipHostMalloc((void **)&c->h_spec_in, (3 * (size_t)R + 4096) * sizeof(int32_t)) != hipSuccess ||
+      hipHostMalloc((void **)&c->h_spec_out, 3 * (size_t)R * sizeof(int32_t)) != hipSuccess ||
       hipHostMalloc((void **)&c->h_out, R * (3 + 2 * 256) * sizeof(int32_t)) != hipSuccess) {
     bl_destroy(c);
     return fail(BL_EDEVICE, "hipHostMalloc failed");
@@ -380,7 +383,8 @@ void bl_destroy(bl_ctx *c) {
   if (c->d_voff) hipFree(c->d_voff);
   for (void *p : c->dry_mem)
     if (p) hipFree(p);
-  void *hp[] = {c->h_slot, c->h_bound, c->h_skip, c->h_tok, c->h_status, c->h_lp, c->h_top_ids, c->h_top_lp, c->h_acc, c->h_out};
+  void *hp[] = {c->h_slot, c->h_bound, c->h_skip, c->h_tok, c->h_status, c->h_lp, c->h_top_ids, c->h_top_lp, c->h_out,
+                c->h_spec_in, c->h_spec_out};
   for (void *p : hp)
     if (p) hipHostFree(p);
   for (hipEvent_t e : c->ev)
@@ -1231,19 +1235,31 @@ int bl_spec_verify(bl_ctx *c, const int32_t *slots, int B, int k, const float *d
       return fail(BL_EUNSUPPORTED, "speculative rows with dynatemp_range >= temperature are not supported on the device");
   }
   hipSetDevice(c->device);
+  /* one block in: row slots [0, R), RNG skips [R, 2R), drafts [2R, 2R + Bk), sequence slots [2R + Bk, 2R + Bk + B) */
+  const int nd = B * k;
+  int32_t *hin = c->h_spec_in;
   for (int b = 0; b < B; b++)
     for (int i = 0; i <= k; i++) {
+      hin[b * (k + 1) + i] = slots[b];
+      hin[R + b * (k + 1) + i] = i;
       c->h_slot[b * (k + 1) + i] = slots[b];
-      c->h_skip[b * (k + 1) + i] = i;
     }
-  HIPCHK(hipMemcpyAsync(c->d_slot, c->h_slot, R * sizeof(int32_t), hipMemcpyHostToDevice, c->stream));
-  HIPCHK(hipMemcpyAsync(c->d_skip, c->h_skip, R * sizeof(int32_t), hipMemcpyHostToDevice, c->stream));
-  if (k > 0) HIPCHK(hipMemcpyAsync(c->d_commit_toks, drafts, (size_t)B * k * 4, hipMemcpyHostToDevice, c->stream));
-  HIPCHK(hipMemcpyAsync(c->d_bslot, slots, B * sizeof(int32_t), hipMemcpyHostToDevice, c->stream));
+  if (nd > 0) memcpy(hin + 2 * R, drafts, (size_t)nd * 4);
+  memcpy(hin + 2 * R + nd, slots, B * sizeof(int32_t));
+  HIPCHK(hipMemcpyAsync(c->d_spec_in, hin, ((size_t)2 * R + nd + B) * sizeof(int32_t), hipMemcpyHostToDevice,
+                        c->stream));
+  const int32_t *d_rslot = c->d_spec_in, *d_rskip = c->d_spec_in + R, *d_drafts = c->d_spec_in + 2 * R,
+                *d_sslot = c->d_spec_in + 2 * R + nd;
+  /* one block out: tokens [0, R), statuses [R, 2R), accepted lengths [2R, 2R + B) */
+  int32_t *d_tok = c->d_spec_out, *d_stat = c->d_spec_out + R, *d_acc = c->d_spec_out + 2 * R;
   bl_rows rows = make_rows(c, true, 0, 1);
+  rows.slot = d_rslot;
+  rows.rng_skip = d_rskip;
+  rows.tok = d_tok;
+  rows.status = d_stat;
   rows.lp = nullptr; /* no logprobs are returned for speculative rows */
   if (pen) {
-    hipLaunchKernelGGL(bl_k_spec_delta, dim3(B), dim3(64), 0, c->stream, c->d, c->d_bslot, c->d_commit_toks, k,
+    hipLaunchKernelGGL(bl_k_spec_delta, dim3(B), dim3(64), 0, c->stream, c->d, d_sslot, d_drafts, k,
                        c->d_delta, c->d_delta_n);
     HIPCHK(hipGetLastError());
     rows.delta = c->d_delta;
@@ -1251,18 +1267,18 @@ int bl_spec_verify(bl_ctx *c, const int32_t *slots, int B, int k, const float *d
   }
   mark_stepped(c, slots, B);
   bl_launch_step(c->d, d_rows, ld, rows, R, needs_pass2(c, slots, B), false, c->stream, nullptr);
-  hipLaunchKernelGGL(bl_k_spec_commit, dim3(B), dim3(64), 0, c->stream, c->d, c->d_bslot, c->d_commit_toks, k,
-                     c->d_tok, c->d_status, R, c->d_acc);
+  hipLaunchKernelGGL(bl_k_spec_commit, dim3(B), dim3(64), 0, c->stream, c->d, d_sslot, d_drafts, k, d_tok, d_stat, R,
+                     d_acc);
   HIPCHK(hipGetLastError());
-  HIPCHK(hipMemcpyAsync(c->h_tok, c->d_tok, R * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));
-  HIPCHK(hipMemcpyAsync(c->h_status, c->d_status, R * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));
-  HIPCHK(hipMemcpyAsync(c->h_acc, c->d_acc, B * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(hipMemcpyAsync(c->h_spec_out, c->d_spec_out, ((size_t)2 * R + B) * sizeof(int32_t), hipMemcpyDeviceToHost,
+                        c->stream));
   HIPCHK(wait_stream(c->stream));
+  const int32_t *hout = c->h_spec_out;
   int st = 0;
-  for (int i = 0; i < R; i++) st |= c->h_status[i];
-  memcpy(tokens, c->h_tok, R * sizeof(int32_t));
+  for (int i = 0; i < R; i++) st |= hout[R + i];
+  memcpy(tokens, hout, R * sizeof(int32_t));
   if ((rc = status_error(st))) return rc;
-  memcpy(accepted, c->h_acc, B * sizeof(int32_t));
+  memcpy(accepted, hout + 2 * R, B * sizeof(int32_t));
   return BL_OK;
 }
 
