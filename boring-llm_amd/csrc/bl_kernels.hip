@@ -1336,6 +1336,7 @@ struct sel_cand {
  * list, in the normaliser's LDS (free until norm_prep) */
 #define BL_BOFF_BYTES (((BL_MAX_CHUNKS * BL_SUBS + 1) * 4 + 15) / 16 * 16)
 #define BL_RTILE 4096 /* keys per rank tile */
+#define BL_SPLIT_TIES 8 /* halfway tail terms a plain draw's head/tail split resolves */
 #define BL_CAND_U 8   /* candidate loads in flight per lane */
 static_assert(BL_BOFF_BYTES + BL_RTILE * 8 <= sizeof(sel_norm), "rank tile");
 static_assert(BL_RTILE % BL_SEL_THREADS == 0, "rank tile");
@@ -1368,6 +1369,12 @@ struct sel_shared {
   double ltab[32];                     /* logf's (1/c, log c) table */
   float tns_thr;                       /* top-n-sigma's threshold */
   int tns_st;                          /* its sigma undecided */
+  int split_h;                         /* a plain draw's last ranked bucket */
+  float split_s;                       /* the ranked head's exact sum */
+  int split_nt;                        /* its tail's terms halfway between multiples of u: count, */
+  uint32_t split_par;                  /* parities of the other tail terms before each, */
+  uint64_t split_tk[BL_SPLIT_TIES];    /* keys, */
+  double split_tf[BL_SPLIT_TIES];      /* floor(t / u) */
 };
 /* expf and logf through the selection's LDS copies of their tables */
 #define SEL_EXPF(x) bl_expf_tab((x), [&](uint32_t i_) { return sh.etab[i_]; })
@@ -1410,7 +1417,7 @@ __device__ __forceinline__ float sel_rl(float x, int k) {
  * lanes' values in list order, every lane computing the same sum, so they are the reference's float32
  * sums. *rng_out = the state after the draw (written by lane 0) */
 __device__ __forceinline__ sel_draw ranked_serial(const bl_slot_dev &sp, int n, int64_t n_logical, int64_t keep, uint64_t rng,
-                                 int rng_skip, bool pre, sel_shared &sh, uint64_t *rng_out) {
+                                 int rng_skip, bool pre, float S_whole, sel_shared &sh, uint64_t *rng_out) {
   const int lane = threadIdx.x & 63;
   const float *ser_e = sh.ser_e, *ser_v = sh.ser_v;
   float *ser_r = sh.ser_r;
@@ -1562,6 +1569,7 @@ __device__ __forceinline__ sel_draw ranked_serial(const bl_slot_dev &sp, int n, 
     const int m = n_eff - b0 < 64 ? n_eff - b0 : 64;
     for (int k = 0; k < m; k++) S += sel_rl(e, k);
   }
+  if (S_whole > 0.0f) S = S_whole; /* the list is the head of a longer one whose sum is known */
   const float target = bl_rng_f32(&st) * S;
   float run = 0.0f;
   int64_t f = -1;
@@ -1686,8 +1694,8 @@ __device__ __forceinline__ int typical_filter(const bl_slot_dev &sp, int n, bool
  */
 template <class ValF>
 __device__ __forceinline__ sel_draw sample_ranked_long(const bl_slot_dev &sp, ValF val, int64_t n_list, int64_t n_logical,
-                                      int64_t keep, uint64_t &rng, int rng_skip, bl_grec *recs, double *gsum,
-                                      float *tbuf, sel_shared &sh, int &status) {
+                                      int64_t keep, uint64_t &rng, int rng_skip, float S_whole, bl_grec *recs,
+                                      double *gsum, float *tbuf, sel_shared &sh, int &status) {
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   const float T = sp.temperature;
   const float v0 = val(0);
@@ -1836,6 +1844,7 @@ __device__ __forceinline__ sel_draw sample_ranked_long(const bl_slot_dev &sp, Va
   if (w == 0) {
     float S;
     bl_seq_walk(m, termS, [&](int64_t g) { return recs[g]; }, false, 0.0f, 0, S, lane);
+    if (S_whole > 0.0f) S = S_whole; /* the list is the head of a longer one whose sum is known */
     float r01 = bl_rng_f32(&st);
     float target = r01 * S;
     float S2;
@@ -2874,6 +2883,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
   const uint32_t *gmk = d.gmask + (int64_t)row * gwords;
   auto g_allowed = [&](int32_t id) { return ((gmk[(id >> 6) * 2 + ((id >> 5) & 1)] >> (id & 31)) & 1u) != 0u; };
   float Mc = M; /* the top of the ranked list: the row maximum, or a grammar row's allowed maximum */
+  float split_S = 0.0f; /* > 0: the list is a plain draw's ranked head, and this the whole list's sum */
   bool gfull = false; /* a top-k grammar row's widening went past the merged list */
   int gk = 0;         /* its next level */
   if (sampled && gram && (mode & BL_M_TOPK)) {
@@ -3038,8 +3048,6 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
         const float q = (Mc - v) * scale;
         return q >= 0.0f ? (q < (float)(BL_NBUCKET - 1) ? (int)q : BL_NBUCKET - 1) : 0;
       };
-      for (int b = t; b < BL_NBUCKET; b += BL_SEL_THREADS) cnt[b] = 0u;
-      __syncthreads();
       /* wavefront w reads regions w, w + SEL_NW, ... in batches of 64 * BL_CAND_U candidates; each lane
        * keeps BL_CAND_U loads (values, and ids when asked) in flight, the next batch's issued before this
        * batch's stores (stores share the in-order load counter) */
@@ -3079,73 +3087,244 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
           f(v, id);
         }
       };
-      each_region(std::false_type{}, [&](const float *v, const int32_t *) {
-#pragma unroll
-        for (int u = 0; u < BL_CAND_U; u++)
-          if (v[u] >= thr) atomicAdd(&cnt[bucket(v[u])], 1u);
-      });
-      __syncthreads();
-      /* exclusive offsets: thread t owns buckets [t*PB, (t+1)*PB) */
-      constexpr int PB = BL_NBUCKET / BL_SEL_THREADS;
-      uint32_t loc[PB], own = 0u;
-#pragma unroll
-      for (int q = 0; q < PB; q++) {
-        loc[q] = cnt[t * PB + q];
-        own += loc[q];
-      }
-      const uint32_t incl = (uint32_t)bl_wscan_add((int)own, lane);
-      if (lane == 63) sh.red_i[w] = (int)incl;
-      __syncthreads();
-      uint32_t run = incl - own;
-      int nk = 0;
-      for (int q = 0; q < SEL_NW; q++) {
-        if (q < w) run += (uint32_t)sh.red_i[q];
-        nk += sh.red_i[q];
-      }
-#pragma unroll
-      for (int q = 0; q < PB; q++) {
-        cnt[t * PB + q] = run;
-        run += loc[q];
-      }
-      __syncthreads();
-      each_region(std::true_type{}, [&](const float *v, const int32_t *id) {
-#pragma unroll
-        for (int u = 0; u < BL_CAND_U; u++)
-          if (v[u] >= thr) A[atomicAdd(&cnt[bucket(v[u])], 1u)] = ckey(v[u], id[u]);
-      });
-      __syncthreads(); /* cnt[b] is now the end of bucket b */
-      uint64_t *tile = reinterpret_cast<uint64_t *>(reinterpret_cast<char *>(&sh.n) + BL_BOFF_BYTES);
-      constexpr int TU = BL_RTILE / BL_SEL_THREADS;
-      uint64_t pre[TU]; /* the next tile, loaded before this tile's stores */
-#pragma unroll
-      for (int u = 0; u < TU; u++) pre[u] = t + u * BL_SEL_THREADS < nk ? A[t + u * BL_SEL_THREADS] : 0ull;
-      for (int base = 0; base < nk; base += BL_RTILE) {
-        const int n_t = min(BL_RTILE, nk - base);
-#pragma unroll
-        for (int u = 0; u < TU; u++) tile[t + u * BL_SEL_THREADS] = pre[u];
-        __syncthreads();
-#pragma unroll
-        for (int u = 0; u < TU; u++) {
-          const int i = base + BL_RTILE + t + u * BL_SEL_THREADS;
-          pre[u] = i < nk ? A[i] : 0ull;
+      /* A plain draw (no probability filter) needs the list's order only down to where its float running sum
+       * has entered the binade [2^K, 2^(K+1)) of the final sum S: within one binade each later addition is
+       * s + u round(t / u) (u = 2^(K-23), the rounding of s + t, an exact multiple of u, at any s there),
+       * whatever the order, unless t / u lies exactly halfway. So only the head of the bucketed list is ranked,
+       * down to a bucket whose lower-bounded mass passes both 2^K and the draw's target (with the
+       * approximate sum's margins), and the tail's sum(round(t / u)) is counted in one pass. The head's exact
+       * sum then decides: S = s_head + u sum(round(t / u)) when s_head lies in binade K, S < 2^(K+1) and the
+       * target lies within the head; otherwise every bucket is ranked. A tail term t = u (f + 1/2) rounds to
+       * the even multiple of u: it adds u (f + (N + f) mod 2), N = s / u before it, whose parity is s_head's,
+       * the other tail terms' with larger values (a second pass) and the earlier such terms' (in key order). */
+      bool split = !filt && !gram && !(mode & BL_M_TNS) && T > 0.0f && span > 0.0f;
+      int Kb = 0;
+      float r01 = 0.0f;
+      double need = 0.0;
+      if (split) {
+        const double lo = s_ap * (1.0 - 4.0e-3), hi = s_ap * (1.0 + 4.0e-3);
+        const int klo = (int)((bl_d2u(lo) >> 52) & 0x7ff) - 1023, khi = (int)((bl_d2u(hi) >> 52) & 0x7ff) - 1023;
+        split = lo >= 1.0 && klo == khi && khi < 60;
+        if (split) {
+          Kb = klo;
+          uint64_t st = rng;
+          for (int k = 0; k < skip; k++) st = bl_xorshift(st);
+          r01 = bl_rng_f32(&st);
+          need = fmax(bl_u2d((uint64_t)(Kb + 1023) << 52), (double)r01 * hi) * (1.0 + 4.0e-3);
         }
+      }
+      const int need_c = (sp.min_keep > sp.n_probs ? sp.min_keep : sp.n_probs) + 2;
+      /* a lower bound on a term of bucket b (its values exceed Mc - (b + 1) span / BL_NBUCKET) */
+      const float bstep = span / (float)BL_NBUCKET / T;
+      int nk = 0;
+      for (int pass = split ? 0 : 1;; pass++) {
+        const bool head = pass == 0;
+        for (int b = t; b < BL_NBUCKET; b += BL_SEL_THREADS) cnt[b] = 0u;
+        if (t == 0) {
+          sh.split_h = BL_NBUCKET;
+          sh.split_nt = 0;
+          sh.split_par = 0u;
+        }
+        __syncthreads();
+        each_region(std::false_type{}, [&](const float *v, const int32_t *) {
 #pragma unroll
-        for (int u = 0; u < TU; u++) {
-          const int i = t + u * BL_SEL_THREADS;
-          if (i < n_t) {
-            const uint64_t k = tile[i];
-            const int bk = bucket(ckey_v(k));
-            const int s0 = bk > 0 ? (int)cnt[bk - 1] : 0, e0 = (int)cnt[bk];
-            int r = 0;
-            if (s0 >= base && e0 <= base + n_t) {
-              for (int j = s0 - base; j < e0 - base; j++) r += tile[j] > k ? 1 : 0;
-            } else { /* a bucket across the tile's edge */
-              for (int j = s0; j < e0; j++) r += A[j] > k ? 1 : 0;
+          for (int u = 0; u < BL_CAND_U; u++)
+            if (v[u] >= thr) atomicAdd(&cnt[bucket(v[u])], 1u);
+        });
+        __syncthreads();
+        /* exclusive offsets: thread t owns buckets [t*PB, (t+1)*PB) */
+        constexpr int PB = BL_NBUCKET / BL_SEL_THREADS;
+        uint32_t loc[PB], own = 0u;
+        double om = 0.0;
+#pragma unroll
+        for (int q = 0; q < PB; q++) {
+          loc[q] = cnt[t * PB + q];
+          own += loc[q];
+          const int b = t * PB + q;
+          if (head && b < BL_NBUCKET - 1 && loc[q]) om += (double)loc[q] * (double)__expf(-(float)(b + 1) * bstep * 1.001f) * 0.999;
+        }
+        const uint32_t incl = (uint32_t)bl_wscan_add((int)own, lane);
+        const double mincl = head ? bl_wscan_add_d(om, lane) : 0.0;
+        if (lane == 63) {
+          sh.red_i[w] = (int)incl;
+          sh.c.gsum[w] = mincl;
+        }
+        __syncthreads();
+        uint32_t run = incl - own;
+        double mrun = mincl - om;
+        int nall = 0;
+        for (int q = 0; q < SEL_NW; q++) {
+          if (q < w) {
+            run += (uint32_t)sh.red_i[q];
+            mrun += sh.c.gsum[q];
+          }
+          nall += sh.red_i[q];
+        }
+        if (head) { /* the first bucket where the lower-bounded mass and the count both suffice */
+          uint32_t cc = run;
+#pragma unroll
+          for (int q = 0; q < PB; q++) {
+            const int b = t * PB + q;
+            cc += loc[q];
+            if (b < BL_NBUCKET - 1 && loc[q]) mrun += (double)loc[q] * (double)__expf(-(float)(b + 1) * bstep * 1.001f) * 0.999;
+            if (mrun >= need && (int)cc >= need_c) {
+              atomicMin(&sh.split_h, b);
+              break;
             }
-            Bk[s0 + r] = k;
           }
         }
+#pragma unroll
+        for (int q = 0; q < PB; q++) {
+          cnt[t * PB + q] = run;
+          run += loc[q];
+        }
         __syncthreads();
+        const int h_end = head && sh.split_h < BL_NBUCKET - 1 ? sh.split_h + 1 : BL_NBUCKET;
+        const bool tail = h_end < BL_NBUCKET;
+        nk = tail ? (int)cnt[h_end] : nall; /* the ranked head's length */
+        /* the head scattered by bucket; the tail's ulps of 2^K counted (every thread's own sum is exact: at most
+         * 2^23 per term) */
+        const double tsc = bl_u2d((uint64_t)(23 - Kb + 1023) << 52);
+        double tI = 0.0;
+        each_region(std::true_type{}, [&](const float *v, const int32_t *id) {
+#pragma unroll
+          for (int u = 0; u < BL_CAND_U; u++)
+            if (v[u] >= thr) {
+              const int bk = bucket(v[u]);
+              if (bk < h_end) {
+                A[atomicAdd(&cnt[bk], 1u)] = ckey(v[u], id[u]);
+              } else {
+                const float dd = v[u] - Mc;
+                const float qq = dd / T;
+                const double x = (double)SEL_EXPF(qq) * tsc;
+                const double fl = floor(x), fr = x - fl;
+                if (fr == 0.5) {
+                  const int k = atomicAdd(&sh.split_nt, 1);
+                  if (k < BL_SPLIT_TIES) {
+                    sh.split_tk[k] = ckey(v[u], id[u]);
+                    sh.split_tf[k] = fl;
+                  }
+                } else {
+                  tI += fr > 0.5 ? fl + 1.0 : fl;
+                }
+              }
+            }
+        });
+        __syncthreads(); /* cnt[b] is now the end of bucket b (of the head) */
+        const int nt = sh.split_nt;
+        if (tail) tI = block_sum_d<BL_SEL_THREADS>(tI, sh.c.gsum);
+        if (tail && nt > 0 && nt <= BL_SPLIT_TIES) {
+          /* bit k: the parity of the other tail terms' u-multiples before halfway term k (larger values; a
+           * value equal to a halfway term's is one itself) */
+          float tv[BL_SPLIT_TIES];
+#pragma unroll
+          for (int k = 0; k < BL_SPLIT_TIES; k++) tv[k] = k < nt ? ckey_v(sh.split_tk[k]) : 3.0e38f;
+          uint32_t bits = 0u;
+          each_region(std::false_type{}, [&](const float *v, const int32_t *) {
+#pragma unroll
+            for (int u = 0; u < BL_CAND_U; u++)
+              if (v[u] >= thr && bucket(v[u]) >= h_end) {
+                const float dd = v[u] - Mc;
+                const float qq = dd / T;
+                const double x = (double)SEL_EXPF(qq) * tsc;
+                const double fl = floor(x), fr = x - fl;
+                if (fr != 0.5 && ((fr > 0.5 ? (uint64_t)fl + 1u : (uint64_t)fl) & 1u))
+#pragma unroll
+                  for (int k = 0; k < BL_SPLIT_TIES; k++)
+                    if (v[u] > tv[k]) bits ^= 1u << k;
+              }
+          });
+          uint32_t wb = 0u;
+#pragma unroll
+          for (int k = 0; k < BL_SPLIT_TIES; k++) wb |= (uint32_t)(__popcll(__ballot((bits >> k) & 1u)) & 1) << k;
+          if (lane == 0) sh.red_i[w] = (int)wb;
+          __syncthreads();
+          if (t == 0) {
+            uint32_t pb = 0u;
+            for (int q = 0; q < SEL_NW; q++) pb ^= (uint32_t)sh.red_i[q];
+            sh.split_par = pb;
+          }
+          __syncthreads();
+        }
+        uint64_t *tile = reinterpret_cast<uint64_t *>(reinterpret_cast<char *>(&sh.n) + BL_BOFF_BYTES);
+        constexpr int TU = BL_RTILE / BL_SEL_THREADS;
+        uint64_t pre[TU]; /* the next tile, loaded before this tile's stores */
+#pragma unroll
+        for (int u = 0; u < TU; u++) pre[u] = t + u * BL_SEL_THREADS < nk ? A[t + u * BL_SEL_THREADS] : 0ull;
+        for (int base = 0; base < nk; base += BL_RTILE) {
+          const int n_t = min(BL_RTILE, nk - base);
+#pragma unroll
+          for (int u = 0; u < TU; u++) tile[t + u * BL_SEL_THREADS] = pre[u];
+          __syncthreads();
+#pragma unroll
+          for (int u = 0; u < TU; u++) {
+            const int i = base + BL_RTILE + t + u * BL_SEL_THREADS;
+            pre[u] = i < nk ? A[i] : 0ull;
+          }
+#pragma unroll
+          for (int u = 0; u < TU; u++) {
+            const int i = t + u * BL_SEL_THREADS;
+            if (i < n_t) {
+              const uint64_t k = tile[i];
+              const int bk = bucket(ckey_v(k));
+              const int s0 = bk > 0 ? (int)cnt[bk - 1] : 0, e0 = (int)cnt[bk];
+              int r = 0;
+              if (s0 >= base && e0 <= base + n_t) {
+                for (int j = s0 - base; j < e0 - base; j++) r += tile[j] > k ? 1 : 0;
+              } else { /* a bucket across the tile's edge */
+                for (int j = s0; j < e0; j++) r += A[j] > k ? 1 : 0;
+              }
+              Bk[s0 + r] = k;
+            }
+          }
+          __syncthreads();
+        }
+        if (!tail) break;
+        /* the head's exact sum (the draw's terms exp((v - v0) / T), v0 = Mc the first value), then the checks */
+        bl_grec *hrecs = sh.c.recs;
+        double *hgsum = sh.c.gsum;
+        if ((nk + 63) / 64 > BL_LDS_SORT / 64) {
+          hrecs = reinterpret_cast<bl_grec *>(d.grec) + (int64_t)row * 2 * (V / 64 + 64) + (V / 64 + 64);
+          hgsum = d.gsum + (int64_t)row * (V / 64 + 64);
+        }
+        float *htb = reinterpret_cast<float *>(A); /* the unranked head is spent */
+        block_records((int64_t)nk, [&](int64_t j) { return ckey_v(Bk[j]); }, [&](float v) {
+          const float dd = v - Mc;
+          const float qq = dd / T;
+          return SEL_EXPF(qq);
+        }, hrecs, hgsum, htb);
+        if (w == 0) {
+          float Sh;
+          bl_seq_walk((int64_t)nk, [&](int64_t j) { return htb[j]; }, [&](int64_t g) { return hrecs[g]; }, false, 0.0f, 0,
+                      Sh, lane);
+          if (lane == 0) sh.split_s = Sh;
+        }
+        __syncthreads();
+        const float s_head = sh.split_s;
+        const double uK = bl_u2d((uint64_t)(Kb - 23 + 1023) << 52);
+        bool ok = nt <= BL_SPLIT_TIES && ckey_v(Bk[0]) == Mc && (double)s_head >= bl_u2d((uint64_t)(Kb + 1023) << 52);
+        if (ok && nt > 0) { /* the halfway terms in rank order (every thread alike) */
+          uint32_t done = 0u, par = (uint32_t)((uint64_t)((double)s_head / uK) & 1u);
+          for (int r = 0; r < nt; r++) {
+            int kb = -1;
+            for (int k = 0; k < nt; k++)
+              if (!((done >> k) & 1u) && (kb < 0 || sh.split_tk[k] > sh.split_tk[kb])) kb = k;
+            done |= 1u << kb;
+            const double fl = sh.split_tf[kb];
+            const uint32_t pN = par ^ ((sh.split_par >> kb) & 1u); /* N mod 2 before this term */
+            const uint64_t inc = (uint64_t)fl + (((uint64_t)fl + pN) & 1u);
+            tI += (double)inc;
+            par ^= (uint32_t)(inc & 1u);
+          }
+        }
+        const double Sfull = (double)s_head + uK * tI;
+        ok = ok && Sfull < bl_u2d((uint64_t)(Kb + 1 + 1023) << 52);
+        if (ok) ok = r01 * (float)Sfull <= s_head; /* the draw stops within the head */
+        __syncthreads();
+        if (ok) {
+          split_S = (float)Sfull;
+          break;
+        }
       }
       keys = Bk;
       nl = nk;
@@ -3279,7 +3458,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
   if (norm_row && w == 0)
     norm_chain(d, row, sh, [&](int64_t j) { return SEL_EXPF(bl_row_value(d, sp, rows, row, slot, logits, ld, (int32_t)j) - M); });
   if (sampled && !status && short_list && w == 1) {
-    const sel_draw r = ranked_serial(sp, n_draw, nlog_draw, keep, rng, skip, typ, sh, &sh.rng_out);
+    const sel_draw r = ranked_serial(sp, n_draw, nlog_draw, keep, rng, skip, typ, split_S, sh, &sh.rng_out);
     if (lane == 0) sh.draw = r;
   }
   __syncthreads();
@@ -3318,7 +3497,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
       }
       float *tbuf = reinterpret_cast<float *>(d.sortk + (int64_t)row * 2 * V); /* free once the list is sorted */
       dr = miro ? sample_mirostat(sp, val, n_list, n_logical, mk, rng, skip, recs, gsum, tbuf, sh, status)
-                : sample_ranked_long(sp, val, n_list, n_logical, keep, rng, skip, recs, gsum, tbuf, sh, status);
+                : sample_ranked_long(sp, val, n_list, n_logical, keep, rng, skip, split_S, recs, gsum, tbuf, sh, status);
       pos = dr.pos;
       dterm = tbuf;
       dshift = dr.first;

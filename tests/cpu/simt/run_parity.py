@@ -323,6 +323,75 @@ def run_unfiltered(BL, steps, rows=None):
     return None
 
 
+def halfway_rows(copies=(3, 20), V=151936):
+    """Plain full-vocabulary rows (T 1) whose ranked list has a long tail holding `copies` tokens of one value
+    whose term expf(v - 0) lies exactly halfway between two multiples of u = 2^(K-23), K the binade of the
+    row's float32 sum: the maximum 0 at token 0, 6000 values evenly spread over [-9, -0.5], the copies near
+    -6, every other token at -100. Each such term's rounding follows the parity of the running sum before it;
+    past eight of them the device ranks the whole list. Returns the rows (float32, len(copies) x V)."""
+    import ctypes
+    expf = ctypes.CDLL("libm.so.6").expf
+    expf.restype, expf.argtypes = ctypes.c_float, [ctypes.c_float]
+    bulk = np.linspace(-9.0, -0.5, 6000, dtype=np.float32)
+    pos = np.random.default_rng(41).permutation(np.arange(1, V))
+    out = []
+    for n in copies:
+        def fsum(vh):
+            vals = np.sort(np.concatenate([[np.float32(0.0)], bulk, np.full(n, vh, np.float32)]))[::-1]
+            s = np.float32(0.0)
+            for v in vals:
+                s = np.float32(s + np.float32(expf(float(v))))
+            return s
+        S = fsum(np.float32(-6.0))
+        K = int(np.floor(np.log2(float(S))))
+        u = 2.0 ** (K - 23)
+        vh = np.float32(-6.0)
+        while True:
+            y = float(np.float32(expf(float(vh)))) / u
+            if y - np.floor(y) == 0.5:
+                break
+            vh = np.nextafter(vh, np.float32(-np.inf))
+        S2 = fsum(vh)
+        assert int(np.floor(np.log2(float(S2)))) == K and 1.05 < float(S2) / 2.0 ** K < 1.95, (S2, K)
+        x = np.full(V, -100.0, np.float32)
+        x[0] = 0.0
+        x[pos[:6000]] = bulk
+        x[pos[6000:6000 + n]] = vh
+        out.append(x)
+    return np.stack(out)
+
+
+def run_halfway(BL, steps):
+    """halfway_rows' draws against the oracle's slot step, `steps` steps (the RNG moves the target)."""
+    X = halfway_rows()
+    R, V = X.shape
+    ctx = BL.Context(V, R, R)
+    L = O.lib()
+    hs = []
+    for r in range(R):
+        ctx.slot_reset(r, BL.Params(temperature=1.0), BL.seed_rng(950 + r))
+        op = O.params(temperature=1.0)
+        hs.append(L.orc_slot_new(O.C.byref(op), BL.seed_rng(950 + r), None, 0, None, 0, None, None, 0))
+    buf = MEM.zeros(R * V, np.float32)
+    try:
+        buf.upload(X.reshape(-1))
+        for t in range(steps):
+            tok = ctx.sample_step(list(range(R)), buf.ptr, V)[0]
+            for r in range(R):
+                ot, olp = np.zeros(1, np.int32), np.zeros(1, np.float32)
+                oti, otl = np.zeros(1, np.int32), np.zeros(1, np.float32)
+                eog = O.C.c_int()
+                assert L.orc_slot_step(hs[r], O.fp(np.ascontiguousarray(X[r])), V, 0, 1, O.ip(ot), O.fp(olp),
+                                       O.ip(oti), O.fp(otl), O.C.byref(eog)) == 0
+                if tok[r] != ot[0]:
+                    return f"step {t} row {r}: token {tok[r]} vs {ot[0]}"
+    finally:
+        for h in hs:
+            L.orc_slot_free(h)
+        ctx.close()
+    return None
+
+
 TNS_ROWS = [dict(temperature=0.8, top_k=0, top_n_sigma=1.0),
             dict(temperature=1.0, top_k=64, top_n_sigma=0.5, logprobs=1, n_probs=5),
             dict(temperature=0.7, top_k=0, top_n_sigma=2.0, top_p=0.9),
@@ -1107,6 +1176,8 @@ def main():
         elif kind == "unfilt":
             rows = [int(v) for v in f[2].split(",")] if len(f) > 2 else None
             results.append(("unfiltered rows at V=151936", run_unfiltered(BL, int(f[1]), rows)))
+        elif kind == "halfway":
+            results.append(("halfway tail terms", run_halfway(BL, int(f[1]))))
         elif kind == "noalloc":
             results.append(("allocation-free step", run_noalloc(BL)))
         elif kind == "bigk":

@@ -83,6 +83,16 @@ def test_unfiltered_full_vocabulary_rows():
     assert err is None, err
 
 
+def test_halfway_tail_terms():
+    """A plain draw ranks only the head of its list and counts the tail's ulps of 2^K in any order; a tail
+    term exactly halfway between two multiples of u rounds by the parity of the running sum before it. Row 0
+    holds 3 copies of such a value (resolved from the parities), row 1 holds 20 (past the eight the split
+    resolves: the whole list is ranked)."""
+    print("two constructed rows with halfway tail terms, V=151936: 16 steps", flush=True)
+    err = RP.run_halfway(BL, 16)
+    assert err is None, err
+
+
 def test_mirostat_v2_rows():
     print("three mirostat v2 rows, V=5003: 40 steps", flush=True)
     err = RP.run_mirostat(BL, 40)

@@ -88,9 +88,12 @@ def test_mirostat_v1(simt_lib):
 def test_unfiltered_candidate_cut(simt_lib):
     """Full-vocabulary rows without top-p or min-p at V=151936: the candidates cut at half an ulp of the
     draw's running sum (six rows, 12 steps; the bfloat16 row's draws on equal values include one whose heap
-    subtree reaches past the dense LDS copy, resolved through the deep-position table)."""
-    out = _run(simt_lib, ["unfilt:12"], {"SIMT_ORDER": "rev"})
-    assert "ok   unfiltered rows at V=151936" in out
+    subtree reaches past the dense LDS copy, resolved through the deep-position table). Only the head of each
+    list is ranked, the tail's ulps of 2^K counted in any order; the constructed rows put terms exactly halfway
+    between two multiples of u into the tail (3 copies, resolved by the running sum's parity; 20 copies, past
+    the split's limit, so the whole list is ranked)."""
+    out = _run(simt_lib, ["unfilt:12", "halfway:6"], {"SIMT_ORDER": "rev"})
+    assert "ok   unfiltered rows at V=151936" in out and "ok   halfway tail terms" in out
 
 
 def test_full_vocabulary_workloads(simt_lib):
