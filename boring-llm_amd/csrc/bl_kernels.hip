@@ -1374,7 +1374,11 @@ struct sel_shared {
   int split_nt;                        /* its tail's terms halfway between multiples of u: count, */
   uint32_t split_par;                  /* parities of the other tail terms before each, */
   uint64_t split_tk[BL_SPLIT_TIES];    /* keys, */
-  double split_tf[BL_SPLIT_TIES];      /* floor(t / u) */
+  double split_tf[BL_SPLIT_TIES];      /* floor(t / u), */
+  uint32_t split_ti[BL_SPLIT_TIES];    /* the u-multiples each adds */
+  int split_cb;                        /* a draw in the tail: u-multiples before its bucket, */
+  int split_ne;                        /* that bucket's candidates, */
+  uint64_t split_key;                  /* the drawn key */
 };
 /* expf and logf through the selection's LDS copies of their tables */
 #define SEL_EXPF(x) bl_expf_tab((x), [&](uint32_t i_) { return sh.etab[i_]; })
@@ -2884,6 +2888,8 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
   auto g_allowed = [&](int32_t id) { return ((gmk[(id >> 6) * 2 + ((id >> 5) & 1)] >> (id & 31)) & 1u) != 0u; };
   float Mc = M; /* the top of the ranked list: the row maximum, or a grammar row's allowed maximum */
   float split_S = 0.0f; /* > 0: the list is a plain draw's ranked head, and this the whole list's sum */
+  int split_tail_pos = -1; /* >= 0: the draw landed in the tail, its key stored at this list position */
+  uint64_t split_rng = 0ull; /* then the RNG after the draw */
   bool gfull = false; /* a top-k grammar row's widening went past the merged list */
   int gk = 0;         /* its next level */
   if (sampled && gram && (mode & BL_M_TOPK)) {
@@ -3098,6 +3104,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
        * the even multiple of u: it adds u (f + (N + f) mod 2), N = s / u before it, whose parity is s_head's,
        * the other tail terms' with larger values (a second pass) and the earlier such terms' (in key order). */
       bool split = !filt && !gram && !(mode & BL_M_TNS) && T > 0.0f && span > 0.0f;
+      const bool tail_draw_ok = !((mode & BL_M_PSP) && rows.lp); /* post-sampling probabilities read the head */
       int Kb = 0;
       float r01 = 0.0f;
       double need = 0.0;
@@ -3110,7 +3117,10 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
           uint64_t st = rng;
           for (int k = 0; k < skip; k++) st = bl_xorshift(st);
           r01 = bl_rng_f32(&st);
-          need = fmax(bl_u2d((uint64_t)(Kb + 1023) << 52), (double)r01 * hi) * (1.0 + 4.0e-3);
+          split_rng = st;
+          /* the head also covers the target unless it lies far down (then it is found in the tail) */
+          const float rcov = tail_draw_ok && r01 > 0.9f ? 0.9f : r01;
+          need = fmax(bl_u2d((uint64_t)(Kb + 1023) << 52), (double)rcov * hi) * (1.0 + 4.0e-3);
         }
       }
       const int need_c = (sp.min_keep > sp.n_probs ? sp.min_keep : sp.n_probs) + 2;
@@ -3186,6 +3196,11 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
          * 2^23 per term) */
         const double tsc = bl_u2d((uint64_t)(23 - Kb + 1023) << 52);
         double tI = 0.0;
+        if (tail) { /* a tail bucket's counter becomes its sum of u-multiples (below 2^24 when the split holds) */
+          __syncthreads(); /* every thread has read nk from cnt[h_end] */
+          for (int b = h_end + t; b < BL_NBUCKET; b += BL_SEL_THREADS) cnt[b] = 0u;
+          __syncthreads();
+        }
         each_region(std::true_type{}, [&](const float *v, const int32_t *id) {
 #pragma unroll
           for (int u = 0; u < BL_CAND_U; u++)
@@ -3205,7 +3220,9 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
                     sh.split_tf[k] = fl;
                   }
                 } else {
-                  tI += fr > 0.5 ? fl + 1.0 : fl;
+                  const double inc = fr > 0.5 ? fl + 1.0 : fl;
+                  tI += inc;
+                  if (inc != 0.0) atomicAdd(&cnt[bk], (uint32_t)inc);
                 }
               }
             }
@@ -3315,16 +3332,113 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
             const uint64_t inc = (uint64_t)fl + (((uint64_t)fl + pN) & 1u);
             tI += (double)inc;
             par ^= (uint32_t)(inc & 1u);
+            if (t == 0) {
+              sh.split_ti[kb] = (uint32_t)inc;
+              cnt[bucket(ckey_v(sh.split_tk[kb]))] += (uint32_t)inc;
+            }
           }
+          __syncthreads();
         }
         const double Sfull = (double)s_head + uK * tI;
         ok = ok && Sfull < bl_u2d((uint64_t)(Kb + 1 + 1023) << 52);
-        if (ok) ok = r01 * (float)Sfull <= s_head; /* the draw stops within the head */
-        __syncthreads();
-        if (ok) {
+        const float target = r01 * (float)Sfull;
+        if (ok && target <= s_head) { /* the draw stops within the head */
           split_S = (float)Sfull;
           break;
         }
+        if (ok && tail_draw_ok) {
+          /* the draw stops in the tail, where the running sum is s_head + u c: at the first candidate that
+           * brings c to cstar = (target - s_head) / u (an integer: both lie in binade K). The bucket where the
+           * tail's prefix of u-multiples reaches cstar, then its candidates ranked in LDS and walked */
+          const uint32_t cstar = (uint32_t)(((double)target - (double)s_head) / uK);
+          constexpr int PB = BL_NBUCKET / BL_SEL_THREADS;
+          uint32_t ls = 0u;
+#pragma unroll
+          for (int q = 0; q < PB; q++) ls += t * PB + q >= h_end ? cnt[t * PB + q] : 0u;
+          const uint32_t li = (uint32_t)bl_wscan_add((int)ls, lane);
+          if (lane == 63) sh.red_i[w] = (int)li;
+          if (t == 0) {
+            sh.split_h = -1;
+            sh.split_ne = 0;
+            sh.split_key = 0ull;
+          }
+          __syncthreads();
+          uint32_t run = li - ls;
+          for (int q = 0; q < w; q++) run += (uint32_t)sh.red_i[q];
+#pragma unroll
+          for (int q = 0; q < PB; q++) {
+            const int b = t * PB + q;
+            if (b >= h_end) {
+              const uint32_t c = cnt[b];
+              if (run < cstar && run + c >= cstar) {
+                sh.split_h = b;
+                sh.split_cb = (int)run;
+              }
+              run += c;
+            }
+          }
+          __syncthreads();
+          const int bs = sh.split_h;
+          uint64_t *ek = tile, *sk = tile + 1536;
+          uint32_t *ei = reinterpret_cast<uint32_t *>(tile + 1024), *si = reinterpret_cast<uint32_t *>(tile + 2560);
+          if (bs >= 0) {
+            each_region(std::true_type{}, [&](const float *v, const int32_t *id) {
+#pragma unroll
+              for (int u = 0; u < BL_CAND_U; u++)
+                if (v[u] >= thr && bucket(v[u]) == bs) {
+                  const int k = atomicAdd(&sh.split_ne, 1);
+                  if (k < 1024) {
+                    const uint64_t key = ckey(v[u], id[u]);
+                    const float dd = v[u] - Mc;
+                    const float qq = dd / T;
+                    const double x = (double)SEL_EXPF(qq) * tsc;
+                    const double fl = floor(x), fr = x - fl;
+                    uint32_t inc = (uint32_t)(fr > 0.5 ? fl + 1.0 : fl);
+                    if (fr == 0.5)
+                      for (int j = 0; j < nt; j++)
+                        if (sh.split_tk[j] == key) inc = sh.split_ti[j];
+                    ek[k] = key;
+                    ei[k] = inc;
+                  }
+                }
+            });
+            __syncthreads();
+            const int ne = sh.split_ne;
+            if (ne <= 1024) {
+              for (int i = t; i < ne; i += BL_SEL_THREADS) {
+                const uint64_t k = ek[i];
+                int r = 0;
+                for (int j = 0; j < ne; j++) r += ek[j] > k ? 1 : 0;
+                sk[r] = k;
+                si[r] = ei[i];
+              }
+              __syncthreads();
+              if (t == 0) {
+                uint32_t c = (uint32_t)sh.split_cb;
+                for (int r = 0; r < ne; r++) {
+                  c += si[r];
+                  if (c >= cstar) {
+                    const float vr = ckey_v(sk[r]);
+                    /* equal values: the heap's order among them is not simulated here */
+                    const bool tie = (r > 0 && ckey_v(sk[r - 1]) == vr) || (r + 1 < ne && ckey_v(sk[r + 1]) == vr);
+                    if (!tie) sh.split_key = sk[r];
+                    break;
+                  }
+                }
+              }
+            }
+          }
+          __syncthreads();
+          const uint64_t ck = sh.split_key;
+          __syncthreads();
+          if (ck) {
+            Bk[nk] = ck;
+            split_tail_pos = nk;
+            split_S = (float)Sfull;
+            break;
+          }
+        }
+        __syncthreads();
       }
       keys = Bk;
       nl = nk;
@@ -3457,7 +3571,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
   __syncthreads();
   if (norm_row && w == 0)
     norm_chain(d, row, sh, [&](int64_t j) { return SEL_EXPF(bl_row_value(d, sp, rows, row, slot, logits, ld, (int32_t)j) - M); });
-  if (sampled && !status && short_list && w == 1) {
+  if (sampled && !status && short_list && split_tail_pos < 0 && w == 1) {
     const sel_draw r = ranked_serial(sp, n_draw, nlog_draw, keep, rng, skip, typ, split_S, sh, &sh.rng_out);
     if (lane == 0) sh.draw = r;
   }
@@ -3478,7 +3592,13 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
   int64_t dshift = 0;
   if (sampled && !status) {
     int pos;
-    if (short_list) {
+    if (split_tail_pos >= 0) { /* drawn in the tail of a plain draw's list (above) */
+      dr.pos = pos = split_tail_pos;
+      dr.first = 0;
+      dr.cut = (int)n_logical;
+      dr.S = split_S;
+      rng = split_rng;
+    } else if (short_list) {
       dr = sh.draw;
       pos = dr.pos;
       if (pos == -2 || pos >= n_draw) {

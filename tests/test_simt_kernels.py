@@ -89,9 +89,10 @@ def test_unfiltered_candidate_cut(simt_lib):
     """Full-vocabulary rows without top-p or min-p at V=151936: the candidates cut at half an ulp of the
     draw's running sum (six rows, 12 steps; the bfloat16 row's draws on equal values include one whose heap
     subtree reaches past the dense LDS copy, resolved through the deep-position table). Only the head of each
-    list is ranked, the tail's ulps of 2^K counted in any order; the constructed rows put terms exactly halfway
-    between two multiples of u into the tail (3 copies, resolved by the running sum's parity; 20 copies, past
-    the split's limit, so the whole list is ranked)."""
+    list is ranked, the tail's ulps of 2^K counted in any order, a draw past the head found through the tail
+    buckets' sums; the constructed rows put terms exactly halfway between two multiples of u into the tail (3
+    copies, resolved by the running sum's parity; 20 copies, past the split's limit, so the whole list is
+    ranked)."""
     out = _run(simt_lib, ["unfilt:12", "halfway:6"], {"SIMT_ORDER": "rev"})
     assert "ok   unfiltered rows at V=151936" in out and "ok   halfway tail terms" in out
 
@@ -164,7 +165,8 @@ def test_small_cases_address_sanitizer():
         assert os.path.isabs(p) and os.path.exists(p), f"{rt} not found"
         pre.append(p)
     env = {"LD_PRELOAD": " ".join(pre), "ASAN_OPTIONS": "detect_leaks=0", "UBSAN_OPTIONS": "print_stacktrace=1"}
-    out = _run(os.path.join(SIMT, "_build", "libbl_simt_asan.so"), ["small:0-20:3", "coarse:1,5:3", "ramp:8:2", "grammar:0-6:20", "q4:2,9:4", "dry:0-8:3"], env)
+    out = _run(os.path.join(SIMT, "_build", "libbl_simt_asan.so"), ["small:0-20:3", "coarse:1,5:3", "ramp:8:2", "grammar:0-6:20", "q4:2,9:4", "dry:0-8:3",
+                                                                   "halfway:3"], env)
     assert "ERROR: AddressSanitizer" not in out and "runtime error" not in out
 
 
