@@ -2306,19 +2306,13 @@ static_assert(BL_NBUCKET % BL_SEL_THREADS == 0, "whole buckets per thread");
 #define BL_TIE_HASH BL_RANK_MAX /* slots of the deep-position table (the counting sort's LDS, free by now) */
 static_assert((BL_TIE_HASH & (BL_TIE_HASH - 1)) == 0, "table size is a power of two");
 __device__ __forceinline__ uint32_t tie_slot(int p) { return ((uint32_t)p * 2654435761u) >> 22 & (BL_TIE_HASH - 1); }
-template <class KeyF>
-__device__ __forceinline__ int heap_tie_id(KeyF key, bool keys_in_lds, int64_t n_list, int64_t pos, int V, int32_t *occ_g,
-                           sel_shared &sh) {
+/* the heap's extractions over the sorted prefix key(0..nb) (every element below it reads as smaller than all
+ * of it): the first extraction i whose element o (a prefix index) satisfies stop(i, o), as that element's
+ * token; -1 when none does or the simulation does not fit */
+template <class KeyF, class StopF>
+__device__ __forceinline__ int heap_extract_until(KeyF key, bool keys_in_lds, int nb, int V, int32_t *occ_g, sel_shared &sh,
+                                                  StopF stop) {
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
-  const float vp = ckey_v(key(pos));
-  /* nb = first index past pos whose value is below vp (the list is sorted: binary search, every thread) */
-  int64_t lo = pos + 1, hi = n_list;
-  while (lo < hi) {
-    const int64_t mid = (lo + hi) >> 1;
-    if (ckey_v(key(mid)) == vp) lo = mid + 1;
-    else hi = mid;
-  }
-  const int nb = (int)lo;
   if (nb > BL_TIE_MAX) return -1;
   /* the prefix's values, in LDS (the list itself when it is there, else a float copy in its place) */
   float *bval = reinterpret_cast<float *>(sh.c.keys);
@@ -2410,9 +2404,9 @@ __device__ __forceinline__ int heap_tie_id(KeyF key, bool keys_in_lds, int64_t n
       }
     };
     int size = V, res = -1;
-    for (int64_t i = 0; i <= pos; i++) {
+    for (int i = 0; i < nb; i++) {
       const int o = lget(0);
-      if (i == pos) {
+      if (stop(i, o)) {
         res = o;
         break;
       }
@@ -2428,6 +2422,20 @@ __device__ __forceinline__ int heap_tie_id(KeyF key, bool keys_in_lds, int64_t n
   const int res = sh.ires[4];
   __syncthreads();
   return res >= 0 ? ckey_i(key(res)) : -1;
+}
+/* the token the heap extracts at position `pos` of the sorted list, whose value has equal neighbours */
+template <class KeyF>
+__device__ __forceinline__ int heap_tie_id(KeyF key, bool keys_in_lds, int64_t n_list, int64_t pos, int V, int32_t *occ_g,
+                           sel_shared &sh) {
+  const float vp = ckey_v(key(pos));
+  /* nb = first index past pos whose value is below vp (the list is sorted: binary search, every thread) */
+  int64_t lo = pos + 1, hi = n_list;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (ckey_v(key(mid)) == vp) lo = mid + 1;
+    else hi = mid;
+  }
+  return heap_extract_until(key, keys_in_lds, (int)lo, V, occ_g, sh, [&](int i, int) { return (int64_t)i == pos; });
 }
 
 /*
@@ -3560,7 +3568,50 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
       } else {
         tok = gi;
         tokv = gm;
-        if (n_eq > 1.0) status |= BL_SE_TIE;
+        if (n_eq > 1.0) {
+          /* equal allowed maxima g: the levels rank by top_k_select (value desc, index asc) while k < V, where
+           * the first allowed is the lowest index gi, found at the first level past its rank r (the keys
+           * above (g, gi)); a level of V ranks by the heap (all_candidates_sorted), whose first allowed
+           * among the values g comes from the extraction replay over every value >= g (sorted in LDS) */
+          int res = -1;
+          if (!(sp.top_n_sigma > 0.0f)) {
+            uint64_t *lst = d.sortk + (int64_t)row * 2 * V;
+            if (t == 0) sh.ires[5] = 0;
+            __syncthreads();
+            double c_gt = 0.0, c_eq = 0.0;
+            for (int j = t; j < V; j += BL_SEL_THREADS) {
+              const float x = bl_row_value(d, sp, rows, row, slot, logits, ld, j);
+              if (x > gm) c_gt += 1.0;
+              else if (x == gm && j < gi) c_eq += 1.0;
+              if (x >= gm) {
+                const int k = atomicAdd(&sh.ires[5], 1);
+                if (k < BL_LDS_SORT) lst[k] = ckey(x, j);
+              }
+            }
+            c_gt = block_sum_d<BL_SEL_THREADS>(c_gt, sh.c.gsum);
+            c_eq = block_sum_d<BL_SEL_THREADS>(c_eq, sh.c.gsum);
+            const int nge = sh.ires[5];
+            const int64_t r = (int64_t)(c_gt + c_eq);
+            int64_t k = sp.top_k > 0 && sp.top_k < V ? sp.top_k : V;
+            while (k <= r && k < V) k = k * 4 < V ? k * 4 : V;
+            if (k < V) {
+              res = gi;
+            } else if (nge <= BL_LDS_SORT) {
+              uint64_t *hk = sh.c.keys;
+              int P = 1;
+              while (P < nge) P <<= 1;
+              for (int i = t; i < P; i += BL_SEL_THREADS) hk[i] = i < nge ? lst[i] : 0ull;
+              __syncthreads();
+              bitonic_desc(hk, P);
+              const int p0 = (int)c_gt; /* the values g follow every larger value */
+              res = heap_extract_until([&](int64_t j) { return hk[j]; }, true, nge, V,
+                                       d.full_i + (int64_t)row * d.nb * BL_EB, sh,
+                                       [&](int i, int o) { return i >= p0 && g_allowed(ckey_i(hk[o])); });
+            }
+          }
+          if (res >= 0) tok = res;
+          else status |= BL_SE_TIE;
+        }
       }
     }
   }

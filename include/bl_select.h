@@ -38,8 +38,10 @@ enum {
                               above 512 candidates; a mirostat draw that falls through to a prefix end past
                               the candidates within 17.6 T of the maximum */
   BL_ETIE = -9,            /* a draw on equal logits whose heap order is past the device simulation (more than
-                              8192 values at or above the tied one), equal allowed maxima of a grammar row,
-                              post-sampling alternatives of a full-vocabulary rank that meet equal values, or a
+                              8192 values at or above the tied one), equal allowed maxima of a greedy grammar
+                              row whose heap order applies with more than 4096 values at or above them or with
+                              top_n_sigma, a sampled grammar row's draw on equal allowed values, post-sampling
+                              alternatives of a full-vocabulary rank that meet equal values, or a
                               top_n_sigma whose float32 sigma the reference's float64 rounding error leaves
                               undecided (the sigma within ~1e-11 relative of a float32 rounding boundary) */
   BL_ESCHEMA = -10         /* a JSON schema that does not parse (src/json.br json_parse messages) or that

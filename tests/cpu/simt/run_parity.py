@@ -914,9 +914,10 @@ GRAMMAR_SAMPLED = [
 ]
 
 
-def run_grammar_case(BL, case, steps, kw=None, sigma=3.0):
+def run_grammar_case(BL, case, steps, kw=None, sigma=3.0, quant=0.0):
     """Masks and tokens of a small grammar against the oracle's slot on random rows: greedy, or sampled with
-    the parameters `kw` (the RNG carried across the replies that end or die); logits N(0, sigma^2)."""
+    the parameters `kw` (the RNG carried across the replies that end or die); logits N(0, sigma^2), rounded to
+    multiples of `quant` when given (equal allowed maxima)."""
     kw = kw or {}
     seed = 77 if kw else 1
     rng = np.random.default_rng(500 + case)
@@ -969,6 +970,8 @@ def run_grammar_case(BL, case, steps, kw=None, sigma=3.0):
                 bad = np.nonzero(got != want)[0]
                 return f"step {t}: mask differs in {len(bad)} words (first {bad[:4]}), forced {forced} vs {of.value}"
             x = (rng.standard_normal(V) * sigma).astype(np.float32)
+            if quant:
+                x = (np.round(x / quant) * quant).astype(np.float32)
             buf.upload(x)
             ot, olp = np.zeros(1, np.int32), np.zeros(1, np.float32)
             oti, otl = np.full(max(n_probs, 1), -1, np.int32), np.zeros(max(n_probs, 1), np.float32)
@@ -1176,6 +1179,11 @@ def main():
         elif kind == "unfilt":
             rows = [int(v) for v in f[2].split(",")] if len(f) > 2 else None
             results.append(("unfiltered rows at V=151936", run_unfiltered(BL, int(f[1]), rows)))
+        elif kind == "gtie":  # gtie:cases[:steps]: greedy grammar rows on logits in steps of 0.5
+            for c in parse_range(f[1]):
+                for kw in ({}, {"top_k": 40}):
+                    results.append((f"grammar ties case {c} top_k {kw.get('top_k', 0)}",
+                                    run_grammar_case(BL, c, int(f[2]) if len(f) > 2 else 30, kw, quant=0.5)))
         elif kind == "halfway":
             results.append(("halfway tail terms", run_halfway(BL, int(f[1]))))
         elif kind == "noalloc":

@@ -92,6 +92,16 @@ def test_sampled_grammar_cases(case):
     assert err is None, err
 
 
+@pytest.mark.parametrize("top_k", [0, 40])
+@pytest.mark.parametrize("case", range(len(RP.GRAMMAR_CASES)))
+def test_greedy_grammar_ties(case, top_k):
+    """Greedy grammar rows on logits in steps of 0.5 (equal allowed maxima at most steps): the lowest index
+    while the widening levels rank by top_k_select, the heap's first allowed token once a level reaches V."""
+    say(f"grammar ties: case {case}, top_k {top_k}")
+    err = RP.run_grammar_case(BL, case, 80, {"top_k": top_k} if top_k else None, quant=0.5)
+    assert err is None, err
+
+
 @pytest.mark.parametrize("case", range(len(RP.JSON_CASES)))
 def test_json_object_cases(case):
     say(f"JSON-object case {case}: {RP.JSON_CASES[case]}")

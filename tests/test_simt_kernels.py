@@ -126,6 +126,14 @@ def test_grammar_masks_and_tokens(simt_lib):
     assert out.count("ok   JSON-object case") == 4
 
 
+def test_greedy_grammar_ties(simt_lib):
+    """Greedy grammar rows whose allowed maximum is shared by several tokens (logits in steps of 0.5), top_k 0
+    and 40: the lowest index while the widening levels rank by top_k_select (value desc, index asc), the
+    first allowed token of the heap's extraction order (all_candidates_sorted) once a level reaches V."""
+    out = _run(simt_lib, ["gtie:0-7:30"], {"SIMT_ORDER": "rand"})
+    assert out.count("ok   grammar ties case") == 16
+
+
 def test_top_n_sigma(simt_lib):
     """Top-n-sigma rows (src/sampling.br:376-407): small cases 21-23 (full-vocabulary and top-k ranks) and
     full-size rows at V=151936, the sigma from the row pass's statistics against the oracle's sequential
