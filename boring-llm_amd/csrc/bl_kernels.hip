@@ -3683,9 +3683,55 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
       if ((mode & BL_M_FULL) || glevel_v) {
         const float vp = val(pos);
         if ((pos > 0 && val(pos - 1) == vp) || (pos + 1 < n_list && val(pos + 1) == vp)) {
-          /* a grammar row's list is the heap order of the whole row restricted to its allowed tokens */
-          const int hid = gram ? -1 : heap_tie_id([&](int64_t j) { return keys[j]; }, keys == sh.c.keys, n_list, pos, V,
-                                                  d.full_i + (int64_t)row * d.nb * BL_EB, sh);
+          int hid = -1;
+          if (gram) {
+            /* a grammar row's list is the heap order of the whole row restricted to its allowed tokens: the
+             * (pos - a0)-th allowed token among the values vp in the extraction order of every value >= vp
+             * (collected and sorted in LDS, at most 4096), a0 the list's first position of value vp */
+            int64_t lo = 0, hi = pos;
+            while (lo < hi) {
+              const int64_t mid = (lo + hi) >> 1;
+              if (val(mid) == vp) hi = mid;
+              else lo = mid + 1;
+            }
+            const int q = (int)(pos - lo);
+            uint64_t *lst = d.sortk + (int64_t)row * 2 * V; /* the list itself is past it, or in LDS */
+            __syncthreads();
+            if (t == 0) sh.ires[5] = 0;
+            __syncthreads();
+            double c_gt = 0.0;
+            for (int j = t; j < V; j += BL_SEL_THREADS) {
+              const float x = bl_row_value(d, sp, rows, row, slot, logits, ld, j);
+              if (x > vp) c_gt += 1.0;
+              if (x >= vp) {
+                const int k = atomicAdd(&sh.ires[5], 1);
+                if (k < BL_LDS_SORT) lst[k] = ckey(x, j);
+              }
+            }
+            c_gt = block_sum_d<BL_SEL_THREADS>(c_gt, sh.c.gsum);
+            const int nge = sh.ires[5];
+            if (nge <= BL_LDS_SORT) {
+              uint64_t *hk = sh.c.keys; /* the list is not read again */
+              int P = 1;
+              while (P < nge) P <<= 1;
+              __syncthreads();
+              for (int i = t; i < P; i += BL_SEL_THREADS) hk[i] = i < nge ? lst[i] : 0ull;
+              __syncthreads();
+              bitonic_desc(hk, P);
+              const int p0 = (int)c_gt;
+              int seen = 0; /* the replay runs on one lane */
+              hid = heap_extract_until([&](int64_t j) { return hk[j]; }, true, nge, V,
+                                       d.full_i + (int64_t)row * d.nb * BL_EB, sh, [&](int i, int o) {
+                                         if (i < p0 || !g_allowed(ckey_i(hk[o]))) return false;
+                                         if (seen == q) return true;
+                                         seen++;
+                                         return false;
+                                       });
+            }
+          } else {
+            hid = heap_tie_id([&](int64_t j) { return keys[j]; }, keys == sh.c.keys, n_list, pos, V,
+                              d.full_i + (int64_t)row * d.nb * BL_EB, sh);
+          }
           if (hid >= 0) tok = hid;
           else status |= BL_SE_TIE;
         }

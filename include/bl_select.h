@@ -38,9 +38,9 @@ enum {
                               above 512 candidates; a mirostat draw that falls through to a prefix end past
                               the candidates within 17.6 T of the maximum */
   BL_ETIE = -9,            /* a draw on equal logits whose heap order is past the device simulation (more than
-                              8192 values at or above the tied one), equal allowed maxima of a greedy grammar
-                              row whose heap order applies with more than 4096 values at or above them or with
-                              top_n_sigma, a sampled grammar row's draw on equal allowed values, post-sampling
+                              8192 values at or above the tied one), equal allowed values of a grammar row
+                              (the greedy maxima, or a draw) where the heap's order applies with more than 4096
+                              values at or above them (or, greedy, with top_n_sigma), post-sampling
                               alternatives of a full-vocabulary rank that meet equal values, or a
                               top_n_sigma whose float32 sigma the reference's float64 rounding error leaves
                               undecided (the sigma within ~1e-11 relative of a float32 rounding boundary) */
@@ -150,7 +150,7 @@ int bl_set_vocab(bl_ctx *ctx, const uint8_t *blob, const uint32_t *offsets, int 
  * temperature > 0, or a grammar whose reachable automaton exceeds 65536 states: a recursive one). A
  * sampled step returns BL_EUNSUPPORTED when the widening reaches a level whose ranks go past the values
  * within the candidate span of the row maximum, and BL_ETIE when a whole-vocabulary draw lands on equal
- * allowed values. */
+ * allowed values with more than 4096 values at or above them. */
 int bl_slot_grammar(bl_ctx *ctx, int slot, const char *gbnf, size_t len);
 
 /* `response_format: {type: json_object}` on a slot set up by bl_slot_reset, before its first step (on = 0

@@ -1184,6 +1184,11 @@ def main():
                 for kw in ({}, {"top_k": 40}):
                     results.append((f"grammar ties case {c} top_k {kw.get('top_k', 0)}",
                                     run_grammar_case(BL, c, int(f[2]) if len(f) > 2 else 30, kw, quant=0.5)))
+        elif kind == "gstie":  # gstie:cases[:steps]: sampled grammar rows (T 0.8) on logits in steps of 0.5
+            for c in parse_range(f[1]):
+                for kw in ({"temperature": 0.8}, {"temperature": 0.8, "top_k": 40}):
+                    results.append((f"sampled grammar ties case {c} top_k {kw.get('top_k', 0)}",
+                                    run_grammar_case(BL, c, int(f[2]) if len(f) > 2 else 30, kw, quant=0.5)))
         elif kind == "halfway":
             results.append(("halfway tail terms", run_halfway(BL, int(f[1]))))
         elif kind == "noalloc":

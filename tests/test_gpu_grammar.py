@@ -102,6 +102,19 @@ def test_greedy_grammar_ties(case, top_k):
     assert err is None, err
 
 
+@pytest.mark.parametrize("top_k", [0, 40])
+@pytest.mark.parametrize("case", range(len(RP.GRAMMAR_CASES)))
+def test_sampled_grammar_ties(case, top_k):
+    """Sampled grammar rows (T 0.8) on logits in steps of 0.5: a draw on equal allowed values takes the
+    allowed token the heap's extraction order puts at the drawn position (top_k 0, or a level of V)."""
+    say(f"sampled grammar ties: case {case}, top_k {top_k}")
+    kw = {"temperature": 0.8}
+    if top_k:
+        kw["top_k"] = top_k
+    err = RP.run_grammar_case(BL, case, 80, kw, quant=0.5)
+    assert err is None, err
+
+
 @pytest.mark.parametrize("case", range(len(RP.JSON_CASES)))
 def test_json_object_cases(case):
     say(f"JSON-object case {case}: {RP.JSON_CASES[case]}")

@@ -129,9 +129,10 @@ def test_grammar_masks_and_tokens(simt_lib):
 def test_greedy_grammar_ties(simt_lib):
     """Greedy grammar rows whose allowed maximum is shared by several tokens (logits in steps of 0.5), top_k 0
     and 40: the lowest index while the widening levels rank by top_k_select (value desc, index asc), the
-    first allowed token of the heap's extraction order (all_candidates_sorted) once a level reaches V."""
-    out = _run(simt_lib, ["gtie:0-7:30"], {"SIMT_ORDER": "rand"})
-    assert out.count("ok   grammar ties case") == 16
+    first allowed token of the heap's extraction order (all_candidates_sorted) once a level reaches V.
+    Sampled rows (T 0.8) whose draw lands on equal allowed values: the allowed token the heap puts there."""
+    out = _run(simt_lib, ["gtie:0-7:30", "gstie:0-7:30"], {"SIMT_ORDER": "rand"})
+    assert out.count("ok   grammar ties case") == 16 and out.count("ok   sampled grammar ties case") == 16
 
 
 def test_top_n_sigma(simt_lib):
