@@ -3241,9 +3241,6 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
         if (tail && nt > 0 && nt <= BL_SPLIT_TIES) {
           /* bit k: the parity of the other tail terms' u-multiples before halfway term k (larger values; a
            * value equal to a halfway term's is one itself) */
-          float tv[BL_SPLIT_TIES];
-#pragma unroll
-          for (int k = 0; k < BL_SPLIT_TIES; k++) tv[k] = k < nt ? ckey_v(sh.split_tk[k]) : 3.0e38f;
           uint32_t bits = 0u;
           each_region(std::false_type{}, [&](const float *v, const int32_t *) {
 #pragma unroll
@@ -3254,9 +3251,8 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
                 const double x = (double)SEL_EXPF(qq) * tsc;
                 const double fl = floor(x), fr = x - fl;
                 if (fr != 0.5 && ((fr > 0.5 ? (uint64_t)fl + 1u : (uint64_t)fl) & 1u))
-#pragma unroll
-                  for (int k = 0; k < BL_SPLIT_TIES; k++)
-                    if (v[u] > tv[k]) bits ^= 1u << k;
+                  for (int k = 0; k < nt; k++)
+                    if (v[u] > ckey_v(sh.split_tk[k])) bits ^= 1u << k;
               }
           });
           uint32_t wb = 0u;
@@ -3305,23 +3301,21 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
           __syncthreads();
         }
         if (!tail) break;
-        /* the head's exact sum (the draw's terms exp((v - v0) / T), v0 = Mc the first value), then the checks */
-        bl_grec *hrecs = sh.c.recs;
-        double *hgsum = sh.c.gsum;
-        if ((nk + 63) / 64 > BL_LDS_SORT / 64) {
-          hrecs = reinterpret_cast<bl_grec *>(d.grec) + (int64_t)row * 2 * (V / 64 + 64) + (V / 64 + 64);
-          hgsum = d.gsum + (int64_t)row * (V / 64 + 64);
-        }
-        float *htb = reinterpret_cast<float *>(A); /* the unranked head is spent */
-        block_records((int64_t)nk, [&](int64_t j) { return ckey_v(Bk[j]); }, [&](float v) {
-          const float dd = v - Mc;
-          const float qq = dd / T;
-          return SEL_EXPF(qq);
-        }, hrecs, hgsum, htb);
+        /* the head's exact sum (the draw's terms exp((v - v0) / T), v0 = Mc the first value), by wavefront 0:
+         * each lane's term, 64 at a time, added in list order through readlane (every lane alike) */
         if (w == 0) {
-          float Sh;
-          bl_seq_walk((int64_t)nk, [&](int64_t j) { return htb[j]; }, [&](int64_t g) { return hrecs[g]; }, false, 0.0f, 0,
-                      Sh, lane);
+          float Sh = 0.0f;
+          for (int b0 = 0; b0 < nk; b0 += 64) {
+            const int j = b0 + lane;
+            float e = 0.0f;
+            if (j < nk) {
+              const float dd = ckey_v(Bk[j]) - Mc;
+              const float qq = dd / T;
+              e = SEL_EXPF(qq);
+            }
+            const int m = nk - b0 < 64 ? nk - b0 : 64;
+            for (int k = 0; k < m; k++) Sh += sel_rl(e, k);
+          }
           if (lane == 0) sh.split_s = Sh;
         }
         __syncthreads();
