@@ -1697,9 +1697,10 @@ __device__ __forceinline__ int typical_filter(const bl_slot_dev &sp, int n, bool
  * holds the draw's terms from its first candidate (tbuf[j - first]).
  */
 template <class ValF>
-__device__ __forceinline__ sel_draw sample_ranked_long(const bl_slot_dev &sp, ValF val, int64_t n_list, int64_t n_logical,
+__device__ __forceinline__ sel_draw sample_ranked_long(const bl_slot_dev &sp, ValF val, int64_t &n_list, int64_t n_logical,
                                       int64_t keep, uint64_t &rng, int rng_skip, float S_whole, bl_grec *recs,
-                                      double *gsum, float *tbuf, sel_shared &sh, int &status) {
+                                      double *gsum, float *tbuf, sel_shared &sh, int &status, uint64_t *keys_w = nullptr,
+                                      int32_t *tmerged = nullptr, int32_t *trank = nullptr) {
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   const float T = sp.temperature;
   const float v0 = val(0);
@@ -1723,6 +1724,124 @@ __device__ __forceinline__ sel_draw sample_ranked_long(const bl_slot_dev &sp, Va
     __syncthreads();
     sum_exp = sh.fres[0];
     __syncthreads();
+    if (keys_w) {
+      /* typical_filter (src/sampling.br:424-465) over the whole list (every value whose term exp(v - v0) is
+       * not 0; the later ones have probability 0 and take no part). Along the list -ln p only grows, so the
+       * distance |-ln p - H| falls until -ln p reaches H (positions [0, m)) and grows after it ([m, n)): the
+       * order of the selection (distance, then position) merges the two runs, each element's place found by
+       * binary search in the other run (and, in the falling run, among its equal distances). The probabilities
+       * added in that order reach typical_p (and min_keep) at the walk's stop; the kept entries are compacted
+       * in list order, the list's first value and sum staying those of the whole list */
+      int64_t lo = 0, hi = n_list; /* n = first position whose probability is 0 */
+      while (lo < hi) {
+        const int64_t mid = (lo + hi) >> 1;
+        if (termPv(val(mid)) > 0.0f) lo = mid + 1;
+        else hi = mid;
+      }
+      const int64_t n = lo;
+      block_records(n, val, [&](float v) {
+        const float q = termPv(v);
+        return q > 0.0f ? -(q * bl_logf(q)) : 0.0f;
+      }, recs, gsum, tbuf);
+      if (w == 0) {
+        float S;
+        bl_seq_walk(n, termS, [&](int64_t g) { return recs[g]; }, false, 0.0f, 0, S, lane);
+        if (lane == 0) sh.fres[3] = S;
+      }
+      __syncthreads();
+      const float H = sh.fres[3];
+      __syncthreads();
+      /* tbuf[j] = -ln p_j - H (its magnitude is the reference's distance) */
+      for (int64_t j = t; j < n; j += blockDim.x) tbuf[j] = -bl_logf(termPv(val(j))) - H;
+      __syncthreads();
+      lo = 0;
+      hi = n;
+      while (lo < hi) {
+        const int64_t mid = (lo + hi) >> 1;
+        if (tbuf[mid] < 0.0f) lo = mid + 1;
+        else hi = mid;
+      }
+      const int64_t m = lo;
+      for (int64_t j = t; j < n; j += blockDim.x) {
+        const float dj = fabsf(tbuf[j]);
+        int64_t rank;
+        if (j >= m) {
+          /* rising run: its own earlier entries, and the falling run's entries at distance <= dj (a suffix) */
+          int64_t a = 0, b = m;
+          while (a < b) {
+            const int64_t c = (a + b) >> 1;
+            if (fabsf(tbuf[c]) <= dj) b = c;
+            else a = c + 1;
+          }
+          rank = (j - m) + (m - a);
+        } else {
+          /* falling run: its entries at a smaller distance (after its run of distance dj), its equal ones
+           * before j, and the rising run's entries at a smaller distance (a prefix) */
+          int64_t a = 0, b = m; /* first position of distance dj */
+          while (a < b) {
+            const int64_t c = (a + b) >> 1;
+            if (fabsf(tbuf[c]) <= dj) b = c;
+            else a = c + 1;
+          }
+          const int64_t first_eq = a;
+          a = j;
+          b = m; /* first position past the run of distance dj */
+          while (a < b) {
+            const int64_t c = (a + b) >> 1;
+            if (fabsf(tbuf[c]) < dj) b = c;
+            else a = c + 1;
+          }
+          const int64_t past_eq = a;
+          a = m;
+          b = n; /* first rising position at distance >= dj */
+          while (a < b) {
+            const int64_t c = (a + b) >> 1;
+            if (fabsf(tbuf[c]) < dj) a = c + 1;
+            else b = c;
+          }
+          rank = (m - past_eq) + (j - first_eq) + (a - m);
+        }
+        tmerged[rank] = (int32_t)j;
+        trank[j] = (int32_t)rank;
+      }
+      __syncthreads();
+      /* the probabilities in selection order, added until they reach typical_p with at least min_keep */
+      const int64_t req = keep > 1 ? keep : 1;
+      block_records(n, [&](int64_t k) { return val(tmerged[k]); }, termPv, recs, gsum, tbuf);
+      if (w == 0) {
+        float S;
+        const int f = bl_seq_walk(n, termS, [&](int64_t g) { return recs[g]; }, true, sp.typical_p, req - 1, S, lane);
+        if (lane == 0) sh.ires[0] = f;
+      }
+      __syncthreads();
+      const int f = sh.ires[0];
+      const int64_t nk = f >= 0 ? f + 1 : n;
+      /* equal values on both sides of the stop: which of them the reference keeps is the heap's order */
+      if (nk < n && val(tmerged[nk - 1]) == val(tmerged[nk])) status |= BL_SE_TIE;
+      __syncthreads();
+      /* stable compaction of the kept entries to the list's front, a tile at a time */
+      int64_t off = 0;
+      for (int64_t base = 0; base < n; base += blockDim.x) {
+        const int64_t j = base + t;
+        const uint64_t k = j < n ? keys_w[j] : 0ull;
+        const int fl = j < n && trank[j] < nk ? 1 : 0;
+        const int incl = bl_wscan_add(fl, lane);
+        if (lane == 63) sh.red_i[w] = incl;
+        __syncthreads();
+        int before = incl - fl, tot = 0;
+        for (int q = 0; q < SEL_NW; q++) {
+          if (q < w) before += sh.red_i[q];
+          tot += sh.red_i[q];
+        }
+        if (fl) keys_w[off + before] = k;
+        off += tot;
+        __syncthreads();
+      }
+      n_list = nk;
+      cutoff = nk;
+      if (keep > nk) keep = nk;
+      if (status) return out;
+    }
     if (sp.top_p < 1.0f) {
       block_records(n_list, val, termPv, recs, gsum, tbuf);
       if (w == 0) {
@@ -3036,6 +3155,8 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
       const float T = sp.temperature;
       /* the exponent pass's candidates (four spans deep for a top-k grammar row), top-n-sigma's survivors */
       float thr = fmaxf(Mc - (gram && (mode & BL_M_TOPK) ? 4.0f : 1.0f) * bl_cand_span(sp), tns_thr);
+      /* typical_p keeps every value: those below Mc - 104 have exp(v - v0) = 0, probability 0 */
+      if (sp.typical_p < 1.0f && !gram) thr = fmaxf(thr, Mc - 104.0f);
       if (!filt && !(gram && (mode & BL_M_TOPK))) { /* a top-k grammar row draws from a subset: no cut */
         /* the draw adds exp((v - M) / T) in descending order. With u = 2^-24 and m <= V terms, the float
          * running sum past every term >= 2^(k-24) is at least (1 - g) (S - V 2^(k-24)), g = m u / (1 - m u)
@@ -3510,23 +3631,28 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
   auto val = [&](int64_t j) -> float { return keys[j] ? ckey_v(keys[j]) : -1.0e30f; };
   int64_t keep = 1;
   const bool miro = sampled && (mode & BL_M_MIRO) != 0;
-  const bool short_list = !miro && n_list <= BL_SERIAL_MAX;
+  bool short_list = !miro && n_list <= BL_SERIAL_MAX;
   if (sampled && !miro) {
     if (!ranked_supported(sp, n_list, n_logical, keep)) status |= BL_SE_UNSUPPORTED;
     if (!status && short_list) ranked_terms(sp, val, n_list, sh);
   }
-  /* the typical filter (complete short lists; the candidate span keeps every value for it) */
-  bool typ = false;
+  /* the typical filter: complete short lists by the block (typical_filter); a full-vocabulary list, which
+   * holds every value whose probability is not 0 (the candidate span keeps every value for it), inside the
+   * long draw */
+  bool typ = false, typ_long = false;
   int n_draw = (int)n_list;
   int64_t nlog_draw = n_logical;
   if (sampled && !miro && !status && sp.typical_p < 1.0f && n_logical > 1) {
-    if (!short_list || n_list != n_logical) {
-      status |= BL_SE_UNSUPPORTED;
-    } else {
+    if (short_list && n_list == n_logical) {
       typ = true;
       n_draw = typical_filter(sp, (int)n_list, (mode & BL_M_FULL) != 0, sh, status);
       nlog_draw = n_draw;
       if (keep > n_draw) keep = n_draw;
+    } else if ((mode & BL_M_FULL) && !gram) {
+      typ_long = true;
+      short_list = false;
+    } else {
+      status |= BL_SE_UNSUPPORTED;
     }
   }
   /* a draw position -> its list position */
@@ -3662,7 +3788,9 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
       }
       float *tbuf = reinterpret_cast<float *>(d.sortk + (int64_t)row * 2 * V); /* free once the list is sorted */
       dr = miro ? sample_mirostat(sp, val, n_list, n_logical, mk, rng, skip, recs, gsum, tbuf, sh, status)
-                : sample_ranked_long(sp, val, n_list, n_logical, keep, rng, skip, split_S, recs, gsum, tbuf, sh, status);
+                : sample_ranked_long(sp, val, n_list, n_logical, keep, rng, skip, split_S, recs, gsum, tbuf, sh, status,
+                                     typ_long ? keys : nullptr, reinterpret_cast<int32_t *>(d.full_v) + (int64_t)row * d.nb * BL_EB,
+                                     d.full_i + (int64_t)row * d.nb * BL_EB);
       pos = dr.pos;
       dterm = tbuf;
       dshift = dr.first;
@@ -3722,7 +3850,7 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
                                          return false;
                                        });
             }
-          } else {
+          } else if (!typ_long) { /* a typical row's list is compacted: the heap's prefix is gone (a tie) */
             hid = heap_tie_id([&](int64_t j) { return keys[j]; }, keys == sh.c.keys, n_list, pos, V,
                               d.full_i + (int64_t)row * d.nb * BL_EB, sh);
           }

@@ -34,8 +34,8 @@ enum {
   BL_EUNSUPPORTED = -8,    /* a sampler stage this library does not run on the device yet: DRY windows above
                               2048 tokens or a negative dry_allowed_length (rejected by bl_slot_reset); XTC,
                               mirostat, adaptive-p, DRY or a grammar on speculative rows, or more than 32
-                              drafts with history-dependent penalties; typical_p over a full-vocabulary list
-                              above 512 candidates; a mirostat draw that falls through to a prefix end past
+                              drafts with history-dependent penalties; typical_p over a list that is neither
+                              complete nor a full-vocabulary rank; a mirostat draw that falls through to a prefix end past
                               the candidates within 17.6 T of the maximum */
   BL_ETIE = -9,            /* a draw on equal logits whose heap order is past the device simulation (more than
                               8192 values at or above the tied one), equal allowed values of a grammar row

@@ -392,6 +392,49 @@ def run_halfway(BL, steps):
     return None
 
 
+TYPICAL_ROWS = [(dict(temperature=0.8, typical_p=0.9), 3.0),
+                (dict(temperature=1.0, typical_p=0.5, min_keep=3), 2.0),
+                (dict(temperature=0.7, typical_p=0.95, top_p=0.9, min_p=0.02), 3.0),
+                (dict(temperature=1.2, typical_p=0.8, dynatemp_range=0.5), 1.5),
+                (dict(temperature=0.9, typical_p=0.3), 4.0)]
+
+
+def run_typical(BL, steps, V):
+    """typical_p over full-vocabulary lists (every token a candidate) at vocabulary V: entropy, the selection
+    order by distance |-ln p - H| (the two monotone runs of the ranked list merged), the walk to typical_p and
+    min_keep, then top-p / min-p / dynamic temperature and the draw over the kept entries, against the oracle's
+    slot step (whose selection loop is quadratic: V stays small). Distinct float32 values (no heap ties)."""
+    R = len(TYPICAL_ROWS)
+    rng = np.random.default_rng(61 + V)
+    ctx = BL.Context(V, R, R)
+    L = O.lib()
+    hs = []
+    for r, (kw, _) in enumerate(TYPICAL_ROWS):
+        ctx.slot_reset(r, BL.Params(**kw), BL.seed_rng(990 + r))
+        op = O.params(**kw)
+        hs.append(L.orc_slot_new(O.C.byref(op), BL.seed_rng(990 + r), None, 0, None, 0, None, None, 0))
+    buf = MEM.zeros(R * V, np.float32)
+    try:
+        for t in range(steps):
+            x = np.concatenate([distinct((rng.standard_normal(V) * sg).astype(np.float32)) for (_, sg) in TYPICAL_ROWS])
+            buf.upload(x)
+            tok = ctx.sample_step(list(range(R)), buf.ptr, V)[0]
+            for r in range(R):
+                ot, olp = np.zeros(1, np.int32), np.zeros(1, np.float32)
+                oti, otl = np.zeros(1, np.int32), np.zeros(1, np.float32)
+                eog = O.C.c_int()
+                row = np.ascontiguousarray(x[r * V:(r + 1) * V])
+                assert L.orc_slot_step(hs[r], O.fp(row), V, 0, 1, O.ip(ot), O.fp(olp), O.ip(oti), O.fp(otl),
+                                       O.C.byref(eog)) == 0
+                if tok[r] != ot[0]:
+                    return f"step {t} row {r} {TYPICAL_ROWS[r][0]}: token {tok[r]} vs {ot[0]}"
+    finally:
+        for h in hs:
+            L.orc_slot_free(h)
+        ctx.close()
+    return None
+
+
 TNS_ROWS = [dict(temperature=0.8, top_k=0, top_n_sigma=1.0),
             dict(temperature=1.0, top_k=64, top_n_sigma=0.5, logprobs=1, n_probs=5),
             dict(temperature=0.7, top_k=0, top_n_sigma=2.0, top_p=0.9),
@@ -1189,6 +1232,9 @@ def main():
                 for kw in ({"temperature": 0.8}, {"temperature": 0.8, "top_k": 40}):
                     results.append((f"sampled grammar ties case {c} top_k {kw.get('top_k', 0)}",
                                     run_grammar_case(BL, c, int(f[2]) if len(f) > 2 else 30, kw, quant=0.5)))
+        elif kind == "typical":  # typical:steps:V
+            V = int(f[2]) if len(f) > 2 else SMALL_V
+            results.append((f"typical rows at V={V}", run_typical(BL, int(f[1]), V)))
         elif kind == "halfway":
             results.append(("halfway tail terms", run_halfway(BL, int(f[1]))))
         elif kind == "noalloc":

@@ -58,15 +58,16 @@ def test_bound_rows_survive_sync_steps_and_spec_verify_on_other_slots():
 
 
 def test_async_failure_gives_token_minus_one_and_slot_status():
-    """A full-vocabulary typical_p row is outside the device path (BL_EUNSUPPORTED at the step): through the
-    asynchronous step its token is -1, nothing is committed, bl_slot_status reports the error once, and the
-    other rows of the step are unaffected."""
+    """A full-vocabulary draw on a row of equal logits lands on a tie of V values, past the device's heap
+    simulation (BL_ETIE at the step): through the asynchronous step its token is -1, nothing is committed,
+    bl_slot_status reports the error once, and the other rows of the step are unaffected."""
     dev = torch.device("cuda:0")
     ctx = BL.Context(V, 2, 2)
     reset_c2(ctx, 0, 1)
-    ctx.slot_reset(1, BL.Params(temperature=0.8, top_k=0, typical_p=0.9), BL.seed_rng(9))
+    ctx.slot_reset(1, BL.Params(temperature=0.8, top_k=0), BL.seed_rng(9))
     logits = torch.empty(2 * V, dtype=torch.float32, device=dev)
     ctx.synth_logits(logits.data_ptr(), V, 2, SEED, 0, 2, V)
+    logits[V:].zero_()
     rng_before = ctx.slot_rng(1)
     ctx.bind_rows([0, 1])
     tok = torch.zeros(2, dtype=torch.int32, device=dev)
@@ -77,7 +78,7 @@ def test_async_failure_gives_token_minus_one_and_slot_status():
     assert got[1] == -1 and got[0] >= 0
     with pytest.raises(BL.BLError) as e:
         ctx.slot_status(1)
-    assert e.value.code == BL.BL_EUNSUPPORTED
+    assert e.value.code == BL.BL_ETIE
     ctx.slot_status(1)  # cleared by the first call
     ctx.slot_status(0)
     assert ctx.slot_rng(1) == rng_before  # nothing committed

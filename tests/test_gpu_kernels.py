@@ -93,6 +93,16 @@ def test_halfway_tail_terms():
     assert err is None, err
 
 
+@pytest.mark.parametrize("V", [3000, 5003, 20000])
+def test_typical_full_vocabulary_rows(V):
+    """typical_p over full-vocabulary lists (the LDS sort at V=3000, the bucket sort above 4096 candidates):
+    entropy, the selection order merged from the ranked list's two monotone runs, the walk to typical_p and
+    min_keep, then top-p / min-p / dynamic temperature and the draw, against the oracle's slot step."""
+    print(f"five typical rows, V={V}", flush=True)
+    err = RP.run_typical(BL, 6 if V < 10000 else 2, V)
+    assert err is None, err
+
+
 def test_mirostat_v2_rows():
     print("three mirostat v2 rows, V=5003: 40 steps", flush=True)
     err = RP.run_mirostat(BL, 40)

@@ -252,12 +252,10 @@ def test_errors_are_reported(cuda):
     with pytest.raises(BL.BLError) as e:
         ctx.slot_reset(0, BL.Params(temperature=1.0, mirostat=2, logprobs=1, post_sampling_probs=1), 1)
     assert e.value.code == BL.BL_EPARAM and "standard unconstrained sampling chain" in str(e.value)
-    # the typical filter over a full-vocabulary list longer than the short-list path: reported at the step
+    # the typical filter over a full-vocabulary list longer than the short-list path: drawn on the device
     ctx.slot_reset(0, BL.Params(temperature=1.0, typical_p=0.5), 1)
     row = torch.randn(1000, device=cuda)
-    with pytest.raises(BL.BLError) as e:
-        ctx.sample_step([0], row.data_ptr(), 1000)
-    assert e.value.code == BL.BL_EUNSUPPORTED
+    assert 0 <= ctx.sample_step([0], row.data_ptr(), 1000)[0][0] < 1000
     with pytest.raises(BL.BLError) as e:
         ctx.slot_reset(0, BL.Params(), 1, bias={5000: 1.0})
     assert e.value.code == BL.BL_EPARAM and "outside the vocabulary" in str(e.value)

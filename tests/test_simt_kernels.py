@@ -143,6 +143,14 @@ def test_top_n_sigma(simt_lib):
     assert out.count("ok   small case") == 3 and "ok   top-n-sigma rows at V=151936" in out
 
 
+def test_typical_full_vocabulary(simt_lib):
+    """typical_p over full-vocabulary lists at V=3000 (sorted in LDS) and V=5003 (bucket sort): the selection
+    order merged from the two monotone runs of distance along the ranked list, the walk to typical_p, the
+    compaction and the later stages, against the oracle's typical_filter and slot step."""
+    out = _run(simt_lib, ["typical:6:3000", "typical:6:5003"], {"SIMT_ORDER": "rand"})
+    assert "ok   typical rows at V=3000" in out and "ok   typical rows at V=5003" in out
+
+
 def test_dynatemp_exponents(simt_lib):
     """Dynamic temperature with exponents 0.5 and 2.3 (small cases 24-25: a full-vocabulary min-p row and a
     top-k row with post-sampling probabilities), the normalised entropy raised by the device's glibc powf."""
