@@ -1337,6 +1337,7 @@ struct sel_cand {
 #define BL_BOFF_BYTES (((BL_MAX_CHUNKS * BL_SUBS + 1) * 4 + 15) / 16 * 16)
 #define BL_RTILE 4096 /* keys per rank tile */
 #define BL_SPLIT_TIES 8 /* halfway tail terms a plain draw's head/tail split resolves */
+#define BL_SPLIT_HEAD_MAX 2048 /* longest head the split ranks (its sum is added by one wavefront) */
 #define BL_CAND_U 8   /* candidate loads in flight per lane */
 static_assert(BL_BOFF_BYTES + BL_RTILE * 8 <= sizeof(sel_norm), "rank tile");
 static_assert(BL_RTILE % BL_SEL_THREADS == 0, "rank tile");
@@ -3318,9 +3319,14 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
           run += loc[q];
         }
         __syncthreads();
-        const int h_end = head && sh.split_h < BL_NBUCKET - 1 ? sh.split_h + 1 : BL_NBUCKET;
-        const bool tail = h_end < BL_NBUCKET;
+        int h_end = head && sh.split_h < BL_NBUCKET - 1 ? sh.split_h + 1 : BL_NBUCKET;
+        bool tail = h_end < BL_NBUCKET;
         nk = tail ? (int)cnt[h_end] : nall; /* the ranked head's length */
+        if (tail && nk > BL_SPLIT_HEAD_MAX) { /* a long head: every bucket is ranked (and summed by the draw) */
+          h_end = BL_NBUCKET;
+          tail = false;
+          nk = nall;
+        }
         /* the head scattered by bucket; the tail's ulps of 2^K counted (every thread's own sum is exact: at most
          * 2^23 per term) */
         const double tsc = bl_u2d((uint64_t)(23 - Kb + 1023) << 52);
@@ -3423,7 +3429,8 @@ __global__ __launch_bounds__(BL_SEL_THREADS) void bl_k_select(bl_dev d, const fl
         }
         if (!tail) break;
         /* the head's exact sum (the draw's terms exp((v - v0) / T), v0 = Mc the first value), by wavefront 0:
-         * each lane's term, 64 at a time, added in list order through readlane (every lane alike) */
+         * each lane's term, 64 at a time, added in list order through readlane (every lane alike); the head
+         * holds at most BL_SPLIT_HEAD_MAX entries */
         if (w == 0) {
           float Sh = 0.0f;
           for (int b0 = 0; b0 < nk; b0 += 64) {
