@@ -1426,6 +1426,8 @@ __device__ __forceinline__ sel_draw ranked_serial(const bl_slot_dev &sp, int n, 
   const int lane = threadIdx.x & 63;
   const float *ser_e = sh.ser_e, *ser_v = sh.ser_v;
   float *ser_r = sh.ser_r;
+  constexpr int NBAT = BL_SERIAL_MAX / 64;
+  float pv[NBAT]; /* the draw's running sum after term b*64 + lane, in batch b (when kept: have_p) */
   const bool xtc = bl_xtc_on(sp);
   const bool filt = bl_probs_on(sp);
   int64_t cut = n_logical;
@@ -1433,16 +1435,37 @@ __device__ __forceinline__ sel_draw ranked_serial(const bl_slot_dev &sp, int n, 
   float sum_exp = 0.0f;
   /* term j of a batch: lane j - b0 */
   auto at = [&](const float *arr, int j) { return j < n ? arr[j] : 0.0f; };
+  /* without XTC or a dynamic temperature the draw's terms run from position 0 at T: their running sums
+   * (the tempered sum's and the draw's walk, the same float additions) are kept in pv, formed beside the
+   * softmax sum as a second chain of additions; the tempered sum is then one entry and the draw a ballot */
+  const bool pfx = !xtc && !(sp.dynatemp_range > 0.0f) && !pre;
+  bool have_p = false;
+#pragma unroll
+  for (int b = 0; b < NBAT; b++) pv[b] = 0.0f;
   if (filt) {
     /* `pre`: ser_e already holds the probabilities (after the typical filter), divided here by 1 */
     if (pre) {
       sum_exp = 1.0f;
     } else {
-      for (int b0 = 0; b0 < n; b0 += 64) {
+      float tp = 0.0f;
+#pragma unroll
+      for (int b = 0; b < NBAT; b++) {
+        const int b0 = b * 64;
+        if (b0 >= n) break;
         const float e = at(ser_e, b0 + lane);
+        const float r = pfx ? at(ser_r, b0 + lane) : 0.0f;
         const int m = n - b0 < 64 ? n - b0 : 64;
-        for (int k = 0; k < m; k++) sum_exp += sel_rl(e, k);
+        float mine = 0.0f;
+        for (int k = 0; k < m; k++) {
+          sum_exp += sel_rl(e, k);
+          if (pfx) {
+            tp += sel_rl(r, k);
+            mine = lane == k ? tp : mine;
+          }
+        }
+        pv[b] = mine;
       }
+      have_p = pfx;
     }
     if (sp.top_p < 1.0f) {
       float cum = 0.0f;
@@ -1569,23 +1592,56 @@ __device__ __forceinline__ sel_draw ranked_serial(const bl_slot_dev &sp, int n, 
     }
   }
   float S = 0.0f;
-  for (int b0 = first; b0 < n_eff; b0 += 64) {
-    const float e = b0 + lane < n_eff ? ser_r[b0 + lane] : 0.0f;
-    const int m = n_eff - b0 < 64 ? n_eff - b0 : 64;
-    for (int k = 0; k < m; k++) S += sel_rl(e, k);
+  if (have_p) { /* first = 0: the running sums are pv's */
+    const int last = n_eff - 1;
+#pragma unroll
+    for (int b = 0; b < NBAT; b++)
+      if (last >= 0 && b == (last >> 6)) S = sel_rl(pv[b], last & 63);
+  } else if (pfx) { /* the same with the terms added here (no softmax sum was formed): first = 0 */
+#pragma unroll
+    for (int b = 0; b < NBAT; b++) {
+      const int b0 = b * 64;
+      if (b0 >= n_eff) break;
+      const float e = b0 + lane < n_eff ? ser_r[b0 + lane] : 0.0f;
+      const int m = n_eff - b0 < 64 ? n_eff - b0 : 64;
+      float mine = 0.0f;
+      for (int k = 0; k < m; k++) {
+        S += sel_rl(e, k);
+        mine = lane == k ? S : mine;
+      }
+      pv[b] = mine;
+    }
+    have_p = true;
+  } else {
+    for (int b0 = first; b0 < n_eff; b0 += 64) {
+      const float e = b0 + lane < n_eff ? ser_r[b0 + lane] : 0.0f;
+      const int m = n_eff - b0 < 64 ? n_eff - b0 : 64;
+      for (int k = 0; k < m; k++) S += sel_rl(e, k);
+    }
   }
   if (S_whole > 0.0f) S = S_whole; /* the list is the head of a longer one whose sum is known */
   const float target = bl_rng_f32(&st) * S;
-  float run = 0.0f;
   int64_t f = -1;
-  for (int b0 = first; b0 < n_eff && f < 0; b0 += 64) {
-    const float e = b0 + lane < n_eff ? ser_r[b0 + lane] : 0.0f;
-    const int m = n_eff - b0 < 64 ? n_eff - b0 : 64;
-    for (int k = 0; k < m; k++) {
-      run += sel_rl(e, k);
-      if (run >= target) {
-        f = b0 + k;
-        break;
+  if (have_p) { /* the first position whose running sum reaches the target (the sums never decrease) */
+#pragma unroll
+    for (int b = 0; b < NBAT; b++) {
+      const int b0 = b * 64;
+      if (b0 < n_eff) {
+        const unsigned long long bm = __ballot(b0 + lane < n_eff && pv[b] >= target);
+        if (bm && f < 0) f = b0 + __ffsll((long long)bm) - 1;
+      }
+    }
+  } else {
+    float run = 0.0f;
+    for (int b0 = first; b0 < n_eff && f < 0; b0 += 64) {
+      const float e = b0 + lane < n_eff ? ser_r[b0 + lane] : 0.0f;
+      const int m = n_eff - b0 < 64 ? n_eff - b0 : 64;
+      for (int k = 0; k < m; k++) {
+        run += sel_rl(e, k);
+        if (run >= target) {
+          f = b0 + k;
+          break;
+        }
       }
     }
   }
