@@ -99,7 +99,9 @@ const char *bl_last_error(void);
 /* The HIP stream the context's work is ordered on (hipStream_t); NULL selects the context's own. */
 int bl_set_stream(bl_ctx *ctx, void *stream);
 
-/* End-of-generation registry: src/sampling.br:200-237 (set_eog_tokens / is_eog_token). */
+/* End-of-generation registry: src/sampling.br:200-237 (set_eog_tokens / is_eog_token). Every step reads the
+ * current registry (ignore_eos suppression, the grammar's end of sequence); a step graph captured before
+ * a change holds the old registry's length: create a new graph after bl_set_eog. */
 int bl_set_eog(bl_ctx *ctx, int32_t eos_id, const int32_t *eog_ids, int n_eog);
 
 /* Request seeds (host arithmetic, no device work; callable without a GPU):
@@ -222,8 +224,8 @@ int bl_sample_rows_noalloc(int device, void *stream, const bl_params *params, ui
  * stream; bl_stream_sync waits for the stream. A replay reads the slots' current state and parameters,
  * so it follows later bl_slot_commit calls and resets that keep each row's kind; rebinding rows,
  * changing buffers, or a reset that changes which passes a row needs (logprobs, top-k / n_probs, a
- * grammar, full-vocabulary sampling) needs a new graph. BL_EPARAM while kernel timing is enabled (it
- * synchronises). */
+ * grammar, full-vocabulary sampling) needs a new graph, as does bl_set_eog. BL_EPARAM while kernel timing is
+ * enabled (it synchronises). */
 int bl_step_graph_create(bl_ctx *ctx, int B, const float *d_logits, int64_t ld, int32_t *d_tokens, float *d_logprobs,
                          int32_t *d_top_ids, float *d_top_logprobs, int top_stride, void **graph_out);
 int bl_step_graph_launch(bl_ctx *ctx, void *graph);
