@@ -92,7 +92,9 @@ void bl_params_default(bl_params *p);
 
 /* Context on `device` for up to `max_slots` (<= 32767) concurrent requests and `max_rows` rows per call,
  * over a vocabulary of `vocab` tokens (<= 4,194,304). Replaces nothing in the reference (it holds no
- * device state). */
+ * device state). Device memory: about 20 * vocab bytes per slot (a 16-byte record slot and a 4-byte index
+ * per token: 3 MB at V = 151936, 5.2 MB at V = 262144), plus windows and per-row buffers; BL_EDEVICE
+ * when an allocation fails. */
 int bl_create(int device, int max_slots, int max_rows, int vocab, bl_ctx **out);
 void bl_destroy(bl_ctx *ctx);
 const char *bl_last_error(void);
