@@ -183,7 +183,7 @@ def test_small_cases_address_sanitizer():
         pre.append(p)
     env = {"LD_PRELOAD": " ".join(pre), "ASAN_OPTIONS": "detect_leaks=0", "UBSAN_OPTIONS": "print_stacktrace=1"}
     out = _run(os.path.join(SIMT, "_build", "libbl_simt_asan.so"), ["small:0-20:3", "coarse:1,5:3", "ramp:8:2", "grammar:0-6:20", "q4:2,9:4", "dry:0-8:3",
-                                                                   "halfway:3"], env)
+                                                                   "halfway:3", "typical:1:3000", "gstie:0-1:10"], env)
     assert "ERROR: AddressSanitizer" not in out and "runtime error" not in out
 
 
