@@ -1259,7 +1259,7 @@ int bl_spec_verify(bl_ctx *c, const int32_t *slots, int B, int k, const float *d
   rows.status = d_stat;
   rows.lp = nullptr; /* no logprobs are returned for speculative rows */
   if (pen) {
-    hipLaunchKernelGGL(bl_k_spec_delta, dim3(B), dim3(64), 0, c->stream, c->d, d_sslot, d_drafts, k,
+    hipLaunchKernelGGL(bl_k_spec_delta, dim3(B), dim3(BL_SPEC_DCAP / 2 + 64), 0, c->stream, c->d, d_sslot, d_drafts, k,
                        c->d_delta, c->d_delta_n);
     HIPCHK(hipGetLastError());
     rows.delta = c->d_delta;

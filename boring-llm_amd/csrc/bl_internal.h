@@ -97,7 +97,7 @@ struct alignas(16) bl_rec {
 /* A speculative row's correction to one token's counts: row i of a sequence is sampled with the drafts
  * before it appended to the history (src/server.br:1173-1216), so each such draft adds to its reply count
  * and window count, and window entries the drafts push out subtract from theirs. */
-#define BL_SPEC_DCAP 64 /* corrections per row: drafts before the row plus the entries they evict */
+#define BL_SPEC_DCAP 256 /* corrections per row: drafts before the row plus the entries they evict (2 k) */
 struct bl_sdelta {
   int32_t tok;
   int16_t dcnt;  /* reply count */

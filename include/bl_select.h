@@ -33,7 +33,7 @@ enum {
   BL_EGRAMMAR_AMBIG = -7,  /* "grammar is left-recursive or too ambiguous to match" (src/grammar.br:354) */
   BL_EUNSUPPORTED = -8,    /* a sampler stage this library does not run on the device yet: DRY windows above
                               2048 tokens or a negative dry_allowed_length (rejected by bl_slot_reset); XTC,
-                              mirostat, adaptive-p, DRY or a grammar on speculative rows, or more than 32
+                              mirostat, adaptive-p, DRY or a grammar on speculative rows, or more than 128
                               drafts with history-dependent penalties; typical_p over a list that is neither
                               complete nor a full-vocabulary rank; a mirostat draw that falls through to a prefix end past
                               the candidates within 17.6 T of the maximum */

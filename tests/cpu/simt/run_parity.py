@@ -706,12 +706,13 @@ def run_w5(BL, steps):
     return None
 
 
-def run_spec_penalties(BL, rounds):
+def run_spec_penalties(BL, rounds, K=6):
     """Speculative verification of rows with frequency/presence/repeat penalties (row i sees the drafts before
     it in its history and reply): every row's token, the accepted length and, at the end, the RNG state equal
     the oracle's spec_verify over the same rows, round after round (the device commits in between). Drafts
-    repeat a few hot tokens so that the penalties decide rows; a 3-token window makes drafts leave it."""
-    V, K = 997, 6
+    repeat a few hot tokens so that the penalties decide rows; a 3-token window makes drafts leave it. K drafts
+    per sequence (row K holds up to 2 K count corrections)."""
+    V = 997
     confs = [dict(temperature=0.0, repeat_penalty=1.3, repeat_last_n=3, frequency_penalty=0.4, presence_penalty=0.2),
              dict(temperature=0.8, top_k=0, repeat_penalty=1.2, repeat_last_n=8, frequency_penalty=0.3,
                   presence_penalty=0.1),
@@ -1198,8 +1199,9 @@ def main():
             results.append(("workload 4", run_w4(BL, int(f[1]), int(f[2]) if len(f) > 2 else 32)))
         elif kind == "w5":
             results.append(("workload 5", run_w5(BL, int(f[1]))))
-        elif kind == "specpen":
-            results.append(("speculative rows with penalties", run_spec_penalties(BL, int(f[1]))))
+        elif kind == "specpen":  # specpen:rounds[:K]
+            K = int(f[2]) if len(f) > 2 else 6
+            results.append((f"speculative rows with penalties, {K} drafts", run_spec_penalties(BL, int(f[1]), K)))
         elif kind == "async":
             results.append(("asynchronous step", run_async(BL, int(f[1]))))
         elif kind == "pair":

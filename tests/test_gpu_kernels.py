@@ -143,3 +143,7 @@ def test_spec_verify_with_penalties():
     print("speculative rows with penalties: 12 rounds x 4 sequences x 7 rows", flush=True)
     err = RP.run_spec_penalties(BL, 12)
     assert err is None, err
+    # 100 drafts: the last row carries up to 200 count corrections
+    print("speculative rows with penalties: 3 rounds x 4 sequences x 101 rows", flush=True)
+    err = RP.run_spec_penalties(BL, 3, 100)
+    assert err is None, err

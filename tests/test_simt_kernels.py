@@ -109,8 +109,8 @@ def test_full_vocabulary_workloads(simt_lib):
 def test_spec_verify_with_penalties(simt_lib):
     """Speculative rows whose frequency/presence/repeat penalties count the drafts before them (and the window
     entries those drafts evict) against the oracle's spec_verify, over rounds of device commits."""
-    out = _run(simt_lib, ["specpen:8"], {"SIMT_ORDER": "rand"})
-    assert "ok   speculative rows with penalties" in out
+    out = _run(simt_lib, ["specpen:8", "specpen:2:100"], {"SIMT_ORDER": "rand"})
+    assert "ok   speculative rows with penalties, 6 drafts" in out and "ok   speculative rows with penalties, 100 drafts" in out
 
 
 def test_grammar_masks_and_tokens(simt_lib):
