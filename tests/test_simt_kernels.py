@@ -93,7 +93,7 @@ def test_unfiltered_candidate_cut(simt_lib):
     buckets' sums; the constructed rows put terms exactly halfway between two multiples of u into the tail (3
     copies, resolved by the running sum's parity; 20 copies, past the split's limit, so the whole list is
     ranked)."""
-    out = _run(simt_lib, ["unfilt:12", "halfway:6"], {"SIMT_ORDER": "rev"})
+    out = _run(simt_lib, ["unfilt:12", "halfway:3"], {"SIMT_ORDER": "rev"})
     assert "ok   unfiltered rows at V=151936" in out and "ok   halfway tail terms" in out
 
 
@@ -109,7 +109,7 @@ def test_full_vocabulary_workloads(simt_lib):
 def test_spec_verify_with_penalties(simt_lib):
     """Speculative rows whose frequency/presence/repeat penalties count the drafts before them (and the window
     entries those drafts evict) against the oracle's spec_verify, over rounds of device commits."""
-    out = _run(simt_lib, ["specpen:8", "specpen:2:100"], {"SIMT_ORDER": "rand"})
+    out = _run(simt_lib, ["specpen:6", "specpen:1:100"], {"SIMT_ORDER": "rand"})
     assert "ok   speculative rows with penalties, 6 drafts" in out and "ok   speculative rows with penalties, 100 drafts" in out
 
 
@@ -131,7 +131,7 @@ def test_greedy_grammar_ties(simt_lib):
     and 40: the lowest index while the widening levels rank by top_k_select (value desc, index asc), the
     first allowed token of the heap's extraction order (all_candidates_sorted) once a level reaches V.
     Sampled rows (T 0.8) whose draw lands on equal allowed values: the allowed token the heap puts there."""
-    out = _run(simt_lib, ["gtie:0-7:30", "gstie:0-7:30"], {"SIMT_ORDER": "rand"})
+    out = _run(simt_lib, ["gtie:0-7:20", "gstie:0-7:20"], {"SIMT_ORDER": "rand"})
     assert out.count("ok   grammar ties case") == 16 and out.count("ok   sampled grammar ties case") == 16
 
 
@@ -147,7 +147,7 @@ def test_typical_full_vocabulary(simt_lib):
     """typical_p over full-vocabulary lists at V=3000 (sorted in LDS) and V=5003 (bucket sort): the selection
     order merged from the two monotone runs of distance along the ranked list, the walk to typical_p, the
     compaction and the later stages, against the oracle's typical_filter and slot step."""
-    out = _run(simt_lib, ["typical:6:3000", "typical:6:5003"], {"SIMT_ORDER": "rand"})
+    out = _run(simt_lib, ["typical:4:3000", "typical:3:5003"], {"SIMT_ORDER": "rand"})
     assert "ok   typical rows at V=3000" in out and "ok   typical rows at V=5003" in out
 
 
@@ -183,7 +183,7 @@ def test_small_cases_address_sanitizer():
         pre.append(p)
     env = {"LD_PRELOAD": " ".join(pre), "ASAN_OPTIONS": "detect_leaks=0", "UBSAN_OPTIONS": "print_stacktrace=1"}
     out = _run(os.path.join(SIMT, "_build", "libbl_simt_asan.so"), ["small:0-20:3", "coarse:1,5:3", "ramp:8:2", "grammar:0-6:20", "q4:2,9:4", "dry:0-8:3",
-                                                                   "halfway:3", "typical:1:3000", "gstie:0-1:10"], env)
+                                                                   "halfway:1", "typical:1:3000", "gstie:0-1:10"], env)
     assert "ERROR: AddressSanitizer" not in out and "runtime error" not in out
 
 
